@@ -1,0 +1,150 @@
+/*
+ * nurostream_amd -- C ABI of the MI355X (gfx950) MoE expert hot path.
+ *
+ * Every entry point takes plain device pointers, element/byte counts and a
+ * HIP stream handle (`void *stream`, a hipStream_t; NULL = the null stream),
+ * returns an NSX_* status code, and never allocates device memory. The
+ * message of the last failure on the calling thread is nsx_last_error().
+ *
+ * The reference (hareramray/nurostream, Python + Triton) has no C ABI; each
+ * function below names the Python seam it replaces (paths relative to the
+ * reference's neurostream/ package).
+ */
+#ifndef NUROSTREAM_AMD_H
+#define NUROSTREAM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSX_ABI_VERSION 1
+
+/* status codes; the Python shim maps them onto the reference's exceptions */
+enum {
+  NSX_OK = 0,
+  NSX_EINVAL = 1,   /* ValueError: shapes, sizes, windows */
+  NSX_ETYPE = 2,    /* TypeError: wrong buffer element type */
+  NSX_ENOTIMPL = 3, /* NotImplementedError: unsupported ggml type */
+  NSX_EHIP = 4,     /* RuntimeError: HIP runtime failure */
+  NSX_EKERNEL = 5   /* RuntimeError: a kernel's own bounded check failed */
+};
+
+/* ggml type ids (format/gguf.py:19-35) */
+enum {
+  NSX_F32 = 0, NSX_F16 = 1, NSX_Q4_0 = 2, NSX_Q8_0 = 8, NSX_Q4_K = 12,
+  NSX_BF16 = 30, NSX_MXFP4 = 39
+};
+
+/* activation / output element types */
+enum { NSX_DT_F32 = 0, NSX_DT_F16 = 1, NSX_DT_BF16 = 2 };
+
+/* expert weight layouts */
+enum {
+  NSX_LAYOUT_GGUF = 0, /* raw GGUF rows, as read from the file */
+  NSX_LAYOUT_T64 = 1   /* 64-row interleaved tiles (nsx_t64_pack) */
+};
+
+/* routers and activations */
+enum { NSX_ROUTE_GPTOSS = 0, NSX_ROUTE_QWEN3 = 1 };
+enum { NSX_ACT_CLAMPED_SWIGLU = 0, NSX_ACT_SILU_MUL = 1 };
+
+const char *nsx_last_error(void);
+int nsx_abi_version(void);
+
+/* Checks, on the current device, that the gfx950 FP4 conversion instruction
+ * decodes all 256 byte values exactly as the MXFP4 table does; `scratch` is
+ * one device uint32. No reference counterpart (a load-time self test). */
+int nsx_selftest(uint32_t *scratch, void *stream);
+
+/* compute/quant.py:153-184 dequantize(raw, dtype, n_elements, out_dtype).
+ * raw: `raw_bytes` bytes of ggml blocks (any alignment); out: n_elements of
+ * out_dtype. Bit-exact with the reference for Q4_0, Q8_0, Q4_K, MXFP4. */
+int nsx_dequantize(int ggml_type, const void *raw, int64_t raw_bytes,
+                   int64_t n_elements, void *out, int out_dtype, void *stream);
+
+/* compute/triton_kernels.py:199-228 fused_gemv(raw, dtype, x, n_rows, K).
+ * y[t, r] = sum_k x[t, k] * dequant(raw)[r, k] for t < T, fp32 accumulate.
+ * raw: n_rows * row_bytes GGUF bytes (any alignment for 32-element formats,
+ * 4-byte aligned for Q4_K); x: (T, K) row-major in x_dtype; y: (T, n_rows)
+ * fp32. The reference fuses only T == 1; here T <= 16. */
+int nsx_fused_gemv(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
+                   const void *x, int x_dtype, int64_t T, float *y, void *stream);
+
+/* 64-row interleaved tiles for VRAM-resident expert slabs. No reference
+ * counterpart: residency/cache.py:369-389 admit_slab keeps the raw bytes;
+ * here admission re-lays the same bits out so one 128-bit load per lane
+ * covers one row's block (MXFP4 only). pack/unpack are exact inverses. */
+int64_t nsx_t64_bytes(int ggml_type, int64_t n_rows, int64_t K);
+int nsx_t64_pack(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
+                 void *t64, void *stream);
+int nsx_t64_unpack(int ggml_type, const void *t64, int64_t n_rows, int64_t K,
+                   void *raw, void *stream);
+/* fused_gemv over rows [row_lo, row_hi) of a t64 matrix; y: (T, row_hi-row_lo) */
+int nsx_t64_gemv(int ggml_type, const void *t64, int64_t n_rows, int64_t K,
+                 int64_t row_lo, int64_t row_hi, const void *x, int x_dtype,
+                 int64_t T, float *y, void *stream);
+
+/* moe/router.py:59-69 route() (mode NSX_ROUTE_QWEN3) and
+ * model/gpt_oss.py:116-121 _route() (mode NSX_ROUTE_GPTOSS).
+ * h: (T, K) fp32; w: (n_expert, K) in w_dtype (NSX_F32 / NSX_BF16 / NSX_F16);
+ * bias: (n_expert,) fp32 or NULL. ids/weights: (T, top_k), ordered by
+ * descending value with ties to the lower expert index; logits: (T, n_expert)
+ * fp32 output. */
+int nsx_router_topk(const float *h, int64_t T, int64_t K, const void *w,
+                    int w_dtype, const float *bias, int64_t n_expert, int top_k,
+                    int mode, int32_t *ids, float *weights, float *logits,
+                    void *stream);
+
+/* One MoE FFN layer: router -> routed experts -> weighted combine.
+ * model/gpt_oss.py:123-177 _ffn_block (neuron path, without the residual)
+ * and moe/router.py:173-219 moe_ffn. Expert tensors are given per expert as
+ * device arrays of device addresses (n_expert entries each). */
+typedef struct nsx_moe_layer {
+  int32_t ggml_type;    /* expert weight format (NSX_MXFP4 / NSX_Q4_K / NSX_Q4_0) */
+  int32_t layout;       /* NSX_LAYOUT_GGUF or NSX_LAYOUT_T64 */
+  int32_t n_expert;
+  int32_t top_k;
+  int32_t n_embd;       /* hidden size: K of gate/up, rows of down */
+  int32_t n_ff;         /* expert width: rows of gate/up, K of down */
+  int32_t router_mode;  /* NSX_ROUTE_* */
+  int32_t act;          /* NSX_ACT_* */
+  float alpha;          /* clamped SwiGLU alpha (1.702) */
+  float limit;          /* clamped SwiGLU limit (7.0) */
+  const void *router_w; /* (n_expert, n_embd) */
+  int32_t router_dtype; /* NSX_F32 / NSX_BF16 / NSX_F16 */
+  int32_t reserved0;
+  const float *router_bias;  /* (n_expert,) or NULL */
+  /* Expert e of a projection lives at base + e * stride when base is not
+   * NULL, else at ptrs[e] (a device array of n_expert device addresses). */
+  const uint64_t *gate_ptrs;
+  const uint64_t *up_ptrs;
+  const uint64_t *down_ptrs;
+  const float *gate_bias; /* (n_expert, n_ff) or NULL */
+  const float *up_bias;   /* (n_expert, n_ff) or NULL */
+  const float *down_bias; /* (n_expert, n_embd) or NULL */
+  const void *gate_base;
+  const void *up_base;
+  const void *down_base;
+  int64_t gate_stride;
+  int64_t up_stride;
+  int64_t down_stride;
+} nsx_moe_layer;
+
+/* Bytes of caller-provided workspace for T tokens. The caller zeroes the
+ * workspace once before its first use (padding inside it must read as zero);
+ * calls that share one workspace must not overlap. */
+int64_t nsx_moe_workspace_bytes(const nsx_moe_layer *L, int64_t T);
+
+/* out: (T, n_embd) fp32 = sum over the token's experts, in ascending expert
+ * id, of weight * expert_ffn(h). ids/weights: (T, top_k) outputs. */
+int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
+                    float *out, int32_t *ids, float *weights, void *workspace,
+                    int64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NUROSTREAM_AMD_H */

@@ -1,0 +1,152 @@
+"""ctypes binding of libnsx.so (the C ABI declared in include/nurostream_amd.h).
+
+The library is the only compute path for quantized weights: if it is missing,
+or no GPU is present, the product functions raise instead of falling back to
+a CPU implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+from .format.gguf import GGMLType
+
+LIB_PATH = Path(__file__).resolve().parent / "libnsx.so"
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nurostream_amd.h"
+
+# status codes (nurostream_amd.h)
+OK, EINVAL, ETYPE, ENOTIMPL, EHIP, EKERNEL = 0, 1, 2, 3, 4, 5
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+LAYOUT_GGUF, LAYOUT_T64 = 0, 1
+ROUTE_GPTOSS, ROUTE_QWEN3 = 0, 1
+ACT_CLAMPED_SWIGLU, ACT_SILU_MUL = 0, 1
+
+BLOCK_TYPES = frozenset({GGMLType.Q4_0, GGMLType.Q8_0, GGMLType.Q4_K, GGMLType.MXFP4})
+
+_p = C.c_void_p
+_i64 = C.c_int64
+_i = C.c_int
+
+
+class MoeLayerC(C.Structure):
+    """nsx_moe_layer (field order and types follow the header)."""
+
+    _fields_ = [
+        ("ggml_type", C.c_int32), ("layout", C.c_int32), ("n_expert", C.c_int32),
+        ("top_k", C.c_int32), ("n_embd", C.c_int32), ("n_ff", C.c_int32),
+        ("router_mode", C.c_int32), ("act", C.c_int32), ("alpha", C.c_float),
+        ("limit", C.c_float), ("router_w", _p), ("router_dtype", C.c_int32),
+        ("reserved0", C.c_int32), ("router_bias", _p), ("gate_ptrs", _p),
+        ("up_ptrs", _p), ("down_ptrs", _p), ("gate_bias", _p), ("up_bias", _p),
+        ("down_bias", _p), ("gate_base", _p), ("up_base", _p), ("down_base", _p),
+        ("gate_stride", C.c_int64), ("up_stride", C.c_int64), ("down_stride", C.c_int64),
+    ]
+
+
+_SIGS = {
+    "nsx_last_error": (C.c_char_p, []),
+    "nsx_abi_version": (_i, []),
+    "nsx_selftest": (_i, [_p, _p]),
+    "nsx_dequantize": (_i, [_i, _p, _i64, _i64, _p, _i, _p]),
+    "nsx_fused_gemv": (_i, [_i, _p, _i64, _i64, _p, _i, _i64, _p, _p]),
+    "nsx_t64_bytes": (_i64, [_i, _i64, _i64]),
+    "nsx_t64_pack": (_i, [_i, _p, _i64, _i64, _p, _p]),
+    "nsx_t64_unpack": (_i, [_i, _p, _i64, _i64, _p, _p]),
+    "nsx_t64_gemv": (_i, [_i, _p, _i64, _i64, _i64, _i64, _p, _i, _i64, _p, _p]),
+    "nsx_router_topk": (_i, [_p, _i64, _i64, _p, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),
+    "nsx_moe_workspace_bytes": (_i64, [C.POINTER(MoeLayerC), _i64]),
+    "nsx_moe_forward": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p, _i64, _p]),
+}
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+_lib = None
+_load_error: Exception | None = None
+
+
+def header_functions() -> list[str]:
+    """Every function the public header declares."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(nsx_\w+)\s*\(", text, re.M)))
+
+
+def load():
+    """The ctypes handle of libnsx.so; raises if it was never built."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise NativeError(
+            f"{LIB_PATH} is missing: build it with `python -m nurostream_amd.build` "
+            "(the HIP library is the only compute path for quantized weights)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.nsx_abi_version() != 1:
+        raise NativeError("libnsx.so ABI version mismatch")
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc == OK:
+        return
+    msg = load().nsx_last_error().decode(errors="replace")
+    if what:
+        msg = f"{what}: {msg}"
+    if rc == EINVAL:
+        raise ValueError(msg)
+    if rc == ETYPE:
+        raise TypeError(msg)
+    if rc == ENOTIMPL:
+        raise NotImplementedError(msg)
+    raise NativeError(msg)
+
+
+def require_device(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise NativeError(
+                "the nurostream_amd compute path runs on the GPU only "
+                f"(got a {t.device} tensor); there is no CPU fallback")
+
+
+def stream_ptr(device=None) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def act_dtype_code(dtype) -> int:
+    import torch
+
+    if dtype == torch.float32:
+        return DT_F32
+    if dtype == torch.float16:
+        return DT_F16
+    if dtype == torch.bfloat16:
+        return DT_BF16
+    raise TypeError(f"unsupported activation dtype {dtype}")
+
+
+_selftested: set = set()
+
+
+def ensure_selftest(device) -> None:
+    """Run the FP4 conversion self test once per device."""
+    import torch
+
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    if idx in _selftested:
+        return
+    scratch = torch.zeros(1, dtype=torch.int32, device=f"cuda:{idx}")
+    with torch.cuda.device(idx):
+        check(load().nsx_selftest(scratch.data_ptr(), stream_ptr(idx)), "selftest")
+    _selftested.add(idx)

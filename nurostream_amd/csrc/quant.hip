@@ -1,0 +1,433 @@
+// Dequantization, raw-GGUF fused GEMV, and the t64 tile layout (gfx950).
+//
+// Semantics follow the reference's compute/quant.py (dequantize, bit-exact)
+// and compute/triton_kernels.py fused_gemv (fp32 accumulate); the kernels
+// themselves are written for CDNA4: wave64, buffer loads with hardware range
+// checking, the gfx950 FP4 conversion instruction, and wave reductions.
+#include "nsx_common.h"
+#include "raw_dot.h"
+
+#include <algorithm>
+#include <string.h>
+
+// ---------------------------------------------------------------------------
+// error state
+
+static thread_local char g_err[512] = "";
+
+int nsx_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+extern "C" const char* nsx_last_error(void) { return g_err; }
+extern "C" int nsx_abi_version(void) { return NSX_ABI_VERSION; }
+
+static inline hipStream_t S(void* s) { return (hipStream_t)s; }
+
+// ---------------------------------------------------------------------------
+// FP4 conversion self test: v_cvt_scalef32_pk_f32_fp4 with scale 1.0 must give
+// the e2m1 value of the low nibble in .x and of the high nibble in .y for the
+// byte selected by the third operand.
+
+__global__ void selftest_zero_kernel(uint32_t* bad) { *bad = 0; }
+
+__global__ void selftest_kernel(uint32_t* bad) {
+  const uint32_t b = threadIdx.x;  // 256 threads, one byte value each
+  const uint32_t word = b << 16;   // byte 2
+  v2f c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2);
+  const float lo = kE2M1x2[b & 15] * 0.5f, hi = kE2M1x2[b >> 4] * 0.5f;
+  // code 8 may decode to -0.0; compare values, not bits
+  if (c.x != lo || c.y != hi) atomicAdd(bad, 1u);
+}
+
+extern "C" int nsx_selftest(uint32_t* scratch, void* stream) {
+  NSX_REQUIRE(scratch, NSX_EINVAL, "null scratch word");
+  hipLaunchKernelGGL(selftest_zero_kernel, dim3(1), dim3(1), 0, S(stream), scratch);
+  NSX_LAUNCHED();
+  hipLaunchKernelGGL(selftest_kernel, dim3(1), dim3(256), 0, S(stream), scratch);
+  NSX_LAUNCHED();
+  uint32_t bad = 0;
+  NSX_HIP(hipMemcpyAsync(&bad, scratch, sizeof bad, hipMemcpyDeviceToHost, S(stream)));
+  NSX_HIP(hipStreamSynchronize(S(stream)));
+  NSX_REQUIRE(bad == 0, NSX_EKERNEL, "fp4 conversion self test: %u byte values decoded wrongly", bad);
+  return NSX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// dequantize (quant.py:118-140, 24-56, 110-115)
+//
+// A workgroup stages BPW consecutive blocks into LDS with range-checked dword
+// buffer loads (the source may start at any byte), then each thread expands
+// four consecutive elements and writes them with one vector store.
+
+constexpr int DQ_THREADS = 256;
+
+template <int FMT>
+struct Fmt;
+template <> struct Fmt<NSX_MXFP4> { static constexpr int BE = 32, BB = 17, BPW = 32; };
+template <> struct Fmt<NSX_Q4_0> { static constexpr int BE = 32, BB = 18, BPW = 32; };
+template <> struct Fmt<NSX_Q8_0> { static constexpr int BE = 32, BB = 34, BPW = 32; };
+template <> struct Fmt<NSX_Q4_K> { static constexpr int BE = 256, BB = 144, BPW = 4; };
+
+template <int FMT>
+__device__ __forceinline__ float dq_elem(const uint8_t* B, int blk, int j) {
+  constexpr int BB = Fmt<FMT>::BB;
+  const uint8_t* p = B + blk * BB;
+  if constexpr (FMT == NSX_MXFP4) {
+    const float scale = nsx_mx_scale_half(p[0]);
+    const uint32_t q = p[1 + (j & 15)];
+    const uint32_t code = j < 16 ? (q & 15u) : (q >> 4);
+    return __fmul_rn(scale, kE2M1x2[code]);
+  } else if constexpr (FMT == NSX_Q4_0) {
+    const float d = nsx_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+    const uint32_t q = p[2 + (j & 15)];
+    const int v = (int)(j < 16 ? (q & 15u) : (q >> 4)) - 8;
+    return __fmul_rn(d, (float)v);
+  } else if constexpr (FMT == NSX_Q8_0) {
+    const float d = nsx_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+    const int v = (int)(int8_t)p[2 + j];
+    return __fmul_rn(d, (float)v);
+  } else {  // Q4_K
+    const float d = nsx_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+    const float dmin = nsx_h2f((uint32_t)p[2] | ((uint32_t)p[3] << 8));
+    const int s = j >> 5, l = j & 31;
+    uint32_t sc, m;
+    nsx_q4k_scale_min(p + 4, s, sc, m);
+    const uint32_t q = (p[16 + (s >> 1) * 32 + l] >> (4 * (s & 1))) & 15u;
+    const float scale = __fmul_rn(d, (float)sc);   // exact
+    const float off = __fmul_rn(dmin, (float)m);   // exact
+    return __fsub_rn(__fmul_rn(scale, (float)q), off);  // one rounding
+  }
+}
+
+template <int FMT, int OUT>
+__global__ __launch_bounds__(DQ_THREADS) void dequant_kernel(
+    const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int64_t n_blocks,
+    int64_t n_elements, void* __restrict__ out) {
+  constexpr int BE = Fmt<FMT>::BE, BB = Fmt<FMT>::BB, BPW = Fmt<FMT>::BPW;
+  constexpr int CHUNK = BPW * BB;
+  constexpr int NDW = (CHUNK + 3) / 4 + 1;
+  __shared__ uint32_t smem[NDW];
+
+  const int64_t blk0 = (int64_t)blockIdx.x * BPW;
+  if (blk0 >= n_blocks) return;
+  const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
+  const uint32_t c0 = head + (uint32_t)(blk0 * BB);  // byte offset of the chunk from `base`
+  const uint32_t c0a = c0 & ~3u;
+  for (int i = threadIdx.x; i < NDW; i += DQ_THREADS) smem[i] = nsx_bload32(rs, c0a + 4u * i);
+  __syncthreads();
+  const uint8_t* B = (const uint8_t*)smem + (c0 - c0a);
+
+  const int nblk = (int)(n_blocks - blk0 < BPW ? n_blocks - blk0 : BPW);
+  const int64_t e0 = blk0 * BE;
+  for (int q = threadIdx.x; q < nblk * BE / 4; q += DQ_THREADS) {
+    const int i = q * 4;
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = dq_elem<FMT>(B, (i + u) / BE, (i + u) % BE);
+    const int64_t g = e0 + i;
+    if (g >= n_elements) break;
+    if (OUT == NSX_DT_F32) {
+      float* o = (float*)out + g;
+      if (g + 4 <= n_elements) {
+        *(v4f*)o = v4f{v[0], v[1], v[2], v[3]};
+      } else {
+        for (int u = 0; u < 4 && g + u < n_elements; ++u) o[u] = v[u];
+      }
+    } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        // round to fp32 first, exactly as the reference's `.to(out_dtype)` on a
+        // float32 tensor: the barrier stops a fused multiply-to-half (v_fma_mix)
+        float f = v[u];
+        asm volatile("" : "+v"(f));
+        h[u] = (uint16_t)(OUT == NSX_DT_F16 ? nsx_f2h(f) : nsx_f2bf(f));
+      }
+      uint16_t* o = (uint16_t*)out + g;
+      if (g + 4 <= n_elements) {
+        *(v2u*)o = v2u{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+      } else {
+        for (int u = 0; u < 4 && g + u < n_elements; ++u) o[u] = h[u];
+      }
+    }
+  }
+}
+
+template <int FMT, int OUT>
+static int launch_dequant(const void* raw, int64_t n_blocks, int64_t n_elements, void* out,
+                          hipStream_t st) {
+  constexpr int BB = Fmt<FMT>::BB, BPW = Fmt<FMT>::BPW, BE = Fmt<FMT>::BE;
+  // Split so that every launch's byte range fits a 32-bit buffer range.
+  const int64_t max_blocks = ((int64_t)1 << 30) / BB / BPW * BPW;
+  for (int64_t b0 = 0; b0 < n_blocks; b0 += max_blocks) {
+    const int64_t nb = std::min(max_blocks, n_blocks - b0);
+    const uint8_t* p = (const uint8_t*)raw + b0 * BB;
+    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
+    const uint32_t head = (uint32_t)((uintptr_t)p - a);
+    const uint32_t range = head + (uint32_t)(nb * BB);
+    const int64_t ne = std::min(n_elements - b0 * BE, nb * BE);
+    if (ne <= 0) break;
+    const size_t esz = OUT == NSX_DT_F32 ? 4 : 2;
+    void* o = (char*)out + b0 * BE * esz;
+    hipLaunchKernelGGL((dequant_kernel<FMT, OUT>), dim3((unsigned)nsx_cdiv(nb, BPW)), dim3(DQ_THREADS), 0,
+                       st, (const uint8_t*)a, head, range, nb, ne, o);
+    NSX_LAUNCHED();
+  }
+  return NSX_OK;
+}
+
+template <int FMT>
+static int dequant_fmt(const void* raw, int64_t nb, int64_t ne, void* out, int odt, hipStream_t st) {
+  switch (odt) {
+    case NSX_DT_F32: return launch_dequant<FMT, NSX_DT_F32>(raw, nb, ne, out, st);
+    case NSX_DT_F16: return launch_dequant<FMT, NSX_DT_F16>(raw, nb, ne, out, st);
+    case NSX_DT_BF16: return launch_dequant<FMT, NSX_DT_BF16>(raw, nb, ne, out, st);
+  }
+  return nsx_fail(NSX_EINVAL, "unsupported output dtype %d", odt);
+}
+
+extern "C" int nsx_dequantize(int t, const void* raw, int64_t raw_bytes, int64_t n_elements,
+                              void* out, int out_dtype, void* stream) {
+  const int BE = nsx_block_elems(t), BB = nsx_block_bytes(t);
+  NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no dequant kernel for ggml type %d; supported: Q4_0 Q8_0 Q4_K MXFP4", t);
+  NSX_REQUIRE(raw_bytes >= 0 && n_elements >= 0, NSX_EINVAL, "negative size");
+  const int64_t nb = raw_bytes / BB;
+  NSX_REQUIRE(n_elements <= nb * BE, NSX_EINVAL, "%lld elements requested from %lld blocks",
+              (long long)n_elements, (long long)nb);
+  if (n_elements == 0) return NSX_OK;
+  NSX_REQUIRE(raw && out, NSX_EINVAL, "null buffer");
+  const int64_t need = nsx_cdiv(n_elements, BE);
+  hipStream_t st = S(stream);
+  switch (t) {
+    case NSX_MXFP4: return dequant_fmt<NSX_MXFP4>(raw, need, n_elements, out, out_dtype, st);
+    case NSX_Q4_0: return dequant_fmt<NSX_Q4_0>(raw, need, n_elements, out, out_dtype, st);
+    case NSX_Q8_0: return dequant_fmt<NSX_Q8_0>(raw, need, n_elements, out, out_dtype, st);
+    case NSX_Q4_K: return dequant_fmt<NSX_Q4_K>(raw, need, n_elements, out, out_dtype, st);
+  }
+  return nsx_fail(NSX_ENOTIMPL, "ggml type %d", t);
+}
+
+// ---------------------------------------------------------------------------
+// fused GEMV on raw GGUF rows (triton_kernels.py:199-228 seam)
+//
+// One wave per row (grid-stride); lanes take the row's 32-element units and
+// the wave reduces (raw_dot.h). x is staged once per workgroup in LDS.
+
+constexpr int GV_THREADS = 256;
+constexpr int GV_MAXT = 16;
+
+template <int FMT, int NT>
+__global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
+    const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int n_rows, int K,
+    const void* __restrict__ x, int x_dtype, int T, float* __restrict__ y, int64_t ystride) {
+  extern __shared__ float xs[];  // [NT][K] then [NT][K/32] block sums
+  stage_x<NT>(xs, x, x_dtype, K, T, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
+  const float* xsum = xs + NT * K;
+  const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
+  const int lane = __lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = gridDim.x * (GV_THREADS / 64);
+  const uint32_t rb = raw_row_bytes<FMT>(K);
+  const int nu = raw_units<FMT>(K);
+  for (int r = blockIdx.x * (GV_THREADS / 64) + wave; r < n_rows; r += nwaves) {
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.f;
+    const uint32_t o_row = head + (uint32_t)r * rb;
+    for (int u = lane; u < nu; u += 64) raw_unit_dot<FMT, NT>(rs, o_row, u, xs, K, xsum, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float v = nsx_wave_sum(acc[t]);
+      if (lane == 0 && t < T) y[(int64_t)t * ystride + r] = v;
+    }
+  }
+}
+
+template <int FMT, int NT>
+static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const void* x, int xdt,
+                           int64_t T, float* y, hipStream_t st) {
+  const int64_t row_bytes = raw_row_bytes<FMT>((int)K);
+  const int64_t rows_per_launch = std::max<int64_t>(1, ((int64_t)1 << 31) / row_bytes);
+  const size_t lds = (size_t)NT * (K + K / 32) * sizeof(float);
+  if (lds > 64 * 1024)
+    NSX_HIP(hipFuncSetAttribute((const void*)gemv_raw_kernel<FMT, NT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_launch) {
+    const int64_t nr = std::min(rows_per_launch, n_rows - r0);
+    const uint8_t* p = (const uint8_t*)raw + r0 * row_bytes;
+    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
+    const uint32_t head = (uint32_t)((uintptr_t)p - a);
+    const uint32_t range = head + (uint32_t)(nr * row_bytes);
+    const int waves = GV_THREADS / 64;
+    const unsigned grid = (unsigned)std::min<int64_t>(nsx_cdiv(nr, waves), 8192);
+    hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT>), dim3(grid), dim3(GV_THREADS), lds, st,
+                       (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows);
+    NSX_LAUNCHED();
+  }
+  return NSX_OK;
+}
+
+template <int FMT>
+static int gemv_raw_fmt(const void* raw, int64_t n_rows, int64_t K, const void* x, int xdt, int64_t T,
+                        float* y, hipStream_t st) {
+  if (T == 1) return launch_gemv_raw<FMT, 1>(raw, n_rows, K, x, xdt, T, y, st);
+  if (T == 2) return launch_gemv_raw<FMT, 2>(raw, n_rows, K, x, xdt, T, y, st);
+  if (T <= 4) return launch_gemv_raw<FMT, 4>(raw, n_rows, K, x, xdt, T, y, st);
+  if (T <= 8) return launch_gemv_raw<FMT, 8>(raw, n_rows, K, x, xdt, T, y, st);
+  return launch_gemv_raw<FMT, 16>(raw, n_rows, K, x, xdt, T, y, st);
+}
+
+static inline int64_t pad_tokens(int64_t T) { return T == 1 ? 1 : T == 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
+
+extern "C" int nsx_fused_gemv(int t, const void* raw, int64_t n_rows, int64_t K, const void* x,
+                              int x_dtype, int64_t T, float* y, void* stream) {
+  const int BE = nsx_block_elems(t), BB = nsx_block_bytes(t);
+  NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no fused kernel for ggml type %d", t);
+  NSX_REQUIRE(n_rows >= 0 && K > 0 && K % BE == 0, NSX_EINVAL,
+              "K=%lld is not a positive multiple of the %d-element block", (long long)K, BE);
+  NSX_REQUIRE(T >= 1 && T <= GV_MAXT, NSX_EINVAL, "T=%lld outside 1..%d", (long long)T, GV_MAXT);
+  NSX_REQUIRE(x_dtype == NSX_DT_F32 || x_dtype == NSX_DT_F16 || x_dtype == NSX_DT_BF16, NSX_EINVAL,
+              "x dtype %d", x_dtype);
+  NSX_REQUIRE(n_rows < (1ll << 31) && K < (1ll << 20), NSX_EINVAL, "shape too large");
+  if (n_rows == 0) return NSX_OK;
+  NSX_REQUIRE(raw && x && y, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE((K + K / 32) * 4 <= 64 * 1024, NSX_EINVAL, "K=%lld too large for one workgroup's LDS", (long long)K);
+  if (t == NSX_Q4_K)
+    NSX_REQUIRE(((uintptr_t)raw & 3) == 0, NSX_EINVAL, "Q4_K rows must be 4-byte aligned");
+  hipStream_t st = S(stream);
+  // tokens per launch: as many as one workgroup's LDS holds (<= 64 KiB staged)
+  int64_t chunk = 16;
+  while (chunk > 1 && chunk * (K + K / 32) * 4 > 64 * 1024) chunk /= 2;
+  const size_t xsz = x_dtype == NSX_DT_F32 ? 4 : 2;
+  for (int64_t t0 = 0; t0 < T; t0 += chunk) {
+    const int64_t nt = std::min(chunk, T - t0);
+    const void* xc = (const char*)x + t0 * K * xsz;
+    float* yc = y + t0 * n_rows;
+    int rc = NSX_ENOTIMPL;
+    switch (t) {
+      case NSX_MXFP4: rc = gemv_raw_fmt<NSX_MXFP4>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
+      case NSX_Q4_0: rc = gemv_raw_fmt<NSX_Q4_0>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
+      case NSX_Q8_0: rc = gemv_raw_fmt<NSX_Q8_0>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
+      case NSX_Q4_K: rc = gemv_raw_fmt<NSX_Q4_K>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
+    }
+    if (rc) return rc;
+  }
+  return NSX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// t64 layout (MXFP4): 64-row tiles; qs plane [tile][block][row][16 B] then
+// scale plane [tile][block/4][row][4 B]. Rows beyond n_rows and blocks beyond
+// nb inside the last scale group are zero.
+
+struct T64Geom {
+  int64_t tiles, nb, nb4, qs_bytes, sc_bytes;
+};
+static inline T64Geom t64_geom(int64_t n_rows, int64_t K) {
+  T64Geom g;
+  g.tiles = nsx_cdiv(n_rows, 64);
+  g.nb = K / 32;
+  g.nb4 = nsx_cdiv(g.nb, 4);
+  g.qs_bytes = g.tiles * g.nb * 1024;
+  g.sc_bytes = g.tiles * g.nb4 * 256;
+  return g;
+}
+
+extern "C" int64_t nsx_t64_bytes(int t, int64_t n_rows, int64_t K) {
+  if (t != NSX_MXFP4 || K <= 0 || K % 32 || n_rows < 0) return -1;
+  const T64Geom g = t64_geom(n_rows, K);
+  return g.qs_bytes + g.sc_bytes;
+}
+
+// one thread per (row slot, block slot) of the padded tile grid
+__global__ void t64_pack_kernel(const uint8_t* __restrict__ base, uint32_t head, uint32_t range,
+                                int64_t n_rows, int nb, int nb4, int64_t tiles,
+                                uint8_t* __restrict__ dst, int64_t qs_bytes) {
+  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over tiles*64*nb4*4
+  const int64_t total = tiles * 64 * (int64_t)nb4 * 4;
+  if (slot >= total) return;
+  const int lane = (int)(slot & 63);
+  const int64_t rest = slot >> 6;
+  const int b = (int)(rest % (nb4 * 4));
+  const int64_t tile = rest / (nb4 * 4);
+  const int64_t row = tile * 64 + lane;
+  const bool real = row < n_rows && b < nb;
+  uint32_t q[4] = {0, 0, 0, 0};
+  uint32_t e = 0;
+  if (real) {
+    const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
+    const uint32_t o = head + (uint32_t)((row * nb + b) * 17);
+    const uint32_t s = o & 3u, oa = o & ~3u;
+    uint32_t D[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) D[i] = nsx_bload32(rs, oa + 4u * i);
+    uint32_t E[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) E[i] = nsx_alignbyte(D[i + 1], D[i], s);
+    e = E[0] & 0xffu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = nsx_alignbyte(E[i + 1], E[i], 1);
+  }
+  if (b < nb) {
+    uint8_t* qd = dst + ((tile * nb + b) * 64 + lane) * 16;
+    *(v4u*)qd = v4u{q[0], q[1], q[2], q[3]};
+  }
+  dst[qs_bytes + ((tile * nb4 + b / 4) * 64 + lane) * 4 + (b & 3)] = (uint8_t)e;
+}
+
+__global__ void t64_unpack_kernel(const uint8_t* __restrict__ src, int64_t n_rows, int nb, int nb4,
+                                  int64_t qs_bytes, uint8_t* __restrict__ raw) {
+  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over n_rows*nb
+  if (slot >= n_rows * nb) return;
+  const int64_t row = slot / nb;
+  const int b = (int)(slot % nb);
+  const int64_t tile = row >> 6;
+  const int lane = (int)(row & 63);
+  const v4u q = *(const v4u*)(src + ((tile * nb + b) * 64 + lane) * 16);
+  const uint8_t e = src[qs_bytes + ((tile * nb4 + b / 4) * 64 + lane) * 4 + (b & 3)];
+  uint8_t* o = raw + slot * 17;
+  o[0] = e;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[1 + 4 * i + j] = (uint8_t)(q[i] >> (8 * j));
+  }
+}
+
+extern "C" int nsx_t64_pack(int t, const void* raw, int64_t n_rows, int64_t K, void* t64, void* stream) {
+  NSX_REQUIRE(t == NSX_MXFP4, NSX_ENOTIMPL, "t64 layout is implemented for MXFP4 only (type %d)", t);
+  NSX_REQUIRE(K > 0 && K % 32 == 0 && n_rows >= 0, NSX_EINVAL, "bad shape %lld x %lld",
+              (long long)n_rows, (long long)K);
+  const T64Geom g = t64_geom(n_rows, K);
+  if (n_rows == 0) return NSX_OK;
+  NSX_REQUIRE(raw && t64, NSX_EINVAL, "null buffer");
+  const int64_t raw_bytes = n_rows * g.nb * 17;
+  NSX_REQUIRE(raw_bytes < (1ll << 32) - 8, NSX_EINVAL, "pack source above 4 GiB: pack per expert");
+  const uint8_t* p = (const uint8_t*)raw;
+  const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
+  const uint32_t head = (uint32_t)((uintptr_t)p - a);
+  const int64_t total = g.tiles * 64 * g.nb4 * 4;
+  hipLaunchKernelGGL(t64_pack_kernel, dim3((unsigned)nsx_cdiv(total, 256)), dim3(256), 0, S(stream),
+                     (const uint8_t*)a, head, (uint32_t)(head + raw_bytes), n_rows, (int)g.nb, (int)g.nb4,
+                     g.tiles, (uint8_t*)t64, g.qs_bytes);
+  NSX_LAUNCHED();
+  return NSX_OK;
+}
+
+extern "C" int nsx_t64_unpack(int t, const void* t64, int64_t n_rows, int64_t K, void* raw, void* stream) {
+  NSX_REQUIRE(t == NSX_MXFP4, NSX_ENOTIMPL, "t64 layout is implemented for MXFP4 only (type %d)", t);
+  NSX_REQUIRE(K > 0 && K % 32 == 0 && n_rows >= 0, NSX_EINVAL, "bad shape");
+  const T64Geom g = t64_geom(n_rows, K);
+  if (n_rows == 0) return NSX_OK;
+  NSX_REQUIRE(raw && t64, NSX_EINVAL, "null buffer");
+  const int64_t total = n_rows * g.nb;
+  hipLaunchKernelGGL(t64_unpack_kernel, dim3((unsigned)nsx_cdiv(total, 256)), dim3(256), 0, S(stream),
+                     (const uint8_t*)t64, n_rows, (int)g.nb, (int)g.nb4, g.qs_bytes, (uint8_t*)raw);
+  NSX_LAUNCHED();
+  return NSX_OK;
+}

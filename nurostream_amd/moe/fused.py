@@ -1,0 +1,146 @@
+"""One MoE FFN layer as a single HIP call sequence (router -> experts -> combine).
+
+`MoELayer` wraps nsx_moe_forward (include/nurostream_amd.h): the router's
+top-k, the routed experts' gate/up GEMVs with bias and activation, the down
+GEMVs with bias and the ascending-expert weighted combine all run on the
+device, with expert ids never leaving it (the reference syncs to the host at
+model/gpt_oss.py:121 and moe/router.py:183 to pick windows).
+
+Expert weights are either one stacked tensor per projection (expert e at
+base + e * expert_bytes: the kernels compute the address, no table lookup) or
+a list of separately admitted slabs (a device table of addresses); all three
+projections of a layer share one layout (raw GGUF rows or t64 tiles).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from .. import _native as N
+from ..format.gguf import GGMLType, TYPE_LAYOUT
+
+_W_CODE = {torch.float32: int(GGMLType.F32), torch.bfloat16: int(GGMLType.BF16),
+           torch.float16: int(GGMLType.F16)}
+
+
+def _addr_table(ptrs, device) -> torch.Tensor:
+    return torch.tensor([int(p) for p in ptrs], dtype=torch.int64, device=device)
+
+
+class MoELayer:
+    def __init__(self, *, ggml_type, n_expert: int, top_k: int, n_embd: int, n_ff: int,
+                 router_w: torch.Tensor, router_b: torch.Tensor | None,
+                 gate, up, down, gate_b=None, up_b=None, down_b=None,
+                 layout: str = "gguf", router_mode: str = "gptoss", act: str = "clamped_swiglu",
+                 alpha: float = 1.702, limit: float = 7.0) -> None:
+        """gate/up/down: either one stacked uint8 device tensor per projection
+        (expert e at offset e * bytes_per_expert) or a list of n_expert device
+        tensors (one slab each)."""
+        self.device = router_w.device
+        N.require_device(router_w)
+        self.ggml_type = GGMLType(ggml_type)
+        self.n_expert, self.top_k, self.n_embd, self.n_ff = n_expert, top_k, n_embd, n_ff
+        self.layout = layout
+        be, bb = TYPE_LAYOUT[self.ggml_type]
+        lib = N.load()
+
+        def table(w, rows, K):
+            """(tensors to keep alive, device address table or None, base address, stride)."""
+            if isinstance(w, (list, tuple)):
+                if len(w) != n_expert:
+                    raise ValueError(f"{len(w)} expert slabs for {n_expert} experts")
+                keep = list(w)
+                return keep, _addr_table([t.data_ptr() for t in keep], self.device), None, 0
+            if layout == "t64":
+                per = lib.nsx_t64_bytes(int(self.ggml_type), rows, K)
+            else:
+                per = rows * (K // be) * bb
+            if w.numel() < per * n_expert:
+                raise ValueError(f"stacked tensor of {w.numel()} bytes, need {per * n_expert}")
+            return [w], None, w.data_ptr(), per
+
+        self._keep = []
+        (k1, self.gate_ptrs, gb, gs), (k2, self.up_ptrs, ub, us), (k3, self.down_ptrs, db, ds) = (
+            table(gate, n_ff, n_embd), table(up, n_ff, n_embd), table(down, n_embd, n_ff))
+        self._keep += k1 + k2 + k3
+        self.router_w = router_w.contiguous()
+        self.router_b = None if router_b is None else router_b.float().contiguous()
+        self.gate_b = None if gate_b is None else gate_b.float().contiguous()
+        self.up_b = None if up_b is None else up_b.float().contiguous()
+        self.down_b = None if down_b is None else down_b.float().contiguous()
+
+        L = N.MoeLayerC()
+        L.ggml_type = int(self.ggml_type)
+        L.layout = N.LAYOUT_T64 if layout == "t64" else N.LAYOUT_GGUF
+        L.n_expert, L.top_k, L.n_embd, L.n_ff = n_expert, top_k, n_embd, n_ff
+        L.router_mode = N.ROUTE_GPTOSS if router_mode == "gptoss" else N.ROUTE_QWEN3
+        L.act = N.ACT_CLAMPED_SWIGLU if act == "clamped_swiglu" else N.ACT_SILU_MUL
+        L.alpha, L.limit = alpha, limit
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        L.router_w = self.router_w.data_ptr()
+        L.router_dtype = _W_CODE[self.router_w.dtype]
+        L.router_bias = ptr(self.router_b)
+        L.gate_ptrs, L.up_ptrs, L.down_ptrs = ptr(self.gate_ptrs), ptr(self.up_ptrs), ptr(self.down_ptrs)
+        L.gate_base, L.up_base, L.down_base = gb, ub, db
+        L.gate_stride, L.up_stride, L.down_stride = gs, us, ds
+        L.gate_bias, L.up_bias, L.down_bias = ptr(self.gate_b), ptr(self.up_b), ptr(self.down_b)
+        self._c = L
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def workspace(self, T: int) -> torch.Tensor:
+        ws = self._ws.get(T)
+        if ws is None:
+            n = N.load().nsx_moe_workspace_bytes(C.byref(self._c), T)
+            if n < 0:
+                raise ValueError(f"bad layer for T={T}")
+            # zeroed once: padding inside the workspace must read as zero
+            ws = torch.zeros(max(n, 256), dtype=torch.uint8, device=self.device)
+            self._ws[T] = ws
+        return ws
+
+    def forward(self, h: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                weights: torch.Tensor | None = None):
+        """h: (T, n_embd) fp32 -> (out (T, n_embd) fp32, ids (T, k) int32, weights (T, k) fp32)."""
+        N.require_device(h)
+        h = h.reshape(-1, self.n_embd)
+        if h.dtype != torch.float32:
+            h = h.float()
+        h = h.contiguous()
+        T = h.shape[0]
+        if out is None:
+            out = torch.empty((T, self.n_embd), dtype=torch.float32, device=self.device)
+        if ids is None:
+            ids = torch.empty((T, self.top_k), dtype=torch.int32, device=self.device)
+        if weights is None:
+            weights = torch.empty((T, self.top_k), dtype=torch.float32, device=self.device)
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            N.check(N.load().nsx_moe_forward(C.byref(self._c), h.data_ptr(), T, out.data_ptr(), ids.data_ptr(),
+                                             weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                                             N.stream_ptr(self.device)), "moe_forward")
+        return out, ids, weights
+
+    __call__ = forward
+
+
+def router_topk(h: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, top_k: int,
+                mode: str = "gptoss"):
+    """Fused router on the device: (ids int32 (T,k), weights fp32 (T,k), logits fp32 (T,E))."""
+    N.require_device(h, w)
+    h = h.reshape(-1, w.shape[-1]).float().contiguous()
+    w = w.contiguous()
+    T, E = h.shape[0], w.shape[0]
+    dev = h.device
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    lib = N.load()
+    b = None if bias is None else bias.float().contiguous()
+    with torch.cuda.device(dev):
+        N.check(lib.nsx_router_topk(h.data_ptr(), T, h.shape[1], w.data_ptr(), _W_CODE[w.dtype],
+                                    None if b is None else b.data_ptr(), E, top_k,
+                                    N.ROUTE_GPTOSS if mode == "gptoss" else N.ROUTE_QWEN3,
+                                    ids.data_ptr(), wts.data_ptr(), logits.data_ptr(), N.stream_ptr(dev)),
+                "router_topk")
+    return ids, wts, logits

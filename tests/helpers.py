@@ -1,0 +1,28 @@
+"""Shared test utilities (comparison metrics, numpy <-> torch)."""
+from __future__ import annotations
+
+import numpy as np
+
+
+def rel_max(y, ref) -> float:
+    """max|y - ref| / max|ref| (norm-relative, the parity metric of the path)."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.abs(ref).max()
+    return float(np.abs(y - ref).max() / (den if den > 0 else 1.0))
+
+
+def to_np(t):
+    return t.detach().cpu().numpy()
+
+
+def bit_mismatches(got: np.ndarray, expect: np.ndarray) -> np.ndarray:
+    """Indices where two float arrays differ bitwise, counting any NaN as equal
+    to any NaN (NaN payloads and signs differ between the reference's own CPU
+    and GPU paths, so they carry no parity meaning)."""
+    got = np.asarray(got)
+    expect = np.asarray(expect)
+    ui = {2: np.uint16, 4: np.uint32}[got.dtype.itemsize]
+    neq = got.view(ui) != expect.view(ui)
+    both_nan = np.isnan(got.astype(np.float32)) & np.isnan(expect.astype(np.float32))
+    return np.nonzero(neq & ~both_nan)[0]

@@ -1,0 +1,144 @@
+"""Parity of the HIP kernels with the CPU oracle (dequant bit-exact, GEMV 1e-3)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bit_mismatches, rel_max, to_np
+from oracle import quant as OQ
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3  # north-star bar (fp32 accumulate); the observed error is far smaller
+GEMV_TIGHT = 2e-5
+
+
+def _lib():
+    from nurostream_amd import _native as N
+    return N
+
+
+def _mxfp4_all_exponents(rng):
+    raw = rng.integers(0, 256, (256 * 4, 17), dtype=np.uint8)
+    raw[:, 0] = np.repeat(np.arange(256, dtype=np.uint8), 4)
+    return raw
+
+
+def _q_special_d(rng, nb, bb):
+    raw = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+    specials = np.array([0x0000, 0x8000, 0x0001, 0x03ff, 0x0400, 0x3c00, 0xbc00, 0x7bff, 0xfbff, 0x0200],
+                        dtype=np.uint16)
+    d = rng.choice(specials, nb).astype(np.uint16)
+    raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    return raw
+
+
+@pytest.mark.parametrize("fmt", ["MXFP4", "Q4_0", "Q8_0", "Q4_K"])
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_dequant_bit_exact(dev, fmt, offset):
+    from nurostream_amd.compute.quant import dequantize
+    rng = np.random.default_rng(7 + offset)
+    t = getattr(OQ, fmt)
+    be, bb = OQ.LAYOUT[t]
+    if fmt == "MXFP4":
+        raw = _mxfp4_all_exponents(rng)
+    elif fmt == "Q4_K":
+        raw = rng.integers(0, 256, (300, bb), dtype=np.uint8)
+        raw[:150, 0:4] = _q_special_d(rng, 150, 4)[:, 0:4]
+    else:
+        raw = _q_special_d(rng, 777, bb)
+    flat = raw.reshape(-1)
+    buf = np.zeros(flat.size + 8, dtype=np.uint8)
+    buf[offset:offset + flat.size] = flat
+    gpu = torch.from_numpy(buf).to(dev)[offset:offset + flat.size]
+    n = raw.shape[0] * be - 5  # truncated like the reference's n_elements
+    expect = OQ.dequantize(flat, t, n)
+    got = to_np(dequantize(gpu, t, n))
+    assert got.shape == expect.shape
+    bad = bit_mismatches(got, expect)
+    if bad.size:
+        i = bad[:8]
+        blocks = raw[i // be]
+        pytest.fail(f"{bad.size} mismatches at {i.tolist()}: got {got[i].tolist()} "
+                    f"({[hex(v) for v in got.view(np.uint32)[i]]}) expected {expect[i].tolist()} "
+                    f"({[hex(v) for v in expect.view(np.uint32)[i]]}); block head bytes "
+                    f"{[b[:4].tolist() for b in blocks]}")
+    for odt in (torch.float16, torch.bfloat16):
+        g2 = dequantize(gpu, t, n, out_dtype=odt).cpu()
+        ref = torch.from_numpy(expect).to(odt)  # torch's own float32 -> half rounding
+        bad = bit_mismatches(g2.view(torch.int16).numpy().view(np.float16) if odt == torch.float16
+                             else g2.float().numpy(),
+                             ref.view(torch.int16).numpy().view(np.float16) if odt == torch.float16
+                             else ref.float().numpy())
+        assert bad.size == 0, (odt, bad[:8].tolist())
+
+
+def test_mxfp4_reference_known_answer_input(dev):
+    """The reference's MXFP4 KAT input (tests/test_gpt_oss.py:103-109): every exponent 0..253."""
+    from nurostream_amd.compute.quant import dequantize
+    rng = np.random.default_rng(42)
+    raw = rng.integers(0, 256, (254, 17), dtype=np.uint8)
+    raw[:, 0] = np.arange(254, dtype=np.uint8)
+    expect = OQ.dequantize(raw.reshape(-1), OQ.MXFP4, 254 * 32)
+    got = to_np(dequantize(torch.from_numpy(raw.reshape(-1)).to(dev), OQ.MXFP4, 254 * 32))
+    assert bit_mismatches(got, expect).size == 0
+
+
+def _gemv_case(fmt, rows, K, seed, e_lo=117, e_hi=123):
+    from nurostream_amd import synth
+    g = synth.generator(seed, "cpu")
+    raw = synth.matrix_bytes(getattr(OQ, fmt), rows, K, g, "cpu", e_lo=e_lo, e_hi=e_hi)
+    return raw.numpy()
+
+
+@pytest.mark.parametrize("fmt,rows,K", [("MXFP4", 19, 2880), ("Q8_0", 19, 2880), ("MXFP4", 2880, 2880),
+                                        ("Q4_0", 512, 4096), ("Q4_K", 1536, 4096), ("Q4_K", 96, 1536),
+                                        ("Q4_0", 7, 64), ("MXFP4", 1, 32)])
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_fused_gemv_matches_oracle(dev, fmt, rows, K, T):
+    from nurostream_amd.compute.kernels import can_fuse, fused_gemv
+    t = getattr(OQ, fmt)
+    raw = _gemv_case(fmt, rows, K, seed=rows + K + T)
+    if T == 1:
+        x = np.linspace(-1, 1, K, dtype=np.float32)[None, :]  # the reference's test input
+    else:
+        x = np.random.default_rng(T).standard_normal((T, K)).astype(np.float32)
+    xt = torch.from_numpy(x).to(dev)
+    assert can_fuse(t, xt)
+    y = to_np(fused_gemv(torch.from_numpy(raw).to(dev), t, xt, rows, K, out_dtype=torch.float32))
+    ref = OQ.gemv(raw, t, x, rows, K, f64=True)
+    err = rel_max(y, ref)
+    assert err < GEMV_TIGHT, err
+    np.testing.assert_allclose(y, ref, atol=1e-4 * np.abs(ref).max() + 1e-6, rtol=1e-4)
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_fused_gemv_half_activations(dev, xdt):
+    from nurostream_amd.compute.kernels import fused_gemv
+    rows, K = 64, 2880
+    raw = _gemv_case("MXFP4", rows, K, seed=3)
+    x = torch.randn(2, K).to(xdt)
+    y = to_np(fused_gemv(torch.from_numpy(raw).to(dev), OQ.MXFP4, x.to(dev), rows, K, out_dtype=torch.float32))
+    ref = OQ.gemv(raw, OQ.MXFP4, x.float().numpy(), rows, K, f64=True)
+    assert rel_max(y, ref) < GEMV_TIGHT
+
+
+@pytest.mark.parametrize("rows,K", [(2880, 2880), (100, 64), (64, 4096), (1, 32)])
+def test_t64_roundtrip_and_gemv(dev, rows, K):
+    from nurostream_amd.compute.kernels import T64Rows, fused_gemv, t64_pack
+    raw = _gemv_case("MXFP4", rows, K, seed=rows * 3 + K, e_lo=0, e_hi=255)
+    raw_t = torch.from_numpy(raw).to(dev)
+    tiles = t64_pack(raw_t, OQ.MXFP4, rows, K)
+    win = T64Rows(tiles, OQ.MXFP4, rows, K, 0, rows)
+    back = win.to_gguf()
+    assert torch.equal(back.cpu(), raw_t.cpu())
+    # GEMV over sub-windows, including ones that do not start on a tile
+    x = np.random.default_rng(1).standard_normal((2, K)).astype(np.float32)
+    raw_n = _gemv_case("MXFP4", rows, K, seed=rows + 11)
+    tiles = t64_pack(torch.from_numpy(raw_n).to(dev), OQ.MXFP4, rows, K)
+    ref = OQ.gemv(raw_n, OQ.MXFP4, x, rows, K, f64=True)
+    for lo, hi in [(0, rows), (rows // 3, rows), (min(5, rows - 1), max(min(70, rows), min(5, rows - 1) + 1))]:
+        w = T64Rows(tiles, OQ.MXFP4, rows, K, lo, hi)
+        y = to_np(fused_gemv(w, OQ.MXFP4, torch.from_numpy(x).to(dev), hi - lo, K, out_dtype=torch.float32))
+        assert rel_max(y, ref[:, lo:hi]) < GEMV_TIGHT, (lo, hi)

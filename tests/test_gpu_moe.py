@@ -1,0 +1,148 @@
+"""Parity of the fused router and MoE layer with the CPU oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import rel_max, to_np
+from oracle import moe as OM
+from oracle import quant as OQ
+
+pytestmark = pytest.mark.gpu
+
+FFN_TOL = 1e-3  # north-star parity bar for FFN outputs (max rel, fp32 accumulate)
+
+
+def _near_tie_tokens(logits, k, h, W, b):
+    """Tokens whose k-th/(k+1)-th logit gap is within the fp32 error bound."""
+    bound = 4 * np.finfo(np.float32).eps * (np.abs(h) @ np.abs(W).T).max(axis=1) * np.sqrt(h.shape[1])
+    return OM.topk_margin(logits, k) <= bound
+
+
+@pytest.mark.parametrize("mode", ["gptoss", "qwen3"])
+@pytest.mark.parametrize("T,E,K,k", [(1, 128, 2880, 4), (8, 128, 2880, 4), (33, 128, 4096, 8), (5, 7, 64, 3)])
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+def test_router_topk(dev, mode, T, E, K, k, wdt):
+    from nurostream_amd.moe.fused import router_topk
+    g = torch.Generator().manual_seed(T * 131 + E + K + k)
+    h = torch.randn(T, K, generator=g)
+    W = (torch.randn(E, K, generator=g) * 0.02).to(wdt)
+    b = torch.randn(E, generator=g) * 0.02 if mode == "gptoss" else None
+    ids, wts, logits = router_topk(h.to(dev), W.to(dev), None if b is None else b.to(dev), k, mode)
+    hn, Wn = h.numpy(), W.float().numpy()
+    bn = None if b is None else b.numpy()
+    if mode == "gptoss":
+        rid, rw, rlog = OM.route_gptoss(hn, Wn, bn, k)
+    else:
+        rid, rw, rlog = OM.route_qwen3(hn, Wn, k)
+    assert rel_max(to_np(logits), rlog) < 1e-5
+    tie = _near_tie_tokens(rlog, k, hn, Wn, bn)
+    ok = ~tie
+    np.testing.assert_array_equal(to_np(ids)[ok], rid[ok])
+    np.testing.assert_allclose(to_np(wts)[ok], rw[ok], rtol=2e-5, atol=1e-6)
+
+
+def _expert_set(cfg, t):
+    """oracle.ExpertSet over raw tensors of a synthetic layer (CPU copies)."""
+    raw = {k: t[k].cpu().numpy() for k in ("gate", "up", "down")}
+    bias = {k: t[k + "_b"].cpu().numpy() for k in ("gate", "up", "down")} if cfg.bias else {}
+    return OM.ExpertSet(int(cfg.ggml_type), cfg.n_embd, cfg.n_ff, raw, bias)
+
+
+def _layer(cfg, t, layout, slabs=False):
+    """MoELayer over stacked tensors, or (slabs=True) one tensor per expert."""
+    from nurostream_amd.compute.kernels import t64_pack, t64_pack_stacked
+    from nurostream_amd.moe.fused import MoELayer
+    mats = {}
+    for kind in ("gate", "up", "down"):
+        rows, K = cfg.rows_K(kind)
+        per = cfg.expert_bytes(kind)
+        if layout == "t64" and slabs:
+            mats[kind] = [t64_pack(t[kind][e * per:(e + 1) * per], cfg.ggml_type, rows, K)
+                          for e in range(cfg.n_expert)]
+        elif layout == "t64":
+            mats[kind] = t64_pack_stacked(t[kind], cfg.ggml_type, cfg.n_expert, rows, K)
+        elif slabs:
+            mats[kind] = [t[kind][e * per:(e + 1) * per].clone() for e in range(cfg.n_expert)]
+        else:
+            mats[kind] = t[kind]
+    return MoELayer(ggml_type=cfg.ggml_type, n_expert=cfg.n_expert, top_k=cfg.top_k, n_embd=cfg.n_embd,
+                    n_ff=cfg.n_ff, router_w=t["router_w"], router_b=t["router_b"], gate=mats["gate"],
+                    up=mats["up"], down=mats["down"], gate_b=t["gate_b"], up_b=t["up_b"], down_b=t["down_b"],
+                    layout=layout, router_mode=cfg.router_mode, act=cfg.act)
+
+
+def _oracle_layer(cfg, t, h):
+    """(out, ids, weights, logits) of the reference path for a synthetic layer."""
+    ex = _expert_set(cfg, t)
+    Wr = t["router_w"].float().cpu().numpy()
+    if cfg.router_mode == "gptoss":
+        ids, w, logits = OM.route_gptoss(h, Wr, t["router_b"].cpu().numpy(), cfg.top_k)
+    else:
+        ids, w, logits = OM.route_qwen3(h, Wr, cfg.top_k)
+    act = OM.clamped_swiglu if cfg.act == "clamped_swiglu" else OM.silu_mul
+    return OM.combine(h, ids, w, ex, act), ids, w, logits
+
+
+def _small(name):
+    from nurostream_amd import synth
+    if name == "gptoss-small":
+        return synth.MoEConfig("gptoss-small", synth.GGMLType.MXFP4, 16, 4, 256, 192, "gptoss", "clamped_swiglu",
+                               True, torch.bfloat16)
+    if name == "qwen3-small":
+        return synth.MoEConfig("qwen3-small", synth.GGMLType.Q4_K, 12, 8, 512, 256, "qwen3", "silu_mul", False,
+                               torch.float32)
+    if name == "q4_0-small":
+        return synth.MoEConfig("q40-small", synth.GGMLType.Q4_0, 8, 2, 128, 96, "gptoss", "silu_mul", True,
+                               torch.float32)
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name,layout,slabs", [("gptoss-small", "t64", False), ("gptoss-small", "t64", True),
+                                               ("gptoss-small", "gguf", False), ("gptoss-small", "gguf", True),
+                                               ("qwen3-small", "gguf", False), ("q4_0-small", "gguf", False)])
+@pytest.mark.parametrize("T", [1, 2, 9])
+def test_moe_small_layers(dev, name, layout, slabs, T):
+    from nurostream_amd import synth
+    cfg = _small(name)
+    t = synth.make_layer(cfg, seed=5, device=dev)
+    layer = _layer(cfg, t, layout, slabs)
+    h = synth.activations(T, cfg.n_embd, seed=T, device="cpu")
+    out, ids, w = layer(h.to(dev))
+    ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
+    np.testing.assert_array_equal(np.sort(to_np(ids), 1), np.sort(rid, 1))
+    assert rel_max(to_np(out), ref) < 1e-5
+    # a second call reuses the workspace
+    out2, _, _ = layer(h.to(dev))
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("layout", ["t64", "gguf"])
+def test_gptoss_layer_decode(dev, layout):
+    """GPT-OSS-120B-shaped MXFP4 layer at decode batch 1."""
+    from nurostream_amd import synth
+    cfg = synth.GPTOSS_120B
+    t = synth.make_layer(cfg, seed=0, device=dev)
+    layer = _layer(cfg, t, layout)
+    h = synth.activations(1, cfg.n_embd, seed=1, device="cpu")
+    out, ids, w = layer(h.to(dev))
+    ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
+    np.testing.assert_array_equal(to_np(ids), rid)
+    np.testing.assert_allclose(to_np(w), rw, rtol=1e-5)
+    err = rel_max(to_np(out), ref)
+    assert err < FFN_TOL
+    assert err < 1e-5, err
+
+
+def test_qwen3_layer_decode(dev):
+    """BASELINE config 4 at T=1: Qwen3-235B-shaped Q4_K layer."""
+    from nurostream_amd import synth
+    cfg = synth.QWEN3_235B
+    t = synth.make_layer(cfg, seed=0, device=dev)
+    layer = _layer(cfg, t, "gguf")
+    h = synth.activations(1, cfg.n_embd, seed=2, device="cpu")
+    out, ids, w = layer(h.to(dev))
+    ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
+    np.testing.assert_array_equal(to_np(ids), rid)
+    assert rel_max(to_np(out), ref) < 1e-5
