@@ -143,6 +143,17 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
                     float *out, int32_t *ids, float *weights, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
+/* nsx_moe_forward that also records events[0..NSX_MOE_PHASES] (hipEvent_t,
+ * created by the caller) on the stream: before the router, after the router
+ * and top-k, after gate/up, after down, after the combine. It times the
+ * phases of the same kernels; the reference has no counterpart (its phases
+ * are separate torch calls, model/gpt_oss.py:123-177). */
+#define NSX_MOE_PHASES 4
+int nsx_moe_forward_timed(const nsx_moe_layer *L, const float *h, int64_t T,
+                          float *out, int32_t *ids, float *weights,
+                          void *workspace, int64_t workspace_bytes,
+                          void *stream, void *const *events);
+
 #ifdef __cplusplus
 }
 #endif

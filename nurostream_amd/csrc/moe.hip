@@ -872,13 +872,17 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
   return NSX_OK;
 }
 
-template <int FMT>
-static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st) {
+template <int FMT, typename Mark>
+static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, Mark* mark) {
   const int64_t P = T * d.top_k;
   const size_t lds1 = (size_t)(d.n_embd + d.n_embd / 32) * 4;
   const unsigned g1 = (unsigned)(P * nsx_cdiv(d.n_ff, RAW_ROWS_PER_WG));
   hipLaunchKernelGGL(moe_gu_raw_kernel<FMT>, dim3(g1), dim3(256), lds1, st, d);
   NSX_LAUNCHED();
+  if (mark) {
+    int rc = (*mark)(2);
+    if (rc) return rc;
+  }
   const size_t lds2 = (size_t)d.top_k * (d.n_ff + d.n_ff / 32) * 4;
   if (lds2 > 64 * 1024)
     NSX_HIP(hipFuncSetAttribute((const void*)moe_down_raw_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -886,11 +890,14 @@ static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st) {
   const unsigned g2 = (unsigned)(T * nsx_cdiv(d.n_embd, RAW_ROWS_PER_WG));
   hipLaunchKernelGGL(moe_down_raw_kernel<FMT>, dim3(g2), dim3(256), lds2, st, d);
   NSX_LAUNCHED();
+  if (mark) return (*mark)(3);  // the raw down phase also combines
   return NSX_OK;
 }
 
-extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
-                               float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
+// ev: NULL, or NSX_MOE_PHASES + 1 events recorded on the stream at the phase
+// boundaries (before the router, then after each phase).
+static int moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
+                       void* workspace, int64_t workspace_bytes, void* stream, void* const* ev) {
   int rc = check_layer(L, T);
   if (rc) return rc;
   NSX_REQUIRE(h && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
@@ -934,6 +941,11 @@ extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T
   d.alpha = L->alpha;
   d.limit = L->limit;
 
+  auto mark = [&](int i) -> int {
+    if (ev) NSX_HIP(hipEventRecord((hipEvent_t)ev[i], st));
+    return NSX_OK;
+  };
+  if ((rc = mark(0))) return rc;
   rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
                      (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xfh) : nullptr, st);
   if (rc) return rc;
@@ -946,23 +958,43 @@ extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T
     d.nb4_d = p.nb4_d;
     d.qsb_gu = nsx_cdiv(L->n_ff, 64) * d.nb_gu * 1024;
     d.qsb_d = nsx_cdiv(L->n_embd, 64) * d.nb_d * 1024;
+    if ((rc = mark(1))) return rc;
     hipLaunchKernelGGL(moe_gu_mfma_kernel, dim3((unsigned)(P * (L->n_ff / 64))), dim3(128 * GU_CHUNKS), 0, st, d);
     NSX_LAUNCHED();
+    if ((rc = mark(2))) return rc;
     hipLaunchKernelGGL(moe_down_mfma_kernel, dim3((unsigned)(P * (L->n_embd / 64))), dim3(64 * DN_CHUNKS), 0, st,
                        d);
     NSX_LAUNCHED();
+    if ((rc = mark(3))) return rc;
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
                        d);
     NSX_LAUNCHED();
-    return NSX_OK;
+    return mark(4);
   }
   rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st);
   if (rc) return rc;
+  if ((rc = mark(1))) return rc;
+  auto* mk = ev ? &mark : nullptr;
   switch (L->ggml_type) {
-    case NSX_MXFP4: return launch_raw_phases<NSX_MXFP4>(d, T, st);
-    case NSX_Q4_K: return launch_raw_phases<NSX_Q4_K>(d, T, st);
-    case NSX_Q4_0: return launch_raw_phases<NSX_Q4_0>(d, T, st);
-    case NSX_Q8_0: return launch_raw_phases<NSX_Q8_0>(d, T, st);
+    case NSX_MXFP4: rc = launch_raw_phases<NSX_MXFP4>(d, T, st, mk); break;
+    case NSX_Q4_K: rc = launch_raw_phases<NSX_Q4_K>(d, T, st, mk); break;
+    case NSX_Q4_0: rc = launch_raw_phases<NSX_Q4_0>(d, T, st, mk); break;
+    case NSX_Q8_0: rc = launch_raw_phases<NSX_Q8_0>(d, T, st, mk); break;
+    default: return nsx_fail(NSX_ENOTIMPL, "expert weight type %d", L->ggml_type);
   }
-  return nsx_fail(NSX_ENOTIMPL, "expert weight type %d", L->ggml_type);
+  if (rc) return rc;
+  return mark(4);
+}
+
+extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
+                               float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
+  return moe_forward(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int nsx_moe_forward_timed(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
+                                     float* weights, void* workspace, int64_t workspace_bytes, void* stream,
+                                     void* const* events) {
+  NSX_REQUIRE(events, NSX_EINVAL, "null event array");
+  for (int i = 0; i <= NSX_MOE_PHASES; ++i) NSX_REQUIRE(events[i], NSX_EINVAL, "null event %d", i);
+  return moe_forward(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, events);
 }

@@ -123,6 +123,30 @@ class MoELayer:
 
     __call__ = forward
 
+    def forward_timed(self, h: torch.Tensor, events, out: torch.Tensor | None = None,
+                      ids: torch.Tensor | None = None, weights: torch.Tensor | None = None):
+        """forward() that records len(events) == 5 torch.cuda.Event(enable_timing=True)
+        at the phase boundaries (before router, after router+top-k, after gate/up,
+        after down, after combine) on the current stream."""
+        if len(events) != N.MOE_PHASES + 1:
+            raise ValueError(f"need {N.MOE_PHASES + 1} events")
+        h = h.reshape(-1, self.n_embd).float().contiguous()
+        T = h.shape[0]
+        out = torch.empty((T, self.n_embd), dtype=torch.float32, device=self.device) if out is None else out
+        ids = torch.empty((T, self.top_k), dtype=torch.int32, device=self.device) if ids is None else ids
+        weights = (torch.empty((T, self.top_k), dtype=torch.float32, device=self.device)
+                   if weights is None else weights)
+        for ev in events:
+            if ev.cuda_event == 0:  # torch creates the HIP event lazily, on first record
+                ev.record()
+        handles = (C.c_void_p * len(events))(*[ev.cuda_event for ev in events])
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            N.check(N.load().nsx_moe_forward_timed(C.byref(self._c), h.data_ptr(), T, out.data_ptr(),
+                                                   ids.data_ptr(), weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                   N.stream_ptr(self.device), handles), "moe_forward_timed")
+        return out, ids, weights
+
 
 def router_topk(h: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, top_k: int,
                 mode: str = "gptoss"):
