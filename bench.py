@@ -11,8 +11,12 @@ Weights of `--layers` independently seeded layers (1.7 GB of experts each)
 rotate step by step and every step has its own token, so the expert bytes of
 a step come from HBM rather than the 256 MB Infinity Cache. The K timed steps
 run as one HIP graph (launch overhead as in a serving loop). Per-kernel
-durations come from HIP events recorded between the phases of the same
-kernels (nsx_moe_forward_timed) in an eager pass that follows the timed one.
+durations: `--profile-steps` further tokens, each with its own workspace, go
+through the layer phase by phase (nsx_moe_phase); each phase is one HIP graph
+of that kernel launched back to back over all those tokens, timed with HIP
+events around its replay (an event pair around a single eager launch adds
+several microseconds of marker latency). The phase outputs must equal the
+full forward's.
 
 Prints one JSON line (the driver's contract) with a `roofline` object for the
 dominant kernel (the gate/up dequant-GEMV) and a `cpu_baseline` object: the
@@ -37,7 +41,7 @@ def _parse():
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--layers", type=int, default=6, help="rotating weight copies (1.7 GB each)")
     p.add_argument("--layout", choices=["t64", "gguf"], default="t64")
-    p.add_argument("--profile-steps", type=int, default=96, help="eager steps timed per phase")
+    p.add_argument("--profile-steps", type=int, default=96, help="tokens timed per phase graph")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--seed", type=int, default=0)
@@ -169,23 +173,38 @@ def main():
     ms_per_step = ms_total / K
     tok_s = K * T / (ms_total / 1e3)
 
-    # per-phase durations: eager steps behind a spin kernel so that the host
-    # enqueues ahead of the GPU and the phase gaps are the GPU's own
+    # per-kernel durations: R tokens, one workspace each, phase by phase; each
+    # phase is a graph of R back-to-back launches of that phase's kernel
     P0 = W + K
-    n_prof = args.profile_steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(N.MOE_PHASES + 1)] for _ in range(n_prof)]
-    for row in evs:
-        for e in row:
-            e.record()
+    R = args.profile_steps
+    toks = list(range(P0, P0 + R))
+    wss = [layers[i % n_layers].new_workspace(T) for i in toks]
+    graphs = []
+    with torch.cuda.stream(stream):
+        for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for j, i in enumerate(toks):
+                    layers[i % n_layers].phase(ph, X[i:i + 1], outs[i:i + 1], ids[i:i + 1], wts[i:i + 1], wss[j])
+            graphs.append(g)
     torch.cuda.synchronize()
-    torch.cuda._sleep(50_000_000)
-    for j in range(n_prof):
-        i = P0 + j
-        layers[i % n_layers].forward_timed(X[i:i + 1], evs[j], out=outs[i:i + 1], ids=ids[i:i + 1],
-                                           weights=wts[i:i + 1])
+    for g in graphs:  # first replay: graph upload, untimed
+        g.replay()
     torch.cuda.synchronize()
-    phase_us = [sum(evs[j][p].elapsed_time(evs[j][p + 1]) for j in range(n_prof)) * 1e3 / n_prof
-                for p in range(N.MOE_PHASES)]
+    phase_us = []
+    for g in graphs:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        phase_us.append(e0.elapsed_time(e1) * 1e3 / R)
+    ph_out = outs[P0:P0 + R].clone()
+    for i in toks:
+        step(i)
+    torch.cuda.synchronize()
+    if not torch.equal(ph_out, outs[P0:P0 + R]):
+        raise RuntimeError("phase-by-phase outputs differ from nsx_moe_forward")
 
     gu_bytes, dn_bytes = _expert_bytes_per_token(cfg)
     gu_us = phase_us[1]
@@ -212,7 +231,7 @@ def main():
                    "layout": args.layout, "rotating_layers": n_layers, "hidden": cfg.n_embd,
                    "experts": cfg.n_expert, "top_k": cfg.top_k, "graph": True},
         "layer_GBps": round(layer_bytes / (ms_per_step * 1e-3) / 1e9, 1),
-        "phase_us": {"router_topk": round(phase_us[0], 3), "gate_up": round(phase_us[1], 3),
+        "kernel_us": {"router": round(phase_us[0], 3), "gate_up": round(phase_us[1], 3),
                      "down": round(phase_us[2], 3), "combine": round(phase_us[3], 3)},
         "down_GBps": round(dn_bytes / (phase_us[2] * 1e-6) / 1e9, 1),
         "wall_s": round(wall_s, 4),

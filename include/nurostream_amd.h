@@ -143,16 +143,23 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
                     float *out, int32_t *ids, float *weights, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
-/* nsx_moe_forward that also records events[0..NSX_MOE_PHASES] (hipEvent_t,
- * created by the caller) on the stream: before the router, after the router
- * and top-k, after gate/up, after down, after the combine. It times the
- * phases of the same kernels; the reference has no counterpart (its phases
- * are separate torch calls, model/gpt_oss.py:123-177). */
-#define NSX_MOE_PHASES 4
-int nsx_moe_forward_timed(const nsx_moe_layer *L, const float *h, int64_t T,
-                          float *out, int32_t *ids, float *weights,
-                          void *workspace, int64_t workspace_bytes,
-                          void *stream, void *const *events);
+/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, plus top-k for
+ * the GGUF layout), NSX_PHASE_GATE_UP (expert gate/up GEMVs + activation;
+ * in the t64 layout also the top-k and the ids/weights outputs),
+ * NSX_PHASE_DOWN (expert down GEMVs; in the GGUF layout also the combine) and
+ * NSX_PHASE_COMBINE. A phase reads what the earlier phases of the same call
+ * sequence left in the workspace; running the four in order is
+ * nsx_moe_forward. Callers use it to interleave other work (block reads,
+ * another layer's router) between phases or to time one phase; the
+ * reference runs these steps as separate torch calls
+ * (model/gpt_oss.py:123-177). */
+#define NSX_PHASE_ROUTER 0
+#define NSX_PHASE_GATE_UP 1
+#define NSX_PHASE_DOWN 2
+#define NSX_PHASE_COMBINE 3
+int nsx_moe_phase(const nsx_moe_layer *L, int phase, const float *h, int64_t T,
+                  float *out, int32_t *ids, float *weights, void *workspace,
+                  int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

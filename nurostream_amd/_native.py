@@ -57,9 +57,9 @@ _SIGS = {
     "nsx_router_topk": (_i, [_p, _i64, _i64, _p, _i, _p, _i64, _i, _i, _p, _p, _p, _p]),
     "nsx_moe_workspace_bytes": (_i64, [C.POINTER(MoeLayerC), _i64]),
     "nsx_moe_forward": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p, _i64, _p]),
-    "nsx_moe_forward_timed": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p, _i64, _p, _p]),
+    "nsx_moe_phase": (_i, [C.POINTER(MoeLayerC), _i, _p, _i64, _p, _p, _p, _p, _i64, _p]),
 }
-MOE_PHASES = 4
+PHASE_ROUTER, PHASE_GATE_UP, PHASE_DOWN, PHASE_COMBINE = 0, 1, 2, 3
 
 
 class NativeError(RuntimeError):

@@ -280,10 +280,8 @@ static int check_router(int64_t T, int64_t K, int wdt, int64_t E, int k, int mod
 static int launch_logits(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias, int64_t E,
                          float* logits, uint8_t* xfrag, hipStream_t st) {
   const dim3 grid((unsigned)nsx_cdiv(E, 4), (unsigned)nsx_cdiv(T, RT_TT));
-  hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, h, (int)T, (int)K, w, wdt, bias, (int)E, logits,
-                     xfrag);
-  NSX_LAUNCHED();
-  return NSX_OK;
+  return nsx_launch(router_logits_kernel, grid, dim3(256), 0, st, h, (int)T, (int)K, w, wdt, bias, (int)E, logits,
+                    xfrag);
 }
 
 static int launch_topk(const float* logits, int64_t T, int64_t E, int k, int mode, int32_t* ids, float* wts,
@@ -872,32 +870,28 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
   return NSX_OK;
 }
 
-template <int FMT, typename Mark>
-static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, Mark* mark) {
+template <int FMT>
+static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
   const int64_t P = T * d.top_k;
   const size_t lds1 = (size_t)(d.n_embd + d.n_embd / 32) * 4;
   const unsigned g1 = (unsigned)(P * nsx_cdiv(d.n_ff, RAW_ROWS_PER_WG));
-  hipLaunchKernelGGL(moe_gu_raw_kernel<FMT>, dim3(g1), dim3(256), lds1, st, d);
-  NSX_LAUNCHED();
-  if (mark) {
-    int rc = (*mark)(2);
+  if (gate_up) {
+    int rc = nsx_launch(moe_gu_raw_kernel<FMT>, dim3(g1), dim3(256), lds1, st, d);
     if (rc) return rc;
   }
+  if (!down) return NSX_OK;
   const size_t lds2 = (size_t)d.top_k * (d.n_ff + d.n_ff / 32) * 4;
   if (lds2 > 64 * 1024)
     NSX_HIP(hipFuncSetAttribute((const void*)moe_down_raw_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds2));
   const unsigned g2 = (unsigned)(T * nsx_cdiv(d.n_embd, RAW_ROWS_PER_WG));
-  hipLaunchKernelGGL(moe_down_raw_kernel<FMT>, dim3(g2), dim3(256), lds2, st, d);
-  NSX_LAUNCHED();
-  if (mark) return (*mark)(3);  // the raw down phase also combines
-  return NSX_OK;
+  return nsx_launch(moe_down_raw_kernel<FMT>, dim3(g2), dim3(256), lds2, st, d);
 }
 
-// ev: NULL, or NSX_MOE_PHASES + 1 events recorded on the stream at the phase
-// boundaries (before the router, then after each phase).
-static int moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
-                       void* workspace, int64_t workspace_bytes, void* stream, void* const* ev) {
+// Phases ph0..ph1 of one layer (NSX_PHASE_*); each later phase reads what
+// the earlier ones left in the workspace.
+static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
+                   void* workspace, int64_t workspace_bytes, void* stream, int ph0, int ph1) {
   int rc = check_layer(L, T);
   if (rc) return rc;
   NSX_REQUIRE(h && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
@@ -941,14 +935,13 @@ static int moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float*
   d.alpha = L->alpha;
   d.limit = L->limit;
 
-  auto mark = [&](int i) -> int {
-    if (ev) NSX_HIP(hipEventRecord((hipEvent_t)ev[i], st));
-    return NSX_OK;
-  };
-  if ((rc = mark(0))) return rc;
-  rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
-                     (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xfh) : nullptr, st);
-  if (rc) return rc;
+  auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
+  if (on(NSX_PHASE_ROUTER)) {
+    rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
+                       (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xfh) : nullptr, st);
+    if (rc) return rc;
+    if (!t64 && (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st))) return rc;
+  }
   const int64_t P = T * L->top_k;
 
   if (t64) {
@@ -958,43 +951,37 @@ static int moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float*
     d.nb4_d = p.nb4_d;
     d.qsb_gu = nsx_cdiv(L->n_ff, 64) * d.nb_gu * 1024;
     d.qsb_d = nsx_cdiv(L->n_embd, 64) * d.nb_d * 1024;
-    if ((rc = mark(1))) return rc;
-    hipLaunchKernelGGL(moe_gu_mfma_kernel, dim3((unsigned)(P * (L->n_ff / 64))), dim3(128 * GU_CHUNKS), 0, st, d);
-    NSX_LAUNCHED();
-    if ((rc = mark(2))) return rc;
-    hipLaunchKernelGGL(moe_down_mfma_kernel, dim3((unsigned)(P * (L->n_embd / 64))), dim3(64 * DN_CHUNKS), 0, st,
-                       d);
-    NSX_LAUNCHED();
-    if ((rc = mark(3))) return rc;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
-                       d);
-    NSX_LAUNCHED();
-    return mark(4);
+    if (on(NSX_PHASE_GATE_UP) &&
+        (rc = nsx_launch(moe_gu_mfma_kernel, dim3((unsigned)(P * (L->n_ff / 64))), dim3(128 * GU_CHUNKS), 0, st,
+                         d)))
+      return rc;
+    if (on(NSX_PHASE_DOWN) &&
+        (rc = nsx_launch(moe_down_mfma_kernel, dim3((unsigned)(P * (L->n_embd / 64))), dim3(64 * DN_CHUNKS), 0, st,
+                         d)))
+      return rc;
+    if (on(NSX_PHASE_COMBINE) &&
+        (rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
+                         d)))
+      return rc;
+    return NSX_OK;
   }
-  rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st);
-  if (rc) return rc;
-  if ((rc = mark(1))) return rc;
-  auto* mk = ev ? &mark : nullptr;
-  switch (L->ggml_type) {
-    case NSX_MXFP4: rc = launch_raw_phases<NSX_MXFP4>(d, T, st, mk); break;
-    case NSX_Q4_K: rc = launch_raw_phases<NSX_Q4_K>(d, T, st, mk); break;
-    case NSX_Q4_0: rc = launch_raw_phases<NSX_Q4_0>(d, T, st, mk); break;
-    case NSX_Q8_0: rc = launch_raw_phases<NSX_Q8_0>(d, T, st, mk); break;
-    default: return nsx_fail(NSX_ENOTIMPL, "expert weight type %d", L->ggml_type);
+  switch (L->ggml_type) {  // the GGUF-layout down kernel also combines
+    case NSX_MXFP4: return launch_raw_phases<NSX_MXFP4>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+    case NSX_Q4_K: return launch_raw_phases<NSX_Q4_K>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+    case NSX_Q4_0: return launch_raw_phases<NSX_Q4_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+    case NSX_Q8_0: return launch_raw_phases<NSX_Q8_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
   }
-  if (rc) return rc;
-  return mark(4);
+  return nsx_fail(NSX_ENOTIMPL, "expert weight type %d", L->ggml_type);
 }
 
 extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
                                float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
-  return moe_forward(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, nullptr);
+  return moe_run(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, NSX_PHASE_ROUTER,
+                 NSX_PHASE_COMBINE);
 }
 
-extern "C" int nsx_moe_forward_timed(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
-                                     float* weights, void* workspace, int64_t workspace_bytes, void* stream,
-                                     void* const* events) {
-  NSX_REQUIRE(events, NSX_EINVAL, "null event array");
-  for (int i = 0; i <= NSX_MOE_PHASES; ++i) NSX_REQUIRE(events[i], NSX_EINVAL, "null event %d", i);
-  return moe_forward(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, events);
+extern "C" int nsx_moe_phase(const nsx_moe_layer* L, int phase, const float* h, int64_t T, float* out, int32_t* ids,
+                             float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
+  NSX_REQUIRE(phase >= NSX_PHASE_ROUTER && phase <= NSX_PHASE_COMBINE, NSX_EINVAL, "phase %d", phase);
+  return moe_run(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, phase, phase);
 }

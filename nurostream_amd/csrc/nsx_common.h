@@ -36,6 +36,14 @@ int nsx_fail(int code, const char* fmt, ...);
       return nsx_fail(NSX_EHIP, "kernel launch failed: %s", hipGetErrorString(e_)); \
   } while (0)
 
+// Launch `kernel` on `st` and report a failed launch.
+template <typename... KA, typename... A>
+static inline int nsx_launch(void (*kernel)(KA...), dim3 grid, dim3 block, size_t lds, hipStream_t st, A... args) {
+  hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+  NSX_LAUNCHED();
+  return NSX_OK;
+}
+
 static inline int64_t nsx_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // (elements per block, bytes per block) for the block formats the kernels handle.

@@ -123,29 +123,27 @@ class MoELayer:
 
     __call__ = forward
 
-    def forward_timed(self, h: torch.Tensor, events, out: torch.Tensor | None = None,
-                      ids: torch.Tensor | None = None, weights: torch.Tensor | None = None):
-        """forward() that records len(events) == 5 torch.cuda.Event(enable_timing=True)
-        at the phase boundaries (before router, after router+top-k, after gate/up,
-        after down, after combine) on the current stream."""
-        if len(events) != N.MOE_PHASES + 1:
-            raise ValueError(f"need {N.MOE_PHASES + 1} events")
-        h = h.reshape(-1, self.n_embd).float().contiguous()
+    def phase(self, phase: int, h: torch.Tensor, out: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+              workspace: torch.Tensor | None = None) -> None:
+        """Run one phase (_native.PHASE_*) of forward(); later phases read what
+        earlier ones left in `workspace` (default: this layer's for h's T)."""
+        N.require_device(h, out, ids, weights)
+        h = h.reshape(-1, self.n_embd)
+        if h.dtype != torch.float32 or not h.is_contiguous():
+            raise TypeError("phase() takes a contiguous fp32 h")
         T = h.shape[0]
-        out = torch.empty((T, self.n_embd), dtype=torch.float32, device=self.device) if out is None else out
-        ids = torch.empty((T, self.top_k), dtype=torch.int32, device=self.device) if ids is None else ids
-        weights = (torch.empty((T, self.top_k), dtype=torch.float32, device=self.device)
-                   if weights is None else weights)
-        for ev in events:
-            if ev.cuda_event == 0:  # torch creates the HIP event lazily, on first record
-                ev.record()
-        handles = (C.c_void_p * len(events))(*[ev.cuda_event for ev in events])
-        ws = self.workspace(T)
+        ws = self.workspace(T) if workspace is None else workspace
         with torch.cuda.device(self.device):
-            N.check(N.load().nsx_moe_forward_timed(C.byref(self._c), h.data_ptr(), T, out.data_ptr(),
-                                                   ids.data_ptr(), weights.data_ptr(), ws.data_ptr(), ws.numel(),
-                                                   N.stream_ptr(self.device), handles), "moe_forward_timed")
-        return out, ids, weights
+            N.check(N.load().nsx_moe_phase(C.byref(self._c), int(phase), h.data_ptr(), T, out.data_ptr(),
+                                           ids.data_ptr(), weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                                           N.stream_ptr(self.device)), f"moe_phase {phase}")
+
+    def new_workspace(self, T: int) -> torch.Tensor:
+        """A separate zeroed workspace for T tokens (for phase runs that overlap)."""
+        n = N.load().nsx_moe_workspace_bytes(C.byref(self._c), T)
+        if n < 0:
+            raise ValueError(f"bad layer for T={T}")
+        return torch.zeros(max(n, 256), dtype=torch.uint8, device=self.device)
 
 
 def router_topk(h: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, top_k: int,
