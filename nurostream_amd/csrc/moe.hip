@@ -836,8 +836,10 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   return p;
 }
 
+static int check_layer(const nsx_moe_layer* L, int64_t T);
+
 extern "C" int64_t nsx_moe_workspace_bytes(const nsx_moe_layer* L, int64_t T) {
-  if (!L || T < 1) return -1;
+  if (check_layer(L, T) != NSX_OK) return -1;
   return moe_plan(L, T).total;
 }
 

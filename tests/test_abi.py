@@ -1,0 +1,92 @@
+"""The C-ABI library loads and exports what include/nurostream_amd.h declares (CPU only).
+
+Only host-side entry points (sizes, version, argument validation that
+returns before any HIP call) are called here; compute calls need a GPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+
+import pytest
+
+from nurostream_amd import _native as N
+from nurostream_amd.format.gguf import GGMLType
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not N.LIB_PATH.exists():
+        from nurostream_amd import build
+        build.build()
+    return N.load()
+
+
+def test_every_header_function_is_exported(lib):
+    names = N.header_functions()
+    assert len(names) >= 12, names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the ctypes binding covers every one of them
+    assert sorted(N._SIGS) == names
+
+
+def test_exported_symbols_are_the_header_set(lib):
+    """nm: the .so exports no other nsx_* entry point than the header declares."""
+    out = subprocess.run(["nm", "-D", "--defined-only", str(N.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = sorted({ln.split()[-1] for ln in out.stdout.splitlines() if ln.split()[-1].startswith("nsx_")})
+    assert exported == N.header_functions()
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.nsx_abi_version() == 1
+    assert isinstance(lib.nsx_last_error(), bytes)
+
+
+def test_t64_sizes(lib):
+    # 64-row tiles: qs 1024 B per (tile, 32-column block) + e8m0 scales, rows padded to 64
+    per = lib.nsx_t64_bytes(int(GGMLType.MXFP4), 2880, 2880)
+    assert per >= 2880 * 90 * 17
+    assert per < 2880 * 90 * 17 * 1.01
+    assert lib.nsx_t64_bytes(int(GGMLType.MXFP4), 1, 32) > 0
+    assert lib.nsx_t64_bytes(int(GGMLType.Q4_K), 64, 256) < 0  # MXFP4 only
+    assert lib.nsx_t64_bytes(int(GGMLType.MXFP4), 64, 33) < 0  # K must be whole blocks
+
+
+def _gptoss_layer(layout=N.LAYOUT_T64):
+    L = N.MoeLayerC()
+    L.ggml_type = int(GGMLType.MXFP4)
+    L.layout = layout
+    L.n_expert, L.top_k, L.n_embd, L.n_ff = 128, 4, 2880, 2880
+    L.router_mode, L.act, L.alpha, L.limit = N.ROUTE_GPTOSS, N.ACT_CLAMPED_SWIGLU, 1.702, 7.0
+    L.router_w = 1  # never dereferenced by the host-side checks
+    L.router_dtype = int(GGMLType.BF16)
+    L.gate_base = L.up_base = L.down_base = 1
+    L.gate_stride = L.up_stride = L.down_stride = 1 << 22
+    return L
+
+
+def test_workspace_bytes(lib):
+    L = _gptoss_layer()
+    w1 = lib.nsx_moe_workspace_bytes(C.byref(L), 1)
+    w8 = lib.nsx_moe_workspace_bytes(C.byref(L), 8)
+    assert 0 < w1 < w8 < 64 << 20
+    L.top_k = 0
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 1) < 0
+
+
+def test_validation_errors_return_codes(lib):
+    # unsupported block type: NotImplemented, with a message
+    rc = lib.nsx_dequantize(14, None, 210, 256, None, N.DT_F32, None)
+    assert rc == N.ENOTIMPL and b"Q4_K" in lib.nsx_last_error()
+    rc = lib.nsx_dequantize(int(GGMLType.Q8_0), None, 34, 64, None, N.DT_F32, None)
+    assert rc == N.EINVAL  # more elements than blocks
+    # router: top_k above n_expert
+    rc = lib.nsx_router_topk(None, 1, 64, None, int(GGMLType.F32), None, 4, 5, N.ROUTE_GPTOSS, None, None, None, None)
+    assert rc == N.EINVAL
+    # layer phase out of range
+    L = _gptoss_layer()
+    rc = lib.nsx_moe_phase(C.byref(L), 7, None, 1, None, None, None, None, 0, None)
+    assert rc == N.EINVAL
+    with pytest.raises(ValueError):
+        N.check(rc)
