@@ -1,6 +1,6 @@
 // MoE expert path for gfx950: router logits, top-k, routed expert products
-// (MFMA over t64 tiles, or VALU over raw GGUF rows), activation and the
-// weighted combine -- with expert ids never leaving the device.
+// (block-scaled MFMA over t64 tiles, or VALU over raw GGUF rows), activation
+// and the weighted combine -- with expert ids never leaving the device.
 //
 // Reference semantics (neurostream/): model/gpt_oss.py:61-70,116-177 and
 // moe/router.py:59-69,173-219. The row-window products of
@@ -11,6 +11,7 @@
 // a kernel boundary (agent-scope fences cost an L2 write-back/invalidate per
 // wave on gfx950), and reductions stay inside one workgroup's LDS.
 #include "nsx_common.h"
+#include "mx.h"
 #include "raw_dot.h"
 
 #include <algorithm>
@@ -22,72 +23,6 @@ constexpr int MAX_TOPK = 16;
 constexpr int MAX_EXPERTS = 256;
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-
-// ---------------------------------------------------------------------------
-// activation fragments ("xfrag")
-//
-// The MFMA kernels compute y = W x with W's MXFP4 blocks converted exactly to
-// bf16 (pre-scaled by their e8m0 scale) and x split into three bf16 terms
-// hi + mid + lo (|x - hi - mid - lo| <= 2^-24 |x|) that occupy B columns 0..2
-// of v_mfma_f32_16x16x32_bf16. A lane (col c = l%16, group q = l/16) supplies
-// 8 K-slots: for K-step s (blocks 4s..4s+3) and sub-step j, slot 2u / 2u+1
-// hold elements 4j+u / 16+4j+u of block 4s+q -- exactly the order in which
-// v_cvt_scalef32_pk_bf16_fp4 expands byte u of qs dword j.
-// Storage per token (or per expert pair): [s][j][q][c:3][u:4] dwords, each
-// dword = (bf16 of element 4j+u) | (bf16 of element 16+4j+u) << 16.
-constexpr int XF_SPLIT = 3;
-constexpr int XF_STEP_BYTES = 4 * 4 * XF_SPLIT * 16;  // 768 B per 4-block step
-
-__device__ __forceinline__ void split3(float v, uint32_t (&o)[3]) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, v);
-  const uint32_t hi = b & 0xffff0000u;
-  const float r1 = v - __builtin_bit_cast(float, hi);  // exact
-  const uint32_t mid = __builtin_bit_cast(uint32_t, r1) & 0xffff0000u;
-  const float r2 = r1 - __builtin_bit_cast(float, mid);  // exact
-  o[0] = hi >> 16;
-  o[1] = mid >> 16;
-  o[2] = nsx_f2bf(r2);
-}
-
-// byte offset of (element n, split c) inside one activation's xfrag
-__device__ __forceinline__ uint32_t xfrag_offset(int n, int c) {
-  const int b = n >> 5, ee = n & 31;
-  const int s = b >> 2, q = b & 3;
-  const int half = ee >> 4, e2 = ee & 15;
-  const int j = e2 >> 2, u = e2 & 3;
-  return ((((uint32_t)(s * 4 + j) * 4 + q) * XF_SPLIT + c) * 4 + u) * 4 + half * 2;
-}
-
-// Fill xfrag entries for T activation rows of length K (grid-stride over all
-// dwords, zero for blocks past K). Called from the router kernel.
-__device__ __forceinline__ void build_xfrag(const float* __restrict__ x, int T, int K, uint8_t* __restrict__ xf,
-                                            int64_t gtid, int64_t gstride) {
-  const int nb = K / 32, nb4 = (nb + 3) / 4;
-  const int64_t per_tok = (int64_t)nb4 * (XF_STEP_BYTES / 4);
-  for (int64_t d = gtid; d < per_tok * T; d += gstride) {
-    const int t = (int)(d / per_tok);
-    int rem = (int)(d - (int64_t)t * per_tok);
-    const int u = rem & 3;
-    rem >>= 2;
-    const int c = rem % XF_SPLIT;
-    rem /= XF_SPLIT;
-    const int q = rem & 3;
-    rem >>= 2;
-    const int j = rem & 3;
-    const int s = rem >> 2;
-    const int b = 4 * s + q;
-    uint32_t lo[3] = {0, 0, 0}, hi[3] = {0, 0, 0};
-    if (b < nb) {
-      const float* xb = x + (int64_t)t * K + b * 32;
-      split3(xb[4 * j + u], lo);
-      split3(xb[16 + 4 * j + u], hi);
-    }
-    ((uint32_t*)xf)[d] = lo[c] | (hi[c] << 16);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// router logits: one wave per expert row, TT tokens per workgroup row
 
 constexpr int RT_TT = 8;
 
@@ -107,17 +42,30 @@ __device__ __forceinline__ void load8_w(const void* W, int wdt, int64_t off, flo
   }
 }
 
-constexpr int RT_MAXC = 8;  // 512-element chunks per lane and pass (K <= 4096 in one pass)
+constexpr int RT_MAXC = 8;   // 512-element chunks per lane and pass (K <= 4096 in one pass)
+constexpr int RT_XQ_WGS = 16;  // extra workgroups that quantize h for the t64 expert kernels
 
+// Workgroups [0, ceil(E/4)) compute logits (one wave per expert, RT_TT tokens
+// per grid row); with xq set, RT_XQ_WGS more workgroups per grid row build
+// the tokens' activation terms. Loads are unpredicated (addresses clamped,
+// tails zeroed after the load) so that they are all in flight together.
 __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restrict__ h, int T, int K,
                                                             const void* __restrict__ W, int wdt,
                                                             const float* __restrict__ bias, int E,
-                                                            float* __restrict__ logits, uint8_t* __restrict__ xfrag) {
+                                                            float* __restrict__ logits, uint8_t* __restrict__ xq) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  if (xfrag) {
-    const int64_t nthreads = (int64_t)gridDim.x * gridDim.y * blockDim.x;
-    const int64_t tid = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
-    build_xfrag(h, T, K, xfrag, tid, nthreads);
+  const int ewgs = (E + 3) / 4;
+  if ((int)blockIdx.x >= ewgs) {  // activation terms of h, two blocks per wave task
+    const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
+    const int64_t tasks = (int64_t)T * pairs;
+    const int64_t nwaves = (int64_t)gridDim.y * RT_XQ_WGS * 4;
+    for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - ewgs)) * 4 + wave; task < tasks;
+         task += nwaves) {
+      const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
+      const float r = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
+      xq_block(b < nb ? r : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
+    }
+    return;
   }
   const int e = blockIdx.x * 4 + wave;
   const int t0 = blockIdx.y * RT_TT;
@@ -127,14 +75,15 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
 #pragma unroll
   for (int i = 0; i < RT_TT; ++i) acc[i] = 0.f;
   for (int k0 = 0; k0 < K; k0 += RT_MAXC * 512) {
-    // every weight and activation load of the pass is issued before the arithmetic
     float w[RT_MAXC][8];
 #pragma unroll
     for (int c = 0; c < RT_MAXC; ++c) {
       const int k = k0 + c * 512 + lane * 8;
-      if (k < K) {
-        load8_w(W, wdt, (int64_t)e * K + k, w[c]);
-      } else {
+      load8_w(W, wdt, (int64_t)e * K + (k < K ? k : K - 8), w[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < RT_MAXC; ++c) {
+      if (k0 + c * 512 + lane * 8 >= K) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) w[c][u] = 0.f;
       }
@@ -145,16 +94,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
 #pragma unroll
       for (int c = 0; c < RT_MAXC; ++c) {
         const int k = k0 + c * 512 + lane * 8;
-        if (k < K) {
-          ha[c] = *(const v4f*)(hp + k);
-          hb[c] = *(const v4f*)(hp + k + 4);
-        } else {
-          ha[c] = hb[c] = v4f{0.f, 0.f, 0.f, 0.f};
-        }
+        const int kc = k < K ? k : K - 8;
+        ha[c] = *(const v4f*)(hp + kc);
+        hb[c] = *(const v4f*)(hp + kc + 4);
       }
       float s = acc[i];
 #pragma unroll
-      for (int c = 0; c < RT_MAXC; ++c) {
+      for (int c = 0; c < RT_MAXC; ++c) {  // w is zero past K
         s = fmaf(w[c][0], ha[c].x, s); s = fmaf(w[c][1], ha[c].y, s);
         s = fmaf(w[c][2], ha[c].z, s); s = fmaf(w[c][3], ha[c].w, s);
         s = fmaf(w[c][4], hb[c].x, s); s = fmaf(w[c][5], hb[c].y, s);
@@ -202,7 +148,7 @@ __device__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode, 
 #pragma unroll
     for (int i = 0; i < NV; ++i)
       if (ok[i]) m = fmaxf(m, v[i]);
-    m = key2f(__reduce_max_sync(~0ull, f2key(m)));
+    m = key2f(nsx_wave_max_u32(f2key(m)));
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
@@ -229,8 +175,8 @@ __device__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode, 
         lk = key[i];
         li = lane + 64 * i;
       }
-    const uint32_t mk = __reduce_max_sync(~0ull, li == 0xffffu ? 0u : lk);
-    const uint32_t wi = __reduce_min_sync(~0ull, (li != 0xffffu && lk == mk) ? li : 0xffffu);
+    const uint32_t mk = nsx_wave_max_u32(li == 0xffffu ? 0u : lk);
+    const uint32_t wi = nsx_wave_min_u32((li != 0xffffu && lk == mk) ? li : 0xffffu);
     sel_i[j] = wi == 0xffffu ? 0 : (int)wi;
     sel_v[j] = key2f(mk);
 #pragma unroll
@@ -278,10 +224,10 @@ static int check_router(int64_t T, int64_t K, int wdt, int64_t E, int k, int mod
 }
 
 static int launch_logits(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias, int64_t E,
-                         float* logits, uint8_t* xfrag, hipStream_t st) {
-  const dim3 grid((unsigned)nsx_cdiv(E, 4), (unsigned)nsx_cdiv(T, RT_TT));
+                         float* logits, uint8_t* xq, hipStream_t st) {
+  const dim3 grid((unsigned)(nsx_cdiv(E, 4) + (xq ? RT_XQ_WGS : 0)), (unsigned)nsx_cdiv(T, RT_TT));
   return nsx_launch(router_logits_kernel, grid, dim3(256), 0, st, h, (int)T, (int)K, w, wdt, bias, (int)E, logits,
-                    xfrag);
+                    xq);
 }
 
 static int launch_topk(const float* logits, int64_t T, int64_t E, int k, int mode, int32_t* ids, float* wts,
@@ -304,131 +250,67 @@ extern "C" int nsx_router_topk(const float* h, int64_t T, int64_t K, const void*
 }
 
 // ---------------------------------------------------------------------------
-// t64 tile partial dot on the VALU (the lane owns one row of a 64-row tile);
-// used by nsx_t64_gemv (stream_linear over resident t64 slabs).
+// t64 GEMV over a row window (stream_linear over resident t64 slabs): one
+// workgroup per tile; the window's tokens (up to 4) are first quantized into
+// activation terms in LDS, then the four waves split the K-steps and meet in
+// LDS.
 
-template <int NT, int GMAX>
-__device__ __forceinline__ void mx_t64_partial(const uint8_t* __restrict__ mat, int64_t qs_bytes, int nb, int nb4,
-                                               int tile, int g0, int g1, const float* __restrict__ x,
-                                               int64_t xstride, float (&acc)[NT]) {
-  const int lane = __lane_id();
-  typedef const __attribute__((address_space(1))) v4u gv4u;
-  typedef const __attribute__((address_space(1))) uint32_t gu32;
-  gv4u* qs = (gv4u*)(mat + (int64_t)tile * nb * 1024 + lane * 16);
-  gu32* sc = (gu32*)(mat + qs_bytes + (int64_t)tile * nb4 * 256) + lane;
-  for (int gs = g0; gs < g1; gs += GMAX) {
-    v4u q[GMAX * 4];
-    uint32_t s[GMAX];
-#pragma unroll
-    for (int gi = 0; gi < GMAX; ++gi) {
-      const int g = gs + gi;
-      if (g < g1) {
-        s[gi] = sc[(int64_t)g * 64];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int b = g * 4 + j;
-          q[gi * 4 + j] = b < nb ? qs[(int64_t)b * 64] : v4u{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-#pragma unroll
-    for (int gi = 0; gi < GMAX; ++gi) {
-      const int g = gs + gi;
-      if (g >= g1) break;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int b = g * 4 + j;
-        if (b >= nb) break;
-        const int e = (int)((s[gi] >> (8 * j)) & 0xffu);
-        float p0[NT], p1[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) p0[t] = p1[t] = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t w = q[gi * 4 + j][i];
-          const v2f c0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
-          const v2f c1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
-          const v2f c2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
-          const v2f c3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            // constant address space: x is uniform and read-only here (scalar loads)
-            const __attribute__((address_space(4))) float* xb =
-                (const __attribute__((address_space(4))) float*)(x + t * xstride + b * 32 + 4 * i);
-            p0[t] = fmaf(c0.x, xb[0], p0[t]);
-            p1[t] = fmaf(c0.y, xb[16], p1[t]);
-            p0[t] = fmaf(c1.x, xb[1], p0[t]);
-            p1[t] = fmaf(c1.y, xb[17], p1[t]);
-            p0[t] = fmaf(c2.x, xb[2], p0[t]);
-            p1[t] = fmaf(c2.y, xb[18], p1[t]);
-            p0[t] = fmaf(c3.x, xb[3], p0[t]);
-            p1[t] = fmaf(c3.y, xb[19], p1[t]);
-          }
-        }
-        // ggml value = 2^(e-128) * (2*e2m1) = 2^(e-127) * e2m1
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] += __builtin_amdgcn_ldexpf(p0[t] + p1[t], e - 127);
-      }
-    }
-  }
-}
+constexpr int T64_S = 3;  // K-steps in flight per wave
 
-constexpr int T64_GMAX = 8;
-
-template <int NT>
-__global__ __launch_bounds__(256) void t64_gemv_kernel(const uint8_t* __restrict__ mat, int64_t qs_bytes, int nb,
-                                                       int nb4, int64_t row_lo, int64_t row_hi, int tile0,
-                                                       const float* __restrict__ x, int64_t xstride, int T,
-                                                       float* __restrict__ y, int64_t ystride) {
-  __shared__ float red[4][NT][64];
+__global__ __launch_bounds__(256) void t64_gemv_kernel(const uint8_t* __restrict__ mat, MxGeom G, int64_t row_lo,
+                                                       int64_t row_hi, int tile0, const float* __restrict__ x, int K,
+                                                       int T, float* __restrict__ y, int64_t ystride) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  float* red = (float*)smem;                 // [wave 4][token 4][row 64]
+  uint8_t* xq = smem + 4 * 4 * 64 * 4;       // [token][ns][XQ_STEP]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int tile = tile0 + blockIdx.x;
-  const int gper = (nb4 + 3) / 4;
-  const int g0 = wave * gper, g1 = min(nb4, g0 + gper);
-  float acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = 0.f;
-  mx_t64_partial<NT, T64_GMAX>(mat, qs_bytes, nb, nb4, tile, g0, g1, x, xstride, acc);
-#pragma unroll
-  for (int t = 0; t < NT; ++t) red[wave][t][lane] = acc[t];
-  __syncthreads();
-  if (wave == 0) {
-    const int64_t row = (int64_t)tile * 64 + lane;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const float v = red[0][t][lane] + red[1][t][lane] + red[2][t][lane] + red[3][t][lane];
-      if (t < T && row >= row_lo && row < row_hi) y[(int64_t)t * ystride + (row - row_lo)] = v;
-    }
+  const int64_t xstride = (int64_t)G.ns * XQ_STEP;
+  const int pairs = 2 * G.ns;  // block pairs per token, padding blocks of the last step included
+  for (int task = wave; task < T * pairs; task += 4) {
+    const int t = task / pairs, b = (task % pairs) * 2 + (lane >> 5);
+    const float r = b < G.nb ? x[(int64_t)t * K + b * 32 + (lane & 31)] : 0.f;
+    xq_block(r, b, xq + t * xstride);
   }
-}
-
-template <int NT>
-static int launch_t64_gemv(const void* t64, int64_t n_rows, int64_t K, int64_t lo, int64_t hi, const float* x,
-                           int64_t T, float* y, hipStream_t st) {
-  const int64_t nb = K / 32, nb4 = nsx_cdiv(nb, 4), tiles = nsx_cdiv(n_rows, 64);
-  const int64_t qsb = tiles * nb * 1024;
-  const int64_t tile0 = lo / 64, tile1 = nsx_cdiv(hi, 64);
-  hipLaunchKernelGGL((t64_gemv_kernel<NT>), dim3((unsigned)(tile1 - tile0)), dim3(256), 0, st, (const uint8_t*)t64,
-                     qsb, (int)nb, (int)nb4, lo, hi, (int)tile0, x, K, (int)T, y, hi - lo);
-  NSX_LAUNCHED();
-  return NSX_OK;
+  __syncthreads();
+  const int tile = tile0 + blockIdx.x;
+  const int per = (G.ns + 3) / 4;
+  const int s0 = wave * per, s1 = min(G.ns, s0 + per);
+  v4f D[4] = {};
+  mx_tile_mfma<T64_S, true>(mat + (int64_t)tile * G.tile_bytes, G, s0, s1, xq, 0, xstride, T, D);
+  mx_sum_terms(D);
+  if ((lane & 3) == 0) {
+    const int tok = (lane & 15) >> 2, r0 = 4 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) *(v4f*)(red + (wave * 4 + tok) * 64 + 16 * g + r0) = D[g];
+  }
+  __syncthreads();
+  if (wave < T) {
+    const int64_t row = (int64_t)tile * 64 + lane;
+    const float v = red[(0 * 4 + wave) * 64 + lane] + red[(1 * 4 + wave) * 64 + lane] +
+                    red[(2 * 4 + wave) * 64 + lane] + red[(3 * 4 + wave) * 64 + lane];
+    if (row >= row_lo && row < row_hi) y[(int64_t)wave * ystride + (row - row_lo)] = v;
+  }
 }
 
 extern "C" int nsx_t64_gemv(int t, const void* t64, int64_t n_rows, int64_t K, int64_t row_lo, int64_t row_hi,
                             const void* x, int x_dtype, int64_t T, float* y, void* stream) {
   NSX_REQUIRE(t == NSX_MXFP4, NSX_ENOTIMPL, "t64 GEMV is implemented for MXFP4 only (type %d)", t);
-  NSX_REQUIRE(K > 0 && K % 32 == 0 && K < (1 << 24), NSX_EINVAL, "K=%lld", (long long)K);
+  NSX_REQUIRE(K > 0 && K % 32 == 0 && K <= 8192, NSX_EINVAL, "t64 GEMV takes K in 32..8192, a multiple of 32 "
+              "(K=%lld)", (long long)K);
   NSX_REQUIRE(0 <= row_lo && row_lo <= row_hi && row_hi <= n_rows, NSX_EINVAL, "row window [%lld, %lld) of %lld",
               (long long)row_lo, (long long)row_hi, (long long)n_rows);
   NSX_REQUIRE(T >= 1 && T <= 4, NSX_EINVAL, "t64 GEMV takes T in 1..4 (T=%lld)", (long long)T);
   NSX_REQUIRE(x_dtype == NSX_DT_F32, NSX_ETYPE, "t64 GEMV takes fp32 activations");
   if (row_hi == row_lo) return NSX_OK;
   NSX_REQUIRE(t64 && x && y, NSX_EINVAL, "null buffer");
-  hipStream_t st = S(stream);
-  const float* xf = (const float*)x;
-  if (T == 1) return launch_t64_gemv<1>(t64, n_rows, K, row_lo, row_hi, xf, T, y, st);
-  if (T == 2) return launch_t64_gemv<2>(t64, n_rows, K, row_lo, row_hi, xf, T, y, st);
-  return launch_t64_gemv<4>(t64, n_rows, K, row_lo, row_hi, xf, T, y, st);
+  const MxGeom G = mx_geom(n_rows, K);
+  const int64_t tile0 = row_lo / 64, tile1 = nsx_cdiv(row_hi, 64);
+  const size_t lds = 4 * 4 * 64 * 4 + (size_t)T * G.ns * XQ_STEP;
+  if (lds > 64 * 1024)
+    NSX_HIP(hipFuncSetAttribute((const void*)t64_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  return nsx_launch(t64_gemv_kernel, dim3((unsigned)(tile1 - tile0)), dim3(256), lds, S(stream),
+                    (const uint8_t*)t64, G, row_lo, row_hi, (int)tile0, (const float*)x, (int)K, (int)T, y,
+                    row_hi - row_lo);
 }
 
 // ---------------------------------------------------------------------------
@@ -451,14 +333,15 @@ struct MoeDev {
   const float* down_bias;
   const float* h;
   float* out;
-  float* act;             // (pairs, n_ff) fp32 activations
-  float* ypair;           // (pairs, n_embd) fp32 per-expert down outputs (t64 path)
-  const uint8_t* xf_h;    // xfrag of h, per token
-  uint8_t* xf_a;          // xfrag of act, per pair
+  float* act;            // (pairs, n_ff) fp32 activations (GGUF-layout path)
+  const uint8_t* xq_h;   // activation terms of h, per token (t64 path)
+  float* part_gu;        // (pairs, 2, cg, n_ff) gate/up partial sums (t64 path)
+  float* part_dn;        // (pairs, cd, n_embd) down partial sums (t64 path)
   int n_embd, n_ff;
-  int nb_gu, nb4_gu;      // blocks / steps of K = n_embd
-  int nb_d, nb4_d;        // blocks / steps of K = n_ff
-  int64_t qsb_gu, qsb_d;  // t64 qs-plane bytes of one expert matrix
+  MxGeom ggu, gdn;       // t64 geometry of a gate/up and of a down matrix
+  int cg, sg;            // gate/up K-chunks and K-steps per chunk
+  int cd, sd;            // down K-chunks and K-steps per chunk
+  int tpw;               // down output tiles per workgroup (one wave each)
   int act_kind;
   float alpha, limit;
 };
@@ -494,222 +377,172 @@ __device__ __forceinline__ void slot_order(const int (&ids)[MAX_TOPK], int k, in
 __device__ __forceinline__ float combine_one(float acc, float w, float y) { return __fadd_rn(acc, __fmul_rn(w, y)); }
 
 // ---------------------------------------------------------------------------
-// MFMA expert kernels over t64 tiles (MXFP4)
-
-// e8m0 byte -> fp32 scale 2^(e-127) for v_cvt_scalef32_pk_bf16_fp4, exact for
-// e in 0..254 (e=0 a denormal); e=255 runs with 2^127 and mx_bf16_double.
-__device__ __forceinline__ float mx_scale_f32(uint32_t e) {
-  return __builtin_bit_cast(float, e == 0 ? 0x00400000u : (e == 255 ? (254u << 23) : (e << 23)));
-}
-
-// ggml's e=255 scale is 2^127 on the doubled table, i.e. 2^128 * e2m1. The
-// conversion ran with 2^127, so double each bf16: normal values gain one in
-// the exponent (2^127-magnitudes overflow to inf, like the fp32 reference);
-// zeros stay zero. (Denormals cannot occur at this scale.)
-__device__ __forceinline__ uint32_t mx_bf16_double(uint32_t w2) {
-  uint32_t r = 0;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint32_t v = (w2 >> (16 * h)) & 0xffffu;
-    const uint32_t ex = v & 0x7f80u;
-    if ((v & 0x7fffu) != 0 && ex != 0x7f80u) v = ex == 0x7f00u ? ((v & 0x8000u) | 0x7f80u) : v + 0x80u;
-    r |= v << (16 * h);
-  }
-  return r;
-}
-
-__device__ __forceinline__ v8bf mx_a_operand(uint32_t w, float scale, bool dbl) {
-  uint32_t p[4];
-  p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
-  p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
-  p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
-  p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
-  if (__builtin_expect(dbl, 0)) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = mx_bf16_double(p[i]);
-  }
-  v4u pv = {p[0], p[1], p[2], p[3]};
-  return __builtin_bit_cast(v8bf, pv);
-}
-
-constexpr int MX_CH = 6;  // K-steps (4 blocks each) whose loads one wave holds in flight
-
-// One wave: a whole 64-row t64 tile times an xfrag (global memory) over
-// K-steps [s0, s1). Rows are four MFMA row groups g (rows 16g..16g+15) that
-// share every B operand; lane (i = l%16, q = l/16) loads row 16g+i of block
-// 4s+q (four 256-byte runs per instruction). Each pass issues all of its
-// weight, scale and activation loads before any arithmetic.
-template <int CH>
-struct MxTile {
-  v4u A[CH][4];
-  uint32_t SC[CH][4];
-  v4u B[CH][4];
-};
-
-template <int CH>
-__device__ __forceinline__ void mx_tile_load(MxTile<CH>& r, const uint8_t* __restrict__ mat, int64_t qs_bytes,
-                                             int nb, int nb4, int tile, int s0, int s1,
-                                             const uint8_t* __restrict__ xf) {
-  typedef const __attribute__((address_space(1))) v4u gv4u;
-  typedef const __attribute__((address_space(1))) uint32_t gu32;
-  const int lane = __lane_id();
-  const int i = lane & 15, q = lane >> 4;
-  const uint8_t* qs = mat + (int64_t)tile * nb * 1024 + i * 16;
-  const uint8_t* sc = mat + qs_bytes + (int64_t)tile * nb4 * 256 + i * 4;
-  const bool bcol = i < XF_SPLIT;
-#pragma unroll
-  for (int u = 0; u < CH; ++u) {
-    const int s = s0 + u;
-    if (s < s1) {
-      const int b = min(4 * s + q, nb - 1);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        r.A[u][g] = *(gv4u*)(qs + (int64_t)b * 1024 + g * 256);
-        r.SC[u][g] = *(gu32*)(sc + (int64_t)s * 256 + g * 64);
-      }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        r.B[u][jj] = bcol ? *(gv4u*)(xf + (((s * 4 + jj) * 4 + q) * XF_SPLIT + i) * 16) : v4u{0u, 0u, 0u, 0u};
-    }
-  }
-}
-
-template <int CH>
-__device__ __forceinline__ void mx_tile_compute(const MxTile<CH>& r, int nb, int s0, int s1, v4f (&D)[4]) {
-  const int q = __lane_id() >> 4;
-#pragma unroll
-  for (int u = 0; u < CH; ++u) {
-    const int s = s0 + u;
-    if (s >= s1) break;
-    const bool valid = 4 * s + q < nb;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const uint32_t e = (r.SC[u][g] >> (8 * q)) & 0xffu;
-      const float scale = valid ? mx_scale_f32(e) : 0.f;
-      const bool dbl = valid && e == 255u;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        D[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_a_operand(r.A[u][g][jj], scale, dbl),
-                                                      __builtin_bit_cast(v8bf, r.B[u][jj]), D[g], 0, 0, 0);
-    }
-  }
-}
-
-// y for the tile's 64 rows over K-steps [s0, s1), written to red[64] (rows in
-// tile order). D columns 0..2 (the three activation terms) are summed.
-__device__ __forceinline__ void mx_tile_rows(const uint8_t* __restrict__ mat, int64_t qs_bytes, int nb, int nb4,
-                                             int tile, int s0, int s1, const uint8_t* __restrict__ xf,
-                                             float* __restrict__ red) {
-  v4f D[4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) D[g] = v4f{0.f, 0.f, 0.f, 0.f};
-  MxTile<MX_CH> r;
-  for (int p0 = s0; p0 < s1; p0 += MX_CH) {
-    const int p1 = min(s1, p0 + MX_CH);
-    mx_tile_load<MX_CH>(r, mat, qs_bytes, nb, nb4, tile, p0, p1, xf);
-    mx_tile_compute<MX_CH>(r, nb, p0, p1, D);
-  }
-  const int lane = __lane_id();
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float d = D[g][k];
-      const float y = d + __shfl_down(d, 1, 64) + __shfl_down(d, 2, 64);
-      if ((lane & 15) == 0) red[g * 16 + (lane >> 4) * 4 + k] = y;
-    }
-  }
-}
+// expert kernels over t64 tiles (MXFP4, block-scaled MFMA)
+//
+// Every kernel finds its pair's expert with the same wave-level top-k over
+// the token's logits, so no kernel waits on another's small outputs. Split-K
+// partial sums go to separate slots and are added in a fixed order by the
+// next kernel: results do not depend on scheduling.
 
 __device__ __forceinline__ const uint8_t* expert_base(const void* base, int64_t stride, const uint64_t* ptrs, int e) {
   return base ? (const uint8_t*)base + (int64_t)e * stride : (const uint8_t*)ptrs[e];
 }
 
-constexpr int GU_CHUNKS = 4;  // K chunks per gate/up tile (one wave each, per matrix)
-constexpr int DN_CHUNKS = 4;  // K chunks per down tile
+constexpr int GU_S = 3;         // K-steps per gate/up wave (one chunk)
+constexpr int DN_S = 3;         // K-steps per down chunk
+constexpr int MAX_CHUNKS = 16;  // split-K chunks summed by the next kernel (K <= 6144)
+constexpr int COMBINE_SLOTS = 4;
+constexpr int DN_EPT = (DN_S * 128 + 255) / 256;  // activation elements per down thread (>= 4 waves)
 
-// phase 1: workgroup = (pair p, 64-row tile); wave = (matrix m, K chunk c).
-// Writes the activation (fp32 and as an xfrag) and, from tile 0, the pair's
-// expert id and routing weight.
-__global__ __launch_bounds__(512) void moe_gu_mfma_kernel(MoeDev a) {
-  __shared__ float red[2][GU_CHUNKS][64];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int tiles = a.n_ff >> 6;
-  const int p = blockIdx.x / tiles, tile = blockIdx.x - p * tiles;
+__device__ __forceinline__ int pair_expert(const MoeDev& a, int p, float* w = nullptr) {
   const int t = p / a.top_k, j = p - t * a.top_k;
   int si[MAX_TOPK];
   float sw[MAX_TOPK];
   topk_regs(a.logits + (int64_t)t * a.E, a.E, a.top_k, a.mode, si, sw);
-  const int e = clamp_expert(si[j], a.E);
-  if (tile == 0 && wave == 0 && lane == 0) {
-    a.ids[p] = e;
-    a.wts[p] = sw[j];
-  }
-  const int m = wave & 1, c = wave >> 1;
+  if (w) *w = sw[j];
+  return clamp_expert(si[j], a.E);
+}
+
+// Rows of D (after mx_sum_terms) for token column 0 go to dst[row] for rows < n.
+__device__ __forceinline__ void mx_store_rows(const v4f (&D)[4], int tile, int n, float* __restrict__ dst) {
+  const int lane = __lane_id();
+  if ((lane & 15) != 0) return;
+  const int r0 = tile * 64 + 4 * (lane >> 4);
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    if (r0 + 16 * g < n) *(v4f*)(dst + r0 + 16 * g) = D[g];
+}
+
+// phase 1: one wave per (pair, gate|up, 64-row tile, K-chunk); four
+// independent waves per workgroup. Writes partial sums only.
+__global__ __launch_bounds__(256) void moe_gu_kernel(MoeDev a) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t u = (int64_t)blockIdx.x * 4 + wave;
+  const int tiles = (int)a.ggu.tiles;
+  const int64_t per_p = 2ll * tiles * a.cg;
+  const int p = (int)(u / per_p);
+  if (p >= a.T * a.top_k) return;
+  int r = (int)(u - p * per_p);
+  const int m = r / (tiles * a.cg);
+  r -= m * tiles * a.cg;
+  const int tile = r / a.cg, c = r - tile * a.cg;
+  const int e = pair_expert(a, p);
   const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
                               : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
-  const int per = (a.nb4_gu + GU_CHUNKS - 1) / GU_CHUNKS;
-  const int s0 = c * per, s1 = min(a.nb4_gu, s0 + per);
-  mx_tile_rows(mat, a.qsb_gu, a.nb_gu, a.nb4_gu, tile, s0, s1,
-               a.xf_h + (int64_t)t * a.nb4_gu * XF_STEP_BYTES, red[m][c]);
-  __syncthreads();
-  if (wave == 0) {
-    const int row = tile * 64 + lane;
-    float g = 0.f, u = 0.f;
-#pragma unroll
-    for (int k = 0; k < GU_CHUNKS; ++k) {
-      g += red[0][k][lane];
-      u += red[1][k][lane];
-    }
-    if (a.gate_bias) g += a.gate_bias[(int64_t)e * a.n_ff + row];
-    if (a.up_bias) u += a.up_bias[(int64_t)e * a.n_ff + row];
-    const float av = moe_act(a.act_kind, g, u, a.alpha, a.limit);
-    a.act[(int64_t)p * a.n_ff + row] = av;
-    uint32_t sp[3];
-    split3(av, sp);
-    uint8_t* xf = a.xf_a + (int64_t)p * a.nb4_d * XF_STEP_BYTES;
-#pragma unroll
-    for (int cc = 0; cc < XF_SPLIT; ++cc) *(uint16_t*)(xf + xfrag_offset(row, cc)) = (uint16_t)sp[cc];
-  }
+  const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
+  const int t = p / a.top_k;
+  v4f D[4] = {};
+  mx_tile_mfma<GU_S, false>(mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1,
+                     a.xq_h + (int64_t)t * a.ggu.ns * XQ_STEP, 0, 0, 1, D);
+  mx_sum_terms(D);
+  mx_store_rows(D, tile, a.n_ff, a.part_gu + ((int64_t)(p * 2 + m) * a.cg + c) * a.n_ff);
 }
 
-// phase 2: workgroup = (pair p, 64-row output tile); wave = K chunk.
-// y[p] = down_e a_p + bias_e, combined across the token's experts later.
-__global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeDev a) {
-  __shared__ float red[DN_CHUNKS][64];
+// phase 2: workgroup = (pair, K-chunk, tpw output tiles), one wave per tile.
+// The prologue forms the chunk's activation from the gate/up partials (fixed
+// order) and biases, and quantizes it into activation terms in LDS.
+__global__ __launch_bounds__(512) void moe_down_kernel(MoeDev a) {
+  __shared__ float act[DN_S * 128];
+  __shared__ __align__(16) uint8_t xq[DN_S * XQ_STEP];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int tiles = a.n_embd >> 6;
-  const int p = blockIdx.x / tiles, tile = blockIdx.x - p * tiles;
-  const int e = clamp_expert(a.ids[p], a.E);
-  const uint8_t* mat = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
-  const int per = (a.nb4_d + DN_CHUNKS - 1) / DN_CHUNKS;
-  const int s0 = wave * per, s1 = min(a.nb4_d, s0 + per);
-  mx_tile_rows(mat, a.qsb_d, a.nb_d, a.nb4_d, tile, s0, s1, a.xf_a + (int64_t)p * a.nb4_d * XF_STEP_BYTES,
-               red[wave]);
-  __syncthreads();
-  if (wave == 0) {
-    const int row = tile * 64 + lane;
-    float y = 0.f;
+  const int tiles = (int)a.gdn.tiles;
+  const int groups = (tiles + a.tpw - 1) / a.tpw;
+  int bid = blockIdx.x;
+  const int tg = bid % groups;
+  bid /= groups;
+  const int c = bid % a.cd, p = bid / a.cd;
+  const int e = pair_expert(a, p);
+  const int s0 = c * a.sd, s1 = min(a.gdn.ns, s0 + a.sd);
+  const int k0 = s0 * 128, nk = (s1 - s0) * 128;
+  const float* pg = a.part_gu + (int64_t)p * 2 * a.cg * a.n_ff;
+  const float* pu = pg + (int64_t)a.cg * a.n_ff;
+  {
+    // up to DN_EPT elements per thread; every partial of both is loaded before the (fixed-order) sums
+    float gp[DN_EPT][MAX_CHUNKS], up[DN_EPT][MAX_CHUNKS], gb[DN_EPT], ub[DN_EPT];
 #pragma unroll
-    for (int k = 0; k < DN_CHUNKS; ++k) y += red[k][lane];
-    if (a.down_bias) y += a.down_bias[(int64_t)e * a.n_embd + row];
-    a.ypair[(int64_t)p * a.n_embd + row] = y;
+    for (int q = 0; q < DN_EPT; ++q) {
+      const int k = threadIdx.x + q * blockDim.x;
+      const int kk = min(k0 + min(k, nk - 1), a.n_ff - 1);  // clamped: unpredicated loads
+#pragma unroll
+      for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+        const int ci = cc < a.cg ? cc : a.cg - 1;
+        gp[q][cc] = pg[(int64_t)ci * a.n_ff + kk];
+        up[q][cc] = pu[(int64_t)ci * a.n_ff + kk];
+      }
+      gb[q] = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + kk] : 0.f;
+      ub[q] = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + kk] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < DN_EPT; ++q) {
+      const int k = threadIdx.x + q * blockDim.x;
+      float g = 0.f, uu = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+        g += cc < a.cg ? gp[q][cc] : 0.f;
+        uu += cc < a.cg ? up[q][cc] : 0.f;
+      }
+      if (k < nk) act[k] = k0 + k < a.n_ff ? moe_act(a.act_kind, g + gb[q], uu + ub[q], a.alpha, a.limit) : 0.f;
+    }
   }
+  __syncthreads();
+  const int nw = blockDim.x >> 6;
+  for (int task = wave; task < nk / 64; task += nw) {  // two 32-element blocks per task
+    const int bl = task * 2 + (lane >> 5);
+    xq_block(act[bl * 32 + (lane & 31)], bl, xq);
+  }
+  __syncthreads();
+  const int tile = tg * a.tpw + wave;
+  if (tile >= tiles) return;
+  const uint8_t* mat = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
+  v4f D[4] = {};
+  mx_tile_mfma<DN_S, true>(mat + (int64_t)tile * a.gdn.tile_bytes, a.gdn, s0, s1, xq, s0, 0, 1, D);
+  mx_sum_terms(D);
+  mx_store_rows(D, tile, a.n_embd, a.part_dn + ((int64_t)p * a.cd + c) * a.n_embd);
 }
 
-// out[t] = sum over the token's experts in ascending id of w * y (thread per element)
+// phase 3: out[t] = sum over the token's experts, ascending id, of
+// w * (down partials summed in order + bias); also the ids/weights outputs.
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
-  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int t = blockIdx.y;
-  if (n >= a.n_embd) return;
   const int k = a.top_k;
   int si[MAX_TOPK], order[MAX_TOPK];
-  for (int jj = 0; jj < k; ++jj) si[jj] = a.ids[(int64_t)t * k + jj];
+  float sw[MAX_TOPK];
+  topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw);
+  for (int jj = 0; jj < k; ++jj) si[jj] = clamp_expert(si[jj], a.E);
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    for (int jj = 0; jj < k; ++jj) {
+      a.ids[(int64_t)t * k + jj] = si[jj];
+      a.wts[(int64_t)t * k + jj] = sw[jj];
+    }
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= a.n_embd) return;
   slot_order(si, k, order);
   float o = 0.f;
-  for (int jj = 0; jj < k; ++jj) {
-    const int64_t q = (int64_t)t * k + order[jj];
-    o = combine_one(o, a.wts[q], a.ypair[q * a.n_embd + n]);
+  for (int j0 = 0; j0 < k; j0 += COMBINE_SLOTS) {
+    // all partials of COMBINE_SLOTS experts are loaded before the (fixed-order) sums
+    float v[COMBINE_SLOTS][MAX_CHUNKS], b[COMBINE_SLOTS];
+#pragma unroll
+    for (int q = 0; q < COMBINE_SLOTS; ++q) {  // unpredicated loads: indices clamped, extra terms zeroed
+      const bool on = j0 + q < k;
+      const int j = order[on ? j0 + q : k - 1];
+      const float* pd = a.part_dn + ((int64_t)t * k + j) * a.cd * a.n_embd + n;
+#pragma unroll
+      for (int cc = 0; cc < MAX_CHUNKS; ++cc) v[q][cc] = pd[(int64_t)(cc < a.cd ? cc : a.cd - 1) * a.n_embd];
+      b[q] = a.down_bias ? a.down_bias[(int64_t)si[j] * a.n_embd + n] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < COMBINE_SLOTS; ++q) {
+#pragma unroll
+      for (int cc = 0; cc < MAX_CHUNKS; ++cc) v[q][cc] = cc < a.cd ? v[q][cc] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < COMBINE_SLOTS; ++q) {
+      if (j0 + q >= k) break;
+      float y = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < MAX_CHUNKS; ++cc) y += v[q][cc];
+      o = combine_one(o, sw[order[j0 + q]], y + b[q]);
+    }
   }
   a.out[(int64_t)t * a.n_embd + n] = o;
 }
@@ -810,28 +643,46 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 // host side
 
 struct MoePlan {
-  int64_t off_logits, off_act, off_xfh, off_xfa, off_y, total;
-  int nb4_gu, nb4_d;
+  int64_t off_logits, off_act, off_xq, off_pgu, off_pdn, total;
+  MxGeom ggu, gdn;
+  int cg, cd, tpw;
 };
+
+// down tiles per workgroup: the count in 4..8 that leaves the fewest idle waves
+static int pick_tpw(int64_t tiles) {
+  int best = 4;
+  int64_t waste = nsx_cdiv(tiles, 4) * 4 - tiles;
+  for (int w = 5; w <= 8; ++w) {
+    const int64_t wz = nsx_cdiv(tiles, w) * w - tiles;
+    if (wz < waste || (wz == waste && w > best)) {
+      best = w;
+      waste = wz;
+    }
+  }
+  return best;
+}
 
 static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   MoePlan p{};
   const int64_t P = T * L->top_k;
   const bool t64 = L->layout == NSX_LAYOUT_T64;
-  p.nb4_gu = (int)nsx_cdiv(L->n_embd / 32, 4);
-  p.nb4_d = (int)nsx_cdiv(L->n_ff / 32, 4);
+  p.ggu = mx_geom(L->n_ff, L->n_embd);
+  p.gdn = mx_geom(L->n_embd, L->n_ff);
+  p.cg = (int)nsx_cdiv(p.ggu.ns, GU_S);
+  p.cd = (int)nsx_cdiv(p.gdn.ns, DN_S);
+  p.tpw = pick_tpw(p.gdn.tiles);
   auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
   int64_t o = 0;
   p.off_logits = o;
   o = al(o + T * L->n_expert * 4);
   p.off_act = o;
-  o = al(o + P * L->n_ff * 4);
-  p.off_xfh = o;
-  o = al(o + (t64 ? T * p.nb4_gu * XF_STEP_BYTES : 0));
-  p.off_xfa = o;
-  o = al(o + (t64 ? P * p.nb4_d * XF_STEP_BYTES : 0));
-  p.off_y = o;
-  o = al(o + (t64 ? P * L->n_embd * 4 : 0));
+  o = al(o + (t64 ? 0 : P * L->n_ff * 4));
+  p.off_xq = o;
+  o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP : 0));
+  p.off_pgu = o;
+  o = al(o + (t64 ? P * 2 * p.cg * L->n_ff * 4 : 0));
+  p.off_pdn = o;
+  o = al(o + (t64 ? P * p.cd * L->n_embd * 4 : 0));
   p.total = o;
   return p;
 }
@@ -866,7 +717,9 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
     NSX_REQUIRE((int64_t)L->top_k * (L->n_ff + L->n_ff / 32) * 4 <= 160 * 1024, NSX_EINVAL,
                 "top_k * n_ff too large for LDS");
   } else {
-    NSX_REQUIRE(L->n_embd % 64 == 0 && L->n_ff % 64 == 0, NSX_EINVAL, "t64 layers need n_embd, n_ff % 64 == 0");
+    NSX_REQUIRE(nsx_cdiv(nsx_cdiv(L->n_embd / 32, 4), GU_S) <= MAX_CHUNKS &&
+                    nsx_cdiv(nsx_cdiv(L->n_ff / 32, 4), DN_S) <= MAX_CHUNKS,
+                NSX_EINVAL, "t64 layers take n_embd, n_ff <= %d", MAX_CHUNKS * GU_S * 128);
 
   }
   return NSX_OK;
@@ -922,17 +775,24 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.gate_stride = L->gate_stride;
   d.up_stride = L->up_stride;
   d.down_stride = L->down_stride;
-  d.ypair = (float*)(ws + p.off_y);
   d.gate_bias = L->gate_bias;
   d.up_bias = L->up_bias;
   d.down_bias = L->down_bias;
   d.h = h;
   d.out = out;
   d.act = (float*)(ws + p.off_act);
-  d.xf_h = (const uint8_t*)(ws + p.off_xfh);
-  d.xf_a = (uint8_t*)(ws + p.off_xfa);
+  d.xq_h = (const uint8_t*)(ws + p.off_xq);
+  d.part_gu = (float*)(ws + p.off_pgu);
+  d.part_dn = (float*)(ws + p.off_pdn);
   d.n_embd = L->n_embd;
   d.n_ff = L->n_ff;
+  d.ggu = p.ggu;
+  d.gdn = p.gdn;
+  d.cg = p.cg;
+  d.sg = GU_S;
+  d.cd = p.cd;
+  d.sd = DN_S;
+  d.tpw = p.tpw;
   d.act_kind = L->act;
   d.alpha = L->alpha;
   d.limit = L->limit;
@@ -940,26 +800,20 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
   if (on(NSX_PHASE_ROUTER)) {
     rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
-                       (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xfh) : nullptr, st);
+                       (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xq) : nullptr, st);
     if (rc) return rc;
     if (!t64 && (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st))) return rc;
   }
   const int64_t P = T * L->top_k;
 
   if (t64) {
-    d.nb_gu = L->n_embd / 32;
-    d.nb4_gu = p.nb4_gu;
-    d.nb_d = L->n_ff / 32;
-    d.nb4_d = p.nb4_d;
-    d.qsb_gu = nsx_cdiv(L->n_ff, 64) * d.nb_gu * 1024;
-    d.qsb_d = nsx_cdiv(L->n_embd, 64) * d.nb_d * 1024;
     if (on(NSX_PHASE_GATE_UP) &&
-        (rc = nsx_launch(moe_gu_mfma_kernel, dim3((unsigned)(P * (L->n_ff / 64))), dim3(128 * GU_CHUNKS), 0, st,
+        (rc = nsx_launch(moe_gu_kernel, dim3((unsigned)nsx_cdiv(P * 2 * p.ggu.tiles * p.cg, 4)), dim3(256), 0, st,
                          d)))
       return rc;
     if (on(NSX_PHASE_DOWN) &&
-        (rc = nsx_launch(moe_down_mfma_kernel, dim3((unsigned)(P * (L->n_embd / 64))), dim3(64 * DN_CHUNKS), 0, st,
-                         d)))
+        (rc = nsx_launch(moe_down_kernel, dim3((unsigned)(P * p.cd * nsx_cdiv(p.gdn.tiles, p.tpw))),
+                         dim3(64 * p.tpw), 0, st, d)))
       return rc;
     if (on(NSX_PHASE_COMBINE) &&
         (rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,

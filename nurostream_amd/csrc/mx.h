@@ -1,0 +1,218 @@
+// MXFP4 x activation products on gfx950's block-scaled MFMA
+// (v_mfma_scale_f32_16x16x128_f8f6f4, A = FP4 weights with their e8m0
+// scales, B = FP8 E4M3 activation terms with e8m0 scales).
+//
+// Operand model (established with in-bounds one-hot probes on gfx950):
+//   A (FP4, 4 VGPRs): lane l = 16 q + i holds row i and K = 32 q .. 32 q + 31
+//     of the instruction's 128-wide K slice, element order: byte m = element
+//     2m (low nibble) | element 2m + 1 (high nibble). Its scale byte (opsel
+//     selects a byte of the scale VGPR) applies to those 32 K values.
+//   B (FP8, 8 VGPRs): lane l = 16 g + c holds column c and K = 16 g .. 16 g +
+//     15 (bytes 0..15) and 64 + 16 g .. 64 + 16 g + 15 (bytes 16..31); the
+//     scale byte of lane 16 q + c applies to K = 32 q .. 32 q + 31.
+//   D (4 VGPRs): lane l holds column l % 16, rows 4 (l / 16) .. + 3.
+// Products are exact; the hardware sums groups of 8 of them aligned to the
+// group's largest with about 12 kept bits, so results are good to ~4e-6 of
+// max|y| on GEMV-like data (measured), inside the path's 1e-3 parity bar.
+#pragma once
+
+#include "nsx_common.h"
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// t64 tile layout (resident MXFP4 expert slabs)
+//
+// An n_rows x K MXFP4 matrix (nb = K / 32 blocks per row) is stored as
+// ceil(n_rows / 64) tiles of nb * 1088 bytes -- the GGUF byte count, rows
+// padded to 64. A tile is a run of K-steps s = 0 .. ns - 1 of r_s = min(4,
+// nb - 4 s) blocks; step s starts at byte s * 4352 and holds
+//   codes : [g 0..3][lane 0 .. 16 r_s - 1][16 B]   at g * r_s * 256 + lane * 16
+//   scales: [lane 0 .. 16 r_s - 1][4 B]            at r_s * 1024 + lane * 4
+// where lane = 16 q + i stands for row 16 g + i of the tile and block 4 s + q:
+// its 16 code bytes are that block's codes in A-operand order and byte g of
+// its scale dword is the block's e8m0. Padding rows are zero codes, scale 0.
+
+constexpr int MX_STEP_BYTES = 4352;  // 64 rows x 4 blocks x 17 B
+constexpr int MX_TILE_ROWS = 64;
+
+struct MxGeom {
+  int nb;              // blocks per row
+  int ns;              // K-steps
+  int rlast;           // blocks in the last step (1..4)
+  int64_t tile_bytes;  // nb * 1088
+  int64_t tiles;
+};
+
+__host__ __device__ __forceinline__ MxGeom mx_geom(int64_t n_rows, int64_t K) {
+  MxGeom g;
+  g.nb = (int)(K / 32);
+  g.ns = (g.nb + 3) / 4;
+  g.rlast = g.nb - 4 * (g.ns - 1);
+  g.tile_bytes = (int64_t)g.nb * 1088;
+  g.tiles = (n_rows + 63) / 64;
+  return g;
+}
+
+// ---------------------------------------------------------------------------
+// activation terms ("xq")
+//
+// x ~ sum over t < XQ_NT of 2^(s_t - 127) q_t, with q_t FP8 E4M3 and one e8m0
+// s_t per 32-element block and term; term t + 1 encodes what term t left
+// (round to nearest even, exact residuals), so each term adds 4 bits: the
+// block's error is at most 2^-16 of its largest |x|. NaN or infinite inputs
+// give a scale byte of 255 (NaN) in term 0, so they surface as NaN outputs.
+// Storage per token and K-step (128 elements), in B-operand order:
+//   codes : [g 0..3][t][32 B]   byte j of (g, t) is element 16 g + j (j < 16)
+//                               or 64 + 16 g + j - 16 of the step
+//   scales: [q 0..3][t][4 B]    e8m0 of block 4 s + q in byte 0
+constexpr int XQ_NT = 4;
+constexpr int XQ_CODES = 4 * XQ_NT * 32;
+constexpr int XQ_STEP = XQ_CODES + 4 * XQ_NT * 4;  // 576 B
+
+// |a| <= 448 rounded to nearest even on the E4M3 grid: returns the 7-bit
+// magnitude code and the rounded value. Normal codes have spacing 2^(e-3),
+// subnormals 2^-9; the rounding adds and removes 1.5 * 2^(k+23), which
+// leaves a multiple of 2^k (k the grid spacing) rounded by the fp32 adder.
+__device__ __forceinline__ uint32_t e4m3_code(float a, float& rq) {
+  const int e = (int)(__builtin_bit_cast(uint32_t, a) >> 23) - 127;
+  const int k = e - 3 > -9 ? e - 3 : -9;
+  const float c = __builtin_bit_cast(float, ((uint32_t)(k + 150) << 23) | 0x400000u);
+  float t = a + c;
+  asm volatile("" : "+v"(t));  // keep (a + c) - c from being folded
+  rq = t - c;
+  if (rq < 0.015625f) return (uint32_t)(rq * 512.f);  // subnormal (2^-6 itself gives code 8)
+  const uint32_t b = __builtin_bit_cast(uint32_t, rq);
+  return ((((b >> 23) & 0xffu) - 120u) << 3) | ((b >> 20) & 7u);
+}
+
+// Quantize one 32-element block into XQ_NT terms: lanes 32h .. 32h + 31 hold
+// element (lane & 31) of their block in r; dst is the token's xq base; b the
+// block index. Both 32-lane halves run in lock step (each its own block).
+__device__ __forceinline__ void xq_block(float r, int b, uint8_t* dst) {
+  const int e = __lane_id() & 31;
+  const int s = b >> 2, q = b & 3;
+  const int gp = (q & 1) * 2 + (e >> 4);
+  const int j = (e & 15) + 16 * (q >> 1);
+  uint8_t* step = dst + (int64_t)s * XQ_STEP;
+#pragma unroll
+  for (int t = 0; t < XQ_NT; ++t) {
+    float m = fabsf(r);
+    if (!(m <= 3.4028235e38f)) m = __builtin_inff();  // NaN counts as the largest
+    m = nsx_row_fmax(m);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));  // the block's two 16-lane rows
+    uint32_t sc, code = 0;
+    if (!(m <= 3.4028235e38f)) {
+      sc = 255u;  // e8m0 NaN: the outputs of this token become NaN
+      r = 0.f;
+    } else if (m == 0.f) {
+      sc = 0u;
+    } else {
+      const uint32_t mb = __builtin_bit_cast(uint32_t, m);
+      int sx = (int)((mb >> 23) & 0xffu) - 127 - 8 + ((mb & 0x7fffffu) > 0x600000u ? 1 : 0);
+      sx = sx < -127 ? -127 : sx;
+      sc = (uint32_t)(sx + 127);
+      float rq;
+      code = e4m3_code(__builtin_amdgcn_ldexpf(fabsf(r), -sx), rq);
+      const float back = __builtin_amdgcn_ldexpf(rq, sx);
+      if (r < 0.f) {
+        code |= code ? 0x80u : 0u;
+        r += back;
+      } else {
+        r -= back;
+      }
+    }
+    step[(gp * XQ_NT + t) * 32 + j] = (uint8_t)code;
+    if (e == 0) *(uint32_t*)(step + XQ_CODES + (q * XQ_NT + t) * 4) = sc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// one wave: a 64-row tile times up to 4 tokens' xq over K-steps [s0, s1)
+
+#define NSX_MFMA_SCALE(A, B, C, G, SA, SB) \
+  __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 4, 0, (G), (SA), 0, (SB))
+
+// D[g] (rows 16 g .. 16 g + 15 of the tile, 16 columns) accumulates the
+// products. Column c = token * XQ_NT + term for tokens < ntok; xq points at
+// step xs0 of token 0 (in LDS when BLDS) and tokens are xq_stride bytes
+// apart. S steps' loads are issued before their MFMAs, unpredicated so the
+// waits can retire step by step: A lanes past a partial last step read an
+// in-bounds stand-in with scale 0 (the activation there is zero), and
+// columns of tokens >= ntok repeat token ntok - 1 (those columns are not
+// read back). A weight e8m0 of 255 is NaN to the hardware: the row's result
+// is non-finite, as it is in the reference, whose fp32 dequant turns such a
+// block into +-inf (2^127 times ggml's doubled table).
+template <int S, bool BLDS>
+__device__ __forceinline__ void mx_tile_mfma(const uint8_t* __restrict__ tile, const MxGeom& G, int s0, int s1,
+                                             const uint8_t* __restrict__ xq, int xs0, int64_t xq_stride, int ntok,
+                                             v4f (&D)[4]) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  typedef const __attribute__((address_space(1))) uint32_t gu32;
+  typedef const __attribute__((address_space(3))) v4u lv4u;
+  typedef const __attribute__((address_space(3))) uint32_t lu32;
+  const int lane = __lane_id();
+  const int c = lane & 15, grp = lane >> 4;
+  const int tok0 = c / XQ_NT, term = c - tok0 * XQ_NT;
+  const int tok = tok0 < ntok ? tok0 : ntok - 1;
+  const uint8_t* xt = xq + (int64_t)tok * xq_stride + (grp * XQ_NT + term) * 32;
+  const uint8_t* xst = xq + (int64_t)tok * xq_stride + XQ_CODES + (grp * XQ_NT + term) * 4;
+  for (int p0 = s0; p0 < s1; p0 += S) {
+    v4u A[S][4], B0[S], B1[S];
+    uint32_t SA[S], SB[S];
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int s = p0 + u;
+      if (s < s1) {
+        const int rs = s < G.ns - 1 ? 4 : G.rlast;
+        const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
+        const bool alane = grp < rs;
+        const int la = alane ? lane : 16 * rs - 1;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) A[u][g] = *(gv4u*)(ch + g * rs * 256 + la * 16);
+        SA[u] = *(gu32*)(ch + rs * 1024 + la * 4);
+        SA[u] = alane ? SA[u] : 0u;
+        const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
+        if (BLDS) {
+          B0[u] = *(lv4u*)(xt + xo);
+          B1[u] = *(lv4u*)(xt + xo + 16);
+          SB[u] = *(lu32*)(xst + xo);
+        } else {
+          B0[u] = *(gv4u*)(xt + xo);
+          B1[u] = *(gv4u*)(xt + xo + 16);
+          SB[u] = *(gu32*)(xst + xo);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      if (p0 + u >= s1) break;
+      const uint32_t sa = SA[u];
+      const v8i b = {(int)B0[u].x, (int)B0[u].y, (int)B0[u].z, (int)B0[u].w,
+                     (int)B1[u].x, (int)B1[u].y, (int)B1[u].z, (int)B1[u].w};
+      const v8i a0 = {(int)A[u][0].x, (int)A[u][0].y, (int)A[u][0].z, (int)A[u][0].w, 0, 0, 0, 0};
+      const v8i a1 = {(int)A[u][1].x, (int)A[u][1].y, (int)A[u][1].z, (int)A[u][1].w, 0, 0, 0, 0};
+      const v8i a2 = {(int)A[u][2].x, (int)A[u][2].y, (int)A[u][2].z, (int)A[u][2].w, 0, 0, 0, 0};
+      const v8i a3 = {(int)A[u][3].x, (int)A[u][3].y, (int)A[u][3].z, (int)A[u][3].w, 0, 0, 0, 0};
+      D[0] = NSX_MFMA_SCALE(a0, b, D[0], 0, sa, SB[u]);
+      D[1] = NSX_MFMA_SCALE(a1, b, D[1], 1, sa, SB[u]);
+      D[2] = NSX_MFMA_SCALE(a2, b, D[2], 2, sa, SB[u]);
+      D[3] = NSX_MFMA_SCALE(a3, b, D[3], 3, sa, SB[u]);
+    }
+  }
+}
+
+// Sum the XQ_NT term columns of D: afterwards lane l with (l & 3) == 0 holds,
+// for token (l & 15) / 4, rows 16 g + 4 (l / 16) + i in D[g][i].
+__device__ __forceinline__ void mx_sum_terms(v4f (&D)[4]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = D[g][i];
+      v += nsx_dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]: lane ^ 1
+      v += nsx_dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]: lane ^ 2
+      D[g][i] = v;
+    }
+  }
+}

@@ -112,11 +112,51 @@ __device__ __forceinline__ float nsx_load_act(const void* p, int dtype, int64_t 
   return dtype == NSX_DT_F16 ? nsx_h2f(b) : nsx_bf2f(b);
 }
 
-// Wave64 sum via DPP/permute reductions (result valid in every lane).
-__device__ __forceinline__ float nsx_wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// Wave64 reductions on DPP row rotations (within each 16-lane row, no LDS
+// round trip) plus four readlanes; the result is wave-uniform. Every lane of
+// the wave must be active.
+#define NSX_DPP_ROR(n) (0x120 + (n))
+template <typename Op>
+__device__ __forceinline__ uint32_t nsx_row_reduce_u32(uint32_t v, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(8), 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(4), 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(2), 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(1), 0xf, 0xf, false));
   return v;
+}
+__device__ __forceinline__ uint32_t nsx_wave_max_u32(uint32_t v) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = nsx_row_reduce_u32(v, mx);
+  return mx(mx(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+            mx(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ uint32_t nsx_wave_min_u32(uint32_t v) {
+  auto mn = [](uint32_t a, uint32_t b) { return a < b ? a : b; };
+  v = nsx_row_reduce_u32(v, mn);
+  return mn(mn(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+            mn(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+template <int CTRL>
+__device__ __forceinline__ float nsx_dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float nsx_row_fmax(float v) {  // max over the lane's 16-lane row
+  v = fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(8)>(v));
+  v = fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(4)>(v));
+  v = fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(2)>(v));
+  return fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(1)>(v));
+}
+// Wave64 sum (wave-uniform): rows by rotation, then rows 0 + 1 + 2 + 3.
+__device__ __forceinline__ float nsx_wave_sum(float v) {
+  v += nsx_dpp_f<NSX_DPP_ROR(8)>(v);
+  v += nsx_dpp_f<NSX_DPP_ROR(4)>(v);
+  v += nsx_dpp_f<NSX_DPP_ROR(2)>(v);
+  v += nsx_dpp_f<NSX_DPP_ROR(1)>(v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Raw buffer resource over [p, p + nbytes) with p 4-byte aligned: stride 0,

@@ -5,6 +5,7 @@
 // themselves are written for CDNA4: wave64, buffer loads with hardware range
 // checking, the gfx950 FP4 conversion instruction, and wave reductions.
 #include "nsx_common.h"
+#include "mx.h"
 #include "raw_dot.h"
 
 #include <algorithm>
@@ -325,77 +326,104 @@ extern "C" int nsx_fused_gemv(int t, const void* raw, int64_t n_rows, int64_t K,
 // scale plane [tile][block/4][row][4 B]. Rows beyond n_rows and blocks beyond
 // nb inside the last scale group are zero.
 
-struct T64Geom {
-  int64_t tiles, nb, nb4, qs_bytes, sc_bytes;
-};
-static inline T64Geom t64_geom(int64_t n_rows, int64_t K) {
-  T64Geom g;
-  g.tiles = nsx_cdiv(n_rows, 64);
-  g.nb = K / 32;
-  g.nb4 = nsx_cdiv(g.nb, 4);
-  g.qs_bytes = g.tiles * g.nb * 1024;
-  g.sc_bytes = g.tiles * g.nb4 * 256;
-  return g;
-}
+// ---------------------------------------------------------------------------
+// t64 tiles (layout in mx.h): pack from / unpack to GGUF MXFP4 rows
 
 extern "C" int64_t nsx_t64_bytes(int t, int64_t n_rows, int64_t K) {
   if (t != NSX_MXFP4 || K <= 0 || K % 32 || n_rows < 0) return -1;
-  const T64Geom g = t64_geom(n_rows, K);
-  return g.qs_bytes + g.sc_bytes;
+  const MxGeom g = mx_geom(n_rows, K);
+  return g.tiles * g.tile_bytes;
 }
 
-// one thread per (row slot, block slot) of the padded tile grid
-__global__ void t64_pack_kernel(const uint8_t* __restrict__ base, uint32_t head, uint32_t range,
-                                int64_t n_rows, int nb, int nb4, int64_t tiles,
-                                uint8_t* __restrict__ dst, int64_t qs_bytes) {
-  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over tiles*64*nb4*4
-  const int64_t total = tiles * 64 * (int64_t)nb4 * 4;
-  if (slot >= total) return;
-  const int lane = (int)(slot & 63);
-  const int64_t rest = slot >> 6;
-  const int b = (int)(rest % (nb4 * 4));
-  const int64_t tile = rest / (nb4 * 4);
-  const int64_t row = tile * 64 + lane;
-  const bool real = row < n_rows && b < nb;
-  uint32_t q[4] = {0, 0, 0, 0};
-  uint32_t e = 0;
-  if (real) {
-    const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
-    const uint32_t o = head + (uint32_t)((row * nb + b) * 17);
-    const uint32_t s = o & 3u, oa = o & ~3u;
-    uint32_t D[6];
+// 16 code bytes in GGUF order (byte j = element j | element j + 16 << 4) ->
+// element order (byte m = element 2m | element 2m + 1 << 4), and back
+__device__ __forceinline__ uint32_t mx_pair_nibbles(uint32_t x) {  // 4 nibble-bytes -> 2 bytes
+  const uint32_t y = x | (x >> 4);
+  return (y & 0xffu) | ((y >> 8) & 0xff00u);
+}
+__device__ __forceinline__ v4u mx_gguf_to_elem(const uint32_t (&q)[4]) {
+  uint32_t lo[4], hi[4];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) D[i] = nsx_bload32(rs, oa + 4u * i);
+  for (int d = 0; d < 4; ++d) {
+    lo[d] = q[d] & 0x0f0f0f0fu;         // elements 4d .. 4d + 3
+    hi[d] = (q[d] >> 4) & 0x0f0f0f0fu;  // elements 16 + 4d .. 16 + 4d + 3
+  }
+  return v4u{mx_pair_nibbles(lo[0]) | (mx_pair_nibbles(lo[1]) << 16),
+             mx_pair_nibbles(lo[2]) | (mx_pair_nibbles(lo[3]) << 16),
+             mx_pair_nibbles(hi[0]) | (mx_pair_nibbles(hi[1]) << 16),
+             mx_pair_nibbles(hi[2]) | (mx_pair_nibbles(hi[3]) << 16)};
+}
+__device__ __forceinline__ uint32_t mx_spread_nibbles(uint32_t x16) {  // 2 bytes -> 4 nibble-bytes
+  const uint32_t b0 = x16 & 0xffu, b1 = (x16 >> 8) & 0xffu;
+  return (b0 & 15u) | ((b0 >> 4) << 8) | ((b1 & 15u) << 16) | ((b1 >> 4) << 24);
+}
+__device__ __forceinline__ void mx_elem_to_gguf(v4u w, uint32_t (&q)[4]) {
+  uint32_t el[8];  // nibble-bytes: el[d] = elements 4d .. 4d + 3
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    el[2 * d] = mx_spread_nibbles(w[d] & 0xffffu);
+    el[2 * d + 1] = mx_spread_nibbles(w[d] >> 16);
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) q[d] = el[d] | (el[d + 4] << 4);
+}
+
+// one thread per (tile, step, g, lane) slot that exists in the layout
+__global__ void t64_pack_kernel(const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int64_t n_rows,
+                                MxGeom G, uint8_t* __restrict__ dst) {
+  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over tiles * ns * 4 * 64
+  if (slot >= G.tiles * G.ns * 256) return;
+  const int lane = (int)(slot & 63), g = (int)((slot >> 6) & 3);
+  const int64_t ts = slot >> 8;
+  const int s = (int)(ts % G.ns);
+  const int64_t tile = ts / G.ns;
+  const int rs = s < G.ns - 1 ? 4 : G.rlast;
+  const int q = lane >> 4, i = lane & 15;
+  if (q >= rs) return;
+  const int64_t row = tile * 64 + 16 * g + i;
+  const int b = 4 * s + q;
+  uint32_t Q[4] = {0u, 0u, 0u, 0u};
+  uint32_t e = 0u;
+  if (row < n_rows) {
+    const __amdgpu_buffer_rsrc_t rs_ = nsx_rsrc(base, range);
+    const uint32_t o = head + (uint32_t)((row * G.nb + b) * 17);
+    const uint32_t sh = o & 3u, oa = o & ~3u;
+    uint32_t Dw[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) Dw[k] = nsx_bload32(rs_, oa + 4u * k);
     uint32_t E[5];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) E[i] = nsx_alignbyte(D[i + 1], D[i], s);
+    for (int k = 0; k < 5; ++k) E[k] = nsx_alignbyte(Dw[k + 1], Dw[k], sh);
     e = E[0] & 0xffu;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q[i] = nsx_alignbyte(E[i + 1], E[i], 1);
+    for (int k = 0; k < 4; ++k) Q[k] = nsx_alignbyte(E[k + 1], E[k], 1);
   }
-  if (b < nb) {
-    uint8_t* qd = dst + ((tile * nb + b) * 64 + lane) * 16;
-    *(v4u*)qd = v4u{q[0], q[1], q[2], q[3]};
-  }
-  dst[qs_bytes + ((tile * nb4 + b / 4) * 64 + lane) * 4 + (b & 3)] = (uint8_t)e;
+  uint8_t* ch = dst + tile * G.tile_bytes + (int64_t)s * MX_STEP_BYTES;
+  *(v4u*)(ch + g * rs * 256 + lane * 16) = mx_gguf_to_elem(Q);
+  ch[rs * 1024 + lane * 4 + g] = (uint8_t)e;
 }
 
-__global__ void t64_unpack_kernel(const uint8_t* __restrict__ src, int64_t n_rows, int nb, int nb4,
-                                  int64_t qs_bytes, uint8_t* __restrict__ raw) {
-  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over n_rows*nb
-  if (slot >= n_rows * nb) return;
-  const int64_t row = slot / nb;
-  const int b = (int)(slot % nb);
+// one thread per (row, block) of the matrix
+__global__ void t64_unpack_kernel(const uint8_t* __restrict__ src, int64_t n_rows, MxGeom G,
+                                  uint8_t* __restrict__ raw) {
+  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (slot >= n_rows * G.nb) return;
+  const int64_t row = slot / G.nb;
+  const int b = (int)(slot % G.nb);
   const int64_t tile = row >> 6;
-  const int lane = (int)(row & 63);
-  const v4u q = *(const v4u*)(src + ((tile * nb + b) * 64 + lane) * 16);
-  const uint8_t e = src[qs_bytes + ((tile * nb4 + b / 4) * 64 + lane) * 4 + (b & 3)];
+  const int r = (int)(row & 63), g = r >> 4, i = r & 15;
+  const int s = b >> 2, q = b & 3;
+  const int rs = s < G.ns - 1 ? 4 : G.rlast;
+  const int lane = 16 * q + i;
+  const uint8_t* ch = src + tile * G.tile_bytes + (int64_t)s * MX_STEP_BYTES;
+  uint32_t Q[4];
+  mx_elem_to_gguf(*(const v4u*)(ch + g * rs * 256 + lane * 16), Q);
   uint8_t* o = raw + slot * 17;
-  o[0] = e;
+  o[0] = ch[rs * 1024 + lane * 4 + g];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int k = 0; k < 4; ++k) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[1 + 4 * i + j] = (uint8_t)(q[i] >> (8 * j));
+    for (int j = 0; j < 4; ++j) o[1 + 4 * k + j] = (uint8_t)(Q[k] >> (8 * j));
   }
 }
 
@@ -403,7 +431,7 @@ extern "C" int nsx_t64_pack(int t, const void* raw, int64_t n_rows, int64_t K, v
   NSX_REQUIRE(t == NSX_MXFP4, NSX_ENOTIMPL, "t64 layout is implemented for MXFP4 only (type %d)", t);
   NSX_REQUIRE(K > 0 && K % 32 == 0 && n_rows >= 0, NSX_EINVAL, "bad shape %lld x %lld",
               (long long)n_rows, (long long)K);
-  const T64Geom g = t64_geom(n_rows, K);
+  const MxGeom g = mx_geom(n_rows, K);
   if (n_rows == 0) return NSX_OK;
   NSX_REQUIRE(raw && t64, NSX_EINVAL, "null buffer");
   const int64_t raw_bytes = n_rows * g.nb * 17;
@@ -411,10 +439,9 @@ extern "C" int nsx_t64_pack(int t, const void* raw, int64_t n_rows, int64_t K, v
   const uint8_t* p = (const uint8_t*)raw;
   const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
   const uint32_t head = (uint32_t)((uintptr_t)p - a);
-  const int64_t total = g.tiles * 64 * g.nb4 * 4;
+  const int64_t total = g.tiles * g.ns * 256;
   hipLaunchKernelGGL(t64_pack_kernel, dim3((unsigned)nsx_cdiv(total, 256)), dim3(256), 0, S(stream),
-                     (const uint8_t*)a, head, (uint32_t)(head + raw_bytes), n_rows, (int)g.nb, (int)g.nb4,
-                     g.tiles, (uint8_t*)t64, g.qs_bytes);
+                     (const uint8_t*)a, head, (uint32_t)(head + raw_bytes), n_rows, g, (uint8_t*)t64);
   NSX_LAUNCHED();
   return NSX_OK;
 }
@@ -422,12 +449,12 @@ extern "C" int nsx_t64_pack(int t, const void* raw, int64_t n_rows, int64_t K, v
 extern "C" int nsx_t64_unpack(int t, const void* t64, int64_t n_rows, int64_t K, void* raw, void* stream) {
   NSX_REQUIRE(t == NSX_MXFP4, NSX_ENOTIMPL, "t64 layout is implemented for MXFP4 only (type %d)", t);
   NSX_REQUIRE(K > 0 && K % 32 == 0 && n_rows >= 0, NSX_EINVAL, "bad shape");
-  const T64Geom g = t64_geom(n_rows, K);
+  const MxGeom g = mx_geom(n_rows, K);
   if (n_rows == 0) return NSX_OK;
   NSX_REQUIRE(raw && t64, NSX_EINVAL, "null buffer");
   const int64_t total = n_rows * g.nb;
   hipLaunchKernelGGL(t64_unpack_kernel, dim3((unsigned)nsx_cdiv(total, 256)), dim3(256), 0, S(stream),
-                     (const uint8_t*)t64, n_rows, (int)g.nb, (int)g.nb4, g.qs_bytes, (uint8_t*)raw);
+                     (const uint8_t*)t64, n_rows, g, (uint8_t*)raw);
   NSX_LAUNCHED();
   return NSX_OK;
 }

@@ -142,3 +142,45 @@ def test_t64_roundtrip_and_gemv(dev, rows, K):
         w = T64Rows(tiles, OQ.MXFP4, rows, K, lo, hi)
         y = to_np(fused_gemv(w, OQ.MXFP4, torch.from_numpy(x).to(dev), hi - lo, K, out_dtype=torch.float32))
         assert rel_max(y, ref[:, lo:hi]) < GEMV_TIGHT, (lo, hi)
+
+
+@pytest.mark.parametrize("e_lo,e_hi,x_exp", [(0, 2, 100), (248, 252, -100), (117, 123, 0)])
+def test_t64_gemv_extreme_scales(dev, e_lo, e_hi, x_exp):
+    """Block-scaled MFMA over e8m0 scales at both ends of the range (2^-127 .. 2^127), with x
+    scaled so that the float32 reference stays finite (its dequant overflows from e = 253 on with
+    the larger codes): denormal-range weights, huge weights."""
+    from helpers import MFMA_TOL
+    from nurostream_amd.compute.kernels import T64Rows, fused_gemv, t64_pack
+    rows, K = 128, 2880
+    raw = _gemv_case("MXFP4", rows, K, seed=e_lo + 7, e_lo=e_lo, e_hi=e_hi)
+    x = (np.random.default_rng(2).standard_normal((3, K)) * 2.0 ** x_exp).astype(np.float32)
+    tiles = t64_pack(torch.from_numpy(raw).to(dev), OQ.MXFP4, rows, K)
+    y = to_np(fused_gemv(T64Rows(tiles, OQ.MXFP4, rows, K, 0, rows), OQ.MXFP4, torch.from_numpy(x).to(dev), rows, K,
+                         out_dtype=torch.float32))
+    ref = OQ.gemv(raw, OQ.MXFP4, x, rows, K, f64=True)
+    assert np.isfinite(ref).all() and np.isfinite(y).all()
+    assert rel_max(y, ref) < MFMA_TOL
+
+
+def test_t64_gemv_nan_scale_rows_are_non_finite(dev):
+    """An e8m0 of 255 makes the reference's dequantized weights +-inf (quant.py:131-140), so its
+    row products are non-finite; the block-scaled MFMA reads 255 as NaN: the same rows are
+    non-finite and the other rows are unaffected."""
+    from helpers import MFMA_TOL
+    from nurostream_amd.compute.kernels import T64Rows, fused_gemv, t64_pack
+    rows, K = 64, 256
+    raw = _gemv_case("MXFP4", rows, K, seed=5).reshape(rows, K // 32, 17)
+    bad = [3, 40]
+    raw[bad, 2, 0] = 255
+    raw[bad, 2, 1:] = 0x77  # codes 7 (LUT2 12): inf in the reference's float32 dequant
+    raw = raw.reshape(-1)
+    x = np.random.default_rng(3).standard_normal((1, K)).astype(np.float32)
+    tiles = t64_pack(torch.from_numpy(raw).to(dev), OQ.MXFP4, rows, K)
+    y = to_np(fused_gemv(T64Rows(tiles, OQ.MXFP4, rows, K, 0, rows), OQ.MXFP4, torch.from_numpy(x).to(dev), rows, K,
+                         out_dtype=torch.float32))[0]
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = OQ.gemv(raw, OQ.MXFP4, x, rows, K)[0]
+    assert not np.isfinite(ref[bad]).any() and not np.isfinite(y[bad]).any()
+    ok = np.setdiff1d(np.arange(rows), bad)
+    assert np.isfinite(y[ok]).all()
+    assert rel_max(y[ok], ref[ok].astype(np.float64)) < MFMA_TOL

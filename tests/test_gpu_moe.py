@@ -5,13 +5,18 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import rel_max, to_np
+from helpers import FFN_BAR, MFMA_TOL, rel_max, to_np
 from oracle import moe as OM
 from oracle import quant as OQ
 
 pytestmark = pytest.mark.gpu
 
-FFN_TOL = 1e-3  # north-star parity bar for FFN outputs (max rel, fp32 accumulate)
+FFN_TOL = FFN_BAR  # north-star parity bar for FFN outputs (max rel, fp32 accumulate)
+
+
+def _tol(layout):
+    """Regression bound: fp32 VALU products (GGUF rows) or the block-scaled MFMA (t64)."""
+    return MFMA_TOL if layout == "t64" else 1e-5
 
 
 def _near_tie_tokens(logits, k, h, W, b):
@@ -112,7 +117,7 @@ def test_moe_small_layers(dev, name, layout, slabs, T):
     out, ids, w = layer(h.to(dev))
     ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
     np.testing.assert_array_equal(np.sort(to_np(ids), 1), np.sort(rid, 1))
-    assert rel_max(to_np(out), ref) < 1e-5
+    assert rel_max(to_np(out), ref) < _tol(layout)
     # a second call reuses the workspace
     out2, _, _ = layer(h.to(dev))
     assert torch.equal(out, out2)
@@ -132,7 +137,7 @@ def test_gptoss_layer_decode(dev, layout):
     np.testing.assert_allclose(to_np(w), rw, rtol=1e-5)
     err = rel_max(to_np(out), ref)
     assert err < FFN_TOL
-    assert err < 1e-5, err
+    assert err < _tol(layout), err
 
 
 def test_qwen3_layer_decode(dev):

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import rel_max, to_np
+from helpers import MFMA_TOL, rel_max, to_np
 from oracle import moe as OM
 from oracle import quant as OQ
 
@@ -114,5 +114,6 @@ def test_stream_expert_ffn_matches_oracle(dev, mode):
                 pf.close()
         torch.cuda.synchronize()
         ref = OM.expert_ffn(ex, e, x.numpy(), act, block_rows=64)
-        assert rel_max(to_np(y), ref) < 2e-5, (mode, e)
+        tol = MFMA_TOL if mode == "t64-slab" else 2e-5  # t64 slabs run on the block-scaled MFMA
+        assert rel_max(to_np(y), ref) < tol, (mode, e)
     assert src.arena.used == 0
