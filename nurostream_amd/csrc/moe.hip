@@ -19,25 +19,29 @@
 
 static inline hipStream_t S(void* s) { return (hipStream_t)s; }
 
-constexpr int MAX_TOPK = 16;
+constexpr int MAX_TOPK = 8;
 constexpr int MAX_EXPERTS = 256;
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int RT_TT = 8;
 
-__device__ __forceinline__ void load8_w(const void* W, int wdt, int64_t off, float (&w)[8]) {
-  if (wdt == NSX_F32) {
-    const v4f a = *(const v4f*)((const float*)W + off);
-    const v4f b = *(const v4f*)((const float*)W + off + 4);
+// 8 consecutive router weights (f32 / bf16 / f16) as floats, from global memory
+template <int WDT>
+__device__ __forceinline__ void load8_w(const void* W, int64_t off, float (&w)[8]) {
+  typedef const __attribute__((address_space(1))) v4f gv4f;
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  if (WDT == NSX_F32) {
+    const v4f a = *(gv4f*)((const float*)W + off);
+    const v4f b = *(gv4f*)((const float*)W + off + 4);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else {
-    const v4u q = *(const v4u*)((const uint16_t*)W + off);
+    const v4u q = *(gv4u*)((const uint16_t*)W + off);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lo = q[i] & 0xffffu, hi = q[i] >> 16;
-      w[2 * i] = wdt == NSX_BF16 ? nsx_bf2f(lo) : nsx_h2f(lo);
-      w[2 * i + 1] = wdt == NSX_BF16 ? nsx_bf2f(hi) : nsx_h2f(hi);
+      w[2 * i] = WDT == NSX_BF16 ? nsx_bf2f(lo) : nsx_h2f(lo);
+      w[2 * i + 1] = WDT == NSX_BF16 ? nsx_bf2f(hi) : nsx_h2f(hi);
     }
   }
 }
@@ -49,10 +53,12 @@ constexpr int RT_XQ_WGS = 16;  // extra workgroups that quantize h for the t64 e
 // per grid row); with xq set, RT_XQ_WGS more workgroups per grid row build
 // the tokens' activation terms. Loads are unpredicated (addresses clamped,
 // tails zeroed after the load) so that they are all in flight together.
+template <int WDT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restrict__ h, int T, int K,
-                                                            const void* __restrict__ W, int wdt,
+                                                            const void* __restrict__ W,
                                                             const float* __restrict__ bias, int E,
                                                             float* __restrict__ logits, uint8_t* __restrict__ xq) {
+  typedef const __attribute__((address_space(1))) v4f gv4f;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int ewgs = (E + 3) / 4;
   if ((int)blockIdx.x >= ewgs) {  // activation terms of h, two blocks per wave task
@@ -79,24 +85,25 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
 #pragma unroll
     for (int c = 0; c < RT_MAXC; ++c) {
       const int k = k0 + c * 512 + lane * 8;
-      load8_w(W, wdt, (int64_t)e * K + (k < K ? k : K - 8), w[c]);
+      load8_w<WDT>(W, (int64_t)e * K + (k < K ? k : K - 8), w[c]);
     }
 #pragma unroll
     for (int c = 0; c < RT_MAXC; ++c) {
-      if (k0 + c * 512 + lane * 8 >= K) {
+      const bool in = k0 + c * 512 + lane * 8 < K;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) w[c][u] = 0.f;
-      }
+      for (int u = 0; u < 8; ++u) w[c][u] = in ? w[c][u] : 0.f;
     }
-    for (int i = 0; i < nt; ++i) {
+#pragma unroll
+    for (int i = 0; i < RT_TT; ++i) {
+      if (i >= nt) break;
       const float* hp = h + (int64_t)(t0 + i) * K;
       v4f ha[RT_MAXC], hb[RT_MAXC];
 #pragma unroll
       for (int c = 0; c < RT_MAXC; ++c) {
         const int k = k0 + c * 512 + lane * 8;
         const int kc = k < K ? k : K - 8;
-        ha[c] = *(const v4f*)(hp + kc);
-        hb[c] = *(const v4f*)(hp + kc + 4);
+        ha[c] = *(gv4f*)(hp + kc);
+        hb[c] = *(gv4f*)(hp + kc + 4);
       }
       float s = acc[i];
 #pragma unroll
@@ -111,8 +118,9 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
   }
 #pragma unroll
   for (int i = 0; i < RT_TT; ++i) {
+    if (i >= nt) break;
     const float s = nsx_wave_sum(acc[i]);
-    if (lane == 0 && i < nt) logits[(int64_t)(t0 + i) * E + e] = bias ? s + bias[e] : s;
+    if (lane == 0) logits[(int64_t)(t0 + i) * E + e] = bias ? s + bias[e] : s;
   }
 }
 
@@ -129,48 +137,60 @@ __device__ __forceinline__ float key2f(uint32_t k) {
   return __builtin_bit_cast(float, k & 0x80000000u ? (k ^ 0x80000000u) : ~k);
 }
 
-// Each round takes the wave maximum of the lanes' best keys, then the
-// minimum index holding it (wave reductions run on DPP, not LDS permutes).
-__device__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode, int (&sel_i)[MAX_TOPK],
-                          float (&sel_w)[MAX_TOPK]) {
+constexpr int TOPK_NV = MAX_EXPERTS / 64;  // logits per lane
+
+// Issue the loads of one token's logits: lane l holds experts l + 64 i.
+// Unpredicated (index clamped); topk_select masks experts >= E.
+__device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, float (&v)[TOPK_NV]) {
   const int lane = __lane_id();
-  constexpr int NV = MAX_EXPERTS / 64;
-  float v[NV];
-  bool ok[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
+  for (int i = 0; i < TOPK_NV; ++i) {
     const int e = lane + 64 * i;
-    ok[i] = e < E;
-    v[i] = ok[i] ? lg[e] : 0.f;
+    v[i] = lg[e < E ? e : E - 1];
   }
+}
+
+// Each round takes the wave maximum of the lanes' best keys, then the
+// minimum index holding it (DPP reductions). Results are wave-uniform.
+__device__ void topk_select(float (&v)[TOPK_NV], int E, int k, int mode, int (&sel_i)[MAX_TOPK],
+                            float (&sel_w)[MAX_TOPK]) {
+  const int lane = __lane_id();
+  bool ok[TOPK_NV];
+#pragma unroll
+  for (int i = 0; i < TOPK_NV; ++i) ok[i] = lane + 64 * i < E;
   if (mode == NSX_ROUTE_QWEN3) {  // probs = softmax(logits) over all experts, float32 (router.py:65)
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < TOPK_NV; ++i)
       if (ok[i]) m = fmaxf(m, v[i]);
     m = key2f(nsx_wave_max_u32(f2key(m)));
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < TOPK_NV; ++i)
       if (ok[i]) {
         v[i] = expf(v[i] - m);
         s += v[i];
       }
     s = nsx_wave_sum(s);
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < TOPK_NV; ++i)
       if (ok[i]) v[i] = v[i] / s;
   }
-  uint32_t key[NV];
+  uint32_t key[TOPK_NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) key[i] = f2key(v[i]);
+  for (int i = 0; i < TOPK_NV; ++i) key[i] = f2key(v[i]);
   float sel_v[MAX_TOPK];
+#pragma unroll
+  for (int j = 0; j < MAX_TOPK; ++j) {
+    sel_v[j] = 0.f;
+    sel_i[j] = 0;
+  }
 #pragma unroll
   for (int j = 0; j < MAX_TOPK; ++j) {
     if (j >= k) break;
     uint32_t lk = 0, li = 0xffffu;
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < TOPK_NV; ++i)
       if (ok[i] && (key[i] > lk || li == 0xffffu)) {  // i ascending: ties keep the lower index
         lk = key[i];
         li = lane + 64 * i;
@@ -180,21 +200,33 @@ __device__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode, 
     sel_i[j] = wi == 0xffffu ? 0 : (int)wi;
     sel_v[j] = key2f(mk);
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < TOPK_NV; ++i)
       if (lane + 64 * i == (int)wi) ok[i] = false;
   }
+  // static loop bounds (guards on k) keep sel_v / sel_w in registers
+  float s = 0.f;
   if (mode == NSX_ROUTE_GPTOSS) {  // softmax over the selected logits in float32 (gpt_oss.py:120)
-    float s = 0.f;
-    for (int j = 0; j < k; ++j) {
-      sel_w[j] = expf(sel_v[j] - sel_v[0]);
+#pragma unroll
+    for (int j = 0; j < MAX_TOPK; ++j) {
+      sel_w[j] = j < k ? expf(sel_v[j] - sel_v[0]) : 0.f;
       s += sel_w[j];
     }
-    for (int j = 0; j < k; ++j) sel_w[j] = sel_w[j] / s;
   } else {  // renormalise the selected probabilities (router.py:68)
-    float s = 0.f;
-    for (int j = 0; j < k; ++j) s += sel_v[j];
-    for (int j = 0; j < k; ++j) sel_w[j] = sel_v[j] / s;
+#pragma unroll
+    for (int j = 0; j < MAX_TOPK; ++j) {
+      sel_w[j] = j < k ? sel_v[j] : 0.f;
+      s += sel_w[j];
+    }
   }
+#pragma unroll
+  for (int j = 0; j < MAX_TOPK; ++j) sel_w[j] = sel_w[j] / s;
+}
+
+__device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode,
+                                          int (&sel_i)[MAX_TOPK], float (&sel_w)[MAX_TOPK]) {
+  float v[TOPK_NV];
+  topk_load(lg, E, v);
+  topk_select(v, E, k, mode, sel_i, sel_w);
 }
 
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int mode,
@@ -226,7 +258,13 @@ static int check_router(int64_t T, int64_t K, int wdt, int64_t E, int k, int mod
 static int launch_logits(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias, int64_t E,
                          float* logits, uint8_t* xq, hipStream_t st) {
   const dim3 grid((unsigned)(nsx_cdiv(E, 4) + (xq ? RT_XQ_WGS : 0)), (unsigned)nsx_cdiv(T, RT_TT));
-  return nsx_launch(router_logits_kernel, grid, dim3(256), 0, st, h, (int)T, (int)K, w, wdt, bias, (int)E, logits,
+  if (wdt == NSX_BF16)
+    return nsx_launch(router_logits_kernel<NSX_BF16>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E,
+                      logits, xq);
+  if (wdt == NSX_F16)
+    return nsx_launch(router_logits_kernel<NSX_F16>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E,
+                      logits, xq);
+  return nsx_launch(router_logits_kernel<NSX_F32>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E, logits,
                     xq);
 }
 
@@ -335,13 +373,11 @@ struct MoeDev {
   float* out;
   float* act;            // (pairs, n_ff) fp32 activations (GGUF-layout path)
   const uint8_t* xq_h;   // activation terms of h, per token (t64 path)
-  float* part_gu;        // (pairs, 2, cg, n_ff) gate/up partial sums (t64 path)
-  float* part_dn;        // (pairs, cd, n_embd) down partial sums (t64 path)
+  uint8_t* xq_a;         // activation terms of the expert activation, per pair (t64 path)
   int n_embd, n_ff;
   MxGeom ggu, gdn;       // t64 geometry of a gate/up and of a down matrix
   int cg, sg;            // gate/up K-chunks and K-steps per chunk
-  int cd, sd;            // down K-chunks and K-steps per chunk
-  int tpw;               // down output tiles per workgroup (one wave each)
+  int cd, sd;            // down K-chunks per expert and K-steps per chunk
   int act_kind;
   float alpha, limit;
 };
@@ -389,17 +425,19 @@ __device__ __forceinline__ const uint8_t* expert_base(const void* base, int64_t 
 }
 
 constexpr int GU_S = 3;         // K-steps per gate/up wave (one chunk)
-constexpr int DN_S = 3;         // K-steps per down chunk
-constexpr int MAX_CHUNKS = 16;  // split-K chunks summed by the next kernel (K <= 6144)
-constexpr int COMBINE_SLOTS = 4;
-constexpr int DN_EPT = (DN_S * 128 + 255) / 256;  // activation elements per down thread (>= 4 waves)
+constexpr int DC_S = 6;         // K-steps per down wave (one chunk, one row group)
+constexpr int MAX_CHUNKS = 8;   // gate/up K-chunks (waves per matrix) of a workgroup (K <= 3072)
 
-__device__ __forceinline__ int pair_expert(const MoeDev& a, int p, float* w = nullptr) {
-  const int t = p / a.top_k, j = p - t * a.top_k;
+// The pair's expert: issue the token's logit loads first (pair_logits), other
+// independent loads next, then select (pair_expert) -- waiting on the logits only.
+__device__ __forceinline__ void pair_logits(const MoeDev& a, int p, float (&v)[TOPK_NV]) {
+  topk_load(a.logits + (int64_t)(p / a.top_k) * a.E, a.E, v);
+}
+__device__ __forceinline__ int pair_expert(const MoeDev& a, int p, float (&v)[TOPK_NV]) {
+  const int j = p - (p / a.top_k) * a.top_k;
   int si[MAX_TOPK];
   float sw[MAX_TOPK];
-  topk_regs(a.logits + (int64_t)t * a.E, a.E, a.top_k, a.mode, si, sw);
-  if (w) *w = sw[j];
+  topk_select(v, a.E, a.top_k, a.mode, si, sw);
   return clamp_expert(si[j], a.E);
 }
 
@@ -413,138 +451,145 @@ __device__ __forceinline__ void mx_store_rows(const v4f (&D)[4], int tile, int n
     if (r0 + 16 * g < n) *(v4f*)(dst + r0 + 16 * g) = D[g];
 }
 
-// phase 1: one wave per (pair, gate|up, 64-row tile, K-chunk); four
-// independent waves per workgroup. Writes partial sums only.
-__global__ __launch_bounds__(256) void moe_gu_kernel(MoeDev a) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t u = (int64_t)blockIdx.x * 4 + wave;
+// phase 1: workgroup = (pair, 64-row tile of gate/up), one wave per
+// (gate|up, K-chunk), each a single pass over its chunk's steps. The waves
+// meet in LDS (fixed order); wave 0 adds the biases, applies the activation
+// and writes the activation's terms for the down kernel -- the tile's 64
+// rows are exactly two 32-element blocks of the down kernel's K.
+__global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
+  __shared__ float red[2][MAX_CHUNKS][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int tiles = (int)a.ggu.tiles;
-  const int64_t per_p = 2ll * tiles * a.cg;
-  const int p = (int)(u / per_p);
-  if (p >= a.T * a.top_k) return;
-  int r = (int)(u - p * per_p);
-  const int m = r / (tiles * a.cg);
-  r -= m * tiles * a.cg;
-  const int tile = r / a.cg, c = r - tile * a.cg;
-  const int e = pair_expert(a, p);
-  const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
-                              : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
+  const int p = blockIdx.x / tiles, tile = blockIdx.x - p * tiles;
+  const int m = wave / a.cg, c = wave - m * a.cg;
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
   const int t = p / a.top_k;
+  float lg[TOPK_NV];
+  pair_logits(a, p, lg);
+  MxRegs<GU_S> R;
+  mx_load_b<GU_S, false>(R, a.xq_h + (int64_t)t * a.ggu.ns * XQ_STEP, 0, 0, 1, s0, s1);  // no expert needed
+  const int e = pair_expert(a, p, lg);
+  const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
+                              : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
+  mx_load_a<GU_S>(R, mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1);
+  const int row = tile * 64 + lane;
+  const int rowc = min(row, a.n_ff - 1);
+  float gb = 0.f, ub = 0.f;  // wave 0's biases, requested while the weights stream
+  if (wave == 0) {
+    if (a.gate_bias) gb = a.gate_bias[(int64_t)e * a.n_ff + rowc];
+    if (a.up_bias) ub = a.up_bias[(int64_t)e * a.n_ff + rowc];
+  }
   v4f D[4] = {};
-  mx_tile_mfma<GU_S, false>(mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1,
-                     a.xq_h + (int64_t)t * a.ggu.ns * XQ_STEP, 0, 0, 1, D);
+  mx_compute<GU_S>(R, a.ggu, s0, s1, D);
   mx_sum_terms(D);
-  mx_store_rows(D, tile, a.n_ff, a.part_gu + ((int64_t)(p * 2 + m) * a.cg + c) * a.n_ff);
+  if ((lane & 15) == 0) {
+    const int r0 = 4 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) *(v4f*)(&red[m][c][16 * g + r0]) = D[g];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float gs = 0.f, us = 0.f;
+  for (int cc = 0; cc < a.cg; ++cc) {
+    gs += red[0][cc][lane];
+    us += red[1][cc][lane];
+  }
+  const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
+  xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
 }
 
-// phase 2: workgroup = (pair, K-chunk, tpw output tiles), one wave per tile.
-// The prologue forms the chunk's activation from the gate/up partials (fixed
-// order) and biases, and quantizes it into activation terms in LDS.
-__global__ __launch_bounds__(512) void moe_down_kernel(MoeDev a) {
-  __shared__ float act[DN_S * 128];
-  __shared__ __align__(16) uint8_t xq[DN_S * XQ_STEP];
+// phase 2 (down and combine): workgroup = (token, 16-row group of a 64-row
+// output tile); one wave per (expert slot, K-chunk), each a single pass over
+// its steps. The waves meet in LDS; wave 0 sums each expert's chunks in a
+// fixed order (chunk 0 carries the bias) and combines the experts in
+// ascending id: out[rows] = sum of w_e * y_e. The token's first workgroup
+// also writes the ids/weights outputs.
+constexpr int DC_PIECES = DC_S * XQ_STEP / 16;  // 16-byte pieces of one wave's activation terms
+
+__global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
+  __shared__ float red[16][16];  // [wave = slot * cd + chunk][row of the group]
+  __shared__ __align__(16) uint8_t xs[16][DC_S * XQ_STEP];  // each wave's activation terms, staged
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int tiles = (int)a.gdn.tiles;
-  const int groups = (tiles + a.tpw - 1) / a.tpw;
-  int bid = blockIdx.x;
-  const int tg = bid % groups;
-  bid /= groups;
-  const int c = bid % a.cd, p = bid / a.cd;
-  const int e = pair_expert(a, p);
-  const int s0 = c * a.sd, s1 = min(a.gdn.ns, s0 + a.sd);
-  const int k0 = s0 * 128, nk = (s1 - s0) * 128;
-  const float* pg = a.part_gu + (int64_t)p * 2 * a.cg * a.n_ff;
-  const float* pu = pg + (int64_t)a.cg * a.n_ff;
-  {
-    // up to DN_EPT elements per thread; every partial of both is loaded before the (fixed-order) sums
-    float gp[DN_EPT][MAX_CHUNKS], up[DN_EPT][MAX_CHUNKS], gb[DN_EPT], ub[DN_EPT];
-#pragma unroll
-    for (int q = 0; q < DN_EPT; ++q) {
-      const int k = threadIdx.x + q * blockDim.x;
-      const int kk = min(k0 + min(k, nk - 1), a.n_ff - 1);  // clamped: unpredicated loads
-#pragma unroll
-      for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-        const int ci = cc < a.cg ? cc : a.cg - 1;
-        gp[q][cc] = pg[(int64_t)ci * a.n_ff + kk];
-        up[q][cc] = pu[(int64_t)ci * a.n_ff + kk];
-      }
-      gb[q] = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + kk] : 0.f;
-      ub[q] = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + kk] : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < DN_EPT; ++q) {
-      const int k = threadIdx.x + q * blockDim.x;
-      float g = 0.f, uu = 0.f;
-#pragma unroll
-      for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-        g += cc < a.cg ? gp[q][cc] : 0.f;
-        uu += cc < a.cg ? up[q][cc] : 0.f;
-      }
-      if (k < nk) act[k] = k0 + k < a.n_ff ? moe_act(a.act_kind, g + gb[q], uu + ub[q], a.alpha, a.limit) : 0.f;
-    }
-  }
-  __syncthreads();
-  const int nw = blockDim.x >> 6;
-  for (int task = wave; task < nk / 64; task += nw) {  // two 32-element blocks per task
-    const int bl = task * 2 + (lane >> 5);
-    xq_block(act[bl * 32 + (lane & 31)], bl, xq);
-  }
-  __syncthreads();
-  const int tile = tg * a.tpw + wave;
-  if (tile >= tiles) return;
-  const uint8_t* mat = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
-  v4f D[4] = {};
-  mx_tile_mfma<DN_S, true>(mat + (int64_t)tile * a.gdn.tile_bytes, a.gdn, s0, s1, xq, s0, 0, 1, D);
-  mx_sum_terms(D);
-  mx_store_rows(D, tile, a.n_embd, a.part_dn + ((int64_t)p * a.cd + c) * a.n_embd);
-}
-
-// phase 3: out[t] = sum over the token's experts, ascending id, of
-// w * (down partials summed in order + bias); also the ids/weights outputs.
-__global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
-  const int t = blockIdx.y;
+  const int groups = 4 * (int)a.gdn.tiles;
+  const int t = blockIdx.x / groups, hh = blockIdx.x - t * groups;
+  const int tile = hh >> 2, rg = hh & 3;
   const int k = a.top_k;
-  int si[MAX_TOPK], order[MAX_TOPK];
-  float sw[MAX_TOPK];
-  topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw);
-  for (int jj = 0; jj < k; ++jj) si[jj] = clamp_expert(si[jj], a.E);
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    for (int jj = 0; jj < k; ++jj) {
-      a.ids[(int64_t)t * k + jj] = si[jj];
-      a.wts[(int64_t)t * k + jj] = sw[jj];
+  const int j = wave / a.cd, c = wave - j * a.cd;
+  const int p = t * k + j;
+  const int s0 = c * a.sd, s1 = min(a.gdn.ns, s0 + a.sd);
+  float lg[TOPK_NV];
+  topk_load(a.logits + (int64_t)t * a.E, a.E, lg);
+  // this wave's activation terms (steps s0 .. s1 - 1), requested now and staged in LDS below
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  const int npc = (s1 - s0) * (XQ_STEP / 16);
+  const uint8_t* xsrc = a.xq_a + ((int64_t)p * a.gdn.ns + s0) * XQ_STEP;
+  v4u stage[(DC_PIECES + 63) / 64];
+#pragma unroll
+  for (int i = 0; i < (DC_PIECES + 63) / 64; ++i) stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
+  // the top-k, reduced at once to what is used later (static indices: no private arrays):
+  // this wave's expert; in lane jj < k slot jj's expert, weight and rank in ascending expert id
+  int e = 0, my_e = 0, my_rank = 0;
+  float my_w = 0.f;
+  {
+    int si[MAX_TOPK];
+    float sw[MAX_TOPK];
+    topk_select(lg, a.E, k, a.mode, si, sw);
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      e = jj == j ? si[jj] : e;
+      my_e = lane == jj ? si[jj] : my_e;
+      my_w = lane == jj ? sw[jj] : my_w;
     }
-  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= a.n_embd) return;
-  slot_order(si, k, order);
-  float o = 0.f;
-  for (int j0 = 0; j0 < k; j0 += COMBINE_SLOTS) {
-    // all partials of COMBINE_SLOTS experts are loaded before the (fixed-order) sums
-    float v[COMBINE_SLOTS][MAX_CHUNKS], b[COMBINE_SLOTS];
+    e = clamp_expert(e, a.E);
+    my_e = clamp_expert(my_e, a.E);
 #pragma unroll
-    for (int q = 0; q < COMBINE_SLOTS; ++q) {  // unpredicated loads: indices clamped, extra terms zeroed
-      const bool on = j0 + q < k;
-      const int j = order[on ? j0 + q : k - 1];
-      const float* pd = a.part_dn + ((int64_t)t * k + j) * a.cd * a.n_embd + n;
-#pragma unroll
-      for (int cc = 0; cc < MAX_CHUNKS; ++cc) v[q][cc] = pd[(int64_t)(cc < a.cd ? cc : a.cd - 1) * a.n_embd];
-      b[q] = a.down_bias ? a.down_bias[(int64_t)si[j] * a.n_embd + n] : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < COMBINE_SLOTS; ++q) {
-#pragma unroll
-      for (int cc = 0; cc < MAX_CHUNKS; ++cc) v[q][cc] = cc < a.cd ? v[q][cc] : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < COMBINE_SLOTS; ++q) {
-      if (j0 + q >= k) break;
-      float y = 0.f;
-#pragma unroll
-      for (int cc = 0; cc < MAX_CHUNKS; ++cc) y += v[q][cc];
-      o = combine_one(o, sw[order[j0 + q]], y + b[q]);
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      const int ej = clamp_expert(si[jj], a.E);
+      my_rank += (jj < k && (ej < my_e || (ej == my_e && jj < lane))) ? 1 : 0;
     }
   }
-  a.out[(int64_t)t * a.n_embd + n] = o;
+  MxRegs<DC_S, 1> R;
+  mx_load_a<DC_S, 1>(R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) + (int64_t)tile * a.gdn.tile_bytes,
+                     a.gdn, s0, s1, rg);
+  const int r0 = tile * 64 + 16 * rg + 4 * (lane >> 4);
+  v4f bias = {0.f, 0.f, 0.f, 0.f};  // chunk 0's bias rows, requested while the weights stream
+  if (c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd)
+    bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+#pragma unroll
+  for (int i = 0; i < (DC_PIECES + 63) / 64; ++i) {  // (clamped duplicates rewrite the same bytes)
+    const int pc = min(lane + 64 * i, npc - 1);
+    *(v4u*)(&xs[wave][pc * 16]) = stage[i];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes land before its reads
+  __builtin_amdgcn_wave_barrier();
+  mx_load_b<DC_S, true, 1>(R, xs[wave], s0, 0, 1, s0, s1);
+  v4f D[1] = {};
+  mx_compute<DC_S, 1>(R, a.gdn, s0, s1, D, rg);
+  mx_sum_terms<1>(D);
+  if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + bias;
+  __syncthreads();
+  if (wave != 0) return;
+  // slot order of the combine (ascending expert id), exchanged through LDS
+  __shared__ int s_slot[MAX_TOPK];
+  if (lane < k) {
+    if (hh == 0) {
+      a.ids[(int64_t)t * k + lane] = my_e;
+      a.wts[(int64_t)t * k + lane] = my_w;
+    }
+    s_slot[my_rank] = lane;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are visible to its reads
+  __builtin_amdgcn_wave_barrier();
+  const int row = tile * 64 + 16 * rg + (lane & 15);
+  float o = 0.f;
+  for (int jj = 0; jj < k; ++jj) {
+    const int jx = s_slot[jj];
+    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), jx));
+    float y = 0.f;
+    for (int cc = 0; cc < a.cd; ++cc) y += red[jx * a.cd + cc][lane & 15];
+    o = combine_one(o, w, y);
+  }
+  if (lane < 16 && row < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -643,24 +688,10 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 // host side
 
 struct MoePlan {
-  int64_t off_logits, off_act, off_xq, off_pgu, off_pdn, total;
+  int64_t off_logits, off_act, off_xqh, off_xqa, total;
   MxGeom ggu, gdn;
-  int cg, cd, tpw;
+  int cg, cd, sd;
 };
-
-// down tiles per workgroup: the count in 4..8 that leaves the fewest idle waves
-static int pick_tpw(int64_t tiles) {
-  int best = 4;
-  int64_t waste = nsx_cdiv(tiles, 4) * 4 - tiles;
-  for (int w = 5; w <= 8; ++w) {
-    const int64_t wz = nsx_cdiv(tiles, w) * w - tiles;
-    if (wz < waste || (wz == waste && w > best)) {
-      best = w;
-      waste = wz;
-    }
-  }
-  return best;
-}
 
 static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   MoePlan p{};
@@ -669,20 +700,19 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.ggu = mx_geom(L->n_ff, L->n_embd);
   p.gdn = mx_geom(L->n_embd, L->n_ff);
   p.cg = (int)nsx_cdiv(p.ggu.ns, GU_S);
-  p.cd = (int)nsx_cdiv(p.gdn.ns, DN_S);
-  p.tpw = pick_tpw(p.gdn.tiles);
+  const int kk = std::max(1, std::min(L->top_k, 16));
+  p.cd = std::max(1, std::min(p.gdn.ns, 16 / kk));  // top_k * cd waves per down workgroup
+  p.sd = (int)nsx_cdiv(p.gdn.ns, p.cd);
   auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
   int64_t o = 0;
   p.off_logits = o;
   o = al(o + T * L->n_expert * 4);
   p.off_act = o;
   o = al(o + (t64 ? 0 : P * L->n_ff * 4));
-  p.off_xq = o;
+  p.off_xqh = o;
   o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP : 0));
-  p.off_pgu = o;
-  o = al(o + (t64 ? P * 2 * p.cg * L->n_ff * 4 : 0));
-  p.off_pdn = o;
-  o = al(o + (t64 ? P * p.cd * L->n_embd * 4 : 0));
+  p.off_xqa = o;
+  o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : 0));
   p.total = o;
   return p;
 }
@@ -717,9 +747,10 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
     NSX_REQUIRE((int64_t)L->top_k * (L->n_ff + L->n_ff / 32) * 4 <= 160 * 1024, NSX_EINVAL,
                 "top_k * n_ff too large for LDS");
   } else {
-    NSX_REQUIRE(nsx_cdiv(nsx_cdiv(L->n_embd / 32, 4), GU_S) <= MAX_CHUNKS &&
-                    nsx_cdiv(nsx_cdiv(L->n_ff / 32, 4), DN_S) <= MAX_CHUNKS,
-                NSX_EINVAL, "t64 layers take n_embd, n_ff <= %d", MAX_CHUNKS * GU_S * 128);
+    const MoePlan pl = moe_plan(L, T);
+    NSX_REQUIRE(pl.cg <= MAX_CHUNKS, NSX_EINVAL, "t64 layers take n_embd <= %d", MAX_CHUNKS * GU_S * 128);
+    NSX_REQUIRE(pl.sd <= DC_S, NSX_EINVAL, "t64 layers take n_ff <= %d at top_k=%d",
+                DC_S * (16 / std::max(1, L->top_k)) * 128, L->top_k);
 
   }
   return NSX_OK;
@@ -781,9 +812,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.h = h;
   d.out = out;
   d.act = (float*)(ws + p.off_act);
-  d.xq_h = (const uint8_t*)(ws + p.off_xq);
-  d.part_gu = (float*)(ws + p.off_pgu);
-  d.part_dn = (float*)(ws + p.off_pdn);
+  d.xq_h = (const uint8_t*)(ws + p.off_xqh);
+  d.xq_a = (uint8_t*)(ws + p.off_xqa);
   d.n_embd = L->n_embd;
   d.n_ff = L->n_ff;
   d.ggu = p.ggu;
@@ -791,8 +821,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.cg = p.cg;
   d.sg = GU_S;
   d.cd = p.cd;
-  d.sd = DN_S;
-  d.tpw = p.tpw;
+  d.sd = p.sd;
   d.act_kind = L->act;
   d.alpha = L->alpha;
   d.limit = L->limit;
@@ -800,7 +829,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
   if (on(NSX_PHASE_ROUTER)) {
     rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
-                       (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xq) : nullptr, st);
+                       (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
     if (rc) return rc;
     if (!t64 && (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st))) return rc;
   }
@@ -808,18 +837,13 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
 
   if (t64) {
     if (on(NSX_PHASE_GATE_UP) &&
-        (rc = nsx_launch(moe_gu_kernel, dim3((unsigned)nsx_cdiv(P * 2 * p.ggu.tiles * p.cg, 4)), dim3(256), 0, st,
-                         d)))
+        (rc = nsx_launch(moe_gu_kernel, dim3((unsigned)(P * p.ggu.tiles)), dim3(128 * p.cg), 0, st, d)))
       return rc;
     if (on(NSX_PHASE_DOWN) &&
-        (rc = nsx_launch(moe_down_kernel, dim3((unsigned)(P * p.cd * nsx_cdiv(p.gdn.tiles, p.tpw))),
-                         dim3(64 * p.tpw), 0, st, d)))
-      return rc;
-    if (on(NSX_PHASE_COMBINE) &&
-        (rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
+        (rc = nsx_launch(moe_down_kernel, dim3((unsigned)(T * 4 * p.gdn.tiles)), dim3(64 * L->top_k * p.cd), 0, st,
                          d)))
       return rc;
-    return NSX_OK;
+    return NSX_OK;  // the down kernel also combines
   }
   switch (L->ggml_type) {  // the GGUF-layout down kernel also combines
     case NSX_MXFP4: return launch_raw_phases<NSX_MXFP4>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));

@@ -133,20 +133,48 @@ __device__ __forceinline__ void xq_block(float r, int b, uint8_t* dst) {
 #define NSX_MFMA_SCALE(A, B, C, G, SA, SB) \
   __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 4, 0, (G), (SA), 0, (SB))
 
-// D[g] (rows 16 g .. 16 g + 15 of the tile, 16 columns) accumulates the
-// products. Column c = token * XQ_NT + term for tokens < ntok; xq points at
-// step xs0 of token 0 (in LDS when BLDS) and tokens are xq_stride bytes
-// apart. S steps' loads are issued before their MFMAs, unpredicated so the
-// waits can retire step by step: A lanes past a partial last step read an
-// in-bounds stand-in with scale 0 (the activation there is zero), and
-// columns of tokens >= ntok repeat token ntok - 1 (those columns are not
-// read back). A weight e8m0 of 255 is NaN to the hardware: the row's result
-// is non-finite, as it is in the reference, whose fp32 dequant turns such a
-// block into +-inf (2^127 times ggml's doubled table).
-template <int S, bool BLDS>
-__device__ __forceinline__ void mx_tile_mfma(const uint8_t* __restrict__ tile, const MxGeom& G, int s0, int s1,
-                                             const uint8_t* __restrict__ xq, int xs0, int64_t xq_stride, int ntok,
-                                             v4f (&D)[4]) {
+// Operands of up to S K-steps of one wave (G of the tile's four 16-row
+// groups), held in registers.
+template <int S, int G = 4>
+struct MxRegs {
+  v4u A[S][G], B0[S], B1[S];
+  uint32_t SA[S], SB[S];
+};
+
+// Weight operands of steps [s0, min(s1, s0 + S)) of a 64-row tile. Loads are
+// unpredicated so that their waits retire step by step: lanes past a partial
+// last step read an in-bounds stand-in with scale 0 (the activation there is
+// zero). A weight e8m0 of 255 is NaN to the hardware: the row's result is
+// non-finite, as in the reference, whose fp32 dequant makes such a block
+// +-inf (2^127 times ggml's doubled table).
+template <int S, int G = 4>
+__device__ __forceinline__ void mx_load_a(MxRegs<S, G>& R, const uint8_t* __restrict__ tile, const MxGeom& G_,
+                                          int s0, int s1, int g0 = 0) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  typedef const __attribute__((address_space(1))) uint32_t gu32;
+  const int lane = __lane_id(), grp = lane >> 4;
+#pragma unroll
+  for (int u = 0; u < S; ++u) {
+    const int s = s0 + u;
+    if (s < s1) {
+      const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
+      const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
+      const bool alane = grp < rs;
+      const int la = alane ? lane : 16 * rs - 1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) R.A[u][g] = *(gv4u*)(ch + (g0 + g) * rs * 256 + la * 16);
+      R.SA[u] = *(gu32*)(ch + rs * 1024 + la * 4);  // raw: mx_compute selects (no wait in here)
+    }
+  }
+}
+
+// Activation operands of the same steps: column c = token * XQ_NT + term for
+// tokens < ntok; xq points at step xs0 of token 0 (in LDS when BLDS), tokens
+// xq_stride bytes apart; columns of tokens >= ntok repeat token ntok - 1 and
+// are not read back.
+template <int S, bool BLDS, int G = 4>
+__device__ __forceinline__ void mx_load_b(MxRegs<S, G>& R, const uint8_t* __restrict__ xq, int xs0, int64_t xq_stride,
+                                          int ntok, int s0, int s1) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
   typedef const __attribute__((address_space(1))) uint32_t gu32;
   typedef const __attribute__((address_space(3))) v4u lv4u;
@@ -157,56 +185,77 @@ __device__ __forceinline__ void mx_tile_mfma(const uint8_t* __restrict__ tile, c
   const int tok = tok0 < ntok ? tok0 : ntok - 1;
   const uint8_t* xt = xq + (int64_t)tok * xq_stride + (grp * XQ_NT + term) * 32;
   const uint8_t* xst = xq + (int64_t)tok * xq_stride + XQ_CODES + (grp * XQ_NT + term) * 4;
-  for (int p0 = s0; p0 < s1; p0 += S) {
-    v4u A[S][4], B0[S], B1[S];
-    uint32_t SA[S], SB[S];
 #pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int s = p0 + u;
-      if (s < s1) {
-        const int rs = s < G.ns - 1 ? 4 : G.rlast;
-        const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
-        const bool alane = grp < rs;
-        const int la = alane ? lane : 16 * rs - 1;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) A[u][g] = *(gv4u*)(ch + g * rs * 256 + la * 16);
-        SA[u] = *(gu32*)(ch + rs * 1024 + la * 4);
-        SA[u] = alane ? SA[u] : 0u;
-        const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
-        if (BLDS) {
-          B0[u] = *(lv4u*)(xt + xo);
-          B1[u] = *(lv4u*)(xt + xo + 16);
-          SB[u] = *(lu32*)(xst + xo);
-        } else {
-          B0[u] = *(gv4u*)(xt + xo);
-          B1[u] = *(gv4u*)(xt + xo + 16);
-          SB[u] = *(gu32*)(xst + xo);
-        }
+  for (int u = 0; u < S; ++u) {
+    const int s = s0 + u;
+    if (s < s1) {
+      const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
+      if (BLDS) {
+        R.B0[u] = *(lv4u*)(xt + xo);
+        R.B1[u] = *(lv4u*)(xt + xo + 16);
+        R.SB[u] = *(lu32*)(xst + xo);
+      } else {
+        R.B0[u] = *(gv4u*)(xt + xo);
+        R.B1[u] = *(gv4u*)(xt + xo + 16);
+        R.SB[u] = *(gu32*)(xst + xo);
       }
-    }
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      if (p0 + u >= s1) break;
-      const uint32_t sa = SA[u];
-      const v8i b = {(int)B0[u].x, (int)B0[u].y, (int)B0[u].z, (int)B0[u].w,
-                     (int)B1[u].x, (int)B1[u].y, (int)B1[u].z, (int)B1[u].w};
-      const v8i a0 = {(int)A[u][0].x, (int)A[u][0].y, (int)A[u][0].z, (int)A[u][0].w, 0, 0, 0, 0};
-      const v8i a1 = {(int)A[u][1].x, (int)A[u][1].y, (int)A[u][1].z, (int)A[u][1].w, 0, 0, 0, 0};
-      const v8i a2 = {(int)A[u][2].x, (int)A[u][2].y, (int)A[u][2].z, (int)A[u][2].w, 0, 0, 0, 0};
-      const v8i a3 = {(int)A[u][3].x, (int)A[u][3].y, (int)A[u][3].z, (int)A[u][3].w, 0, 0, 0, 0};
-      D[0] = NSX_MFMA_SCALE(a0, b, D[0], 0, sa, SB[u]);
-      D[1] = NSX_MFMA_SCALE(a1, b, D[1], 1, sa, SB[u]);
-      D[2] = NSX_MFMA_SCALE(a2, b, D[2], 2, sa, SB[u]);
-      D[3] = NSX_MFMA_SCALE(a3, b, D[3], 3, sa, SB[u]);
     }
   }
 }
 
-// Sum the XQ_NT term columns of D: afterwards lane l with (l & 3) == 0 holds,
-// for token (l & 15) / 4, rows 16 g + 4 (l / 16) + i in D[g][i].
-__device__ __forceinline__ void mx_sum_terms(v4f (&D)[4]) {
+#define NSX_MFMA_SCALE(A, B, C, G, SA, SB) \
+  __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 4, 0, (G), (SA), 0, (SB))
+
+// D[g] (rows 16 (g0 + g) .. + 15 of the tile, 16 columns) += the loaded steps
+// (the same G_, s0, s1, g0 as mx_load_a).
+template <int S, int G = 4>
+__device__ __forceinline__ void mx_compute(const MxRegs<S, G>& R, const MxGeom& G_, int s0, int s1, v4f (&D)[G],
+                                           int g0 = 0) {
+  const int grp = __lane_id() >> 4;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
+  for (int u = 0; u < S; ++u) {
+    const int s = s0 + u;
+    if (s >= s1) break;
+    const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
+    const uint32_t sa = grp < rs ? R.SA[u] >> (8 * g0) : 0u;  // byte g: group g0 + g; stand-in lanes scale 0
+    const uint32_t sb = R.SB[u];
+    const v8i b = {(int)R.B0[u].x, (int)R.B0[u].y, (int)R.B0[u].z, (int)R.B0[u].w,
+                   (int)R.B1[u].x, (int)R.B1[u].y, (int)R.B1[u].z, (int)R.B1[u].w};
+    const v8i a0 = {(int)R.A[u][0].x, (int)R.A[u][0].y, (int)R.A[u][0].z, (int)R.A[u][0].w, 0, 0, 0, 0};
+    D[0] = NSX_MFMA_SCALE(a0, b, D[0], 0, sa, sb);
+    if constexpr (G >= 2) {
+      const v8i a1 = {(int)R.A[u][1].x, (int)R.A[u][1].y, (int)R.A[u][1].z, (int)R.A[u][1].w, 0, 0, 0, 0};
+      D[1] = NSX_MFMA_SCALE(a1, b, D[1], 1, sa, sb);
+    }
+    if constexpr (G == 4) {
+      const v8i a2 = {(int)R.A[u][2].x, (int)R.A[u][2].y, (int)R.A[u][2].z, (int)R.A[u][2].w, 0, 0, 0, 0};
+      const v8i a3 = {(int)R.A[u][3].x, (int)R.A[u][3].y, (int)R.A[u][3].z, (int)R.A[u][3].w, 0, 0, 0, 0};
+      D[2] = NSX_MFMA_SCALE(a2, b, D[2], 2, sa, sb);
+      D[3] = NSX_MFMA_SCALE(a3, b, D[3], 3, sa, sb);
+    }
+  }
+}
+
+// A whole K range [s0, s1) in passes of S steps.
+template <int S, bool BLDS>
+__device__ __forceinline__ void mx_tile_mfma(const uint8_t* __restrict__ tile, const MxGeom& G, int s0, int s1,
+                                             const uint8_t* __restrict__ xq, int xs0, int64_t xq_stride, int ntok,
+                                             v4f (&D)[4]) {
+  for (int p0 = s0; p0 < s1; p0 += S) {
+    MxRegs<S> R;
+    mx_load_a<S>(R, tile, G, p0, s1);
+    mx_load_b<S, BLDS>(R, xq, xs0, xq_stride, ntok, p0, s1);
+    mx_compute<S>(R, G, p0, s1, D);
+  }
+}
+
+// Sum the XQ_NT term columns of D: afterwards lane l with (l & 3) == 0 holds,
+// for token (l & 15) / 4, rows 16 g + 4 (l / 16) + i (relative to the first
+// row group) in D[g][i].
+template <int G>
+__device__ __forceinline__ void mx_sum_terms(v4f (&D)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float v = D[g][i];
