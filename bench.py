@@ -45,7 +45,22 @@ def _parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="after the run, copy a buffer of this size 3 times (calibrates rocprofv3 byte counters)")
     return p.parse_args()
+
+
+def _traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size),
+    or None when no such measurement is committed."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get("kernels", {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("traffic_bytes")
 
 
 def _expert_bytes_per_token(cfg):
@@ -180,8 +195,8 @@ def main():
     toks = list(range(P0, P0 + R))
     wss = [layers[i % n_layers].new_workspace(T) for i in toks]
     graphs = []
-    with torch.cuda.stream(stream):
-        for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE):
+    with torch.cuda.stream(stream):  # PHASE_COMBINE launches nothing: the down kernels combine
+        for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
                 for j, i in enumerate(toks):
@@ -211,8 +226,9 @@ def main():
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "moe_gu_mfma_kernel" if args.layout == "t64" else "moe_gu_raw_kernel",
+                "kernel": "moe_gu_kernel" if args.layout == "t64" else "moe_gu_raw_kernel",
                 "bytes_per_launch": gu_bytes, "avg_us": round(gu_us, 3)}
+    roofline["traffic"] = _traffic(roofline["kernel"])
     layer_bytes = cfg.layer_bytes_per_token()
     result = {
         "metric": "MoE-FFN decode tok/s (GPT-OSS-120B shape, MXFP4)",
@@ -232,11 +248,19 @@ def main():
                    "experts": cfg.n_expert, "top_k": cfg.top_k, "graph": True},
         "layer_GBps": round(layer_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "kernel_us": {"router": round(phase_us[0], 3), "gate_up": round(phase_us[1], 3),
-                     "down": round(phase_us[2], 3), "combine": round(phase_us[3], 3)},
+                     "down_combine": round(phase_us[2], 3)},
         "down_GBps": round(dn_bytes / (phase_us[2] * 1e-6) / 1e9, 1),
         "wall_s": round(wall_s, 4),
         "roofline": roofline,
     }
+    if args.copy_probe_mib > 0:  # a plain copy of known size for the counter calibration
+        n = args.copy_probe_mib << 18
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu:
         result["cpu_baseline"] = _cpu_baseline(cfg, t_cpu, X[:32].cpu().numpy(), args.cpu_seconds)
     else:

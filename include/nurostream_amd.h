@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define NSX_ABI_VERSION 1
+#define NSX_ABI_VERSION 2
 
 /* status codes; the Python shim maps them onto the reference's exceptions */
 enum {
@@ -49,6 +49,10 @@ enum {
 /* routers and activations */
 enum { NSX_ROUTE_GPTOSS = 0, NSX_ROUTE_QWEN3 = 1 };
 enum { NSX_ACT_CLAMPED_SWIGLU = 0, NSX_ACT_SILU_MUL = 1 };
+/* How nsx_moe_forward runs the routed experts: per (token, expert) pair, or
+ * grouped (pairs sorted by expert; each active expert's weights read once per
+ * work item of up to 16 of its tokens; t64 layout). AUTO groups from T >= 8. */
+enum { NSX_DISPATCH_AUTO = 0, NSX_DISPATCH_PAIRS = 1, NSX_DISPATCH_GROUPED = 2 };
 
 const char *nsx_last_error(void);
 int nsx_abi_version(void);
@@ -114,7 +118,7 @@ typedef struct nsx_moe_layer {
   float limit;          /* clamped SwiGLU limit (7.0) */
   const void *router_w; /* (n_expert, n_embd) */
   int32_t router_dtype; /* NSX_F32 / NSX_BF16 / NSX_F16 */
-  int32_t reserved0;
+  int32_t dispatch;     /* NSX_DISPATCH_* */
   const float *router_bias;  /* (n_expert,) or NULL */
   /* Expert e of a projection lives at base + e * stride when base is not
    * NULL, else at ptrs[e] (a device array of n_expert device addresses). */
@@ -143,11 +147,14 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
                     float *out, int32_t *ids, float *weights, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
-/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, plus top-k for
- * the GGUF layout), NSX_PHASE_GATE_UP (expert gate/up GEMVs + activation;
- * in the t64 layout also the top-k and the ids/weights outputs),
- * NSX_PHASE_DOWN (expert down GEMVs; in the GGUF layout also the combine) and
- * NSX_PHASE_COMBINE. A phase reads what the earlier phases of the same call
+/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, plus top-k and the
+ * ids/weights outputs for the GGUF layout; in the t64 layout also the
+ * activation terms of h), NSX_PHASE_GATE_UP (expert gate/up GEMVs +
+ * activation; the t64 kernel selects the top-k itself), NSX_PHASE_DOWN
+ * (expert down GEMVs and the weighted combine into out; the t64 kernel also
+ * writes ids/weights) and NSX_PHASE_COMBINE (kept for callers that run the
+ * four phases; it launches nothing, as both layouts combine inside the down
+ * phase). A phase reads what the earlier phases of the same call
  * sequence left in the workspace; running the four in order is
  * nsx_moe_forward. Callers use it to interleave other work (block reads,
  * another layer's router) between phases or to time one phase; the

@@ -20,6 +20,7 @@ OK, EINVAL, ETYPE, ENOTIMPL, EHIP, EKERNEL = 0, 1, 2, 3, 4, 5
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 LAYOUT_GGUF, LAYOUT_T64 = 0, 1
 ROUTE_GPTOSS, ROUTE_QWEN3 = 0, 1
+DISPATCH_AUTO, DISPATCH_PAIRS, DISPATCH_GROUPED = 0, 1, 2
 ACT_CLAMPED_SWIGLU, ACT_SILU_MUL = 0, 1
 
 BLOCK_TYPES = frozenset({GGMLType.Q4_0, GGMLType.Q8_0, GGMLType.Q4_K, GGMLType.MXFP4})
@@ -37,7 +38,7 @@ class MoeLayerC(C.Structure):
         ("top_k", C.c_int32), ("n_embd", C.c_int32), ("n_ff", C.c_int32),
         ("router_mode", C.c_int32), ("act", C.c_int32), ("alpha", C.c_float),
         ("limit", C.c_float), ("router_w", _p), ("router_dtype", C.c_int32),
-        ("reserved0", C.c_int32), ("router_bias", _p), ("gate_ptrs", _p),
+        ("dispatch", C.c_int32), ("router_bias", _p), ("gate_ptrs", _p),
         ("up_ptrs", _p), ("down_ptrs", _p), ("gate_bias", _p), ("up_bias", _p),
         ("down_bias", _p), ("gate_base", _p), ("up_base", _p), ("down_base", _p),
         ("gate_stride", C.c_int64), ("up_stride", C.c_int64), ("down_stride", C.c_int64),
@@ -90,7 +91,7 @@ def load():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.nsx_abi_version() != 1:
+    if lib.nsx_abi_version() != 2:
         raise NativeError("libnsx.so ABI version mismatch")
     _lib = lib
     return lib

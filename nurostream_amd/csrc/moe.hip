@@ -380,6 +380,14 @@ struct MoeDev {
   int cd, sd;            // down K-chunks per expert and K-steps per chunk
   int act_kind;
   float alpha, limit;
+  // grouped dispatch (pairs sorted by expert)
+  int4* items;           // work items: (expert, first sorted position, tokens, 0)
+  int* n_items;
+  int32_t* sorted;       // pair ids, ascending expert, ascending pair id inside
+  int32_t* corder;       // per token: its pair ids in ascending expert id
+  float* y;              // (pairs, n_embd) expert outputs, bias included
+  int max_items;
+  int cdg, sdg;          // grouped down: K-chunks and K-steps per chunk
 };
 
 __device__ __forceinline__ float moe_act(int kind, float g, float u, float alpha, float limit) {
@@ -407,6 +415,14 @@ __device__ __forceinline__ void slot_order(const int (&ids)[MAX_TOPK], int k, in
     }
     order[j + 1] = oi;
   }
+}
+
+// The activation terms of K-blocks [2 * tiles, 4 * ns) -- the padding of the
+// down matrix's last K-step, past n_ff -- are zero; the workgroup of the last
+// gate/up tile writes them, so no call relies on what a workspace held before.
+__device__ __forceinline__ void xq_zero_tail(int tile, const MxGeom& ggu, const MxGeom& gdn, uint8_t* dst) {
+  if (tile != (int)ggu.tiles - 1) return;
+  for (int b0 = 2 * (int)ggu.tiles; b0 < 4 * gdn.ns; b0 += 2) xq_block(0.f, b0 + (__lane_id() >> 5), dst);
 }
 
 // out[rows] += w * y in the reference rounds the product and the sum separately
@@ -496,6 +512,7 @@ __global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
   }
   const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
   xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
+  xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
 }
 
 // phase 2 (down and combine): workgroup = (token, 16-row group of a 64-row
@@ -511,7 +528,12 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
   __shared__ __align__(16) uint8_t xs[16][DC_S * XQ_STEP];  // each wave's activation terms, staged
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int groups = 4 * (int)a.gdn.tiles;
-  const int t = blockIdx.x / groups, hh = blockIdx.x - t * groups;
+  // XCD-aware order: workgroup b runs on XCD b % 8, so item = (b % 8) * per + b / 8
+  // keeps the four row groups of a tile (which read the same scale lines) on one L2
+  const int per = (int)(gridDim.x >> 3);
+  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (item >= a.T * groups) return;  // padding workgroups of the 8-way split
+  const int t = item / groups, hh = item - t * groups;
   const int tile = hh >> 2, rg = hh & 3;
   const int k = a.top_k;
   const int j = wave / a.cd, c = wave - j * a.cd;
@@ -590,6 +612,247 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
     o = combine_one(o, w, y);
   }
   if (lane < 16 && row < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
+}
+
+// ---------------------------------------------------------------------------
+// grouped dispatch (several tokens): the (token, expert) pairs are sorted by
+// expert; a work item is up to GRP_TPI tokens of one expert, and a workgroup
+// is (item, 64-row tile), so an expert's tile is read once per item rather
+// than once per pair. Items of one tile sit on one XCD (consecutive items of
+// an expert share its L2). Each token's columns are computed exactly as the
+// per-pair kernels compute them (same K-chunks, same summation order), and
+// the combine adds the experts in ascending id: the outputs do not depend on
+// the dispatch.
+
+constexpr int GRP_TPI = 16;          // tokens per work item
+constexpr int GRP_MAX_PAIRS = 4096;  // pairs per sort (nsx_moe_forward splits larger T)
+constexpr int GRP_CHUNKS = GRP_MAX_PAIRS / 64;
+
+__host__ __device__ __forceinline__ int grp_max_items(int E, int P) {
+  return (E < P ? E : P) + (P + GRP_TPI - 1) / GRP_TPI;
+}
+
+// lanes of this wave whose (valid) expert equals this lane's
+__device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
+  uint64_t m = __builtin_amdgcn_ballot_w64(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(valid && bit);
+    m &= bit ? bal : ~bal;
+  }
+  return valid ? m : 0ull;
+}
+
+// One workgroup: top-k of every token (one wave per token), then a stable
+// counting sort of the pairs by expert (64-pair chunks, per-chunk counts,
+// prefix over chunks), the work items and the per-token combine order.
+__global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
+  __shared__ uint16_t s_run[GRP_CHUNKS][MAX_EXPERTS];  // chunk counts, then exclusive prefix over chunks
+  __shared__ int s_cnt[MAX_EXPERTS], s_off[MAX_EXPERTS];
+  __shared__ uint8_t s_exp[GRP_MAX_PAIRS];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = __lane_id();
+  const int T = a.T, k = a.top_k, E = a.E, P = T * k;
+  const int nch = (P + 63) / 64;
+  for (int i = tid; i < GRP_CHUNKS * MAX_EXPERTS; i += 1024) (&s_run[0][0])[i] = 0;
+  for (int t = wave; t < T; t += 16) {
+    int si[MAX_TOPK];
+    float sw[MAX_TOPK];
+    topk_regs(a.logits + (int64_t)t * E, E, k, a.mode, si, sw);
+    int my_e = 0, rank = 0;
+    float my_w = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      my_e = lane == jj ? si[jj] : my_e;
+      my_w = lane == jj ? sw[jj] : my_w;
+    }
+    my_e = clamp_expert(my_e, E);
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      const int ej = clamp_expert(si[jj], E);
+      rank += (jj < k && (ej < my_e || (ej == my_e && jj < lane))) ? 1 : 0;
+    }
+    if (lane < k) {
+      const int p = t * k + lane;
+      a.ids[p] = my_e;
+      a.wts[p] = my_w;
+      a.corder[t * k + rank] = p;
+      s_exp[p] = (uint8_t)my_e;
+    }
+  }
+  __syncthreads();
+  for (int c = wave; c < nch; c += 16) {  // per-chunk counts (one lane per expert present writes)
+    const int p = c * 64 + lane;
+    const int e = p < P ? s_exp[p] : 0;
+    const uint64_t m = grp_match(p < P, e);
+    if (p < P && (m & ((1ull << lane) - 1ull)) == 0ull) s_run[c][e] = (uint16_t)__popcll(m);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) {
+    int run = 0;
+    for (int c = 0; c < nch; ++c) {
+      const int v = s_run[c][e];
+      s_run[c][e] = (uint16_t)run;
+      run += v;
+    }
+    s_cnt[e] = run;
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scans over experts (4 per lane) of the pair and item counts
+    int cn[MAX_EXPERTS / 64], ni[MAX_EXPERTS / 64];
+    int sc = 0, sn = 0;
+#pragma unroll
+    for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
+      const int e = lane * (MAX_EXPERTS / 64) + i;
+      cn[i] = e < E ? s_cnt[e] : 0;
+      ni[i] = (cn[i] + GRP_TPI - 1) / GRP_TPI;
+      sc += cn[i];
+      sn += ni[i];
+    }
+    int isc = sc, isn = sn;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64);
+      if (lane >= d) {
+        isc += oc;
+        isn += on;
+      }
+    }
+    int bc = isc - sc, bn = isn - sn;
+#pragma unroll
+    for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
+      const int e = lane * (MAX_EXPERTS / 64) + i;
+      if (e < E) {
+        s_off[e] = bc;
+        for (int q = 0; q < ni[i]; ++q)
+          a.items[bn + q] = make_int4(e, bc + q * GRP_TPI, min(GRP_TPI, cn[i] - q * GRP_TPI), 0);
+      }
+      bc += cn[i];
+      bn += ni[i];
+    }
+    if (lane == 63) *a.n_items = isn;
+  }
+  __syncthreads();
+  for (int c = wave; c < nch; c += 16) {  // stable scatter
+    const int p = c * 64 + lane;
+    const int e = p < P ? s_exp[p] : 0;
+    const uint64_t m = grp_match(p < P, e);
+    if (p < P) a.sorted[s_off[e] + s_run[c][e] + __popcll(m & ((1ull << lane) - 1ull))] = p;
+  }
+}
+
+// Workgroup index -> (tile, item), tile-major, XCD-aware (workgroup b runs on XCD b % 8).
+__device__ __forceinline__ bool grp_work(const MoeDev& a, int tiles, int& tile, int4& item) {
+  const int per = (int)(gridDim.x >> 3);
+  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (L >= tiles * a.max_items) return false;
+  tile = L / a.max_items;
+  const int it = L - tile * a.max_items;
+  if (it >= *a.n_items) return false;
+  item = a.items[it];
+  return true;
+}
+
+// gate/up for one (item, tile): the waves are (gate|up, K-chunk) as in
+// moe_gu_kernel; each holds its weights in registers and runs the item's
+// tokens four at a time (16 MFMA columns = 4 tokens x 4 terms).
+__global__ __launch_bounds__(1024) void moe_gu_grouped_kernel(MoeDev a) {
+  __shared__ float red[2][MAX_CHUNKS][GRP_TPI][64];
+  int tile;
+  int4 item;
+  if (!grp_work(a, (int)a.ggu.tiles, tile, item)) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
+  const int m = wave / a.cg, c = wave - m * a.cg;
+  const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
+  const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
+                              : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
+  MxRegs<GU_S> R;
+  mx_load_a<GU_S>(R, mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1);
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
+  const int64_t xs = (int64_t)a.ggu.ns * XQ_STEP;
+  for (int tg = 0; tg * 4 < n; ++tg) {
+    const int tok = tg * 4 + ((lane & 15) >> 2);
+    const int pr = __shfl(my_pair, min(tok, n - 1), 64);
+    mx_load_b_at<GU_S, false>(R, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
+    v4f D[4] = {};
+    mx_compute<GU_S>(R, a.ggu, s0, s1, D);
+    mx_sum_terms(D);
+    if ((lane & 3) == 0 && tok < n) {
+      const int r0 = 4 * (lane >> 4);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(v4f*)(&red[m][c][tok][16 * g + r0]) = D[g];
+    }
+  }
+  __syncthreads();
+  const int nw = 2 * a.cg;
+  if (wave >= n) return;
+  const int row = tile * 64 + lane;
+  const int rowc = min(row, a.n_ff - 1);
+  const float gb = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
+  const float ub = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
+  for (int w = wave; w < n; w += nw) {  // token w of the item
+    float gs = 0.f, us = 0.f;
+    for (int cc = 0; cc < a.cg; ++cc) {
+      gs += red[0][cc][w][lane];
+      us += red[1][cc][w][lane];
+    }
+    const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
+    const int pr = __builtin_amdgcn_readlane(my_pair, w);
+    xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+    xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+  }
+}
+
+// down for one (item, tile): waves = (K-chunk, 16-row group) as in
+// moe_down_kernel; y[pair, rows] = the expert's down product plus its bias.
+__global__ __launch_bounds__(1024) void moe_down_grouped_kernel(MoeDev a) {
+  __shared__ float red[16][GRP_TPI][16];  // [wave = chunk * 4 + group][token][row of the group]
+  int tile;
+  int4 item;
+  if (!grp_work(a, (int)a.gdn.tiles, tile, item)) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
+  const int c = wave >> 2, rg = wave & 3;
+  const int s0 = c * a.sdg, s1 = min(a.gdn.ns, s0 + a.sdg);
+  MxRegs<DC_S, 1> R;
+  mx_load_a<DC_S, 1>(R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) + (int64_t)tile * a.gdn.tile_bytes,
+                     a.gdn, s0, s1, rg);
+  const int r0 = tile * 64 + 16 * rg + 4 * (lane >> 4);
+  v4f bias = {0.f, 0.f, 0.f, 0.f};  // chunk 0 carries the bias, as in moe_down_kernel
+  if (c == 0 && a.down_bias && r0 < a.n_embd) bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
+  const int64_t xs = (int64_t)a.gdn.ns * XQ_STEP;
+  for (int tg = 0; tg * 4 < n; ++tg) {
+    const int tok = tg * 4 + ((lane & 15) >> 2);
+    const int pr = __shfl(my_pair, min(tok, n - 1), 64);
+    mx_load_b_at<DC_S, false, 1>(R, a.xq_a + (int64_t)pr * xs, 0, s0, s1);
+    v4f D[1] = {};
+    mx_compute<DC_S, 1>(R, a.gdn, s0, s1, D, rg);
+    mx_sum_terms<1>(D);
+    if ((lane & 3) == 0 && tok < n) *(v4f*)(&red[wave][tok][4 * (lane >> 4)]) = D[0] + bias;
+  }
+  __syncthreads();
+  const int nw = 4 * a.cdg;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int row = tile * 64 + lane;
+  for (int w = wave; w < n; w += nw) {  // token w of the item
+    float y = 0.f;
+    for (int cc = 0; cc < a.cdg; ++cc) y += red[cc * 4 + g][w][r16];
+    const int pr = __builtin_amdgcn_readlane(my_pair, w);
+    if (row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y;
+  }
+}
+
+// out[t, row] = sum over t's pairs in ascending expert id of w * y (grid: rows/256 x T)
+__global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
+  const int t = blockIdx.y, row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= a.n_embd) return;
+  float o = 0.f;
+  for (int jj = 0; jj < a.top_k; ++jj) {
+    const int p = a.corder[t * a.top_k + jj];
+    o = combine_one(o, a.wts[p], a.y[(int64_t)p * a.n_embd + row]);
+  }
+  a.out[(int64_t)t * a.n_embd + row] = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -689,12 +952,27 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 
 struct MoePlan {
   int64_t off_logits, off_act, off_xqh, off_xqa, total;
+  int64_t off_items, off_nitems, off_sorted, off_corder, off_y;
   MxGeom ggu, gdn;
   int cg, cd, sd;
+  bool grouped;
+  int max_items, cdg, sdg;
 };
+
+constexpr int GRP_AUTO_MIN_T = 8;  // NSX_DISPATCH_AUTO groups from this many tokens
+
+static bool use_grouped(const nsx_moe_layer* L, int64_t T) {
+  if (L->dispatch == NSX_DISPATCH_GROUPED) return true;
+  return L->dispatch == NSX_DISPATCH_AUTO && L->layout == NSX_LAYOUT_T64 && T >= GRP_AUTO_MIN_T;
+}
+
+// tokens per grouped pass (the sort handles GRP_MAX_PAIRS pairs)
+static int64_t grp_chunk_tokens(const nsx_moe_layer* L) { return GRP_MAX_PAIRS / std::max(1, (int)L->top_k); }
 
 static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   MoePlan p{};
+  p.grouped = use_grouped(L, T);
+  if (p.grouped) T = std::min(T, grp_chunk_tokens(L));
   const int64_t P = T * L->top_k;
   const bool t64 = L->layout == NSX_LAYOUT_T64;
   p.ggu = mx_geom(L->n_ff, L->n_embd);
@@ -703,6 +981,9 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   const int kk = std::max(1, std::min(L->top_k, 16));
   p.cd = std::max(1, std::min(p.gdn.ns, 16 / kk));  // top_k * cd waves per down workgroup
   p.sd = (int)nsx_cdiv(p.gdn.ns, p.cd);
+  p.cdg = std::max(1, std::min(p.gdn.ns, 4));  // grouped down: 4 row groups x cdg chunks
+  p.sdg = (int)nsx_cdiv(p.gdn.ns, p.cdg);
+  p.max_items = p.grouped ? grp_max_items(L->n_expert, (int)P) : 0;
   auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
   int64_t o = 0;
   p.off_logits = o;
@@ -713,6 +994,16 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP : 0));
   p.off_xqa = o;
   o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : 0));
+  p.off_items = o;
+  o = al(o + (int64_t)p.max_items * 16);
+  p.off_nitems = o;
+  o = al(o + (p.grouped ? 4 : 0));
+  p.off_sorted = o;
+  o = al(o + (p.grouped ? P * 4 : 0));
+  p.off_corder = o;
+  o = al(o + (p.grouped ? P * 4 : 0));
+  p.off_y = o;
+  o = al(o + (p.grouped ? P * L->n_embd * 4 : 0));
   p.total = o;
   return p;
 }
@@ -749,10 +1040,18 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
   } else {
     const MoePlan pl = moe_plan(L, T);
     NSX_REQUIRE(pl.cg <= MAX_CHUNKS, NSX_EINVAL, "t64 layers take n_embd <= %d", MAX_CHUNKS * GU_S * 128);
-    NSX_REQUIRE(pl.sd <= DC_S, NSX_EINVAL, "t64 layers take n_ff <= %d at top_k=%d",
-                DC_S * (16 / std::max(1, L->top_k)) * 128, L->top_k);
-
+    if (pl.grouped) {
+      NSX_REQUIRE(pl.sdg <= DC_S, NSX_EINVAL, "grouped t64 layers take n_ff <= %d", DC_S * 4 * 128);
+    } else {
+      NSX_REQUIRE(pl.sd <= DC_S, NSX_EINVAL, "t64 layers take n_ff <= %d at top_k=%d",
+                  DC_S * (16 / std::max(1, L->top_k)) * 128, L->top_k);
+    }
   }
+  NSX_REQUIRE(L->dispatch == NSX_DISPATCH_AUTO || L->dispatch == NSX_DISPATCH_PAIRS ||
+                  L->dispatch == NSX_DISPATCH_GROUPED,
+              NSX_EINVAL, "dispatch %d", L->dispatch);
+  NSX_REQUIRE(!use_grouped(L, T) || L->layout == NSX_LAYOUT_T64, NSX_ENOTIMPL,
+              "grouped dispatch is implemented for the t64 layout");
   return NSX_OK;
 }
 
@@ -825,6 +1124,14 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.act_kind = L->act;
   d.alpha = L->alpha;
   d.limit = L->limit;
+  d.items = (int4*)(ws + p.off_items);
+  d.n_items = (int*)(ws + p.off_nitems);
+  d.sorted = (int32_t*)(ws + p.off_sorted);
+  d.corder = (int32_t*)(ws + p.off_corder);
+  d.y = (float*)(ws + p.off_y);
+  d.max_items = p.max_items;
+  d.cdg = p.cdg;
+  d.sdg = p.sdg;
 
   auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
   if (on(NSX_PHASE_ROUTER)) {
@@ -835,13 +1142,31 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   }
   const int64_t P = T * L->top_k;
 
+  if (p.grouped) {
+    const int64_t items = (int64_t)p.max_items;
+    if (on(NSX_PHASE_GATE_UP)) {
+      if ((rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
+      if ((rc = nsx_launch(moe_gu_grouped_kernel, dim3((unsigned)(8 * nsx_cdiv(items * p.ggu.tiles, 8))),
+                           dim3(128 * p.cg), 0, st, d)))
+        return rc;
+    }
+    if (on(NSX_PHASE_DOWN) &&
+        (rc = nsx_launch(moe_down_grouped_kernel, dim3((unsigned)(8 * nsx_cdiv(items * p.gdn.tiles, 8))),
+                         dim3(256 * p.cdg), 0, st, d)))
+      return rc;
+    if (on(NSX_PHASE_COMBINE) &&
+        (rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
+                         d)))
+      return rc;
+    return NSX_OK;
+  }
   if (t64) {
     if (on(NSX_PHASE_GATE_UP) &&
         (rc = nsx_launch(moe_gu_kernel, dim3((unsigned)(P * p.ggu.tiles)), dim3(128 * p.cg), 0, st, d)))
       return rc;
     if (on(NSX_PHASE_DOWN) &&
-        (rc = nsx_launch(moe_down_kernel, dim3((unsigned)(T * 4 * p.gdn.tiles)), dim3(64 * L->top_k * p.cd), 0, st,
-                         d)))
+        (rc = nsx_launch(moe_down_kernel, dim3((unsigned)(8 * nsx_cdiv(T * 4 * p.gdn.tiles, 8))),
+                         dim3(64 * L->top_k * p.cd), 0, st, d)))
       return rc;
     return NSX_OK;  // the down kernel also combines
   }
@@ -856,12 +1181,25 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
 
 extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
                                float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
-  return moe_run(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, NSX_PHASE_ROUTER,
-                 NSX_PHASE_COMBINE);
+  int rc = check_layer(L, T);
+  if (rc) return rc;
+  const int64_t tc = use_grouped(L, T) ? grp_chunk_tokens(L) : T;
+  for (int64_t t0 = 0; t0 < T; t0 += tc) {  // grouped passes of at most GRP_MAX_PAIRS pairs, in token order
+    const int64_t n = std::min(tc, T - t0);
+    const int64_t k = L->top_k;
+    if (h == nullptr || out == nullptr || ids == nullptr || weights == nullptr)
+      return nsx_fail(NSX_EINVAL, "null buffer");
+    rc = moe_run(L, h + t0 * L->n_embd, n, out + t0 * L->n_embd, ids + t0 * k, weights + t0 * k, workspace,
+                 workspace_bytes, stream, NSX_PHASE_ROUTER, NSX_PHASE_COMBINE);
+    if (rc) return rc;
+  }
+  return NSX_OK;
 }
 
 extern "C" int nsx_moe_phase(const nsx_moe_layer* L, int phase, const float* h, int64_t T, float* out, int32_t* ids,
                              float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
   NSX_REQUIRE(phase >= NSX_PHASE_ROUTER && phase <= NSX_PHASE_COMBINE, NSX_EINVAL, "phase %d", phase);
+  NSX_REQUIRE(L == nullptr || !use_grouped(L, T) || T <= grp_chunk_tokens(L), NSX_EINVAL,
+              "grouped phases take at most %d pairs (T=%lld)", GRP_MAX_PAIRS, (long long)T);
   return moe_run(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, phase, phase);
 }

@@ -168,23 +168,20 @@ __device__ __forceinline__ void mx_load_a(MxRegs<S, G>& R, const uint8_t* __rest
   }
 }
 
-// Activation operands of the same steps: column c = token * XQ_NT + term for
-// tokens < ntok; xq points at step xs0 of token 0 (in LDS when BLDS), tokens
-// xq_stride bytes apart; columns of tokens >= ntok repeat token ntok - 1 and
-// are not read back.
+// Activation operands of the same steps for this lane's column, whose token's
+// terms start at xtok (step xs0 of that token; in LDS when BLDS): column
+// c = lane % 16 is term c % XQ_NT of the lane's token.
 template <int S, bool BLDS, int G = 4>
-__device__ __forceinline__ void mx_load_b(MxRegs<S, G>& R, const uint8_t* __restrict__ xq, int xs0, int64_t xq_stride,
-                                          int ntok, int s0, int s1) {
+__device__ __forceinline__ void mx_load_b_at(MxRegs<S, G>& R, const uint8_t* __restrict__ xtok, int xs0, int s0,
+                                             int s1) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
   typedef const __attribute__((address_space(1))) uint32_t gu32;
   typedef const __attribute__((address_space(3))) v4u lv4u;
   typedef const __attribute__((address_space(3))) uint32_t lu32;
   const int lane = __lane_id();
-  const int c = lane & 15, grp = lane >> 4;
-  const int tok0 = c / XQ_NT, term = c - tok0 * XQ_NT;
-  const int tok = tok0 < ntok ? tok0 : ntok - 1;
-  const uint8_t* xt = xq + (int64_t)tok * xq_stride + (grp * XQ_NT + term) * 32;
-  const uint8_t* xst = xq + (int64_t)tok * xq_stride + XQ_CODES + (grp * XQ_NT + term) * 4;
+  const int grp = lane >> 4, term = lane & (XQ_NT - 1);
+  const uint8_t* xt = xtok + (grp * XQ_NT + term) * 32;
+  const uint8_t* xst = xtok + XQ_CODES + (grp * XQ_NT + term) * 4;
 #pragma unroll
   for (int u = 0; u < S; ++u) {
     const int s = s0 + u;
@@ -203,8 +200,16 @@ __device__ __forceinline__ void mx_load_b(MxRegs<S, G>& R, const uint8_t* __rest
   }
 }
 
-#define NSX_MFMA_SCALE(A, B, C, G, SA, SB) \
-  __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 4, 0, (G), (SA), 0, (SB))
+// The same for tokens laid out xq_stride bytes apart from xq (token 0):
+// column c = token * XQ_NT + term for tokens < ntok; columns of tokens >=
+// ntok repeat token ntok - 1 and are not read back.
+template <int S, bool BLDS, int G = 4>
+__device__ __forceinline__ void mx_load_b(MxRegs<S, G>& R, const uint8_t* __restrict__ xq, int xs0, int64_t xq_stride,
+                                          int ntok, int s0, int s1) {
+  const int tok0 = (__lane_id() & 15) / XQ_NT;
+  const int tok = tok0 < ntok ? tok0 : ntok - 1;
+  mx_load_b_at<S, BLDS, G>(R, xq + (int64_t)tok * xq_stride, xs0, s0, s1);
+}
 
 // D[g] (rows 16 (g0 + g) .. + 15 of the tile, 16 columns) += the loaded steps
 // (the same G_, s0, s1, g0 as mx_load_a).

@@ -24,6 +24,9 @@ _W_CODE = {torch.float32: int(GGMLType.F32), torch.bfloat16: int(GGMLType.BF16),
            torch.float16: int(GGMLType.F16)}
 
 
+_DISPATCH = {"auto": 0, "pairs": 1, "grouped": 2}  # NSX_DISPATCH_*
+
+
 def _addr_table(ptrs, device) -> torch.Tensor:
     return torch.tensor([int(p) for p in ptrs], dtype=torch.int64, device=device)
 
@@ -33,10 +36,15 @@ class MoELayer:
                  router_w: torch.Tensor, router_b: torch.Tensor | None,
                  gate, up, down, gate_b=None, up_b=None, down_b=None,
                  layout: str = "gguf", router_mode: str = "gptoss", act: str = "clamped_swiglu",
-                 alpha: float = 1.702, limit: float = 7.0) -> None:
+                 alpha: float = 1.702, limit: float = 7.0, dispatch: str = "auto") -> None:
         """gate/up/down: either one stacked uint8 device tensor per projection
         (expert e at offset e * bytes_per_expert) or a list of n_expert device
-        tensors (one slab each)."""
+        tensors (one slab each). dispatch: "pairs" runs each (token, expert)
+        pair on its own, "grouped" sorts the pairs by expert and reads each
+        active expert once per work item of up to 16 tokens (t64 layout),
+        "auto" groups from 8 tokens on (t64). Both give identical outputs."""
+        if dispatch not in _DISPATCH:
+            raise ValueError(f"dispatch {dispatch!r} not in {sorted(_DISPATCH)}")
         self.device = router_w.device
         N.require_device(router_w)
         self.ggml_type = GGMLType(ggml_type)
@@ -77,6 +85,8 @@ class MoELayer:
         L.router_mode = N.ROUTE_GPTOSS if router_mode == "gptoss" else N.ROUTE_QWEN3
         L.act = N.ACT_CLAMPED_SWIGLU if act == "clamped_swiglu" else N.ACT_SILU_MUL
         L.alpha, L.limit = alpha, limit
+        L.dispatch = _DISPATCH[dispatch]
+        self.dispatch = dispatch
         ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         L.router_w = self.router_w.data_ptr()
         L.router_dtype = _W_CODE[self.router_w.dtype]

@@ -14,6 +14,8 @@ Distribution choices not fixed by the configuration text:
 """
 from __future__ import annotations
 
+import math
+
 from dataclasses import dataclass
 
 import torch
@@ -126,3 +128,21 @@ def zipf_router_bias(n_expert: int, s: float = 1.1, c: float = 1.0, seed: int = 
     p = ranks ** (-s)
     p = p / p.sum()
     return (c * torch.log(p)).float()
+
+
+def zipf_scale(router_w: torch.Tensor) -> float:
+    """c for zipf_router_bias: with h ~ N(0, I) a logit is N(0, |w_e|^2); a
+    Gumbel of the same spread has scale sigma * sqrt(6) / pi, and a bias of
+    scale * log(p_e) under Gumbel noise selects expert e with probability p_e
+    (Plackett-Luce). sigma = the mean row norm of the router."""
+    sigma = router_w.float().norm(dim=1).mean().item()
+    return sigma * math.sqrt(6.0) / math.pi
+
+
+def make_zipf_layer(cfg: MoEConfig, seed: int, device, s: float = 1.1, layer: int = 0):
+    """make_layer with the router bias replaced by zipf_router_bias (BASELINE
+    config 3: expert popularity ~ Zipf(s)); returns (tensors, c)."""
+    t = make_layer(cfg, seed, device, layer)
+    c = zipf_scale(t["router_w"])
+    t["router_b"] = zipf_router_bias(cfg.n_expert, s=s, c=c, seed=layer_seed(seed, layer)).to(device)
+    return t, c

@@ -39,7 +39,7 @@ def test_exported_symbols_are_the_header_set(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.nsx_abi_version() == 1
+    assert lib.nsx_abi_version() == 2
     assert isinstance(lib.nsx_last_error(), bytes)
 
 
@@ -73,6 +73,22 @@ def test_workspace_bytes(lib):
     assert 0 < w1 < w8 < 64 << 20
     L.top_k = 0
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 1) < 0
+
+
+def test_workspace_bytes_by_dispatch(lib):
+    """Grouped passes hold at most 4096 pairs: the workspace stops growing there."""
+    L = _gptoss_layer()
+    L.dispatch = N.DISPATCH_GROUPED
+    w8, w1024, w4096 = (lib.nsx_moe_workspace_bytes(C.byref(L), T) for T in (8, 1024, 4096))
+    assert 0 < w8 < w1024 == w4096
+    L.dispatch = N.DISPATCH_PAIRS
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < w8  # no sort buffers or per-pair outputs
+    L.dispatch = 9
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
+    L.dispatch = N.DISPATCH_GROUPED  # grouped needs the t64 layout
+    L.layout = N.LAYOUT_GGUF
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
+    assert b"grouped" in lib.nsx_last_error()
 
 
 def test_validation_errors_return_codes(lib):

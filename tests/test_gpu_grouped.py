@@ -1,0 +1,111 @@
+"""Grouped dispatch (pairs sorted by expert, one read of an expert's tile per
+work item of up to 16 tokens): identical outputs to the per-pair kernels and
+parity with the oracle, including BASELINE config 3 (T=128, Zipf(1.1))."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import FFN_BAR, MFMA_TOL, rel_max, to_np
+from moe_cases import _expert_set, _layer, _oracle_layer, _small
+from oracle import moe as OM
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair_and_grouped(cfg, t):
+    return _layer(cfg, t, "t64", dispatch="pairs"), _layer(cfg, t, "t64", dispatch="grouped")
+
+
+@pytest.mark.parametrize("T", [1, 3, 8, 17, 64, 200])
+def test_grouped_equals_pairs_bitwise(dev, T):
+    """Same K-chunks and summation order per token: the dispatch does not change a bit."""
+    from nurostream_amd import synth
+    cfg = _small("gptoss-small")
+    t = synth.make_layer(cfg, seed=11, device=dev)
+    lp, lg = _pair_and_grouped(cfg, t)
+    h = synth.activations(T, cfg.n_embd, seed=100 + T, device=dev)
+    op, ip, wp = lp(h)
+    og, ig, wg = lg(h)
+    assert torch.equal(ip, ig) and torch.equal(wp, wg)
+    assert torch.equal(op, og)
+
+
+def test_grouped_one_hot_expert(dev):
+    """Every token routed to the same experts (a bias that dominates the logits):
+    one expert holds all pairs, several items per expert."""
+    from nurostream_amd import synth
+    cfg = _small("gptoss-small")
+    t = synth.make_layer(cfg, seed=12, device=dev)
+    b = torch.full((cfg.n_expert,), -50.0, device=dev)
+    b[[3, 7, 8, 12]] = 50.0
+    t["router_b"] = b
+    lp, lg = _pair_and_grouped(cfg, t)
+    h = synth.activations(40, cfg.n_embd, seed=7, device=dev)
+    op, ip, _ = lp(h)
+    og, ig, _ = lg(h)
+    assert torch.equal(ip, ig) and torch.equal(op, og)
+    assert set(np.unique(to_np(ig)).tolist()) == {3, 7, 8, 12}
+    ref, rid, _, _ = _oracle_layer(cfg, t, h.cpu().numpy())
+    assert rel_max(to_np(og), ref) < MFMA_TOL
+
+
+def test_grouped_splits_large_batches(dev):
+    """More than 4096 pairs: forward runs grouped passes in token order."""
+    from nurostream_amd import synth
+    cfg = _small("gptoss-small")
+    t = synth.make_layer(cfg, seed=13, device=dev)
+    lp, lg = _pair_and_grouped(cfg, t)
+    T = 4096 // cfg.top_k + 77
+    h = synth.activations(T, cfg.n_embd, seed=3, device=dev)
+    op, ip, _ = lp(h)
+    og, ig, _ = lg(h)
+    assert torch.equal(ip, ig) and torch.equal(op, og)
+    ref, rid, _, _ = _oracle_layer(cfg, t, h[-40:].cpu().numpy())
+    assert rel_max(to_np(og[-40:]), ref) < MFMA_TOL
+
+
+def test_grouped_phases_match_forward(dev):
+    from nurostream_amd import _native as N
+    from nurostream_amd import synth
+    cfg = _small("gptoss-small")
+    t = synth.make_layer(cfg, seed=14, device=dev)
+    lg = _layer(cfg, t, "t64", dispatch="grouped")
+    T = 33
+    h = synth.activations(T, cfg.n_embd, seed=4, device=dev)
+    out, ids, w = lg(h)
+    o2 = torch.empty_like(out)
+    i2 = torch.empty_like(ids)
+    w2 = torch.empty_like(w)
+    ws = lg.new_workspace(T)
+    for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE):
+        lg.phase(ph, h, o2, i2, w2, ws)
+    assert torch.equal(out, o2) and torch.equal(ids, i2) and torch.equal(w, w2)
+
+
+def test_config3_gptoss_t128_zipf(dev):
+    """the GPT-OSS-120B-shaped MXFP4 layer at T=128 with
+    router logits skewed to Zipf(1.1) expert popularity. Grouped == per-pair
+    bit for bit on all 128 tokens; the oracle checks 6 of them."""
+    from nurostream_amd import synth
+    cfg = synth.GPTOSS_120B
+    t, c = synth.make_zipf_layer(cfg, seed=0, device=dev)
+    lp, lg = _pair_and_grouped(cfg, t)
+    h = synth.activations(128, cfg.n_embd, seed=5, device=dev)
+    og, ig, wg = lg(h)
+    op, ip, wp = lp(h)
+    assert torch.equal(ig, ip) and torch.equal(og, op)
+    ids = to_np(ig)
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_expert)
+    distinct = int((counts > 0).sum())
+    assert 40 < distinct < 128, distinct  # skewed, not uniform (uniform: ~126 of 128)
+    del lp, op, ip, wp
+    torch.cuda.empty_cache()
+    sub = slice(0, 6)
+    ex = _expert_set(cfg, t)
+    ref, rid, rw, _ = _oracle_layer(cfg, t, h[sub].cpu().numpy(), ex=ex)
+    np.testing.assert_array_equal(ids[sub], rid)
+    np.testing.assert_allclose(to_np(wg)[sub], rw, rtol=1e-5)
+    err = rel_max(to_np(og)[sub], ref)
+    assert err < FFN_BAR and err < MFMA_TOL, err
