@@ -1,27 +1,37 @@
 #!/usr/bin/env python3
-"""Decode throughput of one GPT-OSS-120B-shaped MXFP4 MoE layer on one MI355X.
+"""MoE expert-path throughput on one MI355X (default: GPT-OSS-120B decode).
 
-Workload: BASELINE config 2 -- hidden 2880, 128 experts, top-4 (softmax over
-the selected), gate/up/down [128, 2880, 2880] MXFP4, clamped SwiGLU, batch 1.
-A step is one token through router -> top-k -> 4 experts' gate/up/down
-dequant-GEMVs -> weighted combine (nsx_moe_forward), on seeded synthetic
-weights and activations already resident in HBM.
+Default workload (the driver's line): one GPT-OSS-120B-shaped MXFP4 MoE layer
+at decode batch 1 -- hidden 2880, 128 experts, top-4 (softmax over the
+selected), gate/up/down [128, 2880, 2880] MXFP4, clamped SwiGLU. A step is
+one token through router -> top-k -> 4 experts' gate/up/down dequant-GEMVs ->
+weighted combine (nsx_moe_forward), on seeded synthetic weights and
+activations already resident in HBM.
 
 Weights of `--layers` independently seeded layers (1.7 GB of experts each)
-rotate step by step and every step has its own token, so the expert bytes of
+rotate step by step and every step has its own tokens, so the expert bytes of
 a step come from HBM rather than the 256 MB Infinity Cache. The K timed steps
 run as one HIP graph (launch overhead as in a serving loop). Per-kernel
-durations: `--profile-steps` further tokens, each with its own workspace, go
+durations: `--profile-steps` further steps, each with its own workspace, go
 through the layer phase by phase (nsx_moe_phase); each phase is one HIP graph
-of that kernel launched back to back over all those tokens, timed with HIP
+of that phase launched back to back over all those steps, timed with HIP
 events around its replay (an event pair around a single eager launch adds
 several microseconds of marker latency). The phase outputs must equal the
 full forward's.
 
+Other workloads (`--workload`, one JSON line each, for the design notes):
+  gptoss-t128   BASELINE config 3: T=128 tokens per step, Zipf(1.1) expert
+                popularity, grouped dispatch (sort by expert, grouped MFMA)
+  qwen3-t1      BASELINE config 4: Qwen3-235B-shaped Q4_K layer (GGUF rows), T=1
+  qwen3-t32     the same at T=32
+  stack-t1      BASELINE config 5: 36 GPT-OSS layers resident (61 GB),
+                x <- x + moe_l(rms_norm(x)) per layer, T=1
+  stack-t8      the same at T=8
+
 Prints one JSON line (the driver's contract) with a `roofline` object for the
 dominant kernel (the gate/up dequant-GEMV) and a `cpu_baseline` object: the
 numpy restatement of the reference path (oracle/) on host cores, over a
-bounded sample of the same workload.
+bounded sample of the same workload (default workload only).
 """
 from __future__ import annotations
 
@@ -32,16 +42,29 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8")
+
+# per workload: (config name, T, steps, warmup, rotating layers or stack depth, profile steps)
+_DEFAULTS = {
+    "gptoss-decode": ("GPTOSS_120B", 1, 400, 40, 6, 96),
+    "gptoss-t128": ("GPTOSS_120B", 128, 40, 5, 4, 8),
+    "qwen3-t1": ("QWEN3_235B", 1, 300, 30, 4, 64),
+    "qwen3-t32": ("QWEN3_235B", 32, 60, 6, 4, 8),
+    "stack-t1": ("GPTOSS_120B", 1, 40, 4, 36, 0),
+    "stack-t8": ("GPTOSS_120B", 8, 20, 2, 36, 0),
+}
 
 
 def _parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=400)
-    p.add_argument("--warmup", type=int, default=40)
-    p.add_argument("--layers", type=int, default=6, help="rotating weight copies (1.7 GB each)")
+    p.add_argument("--workload", choices=WORKLOADS, default="gptoss-decode")
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default per workload)")
+    p.add_argument("--warmup", type=int, default=None, help="untimed steps (default per workload)")
+    p.add_argument("--layers", type=int, default=None, help="rotating weight copies, or the stack depth")
     p.add_argument("--layout", choices=["t64", "gguf"], default="t64")
-    p.add_argument("--profile-steps", type=int, default=96, help="tokens timed per phase graph")
+    p.add_argument("--dispatch", choices=["auto", "pairs", "grouped"], default="auto")
+    p.add_argument("--profile-steps", type=int, default=None, help="steps timed per phase graph")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--seed", type=int, default=0)
@@ -63,18 +86,9 @@ def _traffic(kernel):
     return None if rec is None else rec.get("traffic_bytes")
 
 
-def _expert_bytes_per_token(cfg):
-    """Algorithmic bytes of the expert GEMVs of one token (k experts): the
-    quantized gate/up/down rows read once plus their fp32 biases."""
-    gu = cfg.top_k * (cfg.expert_bytes("gate") + cfg.expert_bytes("up") + 2 * cfg.n_ff * 4)
-    dn = cfg.top_k * (cfg.expert_bytes("down") + cfg.n_embd * 4)
-    return gu, dn
-
-
 def _cpu_baseline(cfg, t_cpu, X, budget_s, block_rows=512):
     """oracle.moe_gptoss (numpy restatement of model/gpt_oss.py:123-177 with
     compute/blockffn.py:146-231 block streaming) on host cores."""
-    import numpy as np
     from oracle import moe as OM
     try:
         from threadpoolctl import threadpool_limits
@@ -106,6 +120,248 @@ def _cpu_baseline(cfg, t_cpu, X, budget_s, block_rows=512):
                       f"GEMV on BLAS with {ncores} threads; block_rows {block_rows}) in {dt:.1f} s"}
 
 
+def _build_layer(torch, synth, cfg, li, args, dev, zipf, keep_cpu):
+    from nurostream_amd.compute.kernels import t64_pack_stacked
+    from nurostream_amd.moe.fused import MoELayer
+    if zipf:
+        t, c = synth.make_zipf_layer(cfg, seed=args.seed, device=dev, layer=li)
+    else:
+        t, c = synth.make_layer(cfg, seed=args.seed, device=dev, layer=li), None
+    t_cpu = None
+    if keep_cpu:
+        t_cpu = {k: (None if v is None else v.float().cpu().numpy() if v.dtype != torch.uint8
+                     else v.cpu().numpy()) for k, v in t.items()}
+    layout = args.layout if cfg.ggml_type == synth.GGMLType.MXFP4 else "gguf"
+    if layout == "t64":
+        mats = {k: t64_pack_stacked(t[k], cfg.ggml_type, cfg.n_expert, *cfg.rows_K(k)) for k in ("gate", "up", "down")}
+    else:
+        mats = {k: t[k] for k in ("gate", "up", "down")}
+    layer = MoELayer(ggml_type=cfg.ggml_type, n_expert=cfg.n_expert, top_k=cfg.top_k, n_embd=cfg.n_embd,
+                     n_ff=cfg.n_ff, router_w=t["router_w"], router_b=t["router_b"], gate=mats["gate"],
+                     up=mats["up"], down=mats["down"], gate_b=t["gate_b"], up_b=t["up_b"], down_b=t["down_b"],
+                     layout=layout, router_mode=cfg.router_mode, act=cfg.act, dispatch=args.dispatch)
+    return layer, t_cpu, c, layout
+
+
+def _graph_time(torch, run_steps, W, K):
+    """Eager warm-up steps 0..W-1, then steps W..W+K-1 captured as one graph
+    and replayed once under HIP events: (ms total, wall seconds, stream)."""
+    run_steps(range(W))
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            run_steps(range(W, W + K))
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    ev0.record()
+    graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1), time.perf_counter() - t_wall, stream
+
+
+def _expert_bytes(cfg, n_experts):
+    """Algorithmic bytes of the gate/up and of the down products of n_experts
+    distinct experts: quantized rows read once plus fp32 bias rows."""
+    b = 4 if cfg.bias else 0
+    gu = n_experts * (cfg.expert_bytes("gate") + cfg.expert_bytes("up") + 2 * cfg.n_ff * b)
+    dn = n_experts * (cfg.expert_bytes("down") + cfg.n_embd * b)
+    return gu, dn
+
+
+_METRIC = {"gptoss-decode": "MoE-FFN decode tok/s (GPT-OSS-120B shape, MXFP4)",
+           "gptoss-t128": "MoE-FFN prefill-chunk tok/s (GPT-OSS-120B shape, MXFP4, T=128, Zipf 1.1)",
+           "qwen3-t1": "MoE-FFN decode tok/s (Qwen3-235B-A22B shape, Q4_K)",
+           "qwen3-t32": "MoE-FFN batch-32 tok/s (Qwen3-235B-A22B shape, Q4_K)"}
+_WORKLOAD = {"gptoss-decode": "gpt-oss-120b MoE layer, decode batch 1 (BASELINE config 2)",
+             "gptoss-t128": "gpt-oss-120b MoE layer, T=128, Zipf(1.1) routing (BASELINE config 3)",
+             "qwen3-t1": "qwen3-235b-a22b MoE layer, decode batch 1 (BASELINE config 4)",
+             "qwen3-t32": "qwen3-235b-a22b MoE layer, batch 32 (BASELINE config 4)"}
+
+
+def layer_workload(args, torch, N, synth, dev):
+    name = args.workload
+    cfg_name, T, K0, W0, L0, R0 = _DEFAULTS[name]
+    cfg = getattr(synth, cfg_name)
+    K = args.steps if args.steps is not None else K0
+    W = args.warmup if args.warmup is not None else W0
+    n_layers = max(1, args.layers if args.layers is not None else L0)
+    R = args.profile_steps if args.profile_steps is not None else R0
+    zipf = name == "gptoss-t128"
+    default = name == "gptoss-decode"
+
+    layers, t_cpu, zipf_c, layout = [], None, None, None
+    for li in range(n_layers):
+        keep = default and li == 0 and not args.no_cpu
+        lay, tc, c, layout = _build_layer(torch, synth, cfg, li, args, dev, zipf, keep)
+        layers.append(lay)
+        t_cpu = tc if tc is not None else t_cpu
+        zipf_c = c if c is not None else zipf_c
+        torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    n_steps = W + K + R
+    X = synth.activations(n_steps * T, cfg.n_embd, seed=args.seed + 1, device=dev).view(n_steps, T, cfg.n_embd)
+    outs = torch.empty((n_steps, T, cfg.n_embd), dtype=torch.float32, device=dev)
+    ids = torch.empty((n_steps, T, cfg.top_k), dtype=torch.int32, device=dev)
+    wts = torch.empty((n_steps, T, cfg.top_k), dtype=torch.float32, device=dev)
+    for lay in layers:
+        lay.workspace(T)
+
+    def run_steps(rng):
+        for i in rng:
+            layers[i % n_layers].forward(X[i], out=outs[i], ids=ids[i], weights=wts[i])
+
+    ms_total, wall_s, stream = _graph_time(torch, run_steps, W, K)
+    ms_per_step = ms_total / K
+    tok_s = K * T / (ms_total / 1e3)
+
+    # per-phase durations: R further steps, one workspace each
+    phases = (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE)
+    phase_us = {}
+    if R > 0:
+        P0 = W + K
+        steps = list(range(P0, P0 + R))
+        wss = [layers[i % n_layers].new_workspace(T) for i in steps]
+        graphs = []
+        with torch.cuda.stream(stream):
+            for ph in phases:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    for j, i in enumerate(steps):
+                        layers[i % n_layers].phase(ph, X[i], outs[i], ids[i], wts[i], wss[j])
+                graphs.append(g)
+        torch.cuda.synchronize()
+        for g in graphs:  # first replay: graph upload, untimed
+            g.replay()
+        torch.cuda.synchronize()
+        for ph, g in zip(phases, graphs):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            phase_us[ph] = e0.elapsed_time(e1) * 1e3 / R
+        ph_out = outs[P0:P0 + R].clone()
+        run_steps(steps)
+        torch.cuda.synchronize()
+        if not torch.equal(ph_out, outs[P0:P0 + R]):
+            raise RuntimeError("phase-by-phase outputs differ from nsx_moe_forward")
+
+    # distinct experts per step: the expert bytes a step must read at least once
+    ids_cpu = ids[W:W + K + R].cpu()
+    distinct = [len(torch.unique(ids_cpu[s])) for s in range(ids_cpu.shape[0])]
+    mean_distinct = sum(distinct) / len(distinct)
+    grouped = layout == "t64" and (args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 8))
+    gu_kernel = ("moe_gu_grouped_kernel" if grouped else "moe_gu_kernel") if layout == "t64" else "moe_gu_raw_kernel"
+    gu_bytes, dn_bytes = _expert_bytes(cfg, mean_distinct)
+    roofline = None
+    if R > 0:
+        gu_us = phase_us[N.PHASE_GATE_UP]
+        achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(gu_kernel) if default else None,
+                    "kernel": gu_kernel, "bytes_per_launch": int(gu_bytes), "avg_us": round(gu_us, 3)}
+        if grouped:
+            roofline["note"] = "gate_up phase = moe_sort_kernel + moe_gu_grouped_kernel"
+    step_bytes = sum(_expert_bytes(cfg, mean_distinct))
+    kernel_us = None
+    if R > 0:
+        kernel_us = {"router": round(phase_us[N.PHASE_ROUTER], 3), "gate_up": round(phase_us[N.PHASE_GATE_UP], 3),
+                     "down": round(phase_us[N.PHASE_DOWN], 3)}
+        if grouped:
+            kernel_us["combine"] = round(phase_us[N.PHASE_COMBINE], 3)
+    result = {
+        "metric": _METRIC[name],
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic (seeded {cfg.ggml_type.name} experts, x~N(0,1)); weights resident in HBM",
+        "config": {"workload": _WORKLOAD[name], "tokens_per_step": T, "layout": layout, "dispatch": args.dispatch,
+                   "rotating_layers": n_layers, "hidden": cfg.n_embd, "experts": cfg.n_expert, "top_k": cfg.top_k,
+                   "graph": True},
+        "distinct_experts_per_step": round(mean_distinct, 2),
+        "expert_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "kernel_us": kernel_us,
+        "wall_s": round(wall_s, 4),
+        "roofline": roofline,
+    }
+    if zipf:
+        counts = torch.bincount(ids_cpu.reshape(-1).long(), minlength=cfg.n_expert).tolist()
+        result["zipf"] = {"s": 1.1, "c": round(zipf_c, 5), "top8_counts": sorted(counts, reverse=True)[:8],
+                          "experts_never_chosen": sum(1 for c in counts if c == 0)}
+    if default and not args.no_cpu:
+        result["cpu_baseline"] = _cpu_baseline(cfg, t_cpu, X[:32, 0].cpu().numpy(), args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
+def stack_workload(args, torch, N, synth, dev):
+    """36 resident layers chained x <- x + moe_l(rms_norm(x))."""
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack
+    name = args.workload
+    cfg_name, T, K0, W0, L0, _ = _DEFAULTS[name]
+    cfg = getattr(synth, cfg_name)
+    K = args.steps if args.steps is not None else K0
+    W = args.warmup if args.warmup is not None else W0
+    n_layers = args.layers if args.layers is not None else L0
+    stack = GptOssFFNStack.synthetic(cfg, n_layers, seed=args.seed, device=dev, layout=args.layout,
+                                     dispatch=args.dispatch)
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    n_steps = W + K
+    X = synth.activations(n_steps * T, cfg.n_embd, seed=args.seed + 1, device=dev).view(n_steps, T, cfg.n_embd)
+    Y = torch.empty_like(X)
+
+    def run_steps(rng):
+        for i in rng:
+            stack(X[i], out=Y[i])
+
+    ms_total, wall_s, _ = _graph_time(torch, run_steps, W, K)
+    ids, _ = stack.last_routing(T)
+    ids_cpu = ids.cpu()
+    distinct = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
+    mean_distinct = sum(distinct) / len(distinct)
+    ms_per_step = ms_total / K
+    step_bytes = n_layers * sum(_expert_bytes(cfg, mean_distinct))
+    return {
+        "metric": f"MoE-FFN stack tok/s ({n_layers} GPT-OSS-120B-shaped MXFP4 layers, T={T})",
+        "value": round(K * T / (ms_total / 1e3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded MXFP4 experts per layer, x~N(0,1)); all expert slabs resident in HBM",
+        "config": {"workload": f"gpt-oss-120b FFN stack, {n_layers} layers, T={T} (BASELINE config 5)",
+                   "tokens_per_step": T, "layers": n_layers, "layout": args.layout, "dispatch": args.dispatch,
+                   "graph": True, "chain": "x <- x + moe_l(rms_norm(x)), unit norm weight, eps 1e-5"},
+        "resident_GB": round(n_layers * cfg.n_expert * sum(cfg.expert_bytes(k) for k in ("gate", "up", "down"))
+                             / 1e9, 2),
+        "distinct_experts_per_layer": round(mean_distinct, 2),
+        "expert_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "roofline_tok_s": round(T / (step_bytes / (HBM_PEAK_GBS * 1e9)), 1),
+        "wall_s": round(wall_s, 4),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -119,140 +375,14 @@ def main():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from nurostream_amd import _native as N
     from nurostream_amd import synth
-    from nurostream_amd.compute.kernels import t64_pack_stacked
-    from nurostream_amd.moe.fused import MoELayer
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     N.ensure_selftest(dev)
-    cfg = synth.GPTOSS_120B
-    T = 1
-    K, W = args.steps, args.warmup
-    n_layers = max(1, args.layers)
-
-    layers, t_cpu = [], None
-    for li in range(n_layers):
-        t = synth.make_layer(cfg, seed=args.seed, device=dev, layer=li)
-        if li == 0 and not args.no_cpu:
-            t_cpu = {k: (None if v is None else v.float().cpu().numpy() if v.dtype != torch.uint8
-                         else v.cpu().numpy()) for k, v in t.items()}
-        if args.layout == "t64":
-            mats = {k: t64_pack_stacked(t[k], cfg.ggml_type, cfg.n_expert, *cfg.rows_K(k))
-                    for k in ("gate", "up", "down")}
-            for k in ("gate", "up", "down"):
-                t[k] = None
-        else:
-            mats = {k: t[k] for k in ("gate", "up", "down")}
-        layers.append(MoELayer(ggml_type=cfg.ggml_type, n_expert=cfg.n_expert, top_k=cfg.top_k,
-                               n_embd=cfg.n_embd, n_ff=cfg.n_ff, router_w=t["router_w"], router_b=t["router_b"],
-                               gate=mats["gate"], up=mats["up"], down=mats["down"], gate_b=t["gate_b"],
-                               up_b=t["up_b"], down_b=t["down_b"], layout=args.layout,
-                               router_mode=cfg.router_mode, act=cfg.act))
-        del t, mats
-        torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-
-    n_tok = W + K + args.profile_steps
-    X = synth.activations(n_tok, cfg.n_embd, seed=args.seed + 1, device=dev)
-    outs = torch.empty((n_tok, cfg.n_embd), dtype=torch.float32, device=dev)
-    ids = torch.empty((n_tok, cfg.top_k), dtype=torch.int32, device=dev)
-    wts = torch.empty((n_tok, cfg.top_k), dtype=torch.float32, device=dev)
-    for lay in layers:
-        lay.workspace(T)
-
-    def step(i):
-        lay = layers[i % n_layers]
-        lay.forward(X[i:i + 1], out=outs[i:i + 1], ids=ids[i:i + 1], weights=wts[i:i + 1])
-
-    # warm-up (eager), then capture the K timed steps (tokens W..W+K-1) as one graph
-    for i in range(W):
-        step(i)
-    torch.cuda.synchronize()
-    stream = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(W, W + K):
-                step(i)
-    torch.cuda.synchronize()
-
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    ev0.record()
-    graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t_wall
-    ms_total = ev0.elapsed_time(ev1)
-    ms_per_step = ms_total / K
-    tok_s = K * T / (ms_total / 1e3)
-
-    # per-kernel durations: R tokens, one workspace each, phase by phase; each
-    # phase is a graph of R back-to-back launches of that phase's kernel
-    P0 = W + K
-    R = args.profile_steps
-    toks = list(range(P0, P0 + R))
-    wss = [layers[i % n_layers].new_workspace(T) for i in toks]
-    graphs = []
-    with torch.cuda.stream(stream):  # PHASE_COMBINE launches nothing: the down kernels combine
-        for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                for j, i in enumerate(toks):
-                    layers[i % n_layers].phase(ph, X[i:i + 1], outs[i:i + 1], ids[i:i + 1], wts[i:i + 1], wss[j])
-            graphs.append(g)
-    torch.cuda.synchronize()
-    for g in graphs:  # first replay: graph upload, untimed
-        g.replay()
-    torch.cuda.synchronize()
-    phase_us = []
-    for g in graphs:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        phase_us.append(e0.elapsed_time(e1) * 1e3 / R)
-    ph_out = outs[P0:P0 + R].clone()
-    for i in toks:
-        step(i)
-    torch.cuda.synchronize()
-    if not torch.equal(ph_out, outs[P0:P0 + R]):
-        raise RuntimeError("phase-by-phase outputs differ from nsx_moe_forward")
-
-    gu_bytes, dn_bytes = _expert_bytes_per_token(cfg)
-    gu_us = phase_us[1]
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "moe_gu_kernel" if args.layout == "t64" else "moe_gu_raw_kernel",
-                "bytes_per_launch": gu_bytes, "avg_us": round(gu_us, 3)}
-    roofline["traffic"] = _traffic(roofline["kernel"])
-    layer_bytes = cfg.layer_bytes_per_token()
-    result = {
-        "metric": "MoE-FFN decode tok/s (GPT-OSS-120B shape, MXFP4)",
-        "value": round(tok_s, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded MXFP4 experts, x~N(0,1)); weights resident in HBM",
-        "config": {"workload": "gpt-oss-120b MoE layer, decode batch 1 (BASELINE config 2)",
-                   "layout": args.layout, "rotating_layers": n_layers, "hidden": cfg.n_embd,
-                   "experts": cfg.n_expert, "top_k": cfg.top_k, "graph": True},
-        "layer_GBps": round(layer_bytes / (ms_per_step * 1e-3) / 1e9, 1),
-        "kernel_us": {"router": round(phase_us[0], 3), "gate_up": round(phase_us[1], 3),
-                     "down_combine": round(phase_us[2], 3)},
-        "down_GBps": round(dn_bytes / (phase_us[2] * 1e-6) / 1e9, 1),
-        "wall_s": round(wall_s, 4),
-        "roofline": roofline,
-    }
+    if args.workload.startswith("stack"):
+        result = stack_workload(args, torch, N, synth, dev)
+    else:
+        result = layer_workload(args, torch, N, synth, dev)
     if args.copy_probe_mib > 0:  # a plain copy of known size for the counter calibration
         n = args.copy_probe_mib << 18
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -261,10 +391,6 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    if not args.no_cpu:
-        result["cpu_baseline"] = _cpu_baseline(cfg, t_cpu, X[:32].cpu().numpy(), args.cpu_seconds)
-    else:
-        result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
 
 

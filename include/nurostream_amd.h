@@ -168,6 +168,15 @@ int nsx_moe_phase(const nsx_moe_layer *L, int phase, const float *h, int64_t T,
                   float *out, int32_t *ids, float *weights, void *workspace,
                   int64_t workspace_bytes, void *stream);
 
+/* compute/ops.py:14-20 rms_norm in fp32 over rows of n (n <= 4096), with the
+ * residual add of model/gpt_oss.py:177 folded in: sum = x + r and
+ * y = sum * rsqrt(mean(sum^2) + eps) * w. r, w, sum and y may each be NULL
+ * (no residual, unit weight, no sum or no norm output; not both outputs);
+ * sum and y may alias x or r. */
+int nsx_add_rmsnorm(const float *x, const float *r, int64_t T, int64_t n,
+                    float eps, const float *w, float *sum, float *y,
+                    void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1203,3 +1203,60 @@ extern "C" int nsx_moe_phase(const nsx_moe_layer* L, int phase, const float* h, 
               "grouped phases take at most %d pairs (T=%lld)", GRP_MAX_PAIRS, (long long)T);
   return moe_run(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, phase, phase);
 }
+
+// ---------------------------------------------------------------------------
+// s = x + r and y = rms_norm(s) * w over rows of n (compute/ops.py:14-20
+// rms_norm, fp32: v * rsqrt(mean(v^2) + eps) * w), the link between stacked
+// MoE layers (model/gpt_oss.py:126,177: the residual add, then the next
+// layer's norm). One workgroup per row; r, w, s and y may each be NULL (no
+// residual, unit weight, no sum or no norm output); s and y may alias x or r.
+
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_MAXV = 16;  // values per thread (n <= 4096)
+
+__global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(const float* x, const float* r, int n, float eps,
+                                                                   const float* __restrict__ w, float* sum,
+                                                                   float* y) {
+  __shared__ float part[NORM_THREADS / 64];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * n;
+  const float* rr = r ? r + row * n : nullptr;
+  float v[NORM_MAXV];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_MAXV; ++i) {
+    const int c = threadIdx.x + i * NORM_THREADS;
+    v[i] = 0.f;
+    if (c < n) {
+      v[i] = rr ? xr[c] + rr[c] : xr[c];
+      ss = fmaf(v[i], v[i], ss);
+    }
+  }
+  ss = nsx_wave_sum(ss);
+  if (__lane_id() == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();  // every read of x and r is done before any write below
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_THREADS / 64; ++i) tot += part[i];
+  const float inv = 1.f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+  for (int i = 0; i < NORM_MAXV; ++i) {
+    const int c = threadIdx.x + i * NORM_THREADS;
+    if (c < n) {
+      if (sum) sum[row * n + c] = v[i];
+      if (y) y[row * n + c] = w ? (v[i] * inv) * w[c] : v[i] * inv;
+    }
+  }
+}
+
+extern "C" int nsx_add_rmsnorm(const float* x, const float* r, int64_t T, int64_t n, float eps, const float* w,
+                               float* sum, float* y, void* stream) {
+  NSX_REQUIRE(T >= 0 && T <= (1ll << 31) - 1, NSX_EINVAL, "T=%lld", (long long)T);
+  NSX_REQUIRE(n >= 1 && n <= NORM_THREADS * NORM_MAXV, NSX_EINVAL, "row length %lld outside 1..%d", (long long)n,
+              NORM_THREADS * NORM_MAXV);
+  NSX_REQUIRE(eps >= 0.f, NSX_EINVAL, "eps %g", (double)eps);
+  if (T == 0) return NSX_OK;
+  NSX_REQUIRE(x && (sum || y), NSX_EINVAL, "null buffer");
+  return nsx_launch(add_rmsnorm_kernel, dim3((unsigned)T), dim3(NORM_THREADS), 0, S(stream), x, r, (int)n, eps, w, sum,
+                    y);
+}

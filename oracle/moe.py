@@ -16,6 +16,9 @@ Reference functions restated (paths relative to neurostream/):
   moe_gptoss      model/gpt_oss.py:123-177: per chosen expert in ascending id
                   order, out[rows] += w_e * y_e
   moe_qwen3       moe/router.py:173-219 (same combine, SiLU*up, no biases)
+  rms_norm        compute/ops.py:14-20 (float32: x * rsqrt(mean(x^2) + eps) * w)
+  ffn_stack       model/gpt_oss.py:123-177 per layer, attention left out:
+                  x <- x + moe_l(rms_norm(x)) (composition of the above)
 
 Top-k tie rule: torch.topk leaves the order of equal values unspecified; this
 restatement (and the HIP kernel) takes the lower expert index first.
@@ -24,8 +27,10 @@ Pinning (tests/test_oracle_moe.py): brute force over all k-subsets on tiny
 inputs, closed forms (softmax over the top-k sums to 1 and is monotone in the
 logits, renormalised Qwen3 weights sum to 1), the activation's clamp and
 sigmoid special values, block-decomposition invariance of stream_linear for
-block_rows in {1, 7, 8, 64, 4096} (tests/test_gpt_oss.py:176-192), and the
-reference's known answer 528 (tests/test_tuning.py:135-153).
+block_rows in {1, 7, 8, 64, 4096} (tests/test_gpt_oss.py:176-192), the
+reference's known answer 528 (tests/test_tuning.py:135-153), and for rms_norm
+unit output RMS at eps 0, invariance under power-of-two scaling, and the
+closed form c / sqrt(c^2 + eps) of a constant row.
 """
 from __future__ import annotations
 
@@ -193,3 +198,13 @@ def rms_norm(x, weight=None, eps=1e-5):
     if weight is not None:
         y = y * np.asarray(weight, np.float32)
     return y.astype(np.float32)
+
+
+def ffn_stack(x, layers, k, eps=1e-5, block_rows=0):
+    """x after each layer's FFN block, x <- x + moe_gptoss(rms_norm(x)).
+    layers: [(W_r, b_r, ExpertSet)] (gpt_oss.py:123-177, one per layer)."""
+    x = np.asarray(x, np.float32)
+    for W_r, b_r, ex in layers:
+        out = moe_gptoss(rms_norm(x, eps=eps), W_r, b_r, k, ex, block_rows=block_rows)[0]
+        x = (x + out).astype(np.float32)
+    return x

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from helpers import bit_mismatches, rel_max, to_np
+from oracle import moe as OM
 from oracle import quant as OQ
 
 pytestmark = pytest.mark.gpu
@@ -184,3 +185,26 @@ def test_t64_gemv_nan_scale_rows_are_non_finite(dev):
     ok = np.setdiff1d(np.arange(rows), bad)
     assert np.isfinite(y[ok]).all()
     assert rel_max(y[ok], ref[ok].astype(np.float64)) < MFMA_TOL
+
+
+@pytest.mark.parametrize("T,n,resid,weight", [(1, 2880, True, False), (8, 2880, True, True), (3, 4096, False, True),
+                                             (2, 100, True, True)])
+def test_add_rmsnorm_matches_oracle(dev, T, n, resid, weight):
+    """compute/ops.py:14-20 with the residual folded in (nsx_add_rmsnorm)."""
+    from nurostream_amd.compute.ops import add_rms_norm
+    g = torch.Generator().manual_seed(T * 7 + n)
+    x = torch.randn(T, n, generator=g)
+    r = torch.randn(T, n, generator=g) if resid else None
+    w = torch.randn(n, generator=g) if weight else None
+    y = add_rms_norm(x.to(dev), None if r is None else r.to(dev), None if w is None else w.to(dev), 1e-5)
+    v = x.numpy() + (r.numpy() if resid else 0)
+    ref = OM.rms_norm(v, None if w is None else w.numpy(), eps=1e-5)
+    np.testing.assert_allclose(to_np(y), ref, rtol=2e-6, atol=2e-6)
+    # in place (y aliases x), and the residual sum written back over x
+    xd = x.to(dev)
+    add_rms_norm(xd, None if r is None else r.to(dev), None if w is None else w.to(dev), 1e-5, out=xd)
+    assert torch.equal(xd, y)
+    xd, s = x.to(dev), torch.empty(T, n, device=dev)
+    y2 = add_rms_norm(xd, None if r is None else r.to(dev), None if w is None else w.to(dev), 1e-5, sum_out=xd)
+    assert torch.equal(y2, y)
+    np.testing.assert_array_equal(to_np(xd), v.astype(np.float32))

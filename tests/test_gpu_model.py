@@ -1,0 +1,101 @@
+"""The model-level seams on the device: the GPT-OSS FFN stack (BASELINE
+config 5's chain, model/gpt_oss.py:123-177) and the Qwen3 sparse FFN
+(moe/router.py:173-219) over a cache that mixes HBM slabs and streamed reads."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import FFN_BAR, MFMA_TOL, rel_max, to_np
+from moe_cases import _expert_set, _small
+from oracle import moe as OM
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_layers(cfg, seed, n_layers, dev):
+    from nurostream_amd import synth
+    out = []
+    for li in range(n_layers):
+        t = synth.make_layer(cfg, seed=seed, device=dev, layer=li)
+        out.append((t["router_w"].float().cpu().numpy(), t["router_b"].cpu().numpy(), _expert_set(cfg, t)))
+    return out
+
+
+@pytest.mark.parametrize("T", [1, 2, 9])
+def test_gptoss_ffn_stack_matches_oracle(dev, T):
+    from nurostream_amd import synth
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack
+    cfg = _small("gptoss-small")
+    L = 3
+    stack = GptOssFFNStack.synthetic(cfg, L, seed=21, device=dev)
+    x = synth.activations(T, cfg.n_embd, seed=9, device=dev)
+    y = stack(x)
+    ref = OM.ffn_stack(x.cpu().numpy(), _oracle_layers(cfg, 21, L, dev), cfg.top_k)
+    err = rel_max(to_np(y), ref)
+    assert err < FFN_BAR and err < L * MFMA_TOL, err
+    ids, _ = stack.last_routing(T)
+    assert ids.shape == (L, T, cfg.top_k)
+    # the per-layer seam gives the same first step, and a graph replay the same chain
+    x1 = stack._ffn_block(x, 0)
+    r1 = OM.ffn_stack(x.cpu().numpy(), _oracle_layers(cfg, 21, 1, dev), cfg.top_k)
+    assert rel_max(to_np(x1), r1) < MFMA_TOL
+    assert stack.router_stats.tokens_routed == T
+    g = torch.cuda.CUDAGraph()
+    out = torch.empty_like(x)
+    stack(x, out=out)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        stack(x, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y)
+
+
+def _qwen3_cache(cfg, t, dev, slab_experts):
+    from nurostream_amd.format.gguf import GGMLType, tensor_info
+    from nurostream_amd.io.arena import Arena
+    from nurostream_amd.io.source import HostSource
+    from nurostream_amd.residency.cache import TieredCache
+    tensors = {}
+    Wr = t["router_w"].float().cpu().contiguous()
+    info = tensor_info("blk.0.ffn_gate_inp.weight", (cfg.n_expert, cfg.n_embd), GGMLType.F32)
+    tensors[info.name] = (info, Wr.reshape(-1).view(torch.uint8).clone())
+    for kind in ("gate", "up", "down"):
+        rows, K = cfg.rows_K(kind)
+        info = tensor_info(f"blk.0.ffn_{kind}_exps.weight", (cfg.n_expert, rows, K), cfg.ggml_type)
+        tensors[info.name] = (info, t[kind].cpu())
+    src = HostSource(tensors, Arena(64 << 20), device=dev)
+    cache = TieredCache(src, device=dev, vram_budget=1 << 20)
+    cache.slab_budget = 1 << 30
+    for kind in ("gate", "up", "down"):
+        rows, _ = cfg.rows_K(kind)
+        for e in slab_experts:
+            assert cache.admit_slab(f"blk.0.ffn_{kind}_exps.weight", e * rows, (e + 1) * rows)
+    return src, cache
+
+
+@pytest.mark.parametrize("T", [1, 3, 20])
+def test_qwen3_moe_ffn_over_cache(dev, T):
+    """moe_ffn with half the experts in HBM slabs and the rest streamed from
+    pinned host RAM through submit_expert_reads (T=20: dequantize + matmul)."""
+    from nurostream_amd import synth
+    from nurostream_amd.model.qwen3 import Qwen3MoE, Qwen3MoEConfig
+    cfg = _small("qwen3-small")
+    t = synth.make_layer(cfg, seed=6, device="cpu")
+    src, cache = _qwen3_cache(cfg, t, dev, slab_experts=range(0, cfg.n_expert, 2))
+    model = Qwen3MoE(cache, Qwen3MoEConfig(cfg.n_embd, cfg.n_expert, cfg.top_k, cfg.n_ff), dev)
+    h = synth.activations(T, cfg.n_embd, seed=T, device="cpu")
+    out = model.ffn(h.to(dev), 0)
+    torch.cuda.synchronize()
+    ref, rid, _, _ = OM.moe_qwen3(h.numpy(), t["router_w"].float().numpy(), cfg.top_k, _expert_set(cfg, t))
+    assert rel_max(to_np(out), ref) < 1e-5
+    st = model.router_stats
+    assert st.tokens_routed == T and st.expert_reads == len(np.unique(rid))
+    assert sum(st.hits.values()) == T * cfg.top_k
+    assert src.arena.used == 0
+    assert cache.stats.slab_hits > 0

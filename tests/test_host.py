@@ -186,3 +186,18 @@ def test_quantized_compute_never_falls_back_to_cpu():
         dequantize(raw.view(torch.int8), GGMLType.Q8_0, 128)
     with pytest.raises(NotImplementedError):
         dequantize(raw, GGMLType.Q6_K, 128)
+
+
+def test_router_stats_contract():
+    """moe/router.py:26-56: hits per (layer, expert), top_experts, skew, summary; record() counts ids."""
+    from nurostream_amd.moe.router import RouterStats
+    st = RouterStats()
+    assert st.skew() == 0.0
+    st.record(0, torch.tensor([[3, 1], [3, 2], [3, 1]]))
+    st.record(1, torch.tensor([[0, 5]]))
+    assert st.tokens_routed == 4 and st.expert_reads == 3 + 2
+    assert st.hits[(0, 3)] == 3 and st.hits[(0, 1)] == 2 and st.hits[(1, 5)] == 1
+    assert st.top_experts(0, 2) == [(3, 3), (1, 2)]
+    # 5 (layer, expert) entries: the busiest 20% (one entry, 3 hits) of 8 routings
+    assert st.skew() == pytest.approx(3 / 8)
+    assert "routed 4 tokens" in st.summary() and "5 expert reads" in st.summary()

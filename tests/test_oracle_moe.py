@@ -180,3 +180,17 @@ def test_reference_slab_known_answer_528():
     raw = np.tile(row, 4)
     got = OM.stream_linear(raw, OQ.Q8_0, np.ones((3, 32), np.float32), 4, 32, block_rows=1)
     np.testing.assert_array_equal(got, np.full((3, 4), 528.0, np.float32))
+
+
+def test_rms_norm_closed_forms():
+    """compute/ops.py:14-20: unit RMS (eps 0), scale invariance, constant rows, weight."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 2880)).astype(np.float32)
+    y = OM.rms_norm(x, eps=0.0)
+    np.testing.assert_allclose(np.sqrt((y.astype(np.float64) ** 2).mean(-1)), 1.0, rtol=1e-6)
+    np.testing.assert_array_equal(OM.rms_norm(x * np.float32(8.0), eps=0.0), y)
+    for c in (0.5, -3.0, 1e-3):
+        row = np.full((1, 64), c, np.float32)
+        np.testing.assert_allclose(OM.rms_norm(row, eps=1e-5), c / np.sqrt(c * c + 1e-5), rtol=1e-6)
+    w = rng.standard_normal(2880).astype(np.float32)
+    np.testing.assert_array_equal(OM.rms_norm(x, w, eps=1e-6), (OM.rms_norm(x, eps=1e-6) * w).astype(np.float32))
