@@ -49,81 +49,6 @@ __device__ __forceinline__ void load8_w(const void* W, int64_t off, float (&w)[8
 constexpr int RT_MAXC = 8;   // 512-element chunks per lane and pass (K <= 4096 in one pass)
 constexpr int RT_XQ_WGS = 16;  // extra workgroups that quantize h for the t64 expert kernels
 
-// Workgroups [0, ceil(E/4)) compute logits (one wave per expert, RT_TT tokens
-// per grid row); with xq set, RT_XQ_WGS more workgroups per grid row build
-// the tokens' activation terms. Loads are unpredicated (addresses clamped,
-// tails zeroed after the load) so that they are all in flight together.
-template <int WDT>
-__global__ __launch_bounds__(256) void router_logits_kernel(const float* __restrict__ h, int T, int K,
-                                                            const void* __restrict__ W,
-                                                            const float* __restrict__ bias, int E,
-                                                            float* __restrict__ logits, uint8_t* __restrict__ xq) {
-  typedef const __attribute__((address_space(1))) v4f gv4f;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int ewgs = (E + 3) / 4;
-  if ((int)blockIdx.x >= ewgs) {  // activation terms of h, two blocks per wave task
-    const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
-    const int64_t tasks = (int64_t)T * pairs;
-    const int64_t nwaves = (int64_t)gridDim.y * RT_XQ_WGS * 4;
-    for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - ewgs)) * 4 + wave; task < tasks;
-         task += nwaves) {
-      const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
-      const float r = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
-      xq_block(b < nb ? r : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
-    }
-    return;
-  }
-  const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * RT_TT;
-  const int nt = min(RT_TT, T - t0);
-  if (e >= E) return;
-  float acc[RT_TT];
-#pragma unroll
-  for (int i = 0; i < RT_TT; ++i) acc[i] = 0.f;
-  for (int k0 = 0; k0 < K; k0 += RT_MAXC * 512) {
-    float w[RT_MAXC][8];
-#pragma unroll
-    for (int c = 0; c < RT_MAXC; ++c) {
-      const int k = k0 + c * 512 + lane * 8;
-      load8_w<WDT>(W, (int64_t)e * K + (k < K ? k : K - 8), w[c]);
-    }
-#pragma unroll
-    for (int c = 0; c < RT_MAXC; ++c) {
-      const bool in = k0 + c * 512 + lane * 8 < K;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) w[c][u] = in ? w[c][u] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < RT_TT; ++i) {
-      if (i >= nt) break;
-      const float* hp = h + (int64_t)(t0 + i) * K;
-      v4f ha[RT_MAXC], hb[RT_MAXC];
-#pragma unroll
-      for (int c = 0; c < RT_MAXC; ++c) {
-        const int k = k0 + c * 512 + lane * 8;
-        const int kc = k < K ? k : K - 8;
-        ha[c] = *(gv4f*)(hp + kc);
-        hb[c] = *(gv4f*)(hp + kc + 4);
-      }
-      float s = acc[i];
-#pragma unroll
-      for (int c = 0; c < RT_MAXC; ++c) {  // w is zero past K
-        s = fmaf(w[c][0], ha[c].x, s); s = fmaf(w[c][1], ha[c].y, s);
-        s = fmaf(w[c][2], ha[c].z, s); s = fmaf(w[c][3], ha[c].w, s);
-        s = fmaf(w[c][4], hb[c].x, s); s = fmaf(w[c][5], hb[c].y, s);
-        s = fmaf(w[c][6], hb[c].z, s); s = fmaf(w[c][7], hb[c].w, s);
-      }
-      acc[i] = s;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < RT_TT; ++i) {
-    if (i >= nt) break;
-    const float s = nsx_wave_sum(acc[i]);
-    if (lane == 0) logits[(int64_t)(t0 + i) * E + e] = bias ? s + bias[e] : s;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // top-k over one token's logits, computed by one wave; results are uniform
 // across the wave. Order: larger value first, ties to the lower index.
@@ -227,6 +152,84 @@ __device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, i
   float v[TOPK_NV];
   topk_load(lg, E, v);
   topk_select(v, E, k, mode, sel_i, sel_w);
+}
+
+// Router logits (model/gpt_oss.py:97-99,116-121; moe/router.py:59-69).
+// Workgroups [0, ceil(E/4)) of grid row y compute the logits of tokens
+// 8y .. 8y + 7 (one wave per expert); with xq set, RT_XQ_WGS more workgroups
+// per grid row build the tokens' activation terms. Loads are unpredicated
+// (addresses clamped, tails zeroed after the load) so that they are all in
+// flight together.
+template <int WDT>
+__global__ __launch_bounds__(256) void router_logits_kernel(const float* __restrict__ h, int T, int K,
+                                                            const void* __restrict__ W,
+                                                            const float* __restrict__ bias, int E,
+                                                            float* __restrict__ logits, uint8_t* __restrict__ xq) {
+  typedef const __attribute__((address_space(1))) v4f gv4f;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int ewgs = (E + 3) / 4;
+  if ((int)blockIdx.x >= ewgs) {  // activation terms of h, two blocks per wave task
+    const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
+    const int64_t tasks = (int64_t)T * pairs;
+    const int64_t nwaves = (int64_t)gridDim.y * RT_XQ_WGS * 4;
+    for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - ewgs)) * 4 + wave; task < tasks;
+         task += nwaves) {
+      const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
+      const float r = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
+      xq_block(b < nb ? r : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
+    }
+    return;
+  }
+  const int e = blockIdx.x * 4 + wave;
+  const int t0 = blockIdx.y * RT_TT;
+  const int nt = min(RT_TT, T - t0);
+  if (e < E) {
+    float acc[RT_TT];
+#pragma unroll
+    for (int i = 0; i < RT_TT; ++i) acc[i] = 0.f;
+    for (int k0 = 0; k0 < K; k0 += RT_MAXC * 512) {
+      float w[RT_MAXC][8];
+#pragma unroll
+      for (int c = 0; c < RT_MAXC; ++c) {
+        const int kk = k0 + c * 512 + lane * 8;
+        load8_w<WDT>(W, (int64_t)e * K + (kk < K ? kk : K - 8), w[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < RT_MAXC; ++c) {
+        const bool in = k0 + c * 512 + lane * 8 < K;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[c][u] = in ? w[c][u] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < RT_TT; ++i) {
+        if (i >= nt) break;
+        const float* hp = h + (int64_t)(t0 + i) * K;
+        v4f ha[RT_MAXC], hb[RT_MAXC];
+#pragma unroll
+        for (int c = 0; c < RT_MAXC; ++c) {
+          const int kk = k0 + c * 512 + lane * 8;
+          const int kc = kk < K ? kk : K - 8;
+          ha[c] = *(gv4f*)(hp + kc);
+          hb[c] = *(gv4f*)(hp + kc + 4);
+        }
+        float sacc = acc[i];
+#pragma unroll
+        for (int c = 0; c < RT_MAXC; ++c) {  // w is zero past K
+          sacc = fmaf(w[c][0], ha[c].x, sacc); sacc = fmaf(w[c][1], ha[c].y, sacc);
+          sacc = fmaf(w[c][2], ha[c].z, sacc); sacc = fmaf(w[c][3], ha[c].w, sacc);
+          sacc = fmaf(w[c][4], hb[c].x, sacc); sacc = fmaf(w[c][5], hb[c].y, sacc);
+          sacc = fmaf(w[c][6], hb[c].z, sacc); sacc = fmaf(w[c][7], hb[c].w, sacc);
+        }
+        acc[i] = sacc;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RT_TT; ++i) {
+      if (i >= nt) break;
+      const float sum = nsx_wave_sum(acc[i]);
+      if (lane == 0) logits[(int64_t)(t0 + i) * E + e] = bias ? sum + bias[e] : sum;
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int T, int E, int k, int mode,
@@ -948,6 +951,211 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 }
 
 // ---------------------------------------------------------------------------
+// Q4_K experts over raw GGUF rows (a row is K/256 super-blocks of 144 B, so
+// rows and super-blocks are 16-byte aligned). A row splits into 16-byte code
+// units, 8 per super-block: unit u = 8 sb + 2 g + h holds code bytes
+// 16 h .. 16 h + 15 of sub-block pair g -- low nibbles are elements 16 h + j of
+// sub-block 2 g, high nibbles those of sub-block 2 g + 1 (compute/quant.py:
+// 24-56 dequant_q4_k). Lane l of a wave owns units l, l + 64, ...; it keeps
+// their 32 activations and the two 16-element activation sums in registers
+// for every row it visits, and per row loads the unit's codes and its
+// super-block header (d, dmin, 12 scale bytes) as two 128-bit loads, all rows
+// of a wave in flight together. Per unit:
+//   (d sc_2g) sum q_lo x - (dmin m_2g) sum x + (d sc_2g+1) sum q_hi x - (dmin m_2g+1) sum x
+// with d sc and dmin m exact in fp32 (11-bit times 6-bit integers).
+
+constexpr int Q4K_UMAX = 2;     // units per lane: K <= 64 * 2 * 32 = 4096
+constexpr int Q4K_GU_WAVES = 8;
+constexpr int Q4K_GU_RPW = 2;   // gate and up rows per wave
+constexpr int Q4K_DN_ROWS = 16; // output rows per down workgroup
+
+struct Q4kX {
+  float x0[16], x1[16];
+  float s0, s1;
+};
+
+// the unit's activations (x: the token's K floats, 16-byte aligned; zeros when !valid)
+__device__ __forceinline__ void q4k_unit_x(const float* __restrict__ x, int u, bool valid, Q4kX& X) {
+  const int sb = u >> 3, g = (u >> 1) & 3, h = u & 1;
+  const float* p0 = x + sb * 256 + g * 64 + 16 * h;
+  const float* p1 = p0 + 32;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v4f a = *(const v4f*)(p0 + 4 * i), b = *(const v4f*)(p1 + 4 * i);
+    if (!valid) a = b = v4f{0.f, 0.f, 0.f, 0.f};
+    X.x0[4 * i] = a.x; X.x0[4 * i + 1] = a.y; X.x0[4 * i + 2] = a.z; X.x0[4 * i + 3] = a.w;
+    X.x1[4 * i] = b.x; X.x1[4 * i + 1] = b.y; X.x1[4 * i + 2] = b.z; X.x1[4 * i + 3] = b.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    s0 += X.x0[j];
+    s1 += X.x1[j];
+  }
+  X.s0 = s0;
+  X.s1 = s1;
+}
+
+// get_scale_min_k4 (compute/quant.py:24-40) for sub-block s of the 12 scale bytes in y, z, w
+__device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w, int s, float& sc, float& m) {
+  auto byte = [&](int i) -> uint32_t {
+    const uint32_t d = i < 4 ? y : (i < 8 ? z : w);
+    return (d >> (8 * (i & 3))) & 0xffu;
+  };
+  const uint32_t lo_sc = byte(s & 3) & 63u, lo_m = byte((s & 3) + 4) & 63u;
+  const uint32_t bs4 = byte((s & 3) + 8);  // s >= 4: byte s + 4
+  const uint32_t hi_sc = (bs4 & 0x0fu) | ((byte(s & 3) >> 6) << 4);
+  const uint32_t hi_m = (bs4 >> 4) | ((byte((s & 3) + 4) >> 6) << 4);
+  sc = (float)(s < 4 ? lo_sc : hi_sc);
+  m = (float)(s < 4 ? lo_m : hi_m);
+}
+
+__device__ __forceinline__ float q4k_unit_dot(const v4u& c, const v4u& hd, int u, const Q4kX& X) {
+  const int g = (u >> 1) & 3;
+  float sc0, m0, sc1, m1;
+  q4k_scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, m0);
+  q4k_scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, m1);
+  const float d = nsx_h2f(hd.x & 0xffffu), dmin = nsx_h2f(hd.x >> 16);
+  float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = c[i] & 0x0f0f0f0fu, hi = (c[i] >> 4) & 0x0f0f0f0fu;
+    p0 = fmaf(nsx_ub<0>(lo), X.x0[4 * i], p0);
+    p0 = fmaf(nsx_ub<1>(lo), X.x0[4 * i + 1], p0);
+    p0 = fmaf(nsx_ub<2>(lo), X.x0[4 * i + 2], p0);
+    p0 = fmaf(nsx_ub<3>(lo), X.x0[4 * i + 3], p0);
+    p1 = fmaf(nsx_ub<0>(hi), X.x1[4 * i], p1);
+    p1 = fmaf(nsx_ub<1>(hi), X.x1[4 * i + 1], p1);
+    p1 = fmaf(nsx_ub<2>(hi), X.x1[4 * i + 2], p1);
+    p1 = fmaf(nsx_ub<3>(hi), X.x1[4 * i + 3], p1);
+  }
+  return fmaf(d * sc0, p0, -(dmin * m0) * X.s0) + fmaf(d * sc1, p1, -(dmin * m1) * X.s1);
+}
+
+// codes and header of unit u of `row` (clamped in-bounds loads)
+__device__ __forceinline__ void q4k_unit_load(const uint8_t* __restrict__ mat, int row, uint32_t rb, int u, v4u& c,
+                                              v4u& hd) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  const uint8_t* sbp = mat + (int64_t)row * rb + (u >> 3) * 144;
+  hd = *(gv4u*)sbp;
+  c = *(gv4u*)(sbp + 16 + 16 * (u & 7));
+}
+
+// gate/up: workgroup = (pair, 16 rows), wave = 2 rows of gate and of up
+template <int U>
+__global__ __launch_bounds__(512) void moe_gu_q4k_kernel(MoeDev a) {
+  extern __shared__ __align__(16) float q4k_xs[];
+  constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
+  const int groups = (a.n_ff + RPG - 1) / RPG;
+  const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
+  const int K = a.n_embd, t = p / a.top_k;
+  const int e = clamp_expert(a.ids[p], a.E);
+  for (int i = threadIdx.x; i < K / 4; i += blockDim.x) ((v4f*)q4k_xs)[i] = ((const v4f*)(a.h + (int64_t)t * K))[i];
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int nu = K / 32;
+  const uint32_t rb = (uint32_t)(K / 256) * 144u;
+  const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
+  const uint8_t* um = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
+  v4u cg[Q4K_GU_RPW][U], hg[Q4K_GU_RPW][U], cu[Q4K_GU_RPW][U], hu[Q4K_GU_RPW][U];
+#pragma unroll
+  for (int j = 0; j < Q4K_GU_RPW; ++j) {
+    const int row = min(r0 + wave * Q4K_GU_RPW + j, a.n_ff - 1);
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = min(lane + 64 * i, nu - 1);
+      q4k_unit_load(gm, row, rb, u, cg[j][i], hg[j][i]);
+      q4k_unit_load(um, row, rb, u, cu[j][i], hu[j][i]);
+    }
+  }
+  Q4kX X[U];
+#pragma unroll
+  for (int i = 0; i < U; ++i) q4k_unit_x(q4k_xs, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
+#pragma unroll
+  for (int j = 0; j < Q4K_GU_RPW; ++j) {
+    const int row = r0 + wave * Q4K_GU_RPW + j;
+    float gs = 0.f, us = 0.f;
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = min(lane + 64 * i, nu - 1);
+      gs += q4k_unit_dot(cg[j][i], hg[j][i], u, X[i]);
+      us += q4k_unit_dot(cu[j][i], hu[j][i], u, X[i]);
+    }
+    gs = nsx_wave_sum(gs);
+    us = nsx_wave_sum(us);
+    if (lane == 0 && row < a.n_ff) {
+      if (a.gate_bias) gs += a.gate_bias[(int64_t)e * a.n_ff + row];
+      if (a.up_bias) us += a.up_bias[(int64_t)e * a.n_ff + row];
+      a.act[(int64_t)p * a.n_ff + row] = moe_act(a.act_kind, gs, us, a.alpha, a.limit);
+    }
+  }
+}
+
+// down and combine: workgroup = (token, 16 output rows), wave j = expert slot j
+template <int U>
+__global__ __launch_bounds__(512) void moe_down_q4k_kernel(MoeDev a) {
+  __shared__ float red[MAX_TOPK][Q4K_DN_ROWS];
+  __shared__ int s_slot[MAX_TOPK];
+  const int groups = (a.n_embd + Q4K_DN_ROWS - 1) / Q4K_DN_ROWS;
+  const int t = blockIdx.x / groups, r0 = (blockIdx.x - t * groups) * Q4K_DN_ROWS;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int k = a.top_k, K = a.n_ff;
+  if (wave < k) {
+    const int p = t * k + wave;
+    const int e = clamp_expert(a.ids[p], a.E);
+    if (lane == 0) {  // this slot's rank in ascending expert id (ties: lower slot)
+      int rank = 0;
+      for (int jj = 0; jj < k; ++jj) {
+        const int ej = clamp_expert(a.ids[(int64_t)t * k + jj], a.E);
+        rank += (ej < e || (ej == e && jj < wave)) ? 1 : 0;
+      }
+      s_slot[rank] = wave;
+    }
+    const int nu = K / 32;
+    const uint32_t rb = (uint32_t)(K / 256) * 144u;
+    const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
+    Q4kX X[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i)
+      q4k_unit_x(a.act + (int64_t)p * K, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
+    constexpr int RB = Q4K_DN_ROWS / U;  // rows in flight per batch
+    float mine = 0.f;                    // lane j keeps row j's result
+#pragma unroll
+    for (int j0 = 0; j0 < Q4K_DN_ROWS; j0 += RB) {
+      v4u c[RB][U], hd[RB][U];
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const int row = min(r0 + j0 + j, a.n_embd - 1);
+#pragma unroll
+        for (int i = 0; i < U; ++i) q4k_unit_load(dm, row, rb, min(lane + 64 * i, nu - 1), c[j][i], hd[j][i]);
+      }
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        float y = 0.f;
+#pragma unroll
+        for (int i = 0; i < U; ++i) y += q4k_unit_dot(c[j][i], hd[j][i], min(lane + 64 * i, nu - 1), X[i]);
+        y = nsx_wave_sum(y);
+        mine = lane == j0 + j ? y : mine;
+      }
+    }
+    const int row = r0 + lane;
+    if (lane < Q4K_DN_ROWS) {
+      if (a.down_bias && row < a.n_embd) mine += a.down_bias[(int64_t)e * a.n_embd + row];
+      red[wave][lane] = mine;
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || lane >= Q4K_DN_ROWS) return;
+  const int row = r0 + lane;
+  float o = 0.f;
+  for (int jj = 0; jj < k; ++jj) {
+    const int jx = s_slot[jj];
+    o = combine_one(o, a.wts[(int64_t)t * k + jx], red[jx][lane]);
+  }
+  if (row < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 struct MoePlan {
@@ -1053,6 +1261,41 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
   NSX_REQUIRE(!use_grouped(L, T) || L->layout == NSX_LAYOUT_T64, NSX_ENOTIMPL,
               "grouped dispatch is implemented for the t64 layout");
   return NSX_OK;
+}
+
+// The Q4_K kernels take K <= 4096 and 16-byte aligned expert rows.
+static bool q4k_fast(const MoeDev& d, const nsx_moe_layer* L) {
+  if (L->ggml_type != NSX_Q4_K || L->n_embd > 64 * Q4K_UMAX * 32 || L->n_ff > 64 * Q4K_UMAX * 32) return false;
+  if (L->gate_base) {
+    const uintptr_t m = (uintptr_t)L->gate_base | (uintptr_t)L->up_base | (uintptr_t)L->down_base |
+                        (uintptr_t)L->gate_stride | (uintptr_t)L->up_stride | (uintptr_t)L->down_stride;
+    return (m & 15u) == 0;
+  }
+  return false;  // address tables: alignment unknown on the host
+}
+
+template <int UG, int UD>
+static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
+  const int64_t P = T * d.top_k;
+  if (gate_up) {
+    constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
+    const size_t lds = (size_t)d.n_embd * 4;
+    if (lds > 64 * 1024)
+      NSX_HIP(hipFuncSetAttribute((const void*)moe_gu_q4k_kernel<UG>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds));
+    int rc = nsx_launch(moe_gu_q4k_kernel<UG>, dim3((unsigned)(P * nsx_cdiv(d.n_ff, RPG))), dim3(64 * Q4K_GU_WAVES),
+                        lds, st, d);
+    if (rc) return rc;
+  }
+  if (!down) return NSX_OK;
+  return nsx_launch(moe_down_q4k_kernel<UD>, dim3((unsigned)(T * nsx_cdiv(d.n_embd, Q4K_DN_ROWS))),
+                    dim3(64 * MAX_TOPK), 0, st, d);
+}
+
+static int launch_q4k_any(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
+  const bool g2 = d.n_embd > 64 * 32, d2 = d.n_ff > 64 * 32;  // units per lane of gate/up and of down
+  if (g2) return d2 ? launch_q4k<2, 2>(d, T, st, gate_up, down) : launch_q4k<2, 1>(d, T, st, gate_up, down);
+  return d2 ? launch_q4k<1, 2>(d, T, st, gate_up, down) : launch_q4k<1, 1>(d, T, st, gate_up, down);
 }
 
 template <int FMT>
@@ -1172,7 +1415,9 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   }
   switch (L->ggml_type) {  // the GGUF-layout down kernel also combines
     case NSX_MXFP4: return launch_raw_phases<NSX_MXFP4>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
-    case NSX_Q4_K: return launch_raw_phases<NSX_Q4_K>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+    case NSX_Q4_K:
+      if (q4k_fast(d, L)) return launch_q4k_any(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+      return launch_raw_phases<NSX_Q4_K>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q4_0: return launch_raw_phases<NSX_Q4_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q8_0: return launch_raw_phases<NSX_Q8_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
   }
