@@ -147,14 +147,14 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
                     float *out, int32_t *ids, float *weights, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
-/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, plus top-k and the
- * ids/weights outputs for the GGUF layout; in the t64 layout also the
- * activation terms of h), NSX_PHASE_GATE_UP (expert gate/up GEMVs +
- * activation; the t64 kernel selects the top-k itself), NSX_PHASE_DOWN
- * (expert down GEMVs and the weighted combine into out; the t64 kernel also
- * writes ids/weights) and NSX_PHASE_COMBINE (kept for callers that run the
- * four phases; it launches nothing, as both layouts combine inside the down
- * phase). A phase reads what the earlier phases of the same call
+/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits; the top-k and the
+ * ids/weights outputs except for the per-pair t64 kernels, which select it
+ * themselves; in the t64 layout also the activation terms of h),
+ * NSX_PHASE_GATE_UP (grouped dispatch: the sort by expert; expert gate/up
+ * GEMVs + activation), NSX_PHASE_DOWN (expert down GEMVs; per-pair dispatch
+ * also the weighted combine into out, and the t64 kernel writes ids/weights)
+ * and NSX_PHASE_COMBINE (grouped dispatch: the ascending-expert combine;
+ * otherwise nothing). A phase reads what the earlier phases of the same call
  * sequence left in the workspace; running the four in order is
  * nsx_moe_forward. Callers use it to interleave other work (block reads,
  * another layer's router) between phases or to time one phase; the

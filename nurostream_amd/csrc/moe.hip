@@ -647,9 +647,9 @@ __device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
   return valid ? m : 0ull;
 }
 
-// One workgroup: top-k of every token (one wave per token), then a stable
-// counting sort of the pairs by expert (64-pair chunks, per-chunk counts,
-// prefix over chunks), the work items and the per-token combine order.
+// One workgroup, after the router phase's top-k: a stable counting sort of
+// the pairs by expert (64-pair chunks, per-chunk counts, prefix over chunks),
+// the work items and the per-token combine order.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   __shared__ uint16_t s_run[GRP_CHUNKS][MAX_EXPERTS];  // chunk counts, then exclusive prefix over chunks
   __shared__ int s_cnt[MAX_EXPERTS], s_off[MAX_EXPERTS];
@@ -658,30 +658,16 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   const int T = a.T, k = a.top_k, E = a.E, P = T * k;
   const int nch = (P + 63) / 64;
   for (int i = tid; i < GRP_CHUNKS * MAX_EXPERTS; i += 1024) (&s_run[0][0])[i] = 0;
-  for (int t = wave; t < T; t += 16) {
-    int si[MAX_TOPK];
-    float sw[MAX_TOPK];
-    topk_regs(a.logits + (int64_t)t * E, E, k, a.mode, si, sw);
-    int my_e = 0, rank = 0;
-    float my_w = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < MAX_TOPK; ++jj) {
-      my_e = lane == jj ? si[jj] : my_e;
-      my_w = lane == jj ? sw[jj] : my_w;
+  for (int p = tid; p < P; p += 1024) {  // each pair's expert and its token's combine slot
+    const int t = p / k, j = p - t * k;
+    const int e = clamp_expert(a.ids[p], E);
+    int rank = 0;
+    for (int jj = 0; jj < k; ++jj) {
+      const int ej = clamp_expert(a.ids[(int64_t)t * k + jj], E);
+      rank += (ej < e || (ej == e && jj < j)) ? 1 : 0;
     }
-    my_e = clamp_expert(my_e, E);
-#pragma unroll
-    for (int jj = 0; jj < MAX_TOPK; ++jj) {
-      const int ej = clamp_expert(si[jj], E);
-      rank += (jj < k && (ej < my_e || (ej == my_e && jj < lane))) ? 1 : 0;
-    }
-    if (lane < k) {
-      const int p = t * k + lane;
-      a.ids[p] = my_e;
-      a.wts[p] = my_w;
-      a.corder[t * k + rank] = p;
-      s_exp[p] = (uint8_t)my_e;
-    }
+    a.corder[t * k + rank] = p;
+    s_exp[p] = (uint8_t)e;
   }
   __syncthreads();
   for (int c = wave; c < nch; c += 16) {  // per-chunk counts (one lane per expert present writes)
@@ -1381,7 +1367,9 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
                        (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
     if (rc) return rc;
-    if (!t64 && (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st))) return rc;
+    if ((!t64 || p.grouped) &&  // the per-pair t64 kernels select the top-k themselves
+        (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
+      return rc;
   }
   const int64_t P = T * L->top_k;
 

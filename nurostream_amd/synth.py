@@ -130,19 +130,42 @@ def zipf_router_bias(n_expert: int, s: float = 1.1, c: float = 1.0, seed: int = 
     return (c * torch.log(p)).float()
 
 
-def zipf_scale(router_w: torch.Tensor) -> float:
-    """c for zipf_router_bias: with h ~ N(0, I) a logit is N(0, |w_e|^2); a
-    Gumbel of the same spread has scale sigma * sqrt(6) / pi, and a bias of
-    scale * log(p_e) under Gumbel noise selects expert e with probability p_e
-    (Plackett-Luce). sigma = the mean row norm of the router."""
-    sigma = router_w.float().norm(dim=1).mean().item()
-    return sigma * math.sqrt(6.0) / math.pi
+def _mean_distinct(logit_fn, n_expert: int, top_k: int, tokens: int, trials: int, seed: int) -> float:
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    tot = 0
+    for _ in range(trials):
+        v = logit_fn(rng)
+        top = np.argpartition(-v, top_k - 1, axis=1)[:, :top_k]
+        tot += len(np.unique(top))
+    return tot / trials
+
+
+def zipf_scale(router_w: torch.Tensor, s: float = 1.1, top_k: int = 4, tokens: int = 128,
+               seed: int = 0) -> float:
+    """c for zipf_router_bias such that top-k routing of `tokens` tokens with
+    x ~ N(0, I) touches as many distinct experts as Gumbel-top-k sampling of
+    Zipf(s) popularity does (Plackett-Luce: the reading of "expert popularity
+    is Zipf(s)"). Logit e of a token is N(0, |w_e|^2); the bias c log p_e is
+    found by bisection on the mean distinct count (seeded simulation)."""
+    import numpy as np
+    E = router_w.shape[0]
+    sig = router_w.float().norm(dim=1).cpu().numpy().astype(np.float64)
+    ranks = np.arange(1, E + 1, dtype=np.float64)
+    logp = np.log(ranks ** (-s) / (ranks ** (-s)).sum())
+    target = _mean_distinct(lambda r: logp + r.gumbel(size=(tokens, E)), E, top_k, tokens, 64, seed)
+    lo, hi = 0.0, 20.0 * float(sig.mean())
+    for _ in range(30):  # more bias -> fewer distinct experts
+        c = 0.5 * (lo + hi)
+        got = _mean_distinct(lambda r: c * logp + r.standard_normal((tokens, E)) * sig, E, top_k, tokens, 64, seed + 1)
+        lo, hi = (c, hi) if got > target else (lo, c)
+    return 0.5 * (lo + hi)
 
 
 def make_zipf_layer(cfg: MoEConfig, seed: int, device, s: float = 1.1, layer: int = 0):
     """make_layer with the router bias replaced by zipf_router_bias (BASELINE
     config 3: expert popularity ~ Zipf(s)); returns (tensors, c)."""
     t = make_layer(cfg, seed, device, layer)
-    c = zipf_scale(t["router_w"])
+    c = zipf_scale(t["router_w"], s=s, top_k=cfg.top_k)
     t["router_b"] = zipf_router_bias(cfg.n_expert, s=s, c=c, seed=layer_seed(seed, layer)).to(device)
     return t, c
