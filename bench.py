@@ -27,6 +27,10 @@ Other workloads (`--workload`, one JSON line each, for the design notes):
   stack-t1      BASELINE config 5: 36 GPT-OSS layers resident (61 GB),
                 x <- x + moe_l(rms_norm(x)) per layer, T=1
   stack-t8      the same at T=8
+  stack-t1-host25, stack-t8-host25
+                BASELINE config 5b: the same stack with a seeded 25% of the
+                512-row expert blocks in pinned host RAM, staged per step
+                (eager: one host synchronisation per layer for the routing)
 
 Prints one JSON line (the driver's contract) with a `roofline` object for the
 dominant kernel (the gate/up dequant-GEMV) and a `cpu_baseline` object: the
@@ -42,7 +46,8 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8")
+WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8", "stack-t1-host25",
+             "stack-t8-host25")
 
 # per workload: (config name, T, steps, warmup, rotating layers or stack depth, profile steps)
 _DEFAULTS = {
@@ -52,6 +57,8 @@ _DEFAULTS = {
     "qwen3-t32": ("QWEN3_235B", 32, 60, 6, 4, 8),
     "stack-t1": ("GPTOSS_120B", 1, 40, 4, 36, 0),
     "stack-t8": ("GPTOSS_120B", 8, 20, 2, 36, 0),
+    "stack-t1-host25": ("GPTOSS_120B", 1, 20, 3, 36, 0),
+    "stack-t8-host25": ("GPTOSS_120B", 8, 10, 2, 36, 0),
 }
 
 
@@ -309,15 +316,20 @@ def layer_workload(args, torch, N, synth, dev):
 
 def stack_workload(args, torch, N, synth, dev):
     """36 resident layers chained x <- x + moe_l(rms_norm(x))."""
-    from nurostream_amd.model.gpt_oss import GptOssFFNStack
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack, GptOssHostStreamedStack
     name = args.workload
     cfg_name, T, K0, W0, L0, _ = _DEFAULTS[name]
     cfg = getattr(synth, cfg_name)
     K = args.steps if args.steps is not None else K0
     W = args.warmup if args.warmup is not None else W0
     n_layers = args.layers if args.layers is not None else L0
-    stack = GptOssFFNStack.synthetic(cfg, n_layers, seed=args.seed, device=dev, layout=args.layout,
-                                     dispatch=args.dispatch)
+    streamed = name.endswith("host25")
+    if streamed:
+        stack = GptOssHostStreamedStack.synthetic(cfg, n_layers, seed=args.seed, device=dev, host_fraction=0.25,
+                                                  block_rows=512, dispatch=args.dispatch)
+    else:
+        stack = GptOssFFNStack.synthetic(cfg, n_layers, seed=args.seed, device=dev, layout=args.layout,
+                                         dispatch=args.dispatch)
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     n_steps = W + K
@@ -328,15 +340,36 @@ def stack_workload(args, torch, N, synth, dev):
         for i in rng:
             stack(X[i], out=Y[i])
 
-    ms_total, wall_s, _ = _graph_time(torch, run_steps, W, K)
+    if streamed:  # host synchronisations inside a step: timed eagerly
+        run_steps(range(W))
+        torch.cuda.synchronize()
+        b0 = stack.bytes_from_host
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_wall = time.perf_counter()
+        ev0.record()
+        run_steps(range(W, W + K))
+        ev1.record()
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - t_wall
+        ms_total = ev0.elapsed_time(ev1)
+        host_bytes_step = (stack.bytes_from_host - b0) / K
+    else:
+        ms_total, wall_s, _ = _graph_time(torch, run_steps, W, K)
     ids, _ = stack.last_routing(T)
     ids_cpu = ids.cpu()
     distinct = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
     mean_distinct = sum(distinct) / len(distinct)
     ms_per_step = ms_total / K
     step_bytes = n_layers * sum(_expert_bytes(cfg, mean_distinct))
+    extra = {}
+    if streamed:
+        host_gb = sum(st.host_bytes for st in stack.stores) / 1e9
+        extra = {"host_resident_GB": round(host_gb, 2), "host_bytes_per_step": int(host_bytes_step),
+                 "pcie_GBps": round(host_bytes_step / (ms_total / K * 1e-3) / 1e9, 1),
+                 "note": "value includes the host-to-device copies (PCIe-inclusive); eager, one host sync per layer"}
     return {
-        "metric": f"MoE-FFN stack tok/s ({n_layers} GPT-OSS-120B-shaped MXFP4 layers, T={T})",
+        "metric": f"MoE-FFN stack tok/s ({n_layers} GPT-OSS-120B-shaped MXFP4 layers, T={T}"
+                  + (", 25% of blocks from pinned host RAM)" if streamed else ")"),
         "value": round(K * T / (ms_total / 1e3), 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -348,11 +381,13 @@ def stack_workload(args, torch, N, synth, dev):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded MXFP4 experts per layer, x~N(0,1)); all expert slabs resident in HBM",
-        "config": {"workload": f"gpt-oss-120b FFN stack, {n_layers} layers, T={T} (BASELINE config 5)",
+        "config": {"workload": f"gpt-oss-120b FFN stack, {n_layers} layers, T={T} (BASELINE config "
+                               + ("5b)" if streamed else "5)"),
                    "tokens_per_step": T, "layers": n_layers, "layout": args.layout, "dispatch": args.dispatch,
-                   "graph": True, "chain": "x <- x + moe_l(rms_norm(x)), unit norm weight, eps 1e-5"},
+                   "graph": not streamed, "chain": "x <- x + moe_l(rms_norm(x)), unit norm weight, eps 1e-5"},
         "resident_GB": round(n_layers * cfg.n_expert * sum(cfg.expert_bytes(k) for k in ("gate", "up", "down"))
-                             / 1e9, 2),
+                             / 1e9 - extra.get("host_resident_GB", 0.0), 2),
+        **extra,
         "distinct_experts_per_layer": round(mean_distinct, 2),
         "expert_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "roofline_tok_s": round(T / (step_bytes / (HBM_PEAK_GBS * 1e9)), 1),

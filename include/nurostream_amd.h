@@ -177,6 +177,24 @@ int nsx_add_rmsnorm(const float *x, const float *r, int64_t T, int64_t n,
                     float eps, const float *w, float *sum, float *y,
                     void *stream);
 
+/* Expert blocks split between HBM and pinned host RAM (BASELINE config 5b).
+ * nsx_copy_blocks_async: dst[i] <- src[i] (bytes[i]) for n segments, each a
+ * DMA copy on `stream` (host-to-device from pinned memory, or any direct
+ * copy), then `event` (a hipEvent_t, may be NULL) is recorded on the stream.
+ * The block prefetcher's host-to-device step: io/stream.py:200-216
+ * submit_rows and compute/blockffn.py:341-378 (SURVEY's copy_block_async).
+ * nsx_gather_copy: the same for device-to-device segments (16-byte aligned
+ * addresses and sizes), as one kernel per 128 segments. Every destination
+ * (and gather source) range is checked to lie inside one device allocation
+ * (hipMemGetAddressRange: for memory from a caching allocator that is the
+ * allocator's segment, so staying inside the intended buffer is the
+ * caller's contract). The segment arrays are host arrays, read during the
+ * call. */
+int nsx_copy_blocks_async(int64_t n, const uint64_t *src, const uint64_t *dst,
+                          const int64_t *bytes, void *stream, void *event);
+int nsx_gather_copy(int64_t n, const uint64_t *src, const uint64_t *dst,
+                    const int64_t *bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,8 @@ _SIGS = {
     "nsx_moe_forward": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p, _i64, _p]),
     "nsx_moe_phase": (_i, [C.POINTER(MoeLayerC), _i, _p, _i64, _p, _p, _p, _p, _i64, _p]),
     "nsx_add_rmsnorm": (_i, [_p, _p, _i64, _i64, C.c_float, _p, _p, _p, _p]),
+    "nsx_copy_blocks_async": (_i, [_i64, _p, _p, _p, _p, _p]),
+    "nsx_gather_copy": (_i, [_i64, _p, _p, _p, _p]),
 }
 PHASE_ROUTER, PHASE_GATE_UP, PHASE_DOWN, PHASE_COMBINE = 0, 1, 2, 3
 

@@ -1493,3 +1493,88 @@ extern "C" int nsx_add_rmsnorm(const float* x, const float* r, int64_t T, int64_
   return nsx_launch(add_rmsnorm_kernel, dim3((unsigned)T), dim3(NORM_THREADS), 0, S(stream), x, r, (int)n, eps, w, sum,
                     y);
 }
+
+// ---------------------------------------------------------------------------
+// Staging expert matrices whose blocks are split between HBM and pinned host
+// RAM (BASELINE config 5b): host blocks go device-ward as DMA copies
+// (nsx_copy_blocks_async, the block prefetcher's host-to-device step,
+// compute/blockffn.py:278-393 + io/stream.py:200-216), HBM-resident blocks
+// as one gather kernel (nsx_gather_copy). Every destination range is checked
+// on the host against its device allocation before anything is queued.
+
+constexpr int GATHER_CHUNK = 16384;  // bytes per workgroup
+constexpr int GATHER_MAX = 128;      // segments per launch (kernel arguments: 2.5 KB)
+
+struct GatherList {
+  uint64_t src[GATHER_MAX], dst[GATHER_MAX];
+  uint32_t n16[GATHER_MAX];  // 16-byte units
+  int n;
+};
+
+__global__ __launch_bounds__(256) void gather_copy_kernel(GatherList L) {
+  const int s = blockIdx.y;
+  if (s >= L.n) return;
+  const uint4* src = (const uint4*)L.src[s];
+  uint4* dst = (uint4*)L.dst[s];
+  const int64_t n16 = L.n16[s];
+  const int64_t c0 = (int64_t)blockIdx.x * (GATHER_CHUNK / 16);
+#pragma unroll
+  for (int i = 0; i < GATHER_CHUNK / 16 / 256; ++i) {
+    const int64_t j = c0 + i * 256 + threadIdx.x;
+    if (j < n16) dst[j] = src[j];
+  }
+}
+
+// [p, p + bytes) inside one device allocation
+static int check_dev_range(const void* p, int64_t bytes, const char* what, int64_t i) {
+  void* base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (void*)p) != hipSuccess || base == nullptr) {
+    (void)hipGetLastError();
+    return nsx_fail(NSX_EINVAL, "%s of segment %lld is not device memory", what, (long long)i);
+  }
+  NSX_REQUIRE((const char*)p + bytes <= (const char*)base + size, NSX_EINVAL,
+              "%s of segment %lld runs past its allocation", what, (long long)i);
+  return NSX_OK;
+}
+
+extern "C" int nsx_copy_blocks_async(int64_t n, const uint64_t* src, const uint64_t* dst, const int64_t* bytes,
+                                     void* stream, void* event) {
+  NSX_REQUIRE(n >= 0 && (n == 0 || (src && dst && bytes)), NSX_EINVAL, "bad segment list");
+  for (int64_t i = 0; i < n; ++i) {
+    NSX_REQUIRE(bytes[i] >= 0 && src[i] && dst[i], NSX_EINVAL, "segment %lld", (long long)i);
+    if (bytes[i] == 0) continue;
+    int rc = check_dev_range((const void*)dst[i], bytes[i], "destination", i);
+    if (rc) return rc;
+    NSX_HIP(hipMemcpyAsync((void*)dst[i], (const void*)src[i], (size_t)bytes[i], hipMemcpyDefault, S(stream)));
+  }
+  if (event) NSX_HIP(hipEventRecord((hipEvent_t)event, S(stream)));
+  return NSX_OK;
+}
+
+extern "C" int nsx_gather_copy(int64_t n, const uint64_t* src, const uint64_t* dst, const int64_t* bytes,
+                               void* stream) {
+  NSX_REQUIRE(n >= 0 && (n == 0 || (src && dst && bytes)), NSX_EINVAL, "bad segment list");
+  for (int64_t i0 = 0; i0 < n; i0 += GATHER_MAX) {
+    GatherList L{};
+    int64_t max_chunks = 1;
+    for (int64_t i = i0; i < std::min(n, i0 + GATHER_MAX); ++i) {
+      NSX_REQUIRE(bytes[i] >= 0 && bytes[i] % 16 == 0 && bytes[i] < (16ll << 32) && src[i] % 16 == 0 &&
+                      dst[i] % 16 == 0,
+                  NSX_EINVAL, "segment %lld: 16-byte aligned addresses and sizes required", (long long)i);
+      if (bytes[i] > 0) {
+        int rc = check_dev_range((const void*)src[i], bytes[i], "source", i);
+        if (rc) return rc;
+        if ((rc = check_dev_range((const void*)dst[i], bytes[i], "destination", i))) return rc;
+      }
+      L.src[L.n] = src[i];
+      L.dst[L.n] = dst[i];
+      L.n16[L.n] = (uint32_t)(bytes[i] >> 4);
+      ++L.n;
+      max_chunks = std::max<int64_t>(max_chunks, nsx_cdiv(bytes[i], GATHER_CHUNK));
+    }
+    int rc = nsx_launch(gather_copy_kernel, dim3((unsigned)max_chunks, (unsigned)L.n), dim3(256), 0, S(stream), L);
+    if (rc) return rc;
+  }
+  return NSX_OK;
+}

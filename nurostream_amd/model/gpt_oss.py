@@ -15,6 +15,7 @@ torch.unique(...).tolist() at gpt_oss.py:121).
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
 
 import torch
@@ -134,3 +135,178 @@ class GptOssFFNStack:
                                    router_mode=cfg.router_mode, act=cfg.act, dispatch=dispatch))
             del t, mats
         return cls(layers)
+
+
+class _HostBlockStore:
+    """One layer's expert matrices (t64 tiles) split into row blocks, a seeded
+    share of which lives in pinned host RAM instead of HBM.
+
+    Per projection: `dev` holds the HBM-resident blocks and `host` the others,
+    each packed in (expert, block) order. An expert with no host block is one
+    contiguous run of `dev` and is used in place; the others are assembled
+    per step into a staging slot."""
+
+    def __init__(self, full: dict, rows: dict, K: dict, n_expert: int, block_rows: int, host_fraction: float,
+                 rng, device) -> None:
+        from .. import _native as N
+        if block_rows <= 0 or block_rows % 64:
+            raise ValueError(f"block_rows {block_rows}: a positive multiple of the 64-row tile")
+        lib = N.load()
+        self.kinds = tuple(full)
+        self.per, self.blocks, self.dev, self.host, self.where, self.whole = {}, {}, {}, {}, {}, {}
+        self.host_bytes = 0
+        for kind in self.kinds:
+            per = lib.nsx_t64_bytes(39, rows[kind], K[kind])
+            rb = per // (-(-rows[kind] // 64) * 64)  # bytes per (padded) row
+            spans = [(r0, min(rows[kind], r0 + block_rows)) for r0 in range(0, rows[kind], block_rows)]
+            # byte extent of a block of rows [r0, r1): whole 64-row tiles
+            ext = [(r0 * rb, (-(-r1 // 64) * 64) * rb) for r0, r1 in spans]
+            host = rng.random((n_expert, len(spans))) < host_fraction
+            nd = int(sum((b1 - b0) for e in range(n_expert) for i, (b0, b1) in enumerate(ext) if not host[e, i]))
+            nh = int(sum((b1 - b0) for e in range(n_expert) for i, (b0, b1) in enumerate(ext) if host[e, i]))
+            dev = torch.empty(max(nd, 16), dtype=torch.uint8, device=device)
+            hst = torch.empty(max(nh, 16), dtype=torch.uint8, pin_memory=True)
+            where, od, oh = {}, 0, 0
+            src = full[kind]
+            for e in range(n_expert):
+                for i, (b0, b1) in enumerate(ext):
+                    n = b1 - b0
+                    blk = src[e * per + b0:e * per + b1]
+                    if host[e, i]:
+                        hst[oh:oh + n].copy_(blk)
+                        where[(e, i)] = ("host", oh, b0, n)
+                        oh += n
+                    else:
+                        dev[od:od + n].copy_(blk)
+                        where[(e, i)] = ("dev", od, b0, n)
+                        od += n
+            self.per[kind], self.blocks[kind] = per, len(spans)
+            self.dev[kind], self.host[kind], self.where[kind] = dev, hst, where
+            self.whole[kind] = [not host[e].any() for e in range(n_expert)]
+            self.host_bytes += nh
+        torch.cuda.synchronize(device)
+
+    def address(self, kind: str, e: int) -> int | None:
+        """Device address of expert e's whole matrix when all of it is in HBM."""
+        if not self.whole[kind][e]:
+            return None
+        return self.dev[kind].data_ptr() + self.where[kind][(e, 0)][1]
+
+
+class GptOssHostStreamedStack(GptOssFFNStack):
+    """BASELINE config 5b: the FFN stack with a seeded share (25%) of the
+    experts' row blocks in pinned host RAM.
+
+    Per layer and step: the router runs on the device and its ids come to the
+    host (model/gpt_oss.py:121 does the same to pick its windows); every
+    chosen expert matrix with host blocks is assembled in a staging slot --
+    its host blocks as DMA copies from pinned RAM (nsx_copy_blocks_async, all
+    of the layer's blocks queued at once), its HBM blocks as one gather kernel
+    (nsx_gather_copy) -- and the layer's expert address table points at the
+    slots for this step. The experts then run in the same fused kernels as
+    the resident stack: outputs are identical to it."""
+
+    def __init__(self, layers, stores, eps: float = 1e-5) -> None:
+        super().__init__(layers, eps=eps)
+        self.stores = stores
+        n_slots = min(self.cfg.n_expert, 64)
+        self._slots = {k: torch.empty(n_slots * stores[0].per[k], dtype=torch.uint8, device=self.device)
+                       for k in stores[0].kinds}
+        self._tables = [{k: torch.empty(self.cfg.n_expert, dtype=torch.int64, pin_memory=True)
+                         for k in stores[0].kinds} for _ in layers]
+        # per step every entry starts at valid full-size memory: the expert itself or slot 0
+        self._default = [{k: torch.tensor([st.address(k, e) or self._slots[k].data_ptr()
+                                           for e in range(self.cfg.n_expert)], dtype=torch.int64)
+                          for k in st.kinds} for st in stores]
+        self.bytes_from_host = 0
+
+    def _stage(self, li: int, chosen) -> None:
+        from .. import _native as N
+        st, layer, lib = self.stores[li], self.layers[li], N.load()
+        hs, hd, hl, gs, gd, gl = [], [], [], [], [], []
+        for kind in st.kinds:
+            table = self._tables[li][kind]
+            slot_base, per = self._slots[kind].data_ptr(), st.per[kind]
+            n_slots = self._slots[kind].numel() // per
+            used = 0
+            table.copy_(self._default[li][kind])
+            for e in chosen:
+                if st.whole[kind][e]:
+                    continue
+                if used >= n_slots:
+                    raise RuntimeError(f"more than {n_slots} staged experts in one layer")
+                dst = slot_base + used * per
+                used += 1
+                for i in range(st.blocks[kind]):
+                    loc, off, b0, n = st.where[kind][(e, i)]
+                    if loc == "host":
+                        hs.append(st.host[kind].data_ptr() + off); hd.append(dst + b0); hl.append(n)
+                    else:
+                        gs.append(st.dev[kind].data_ptr() + off); gd.append(dst + b0); gl.append(n)
+                table[e] = dst
+        s = N.stream_ptr(self.device)
+        arr = lambda v: (C.c_uint64 * len(v))(*v)  # noqa: E731
+        lens = lambda v: (C.c_int64 * len(v))(*v)  # noqa: E731
+        with torch.cuda.device(self.device):
+            N.check(lib.nsx_copy_blocks_async(len(hs), arr(hs), arr(hd), lens(hl), s, None), "copy_blocks_async")
+            N.check(lib.nsx_gather_copy(len(gs), arr(gs), arr(gd), lens(gl), s), "gather_copy")
+            for kind, dev_table in (("gate", layer.gate_ptrs), ("up", layer.up_ptrs), ("down", layer.down_ptrs)):
+                dev_table.copy_(self._tables[li][kind], non_blocking=True)
+        self.bytes_from_host += sum(hl)
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """As GptOssFFNStack.forward; one host synchronisation per layer (routing)."""
+        from ..moe.fused import router_topk
+        x = x.reshape(-1, self.cfg.n_embd)
+        T = x.shape[0]
+        h, y, ids, wts = self._buffers(T)
+        res = torch.empty_like(x) if out is None else out
+        eps = self.cfg.rms_eps
+        add_rms_norm(x.float().contiguous(), None, self.norm_weights[0], eps, out=h, sum_out=res)
+        for li, layer in enumerate(self.layers):
+            rid, _, _ = router_topk(h, layer.router_w, layer.router_b, layer.top_k, "gptoss")
+            chosen = torch.unique(rid).tolist()  # device -> host, as the reference
+            self._stage(li, chosen)
+            layer.forward(h, out=y, ids=ids[li], weights=wts[li])
+            if li + 1 < len(self.layers):
+                add_rms_norm(res, y, self.norm_weights[li + 1], eps, out=h, sum_out=res)
+            else:
+                res.add_(y)
+        return res
+
+    __call__ = forward
+
+    @classmethod
+    def synthetic(cls, cfg, n_layers: int, seed: int, device, host_fraction: float = 0.25, block_rows: int = 512,
+                  dispatch: str = "auto"):
+        """BASELINE config 5b: the layers of GptOssFFNStack.synthetic with a
+        seeded host_fraction of their block_rows-row blocks in pinned RAM."""
+        import numpy as np
+        from .. import synth
+        from ..compute.kernels import t64_pack_stacked
+        layers, stores = [], []
+        for li in range(n_layers):
+            t = synth.make_layer(cfg, seed=seed, device=device, layer=li)
+            full = {k: t64_pack_stacked(t[k], cfg.ggml_type, cfg.n_expert, *cfg.rows_K(k))
+                    for k in ("gate", "up", "down")}
+            for k in ("gate", "up", "down"):
+                t[k] = None
+            rng = np.random.default_rng(synth.layer_seed(seed, li) + 99991)
+            st = _HostBlockStore(full, {k: cfg.rows_K(k)[0] for k in full}, {k: cfg.rows_K(k)[1] for k in full},
+                                 cfg.n_expert, block_rows, host_fraction, rng, device)
+            del full
+            views = {}
+            for k in st.kinds:
+                per = st.per[k]
+                views[k] = [st.dev[k][st.where[k][(e, 0)][1]:st.where[k][(e, 0)][1] + per] if st.whole[k][e]
+                            else None for e in range(cfg.n_expert)]
+            slot0 = {k: torch.empty(st.per[k], dtype=torch.uint8, device=device) for k in st.kinds}
+            mats = {k: [v if v is not None else slot0[k] for v in views[k]] for k in st.kinds}
+            layers.append(MoELayer(ggml_type=cfg.ggml_type, n_expert=cfg.n_expert, top_k=cfg.top_k,
+                                   n_embd=cfg.n_embd, n_ff=cfg.n_ff, router_w=t["router_w"], router_b=t["router_b"],
+                                   gate=mats["gate"], up=mats["up"], down=mats["down"], gate_b=t["gate_b"],
+                                   up_b=t["up_b"], down_b=t["down_b"], layout="t64",
+                                   router_mode=cfg.router_mode, act=cfg.act, dispatch=dispatch))
+            stores.append(st)
+            del t
+        return cls(layers, stores)

@@ -99,3 +99,51 @@ def test_qwen3_moe_ffn_over_cache(dev, T):
     assert sum(st.hits.values()) == T * cfg.top_k
     assert src.arena.used == 0
     assert cache.stats.slab_hits > 0
+
+
+@pytest.mark.parametrize("T,frac", [(1, 0.5), (5, 0.25), (9, 1.0)])
+def test_host_streamed_stack_equals_resident(dev, T, frac):
+    """BASELINE config 5b on a small stack: with a share of the row blocks in
+    pinned host RAM, staged per step, the outputs equal the resident stack's."""
+    from nurostream_amd import synth
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack, GptOssHostStreamedStack
+    cfg = _small("gptoss-small")
+    L = 3
+    res = GptOssFFNStack.synthetic(cfg, L, seed=31, device=dev)
+    hs = GptOssHostStreamedStack.synthetic(cfg, L, seed=31, device=dev, host_fraction=frac, block_rows=64)
+    assert sum(st.host_bytes for st in hs.stores) > 0
+    x = synth.activations(T, cfg.n_embd, seed=40 + T, device=dev)
+    for _ in range(2):  # a second step reuses the slots and tables
+        y_res = res(x)
+        y_hs = hs(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y_res, y_hs)
+    assert hs.bytes_from_host > 0
+
+
+def test_gather_and_block_copies_check_ranges(dev):
+    from nurostream_amd import _native as N
+    import ctypes as C
+    lib = N.load()
+    a = torch.arange(4096, dtype=torch.uint8, device=dev)
+    b = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    h = torch.arange(256, dtype=torch.uint8).pin_memory()
+    u64 = lambda *v: (C.c_uint64 * len(v))(*v)  # noqa: E731
+    i64 = lambda *v: (C.c_int64 * len(v))(*v)  # noqa: E731
+    s = N.stream_ptr(dev)
+    assert lib.nsx_gather_copy(2, u64(a.data_ptr(), a.data_ptr() + 1024), u64(b.data_ptr() + 16, b.data_ptr() + 2048),
+                               i64(512, 1024), s) == N.OK
+    assert lib.nsx_copy_blocks_async(1, u64(h.data_ptr()), u64(b.data_ptr() + 3840), i64(256), s, None) == N.OK
+    torch.cuda.synchronize()
+    assert torch.equal(b[16:528], a[:512]) and torch.equal(b[2048:3072], a[1024:2048])
+    assert torch.equal(b[3840:].cpu(), h)
+    # misaligned, or past the end of the device allocation (a segment of its
+    # own: the check sees allocations, not tensors): rejected before any copy
+    assert lib.nsx_gather_copy(1, u64(a.data_ptr() + 8), u64(b.data_ptr()), i64(16), s) == N.EINVAL
+    torch.cuda.empty_cache()
+    big = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    end = big.data_ptr() + big.numel()
+    assert lib.nsx_gather_copy(1, u64(a.data_ptr()), u64(end - 512), i64(1024), s) == N.EINVAL
+    assert lib.nsx_copy_blocks_async(1, u64(h.data_ptr()), u64(end - 128), i64(256), s, None) == N.EINVAL
+    torch.cuda.synchronize()
+    assert int(big.sum()) == 0
