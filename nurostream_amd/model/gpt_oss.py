@@ -153,7 +153,9 @@ class _HostBlockStore:
             raise ValueError(f"block_rows {block_rows}: a positive multiple of the 64-row tile")
         lib = N.load()
         self.kinds = tuple(full)
+        import numpy as np
         self.per, self.blocks, self.dev, self.host, self.where, self.whole = {}, {}, {}, {}, {}, {}
+        self.segs = {}
         self.host_bytes = 0
         for kind in self.kinds:
             per = lib.nsx_t64_bytes(39, rows[kind], K[kind])
@@ -184,6 +186,19 @@ class _HostBlockStore:
             self.dev[kind], self.host[kind], self.where[kind] = dev, hst, where
             self.whole[kind] = [not host[e].any() for e in range(n_expert)]
             self.host_bytes += nh
+            # per expert with host blocks: (host src addresses, dst offsets in a slot, bytes) and the
+            # same for its HBM blocks (gather), as int64 arrays ready for the C calls
+            hp, dp = hst.data_ptr(), dev.data_ptr()
+            segs = {}
+            for e in range(n_expert):
+                if self.whole[kind][e]:
+                    continue
+                h_, g_ = [], []
+                for i in range(len(spans)):
+                    loc, off, b0, n = where[(e, i)]
+                    (h_ if loc == "host" else g_).append((hp + off if loc == "host" else dp + off, b0, n))
+                segs[e] = tuple(np.array(v, dtype=np.int64).reshape(-1, 3) for v in (h_, g_))
+            self.segs[kind] = segs
         torch.cuda.synchronize(device)
 
     def address(self, kind: str, e: int) -> int | None:
@@ -219,40 +234,55 @@ class GptOssHostStreamedStack(GptOssFFNStack):
                                            for e in range(self.cfg.n_expert)], dtype=torch.int64)
                           for k in st.kinds} for st in stores]
         self.bytes_from_host = 0
+        # host blocks spread over several copy streams (default priority), so
+        # several DMA engines share the PCIe link
+        self._copy_streams = [torch.cuda.Stream(self.device) for _ in range(self.COPY_STREAMS)]
+
+    COPY_STREAMS = 4
 
     def _stage(self, li: int, chosen) -> None:
+        import numpy as np
         from .. import _native as N
         st, layer, lib = self.stores[li], self.layers[li], N.load()
-        hs, hd, hl, gs, gd, gl = [], [], [], [], [], []
+        hseg, gseg = [], []
         for kind in st.kinds:
             table = self._tables[li][kind]
             slot_base, per = self._slots[kind].data_ptr(), st.per[kind]
             n_slots = self._slots[kind].numel() // per
-            used = 0
             table.copy_(self._default[li][kind])
+            used = 0
             for e in chosen:
-                if st.whole[kind][e]:
+                seg = st.segs[kind].get(e)
+                if seg is None:
                     continue
                 if used >= n_slots:
                     raise RuntimeError(f"more than {n_slots} staged experts in one layer")
                 dst = slot_base + used * per
                 used += 1
-                for i in range(st.blocks[kind]):
-                    loc, off, b0, n = st.where[kind][(e, i)]
-                    if loc == "host":
-                        hs.append(st.host[kind].data_ptr() + off); hd.append(dst + b0); hl.append(n)
-                    else:
-                        gs.append(st.dev[kind].data_ptr() + off); gd.append(dst + b0); gl.append(n)
+                for lst, arr in zip((hseg, gseg), seg):
+                    if len(arr):
+                        a = arr.copy()
+                        a[:, 1] += dst
+                        lst.append(a)
                 table[e] = dst
+        H = np.concatenate(hseg) if hseg else np.zeros((0, 3), np.int64)
+        G = np.concatenate(gseg) if gseg else np.zeros((0, 3), np.int64)
         s = N.stream_ptr(self.device)
-        arr = lambda v: (C.c_uint64 * len(v))(*v)  # noqa: E731
-        lens = lambda v: (C.c_int64 * len(v))(*v)  # noqa: E731
+        col = lambda a, j: np.ascontiguousarray(a[:, j]).ctypes.data_as(C.c_void_p)  # noqa: E731
         with torch.cuda.device(self.device):
-            N.check(lib.nsx_copy_blocks_async(len(hs), arr(hs), arr(hd), lens(hl), s, None), "copy_blocks_async")
-            N.check(lib.nsx_gather_copy(len(gs), arr(gs), arr(gd), lens(gl), s), "gather_copy")
+            cur = torch.cuda.current_stream(self.device)
+            ns = len(self._copy_streams)
+            for i, cs in enumerate(self._copy_streams[:len(H)]):
+                part = H[i::ns]
+                cs.wait_stream(cur)  # the slots are free once the work queued so far is done
+                N.check(lib.nsx_copy_blocks_async(len(part), col(part, 0), col(part, 1), col(part, 2),
+                                                  cs.cuda_stream, None), "copy_blocks_async")
+            N.check(lib.nsx_gather_copy(len(G), col(G, 0), col(G, 1), col(G, 2), s), "gather_copy")
+            for cs in self._copy_streams[:len(H)]:
+                cur.wait_stream(cs)
             for kind, dev_table in (("gate", layer.gate_ptrs), ("up", layer.up_ptrs), ("down", layer.down_ptrs)):
                 dev_table.copy_(self._tables[li][kind], non_blocking=True)
-        self.bytes_from_host += sum(hl)
+        self.bytes_from_host += int(H[:, 2].sum()) if len(H) else 0
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """As GptOssFFNStack.forward; one host synchronisation per layer (routing)."""
