@@ -1,0 +1,145 @@
+"""Public surface of the reference (api.py:30-237, 342-388) over this build's MoE path.
+
+    ns = NeuroStream.load("model.gguf", mem_budget="2GB", slab_budget="60GB")
+    y = ns.model.ffn_stack(x)          # every layer's routed-expert FFN block
+    ns.pin_hot_experts()
+
+`NeuroStream.load` keeps the reference's keyword arguments and their meaning
+for the parts this build covers: the arena budget (`mem_budget`), VRAM/RAM
+tiers, expert slabs in HBM (`slab_budget`, admitted in layer order as t64
+tiles), `block_rows` and `expert_lookahead` for the streamed neuron path.
+`generate` needs the token embedding, attention (sink attention with YaRN
+RoPE), the output norm, the LM head and the tokenizer, which this build does
+not implement: it raises NotImplementedError instead of producing tokens.
+"""
+from __future__ import annotations
+
+import re
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+
+from .compute.blockffn import DEFAULT_BLOCK_ROWS, DEFAULT_LOOKAHEAD
+from .format.gguf import FLOAT_TYPES, row_geometry
+from .io.arena import Arena
+from .io.source import GGUFSource
+from .residency.cache import TieredCache
+
+_SIZE_RE = re.compile(r"^\s*([\d.]+)\s*([KMGT]?)B?\s*$", re.I)
+_MULT = {"": 1, "K": 1 << 10, "M": 1 << 20, "G": 1 << 30, "T": 1 << 40}
+
+
+def parse_size(v: int | str) -> int:
+    """api.py:30-37: ints pass through; "2GB", "1.5G", "512M", "64K" (powers of 1024)."""
+    if isinstance(v, int):
+        return v
+    m = _SIZE_RE.match(v)
+    if not m:
+        raise ValueError(f"cannot parse size: {v!r}")
+    return int(float(m.group(1)) * _MULT[m.group(2).upper()])
+
+
+@dataclass
+class GenerationStats:
+    prompt_tokens: int = 0
+    generated_tokens: int = 0
+    prefill_seconds: float = 0.0
+    decode_seconds: float = 0.0
+
+    @property
+    def tokens_per_second(self) -> float:
+        return 0.0 if self.decode_seconds <= 0 else self.generated_tokens / self.decode_seconds
+
+
+_EXPERT_TENSORS = ("ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight")
+
+
+class NeuroStream:
+    def __init__(self, path: str | Path, mem_budget: int | str = "2GB", vram_budget: int | str = 0,
+                 ram_budget: int | str = 0, device: str | None = None, compute_dtype: torch.dtype | None = None,
+                 block_rows: int = DEFAULT_BLOCK_ROWS, n_workers: int = 16, prefetch_depth: int = 1,
+                 reserve_vram: int | str = "1.5GB", slab_budget: int | str = 0, strict_neuron: bool = False,
+                 expert_lookahead: int = DEFAULT_LOOKAHEAD, verbose: bool = False) -> None:
+        from .model.gpt_oss import GptOssModel, MoEModelConfig
+        if device is None:
+            device = "cuda" if torch.cuda.is_available() else "cpu"
+        self.device = device
+        self.dtype = compute_dtype or torch.float32
+        self.verbose = verbose
+        self.arena = Arena(parse_size(mem_budget))
+        self.source = GGUFSource(path, self.arena, device=device)
+        self.gguf = self.source.gguf
+        arch = self.gguf.arch()
+        if arch != "gpt-oss":
+            raise ValueError(f"unsupported architecture: {arch} (this build runs GPT-OSS MoE FFN stacks; "
+                             "Qwen3 MoE layers run through nurostream_amd.model.qwen3 / moe.router.moe_ffn)")
+        self.cfg = MoEModelConfig.from_gguf(self.gguf)
+        self.cache = TieredCache(self.source, device=device, compute_dtype=self.dtype,
+                                 vram_budget=parse_size(vram_budget), ram_budget=parse_size(ram_budget))
+        self.cache.slab_budget = parse_size(slab_budget)
+        if self.cache.slab_budget:
+            self._admit_experts()
+        self.model = GptOssModel(self.cache, self.cfg, device, self.dtype, block_rows=block_rows,
+                                 expert_lookahead=expert_lookahead)
+        self.stats = GenerationStats()
+
+    @classmethod
+    def load(cls, path: str | Path, **kw) -> "NeuroStream":
+        return cls(path, **kw)
+
+    def _expert_slabs(self, layer: int, e: int):
+        """[(name, lo, hi, bytes)] of expert e's three matrices in `layer` not yet in HBM."""
+        c, out = self.cfg, []
+        for nm, rpe in zip(_EXPERT_TENSORS, (c.n_ffn_expert, c.n_ffn_expert, c.n_embd)):
+            name = f"blk.{layer}.{nm}"
+            if name not in self.gguf.tensors:
+                continue
+            lo, hi = e * rpe, (e + 1) * rpe
+            if self.cache.is_resident(name) or self.cache.has_slab(name, lo, hi):
+                continue
+            info = self.gguf.tensors[name]
+            if info.dtype in FLOAT_TYPES:
+                continue
+            out.append((name, lo, hi, rpe * row_geometry(info)[2]))
+        return out
+
+    def _admit(self, slabs) -> bool:
+        """All of an expert's slabs or none (api.py:364-386: a partial expert
+        must not consume the budget)."""
+        need = sum(s[3] for s in slabs)
+        if not slabs or need > self.cache.slab_budget - self.cache.slab_bytes:
+            return False
+        for name, lo, hi, _ in slabs:
+            self.cache.admit_slab(name, lo, hi)
+        return True
+
+    def _admit_experts(self) -> int:
+        """Expert slabs into HBM in layer order until the slab budget is spent."""
+        n = 0
+        for layer in range(self.cfg.n_layer):
+            for e in range(self.cfg.n_expert):
+                n += self._admit(self._expert_slabs(layer, e))
+        if self.verbose:
+            print(f"  {n} expert slabs resident ({self.cache.slab_bytes / 1e9:.2f}GB)", flush=True)
+        return n
+
+    def pin_hot_experts(self, verbose: bool = False) -> int:
+        """api.py:342-388: promote the most-routed experts' three slabs into HBM,
+        busiest first, skipping experts that do not fit whole."""
+        rs = getattr(self.model, "router_stats", None)
+        if rs is None or not self.cache.slab_budget:
+            return 0
+        pinned = 0
+        for (layer, e), _count in rs.hits.most_common():
+            pinned += self._admit(self._expert_slabs(layer, e))
+        if verbose:
+            print(f"  pinned {pinned} expert slabs ({self.cache.slab_bytes / 1e9:.2f}GB)", flush=True)
+        return pinned
+
+    def generate(self, prompt, max_tokens: int = 128, temperature: float = 0.0, top_p: float = 0.95,
+                 stop_on_eos: bool = True):
+        raise NotImplementedError(
+            "generate() needs the token embedding, attention (sink attention with YaRN RoPE), the output norm, "
+            "the LM head and the tokenizer; this build implements the MoE expert path only "
+            "(NeuroStream.model.ffn_stack / _ffn_block)")

@@ -193,8 +193,9 @@ class GGUFSource(HostSource):
             for name, info in g.tensors.items():
                 if names is not None and name not in names:
                     continue
-                arr = np.frombuffer(mm, dtype=np.uint8, count=info.nbytes, offset=g.file_offset(info))
-                tensors[name] = (info, torch.from_numpy(arr.copy()))
+                view = np.frombuffer(mm, dtype=np.uint8, count=info.nbytes, offset=g.file_offset(info))
+                tensors[name] = (info, torch.from_numpy(view.copy()))
+                del view  # no export of the map may outlive it
         finally:
             mm.close()
             fh.close()

@@ -340,3 +340,137 @@ class GptOssHostStreamedStack(GptOssFFNStack):
             stores.append(st)
             del t
         return cls(layers, stores)
+
+
+@dataclass
+class MoEModelConfig:
+    """The MoE-path subset of the reference's model config (model/qwen3.py,
+    from_gguf: the same GGUF keys)."""
+    n_layer: int
+    n_embd: int
+    n_expert: int
+    n_expert_used: int
+    n_ffn_expert: int
+    rms_eps: float = 1e-6
+
+    @classmethod
+    def from_gguf(cls, g) -> "MoEModelConfig":
+        n_ffn = int(g.cfg("feed_forward_length", 0) or 0)
+        return cls(n_layer=int(g.cfg("block_count")), n_embd=int(g.cfg("embedding_length")),
+                   n_expert=int(g.cfg("expert_count", 0) or 0), n_expert_used=int(g.cfg("expert_used_count", 0) or 0),
+                   n_ffn_expert=int(g.cfg("expert_feed_forward_length", 0) or 0) or n_ffn,
+                   rms_eps=float(g.cfg("attention.layer_norm_rms_epsilon", 1e-6)))
+
+
+class GptOssModel:
+    """The routed-expert FFN blocks of a GPT-OSS GGUF over a TieredCache
+    (model/gpt_oss.py:97-177 of the reference).
+
+    `_ffn_block(x, layer)` = x + moe(rms_norm(x, post_attention_norm)):
+      * when every expert of the layer has its three slabs in HBM (t64), one
+        fused MoE layer call over the slabs' addresses (no host sync);
+      * otherwise the reference's neuron path: route (ids to the host), one
+        BlockPrefetcher plan for the layer, stream_expert_ffn per chosen expert
+        in ascending id, out[rows] += w_e * y_e -- every block product on the
+        HIP GEMV, slab hits in place, the rest streamed through submit_rows.
+    """
+
+    def __init__(self, cache, cfg: MoEModelConfig, device, dtype=torch.float32, block_rows: int = 1024,
+                 expert_lookahead: int = 2) -> None:
+        self.cache = cache
+        self.gguf = cache.gguf
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.block_rows = block_rows
+        self.expert_lookahead = expert_lookahead
+        self.router_stats = RouterStats()
+        self.neuron_callback = None
+        self._w: dict[str, torch.Tensor] = {}
+        self._fused: dict[int, MoELayer] = {}
+
+    def w(self, name: str) -> torch.Tensor:
+        t = self._w.get(name)
+        if t is None:
+            t = self.cache.get(name).to(self.device, torch.float32)
+            self._w[name] = t
+        return t
+
+    def has(self, name: str) -> bool:
+        return name in self.gguf.tensors
+
+    def _route(self, h: torch.Tensor, layer: int):
+        """(chosen (host list, ascending), ids (T, k) int64, weights (T, k)), gpt_oss.py:116-121."""
+        from ..moe.fused import router_topk
+        p = f"blk.{layer}.ffn_gate_inp"
+        bias = self.w(p + ".bias") if self.has(p + ".bias") else None
+        ids, wts, _ = router_topk(h, self.w(p + ".weight"), bias, self.cfg.n_expert_used, "gptoss")
+        return torch.unique(ids).tolist(), ids.long(), wts
+
+    def _fused_layer(self, layer: int) -> MoELayer | None:
+        """A MoELayer over this layer's t64 slabs when all 3 x n_expert are admitted."""
+        lay = self._fused.get(layer)
+        if lay is not None:
+            return lay
+        c, p = self.cfg, f"blk.{layer}."
+        mats = {}
+        for kind, rpe in (("gate", c.n_ffn_expert), ("up", c.n_ffn_expert), ("down", c.n_embd)):
+            slabs = []
+            for e in range(c.n_expert):
+                ent = self.cache.slab_entry(p + f"ffn_{kind}_exps.weight", e * rpe, (e + 1) * rpe)
+                if ent is None or ent[1] != "t64":
+                    return None
+                slabs.append(ent[0])
+            mats[kind] = slabs
+        bias = lambda n: self.w(n) if self.has(n) else None  # noqa: E731
+        rb = bias(p + "ffn_gate_inp.bias")
+        lay = MoELayer(ggml_type=self.gguf.tensors[p + "ffn_gate_exps.weight"].dtype, n_expert=c.n_expert,
+                       top_k=c.n_expert_used, n_embd=c.n_embd, n_ff=c.n_ffn_expert,
+                       router_w=self.w(p + "ffn_gate_inp.weight"), router_b=rb, gate=mats["gate"], up=mats["up"],
+                       down=mats["down"], gate_b=bias(p + "ffn_gate_exps.bias"), up_b=bias(p + "ffn_up_exps.bias"),
+                       down_b=bias(p + "ffn_down_exps.bias"), layout="t64", router_mode="gptoss",
+                       act="clamped_swiglu")
+        self._fused[layer] = lay
+        return lay
+
+    def _ffn_block(self, x: torch.Tensor, layer: int) -> torch.Tensor:
+        from ..compute.blockffn import BlockPrefetcher, stream_expert_ffn
+        c, p = self.cfg, f"blk.{layer}."
+        x = x.reshape(-1, c.n_embd).to(self.device, torch.float32).contiguous()
+        norm = p + "post_attention_norm.weight"
+        h = add_rms_norm(x, None, self.w(norm) if self.has(norm) else None, c.rms_eps)
+        fused = self._fused_layer(layer)
+        if fused is not None:
+            out, ids, _ = fused.forward(h)
+            self.router_stats.record(layer, ids)
+            return x + out
+        chosen, ids, weights = self._route(h, layer)
+        stats = self.router_stats
+        stats.tokens_routed += h.shape[0]
+        out = torch.zeros_like(h)
+        active = []
+        for e in chosen:
+            mask = ids == e
+            rows = mask.any(-1).nonzero(as_tuple=True)[0]
+            if rows.numel():
+                active.append((e, rows, (weights * mask).sum(-1)[rows, None]))
+        plan = [(p + f"ffn_{kind}_exps.weight", e * span, (e + 1) * span) for e, _r, _w in active
+                for kind, span in (("gate", c.n_ffn_expert), ("up", c.n_ffn_expert), ("down", c.n_embd))]
+        pf = BlockPrefetcher(self.cache, plan, self.block_rows, self.expert_lookahead)
+        try:
+            for e, rows, wgt in active:
+                stats.hits[(layer, e)] += rows.numel()
+                stats.expert_reads += 1
+                out[rows] += wgt * stream_expert_ffn(self.cache, p, e, h[rows], c.n_ffn_expert, c.n_embd,
+                                                     clamped_swiglu, self.block_rows, self.device, torch.float32,
+                                                     bias=True, lookahead=self.expert_lookahead,
+                                                     callback=self.neuron_callback, prefetcher=pf)
+        finally:  # a failed forward must not strand arena leases
+            pf.close()
+        return x + out
+
+    def ffn_stack(self, x: torch.Tensor) -> torch.Tensor:
+        """x after every layer's FFN block."""
+        for layer in range(self.cfg.n_layer):
+            x = self._ffn_block(x, layer)
+        return x

@@ -201,3 +201,26 @@ def test_router_stats_contract():
     # 5 (layer, expert) entries: the busiest 20% (one entry, 3 hits) of 8 routings
     assert st.skew() == pytest.approx(3 / 8)
     assert "routed 4 tokens" in st.summary() and "5 expert reads" in st.summary()
+
+
+def test_parse_size_and_api_on_cpu(tmp_path):
+    """api.py:30-37 sizes; NeuroStream.load parses the GGUF on any device, but
+    its expert path computes on the GPU only (no CPU fallback)."""
+    import sys
+    from nurostream_amd.api import NeuroStream, parse_size
+    assert parse_size("2GB") == 2 << 30 and parse_size("1.5G") == 3 << 29 and parse_size("512M") == 512 << 20
+    assert parse_size(" 64K ") == 64 << 10 and parse_size(123) == 123 and parse_size("7") == 7
+    with pytest.raises(ValueError):
+        parse_size("lots")
+    sys.path.insert(0, str(__import__("pathlib").Path(__file__).parent))
+    from api_cases import write_gptoss_gguf
+    from nurostream_amd import synth
+    cfg = synth.MoEConfig("s", GGMLType.MXFP4, 8, 2, 64, 64, "gptoss", "clamped_swiglu", True, torch.bfloat16)
+    path = tmp_path / "t.gguf"
+    write_gptoss_gguf(path, cfg, n_layers=1, seed=1)
+    ns = NeuroStream.load(path, device="cpu")
+    assert (ns.cfg.n_layer, ns.cfg.n_embd, ns.cfg.n_expert, ns.cfg.n_expert_used, ns.cfg.n_ffn_expert) == (1, 64, 8, 2, 64)
+    with pytest.raises(NotImplementedError):
+        ns.generate([1, 2, 3])
+    with pytest.raises(N.NativeError):
+        ns.model._ffn_block(torch.randn(1, 64), 0)
