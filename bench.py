@@ -227,6 +227,7 @@ def layer_workload(args, torch, N, synth, dev):
     tok_s = K * T / (ms_total / 1e3)
 
     # per-phase durations: R further steps, one workspace each
+    grouped = layout == "t64" and (args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 8))
     phases = (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE)
     phase_us = {}
     if R > 0:
@@ -262,16 +263,15 @@ def layer_workload(args, torch, N, synth, dev):
     ids_cpu = ids[W:W + K + R].cpu()
     distinct = [len(torch.unique(ids_cpu[s])) for s in range(ids_cpu.shape[0])]
     mean_distinct = sum(distinct) / len(distinct)
-    grouped = layout == "t64" and (args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 8))
     gu_kernel = ("moe_gu_grouped_kernel" if grouped else "moe_gu_kernel") if layout == "t64" else "moe_gu_raw_kernel"
     gu_bytes, dn_bytes = _expert_bytes(cfg, mean_distinct)
     roofline = None
     if R > 0:
-        gu_us = phase_us[N.PHASE_GATE_UP]
-        achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+        kname, kbytes, kus = gu_kernel, gu_bytes, phase_us[N.PHASE_GATE_UP]
+        achieved = kbytes / (kus * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(gu_kernel) if default else None,
-                    "kernel": gu_kernel, "bytes_per_launch": int(gu_bytes), "avg_us": round(gu_us, 3)}
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname) if default else None,
+                    "kernel": kname, "bytes_per_launch": int(kbytes), "avg_us": round(kus, 3)}
         if grouped:
             roofline["note"] = "gate_up phase = moe_sort_kernel + moe_gu_grouped_kernel"
     step_bytes = sum(_expert_bytes(cfg, mean_distinct))

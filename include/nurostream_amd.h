@@ -151,8 +151,9 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
  * ids/weights outputs except for the per-pair t64 kernels, which select it
  * themselves; in the t64 layout also the activation terms of h),
  * NSX_PHASE_GATE_UP (grouped dispatch: the sort by expert; expert gate/up
- * GEMVs + activation), NSX_PHASE_DOWN (expert down GEMVs; per-pair dispatch
- * also the weighted combine into out, and the t64 kernel writes ids/weights)
+ * GEMVs + activation; the per-pair t64 kernel also selects the top-k and
+ * writes ids/weights), NSX_PHASE_DOWN (expert down GEMVs; per-pair dispatch
+ * also the weighted combine into out)
  * and NSX_PHASE_COMBINE (grouped dispatch: the ascending-expert combine;
  * otherwise nothing). A phase reads what the earlier phases of the same call
  * sequence left in the workspace; running the four in order is

@@ -470,24 +470,43 @@ __device__ __forceinline__ void mx_store_rows(const v4f (&D)[4], int tile, int n
     if (r0 + 16 * g < n) *(v4f*)(dst + r0 + 16 * g) = D[g];
 }
 
-// phase 1: workgroup = (pair, 64-row tile of gate/up), one wave per
-// (gate|up, K-chunk), each a single pass over its chunk's steps. The waves
-// meet in LDS (fixed order); wave 0 adds the biases, applies the activation
-// and writes the activation's terms for the down kernel -- the tile's 64
-// rows are exactly two 32-element blocks of the down kernel's K.
-__global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
-  __shared__ float red[2][MAX_CHUNKS][64];
+// gate/up of one (pair, 64-row tile) work item, by a whole workgroup: one
+// wave per (gate|up, K-chunk), each a single pass over its chunk's steps. The
+// waves meet in LDS (fixed order); wave 0 adds the biases, applies the
+// activation and writes the activation's terms for the down phase -- the
+// tile's 64 rows are exactly two 32-element blocks of the down matrix's K.
+__device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float (&red)[2][MAX_CHUNKS][64],
+                                        int& s_e) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int tiles = (int)a.ggu.tiles;
-  const int p = blockIdx.x / tiles, tile = blockIdx.x - p * tiles;
   const int m = wave / a.cg, c = wave - m * a.cg;
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
-  const int t = p / a.top_k;
-  float lg[TOPK_NV];
-  pair_logits(a, p, lg);
+  const int k = a.top_k, t = p / k, j = p - t * k;
   MxRegs<GU_S> R;
   mx_load_b<GU_S, false>(R, a.xq_h + (int64_t)t * a.ggu.ns * XQ_STEP, 0, 0, 1, s0, s1);  // no expert needed
-  const int e = pair_expert(a, p, lg);
+  // the top-k by wave 0 alone (sixteen waves selecting at once would share each SIMD four ways);
+  // the token's first item also writes the ids/weights outputs, which the down phase reads
+  if (wave == 0) {
+    float lg[TOPK_NV];
+    topk_load(a.logits + (int64_t)t * a.E, a.E, lg);
+    int si[MAX_TOPK];
+    float sw[MAX_TOPK];
+    topk_select(lg, a.E, k, a.mode, si, sw);
+    int my_e = 0, e = 0;
+    float my_w = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      e = jj == j ? si[jj] : e;
+      my_e = lane == jj ? si[jj] : my_e;
+      my_w = lane == jj ? sw[jj] : my_w;
+    }
+    if (j == 0 && tile == 0 && lane < k) {
+      a.ids[(int64_t)t * k + lane] = clamp_expert(my_e, a.E);
+      a.wts[(int64_t)t * k + lane] = my_w;
+    }
+    if (lane == 0) s_e = clamp_expert(e, a.E);
+  }
+  __syncthreads();
+  const int e = s_e;
   const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
                               : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
   mx_load_a<GU_S>(R, mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1);
@@ -501,6 +520,7 @@ __global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
   v4f D[4] = {};
   mx_compute<GU_S>(R, a.ggu, s0, s1, D);
   mx_sum_terms(D);
+  __syncthreads();  // an earlier item's wave 0 is done with `red`
   if ((lane & 15) == 0) {
     const int r0 = 4 * (lane >> 4);
 #pragma unroll
@@ -518,68 +538,83 @@ __global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
   xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
 }
 
-// phase 2 (down and combine): workgroup = (token, 16-row group of a 64-row
-// output tile); one wave per (expert slot, K-chunk), each a single pass over
-// its steps. The waves meet in LDS; wave 0 sums each expert's chunks in a
+// phase 1 on its own: workgroup = (pair, tile)
+__global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
+  __shared__ float red[2][MAX_CHUNKS][64];
+  __shared__ int s_e;
+  const int tiles = (int)a.ggu.tiles;
+  const int p = blockIdx.x / tiles;
+  gu_item(a, p, blockIdx.x - p * tiles, red, s_e);
+}
+
+// down and combine of one (token, 16-row group of a 64-row output tile) work
+// item, by a whole workgroup: one wave per (expert slot, K-chunk), each a
+// single pass over its steps. down_begin selects the token's top-k and
+// requests the weights and biases; down_end stages the activation terms
+// through LDS, runs the MFMAs and, in wave 0, sums each expert's chunks in a
 // fixed order (chunk 0 carries the bias) and combines the experts in
-// ascending id: out[rows] = sum of w_e * y_e. The token's first workgroup
-// also writes the ids/weights outputs.
+// ascending id: out[rows] = sum of w_e * y_e. The expert ids and weights are
+// the ones the gate/up phase wrote.
 constexpr int DC_PIECES = DC_S * XQ_STEP / 16;  // 16-byte pieces of one wave's activation terms
 
-__global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
-  __shared__ float red[16][16];  // [wave = slot * cd + chunk][row of the group]
-  __shared__ __align__(16) uint8_t xs[16][DC_S * XQ_STEP];  // each wave's activation terms, staged
+struct DownItem {
+  MxRegs<DC_S, 1> R;
+  v4f bias;
+  int t, hh, tile, rg, p, s0, s1, my_e, my_rank;
+  float my_w;
+};
+
+__device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& d) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int groups = 4 * (int)a.gdn.tiles;
-  // XCD-aware order: workgroup b runs on XCD b % 8, so item = (b % 8) * per + b / 8
-  // keeps the four row groups of a tile (which read the same scale lines) on one L2
-  const int per = (int)(gridDim.x >> 3);
-  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  if (item >= a.T * groups) return;  // padding workgroups of the 8-way split
-  const int t = item / groups, hh = item - t * groups;
-  const int tile = hh >> 2, rg = hh & 3;
+  d.t = item / groups;
+  d.hh = item - d.t * groups;
+  d.tile = d.hh >> 2;
+  d.rg = d.hh & 3;
   const int k = a.top_k;
   const int j = wave / a.cd, c = wave - j * a.cd;
-  const int p = t * k + j;
-  const int s0 = c * a.sd, s1 = min(a.gdn.ns, s0 + a.sd);
-  float lg[TOPK_NV];
-  topk_load(a.logits + (int64_t)t * a.E, a.E, lg);
-  // this wave's activation terms (steps s0 .. s1 - 1), requested now and staged in LDS below
+  d.p = d.t * k + j;
+  d.s0 = c * a.sd;
+  d.s1 = min(a.gdn.ns, d.s0 + a.sd);
+  // the token's top-k, written by the gate/up phase: this wave's expert; in
+  // lane jj < k slot jj's expert, weight and rank in ascending expert id
+  const int32_t* tid = a.ids + (int64_t)d.t * k;
+  int idv[MAX_TOPK];
+#pragma unroll
+  for (int jj = 0; jj < MAX_TOPK; ++jj) idv[jj] = clamp_expert(tid[jj < k ? jj : k - 1], a.E);
+  const float my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
+  int e = 0, my_e = 0, my_rank = 0;
+#pragma unroll
+  for (int jj = 0; jj < MAX_TOPK; ++jj) {
+    e = jj == j ? idv[jj] : e;
+    my_e = lane == jj ? idv[jj] : my_e;
+  }
+#pragma unroll
+  for (int jj = 0; jj < MAX_TOPK; ++jj)
+    my_rank += (jj < k && (idv[jj] < my_e || (idv[jj] == my_e && jj < lane))) ? 1 : 0;
+  d.my_e = my_e;
+  d.my_rank = my_rank;
+  d.my_w = my_w;
+  mx_load_a<DC_S, 1>(d.R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) +
+                              (int64_t)d.tile * a.gdn.tile_bytes, a.gdn, d.s0, d.s1, d.rg);
+  const int r0 = d.tile * 64 + 16 * d.rg + 4 * (lane >> 4);
+  d.bias = v4f{0.f, 0.f, 0.f, 0.f};  // chunk 0's bias rows, requested while the weights stream
+  if (c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd)
+    d.bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+}
+
+__device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&red)[16][16],
+                                         uint8_t (&xs)[16][DC_S * XQ_STEP], int (&s_slot)[MAX_TOPK]) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int k = a.top_k;
+  // this wave's activation terms (steps s0 .. s1 - 1), staged in LDS
   typedef const __attribute__((address_space(1))) v4u gv4u;
-  const int npc = (s1 - s0) * (XQ_STEP / 16);
-  const uint8_t* xsrc = a.xq_a + ((int64_t)p * a.gdn.ns + s0) * XQ_STEP;
+  const int npc = (d.s1 - d.s0) * (XQ_STEP / 16);
+  const uint8_t* xsrc = a.xq_a + ((int64_t)d.p * a.gdn.ns + d.s0) * XQ_STEP;
   v4u stage[(DC_PIECES + 63) / 64];
 #pragma unroll
-  for (int i = 0; i < (DC_PIECES + 63) / 64; ++i) stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
-  // the top-k, reduced at once to what is used later (static indices: no private arrays):
-  // this wave's expert; in lane jj < k slot jj's expert, weight and rank in ascending expert id
-  int e = 0, my_e = 0, my_rank = 0;
-  float my_w = 0.f;
-  {
-    int si[MAX_TOPK];
-    float sw[MAX_TOPK];
-    topk_select(lg, a.E, k, a.mode, si, sw);
-#pragma unroll
-    for (int jj = 0; jj < MAX_TOPK; ++jj) {
-      e = jj == j ? si[jj] : e;
-      my_e = lane == jj ? si[jj] : my_e;
-      my_w = lane == jj ? sw[jj] : my_w;
-    }
-    e = clamp_expert(e, a.E);
-    my_e = clamp_expert(my_e, a.E);
-#pragma unroll
-    for (int jj = 0; jj < MAX_TOPK; ++jj) {
-      const int ej = clamp_expert(si[jj], a.E);
-      my_rank += (jj < k && (ej < my_e || (ej == my_e && jj < lane))) ? 1 : 0;
-    }
-  }
-  MxRegs<DC_S, 1> R;
-  mx_load_a<DC_S, 1>(R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) + (int64_t)tile * a.gdn.tile_bytes,
-                     a.gdn, s0, s1, rg);
-  const int r0 = tile * 64 + 16 * rg + 4 * (lane >> 4);
-  v4f bias = {0.f, 0.f, 0.f, 0.f};  // chunk 0's bias rows, requested while the weights stream
-  if (c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd)
-    bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+  for (int i = 0; i < (DC_PIECES + 63) / 64; ++i)
+    stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
 #pragma unroll
   for (int i = 0; i < (DC_PIECES + 63) / 64; ++i) {  // (clamped duplicates rewrite the same bytes)
     const int pc = min(lane + 64 * i, npc - 1);
@@ -587,34 +622,43 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes land before its reads
   __builtin_amdgcn_wave_barrier();
-  mx_load_b<DC_S, true, 1>(R, xs[wave], s0, 0, 1, s0, s1);
+  mx_load_b<DC_S, true, 1>(d.R, xs[wave], d.s0, 0, 1, d.s0, d.s1);
   v4f D[1] = {};
-  mx_compute<DC_S, 1>(R, a.gdn, s0, s1, D, rg);
+  mx_compute<DC_S, 1>(d.R, a.gdn, d.s0, d.s1, D, d.rg);
   mx_sum_terms<1>(D);
-  if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + bias;
+  __syncthreads();  // an earlier item's wave 0 is done with `red` and `s_slot`
+  if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + d.bias;
   __syncthreads();
   if (wave != 0) return;
   // slot order of the combine (ascending expert id), exchanged through LDS
-  __shared__ int s_slot[MAX_TOPK];
-  if (lane < k) {
-    if (hh == 0) {
-      a.ids[(int64_t)t * k + lane] = my_e;
-      a.wts[(int64_t)t * k + lane] = my_w;
-    }
-    s_slot[my_rank] = lane;
-  }
+  if (lane < k) s_slot[d.my_rank] = lane;
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are visible to its reads
   __builtin_amdgcn_wave_barrier();
-  const int row = tile * 64 + 16 * rg + (lane & 15);
+  const int row = d.tile * 64 + 16 * d.rg + (lane & 15);
   float o = 0.f;
   for (int jj = 0; jj < k; ++jj) {
     const int jx = s_slot[jj];
-    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), jx));
+    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d.my_w), jx));
     float y = 0.f;
     for (int cc = 0; cc < a.cd; ++cc) y += red[jx * a.cd + cc][lane & 15];
     o = combine_one(o, w, y);
   }
-  if (lane < 16 && row < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
+  if (lane < 16 && row < a.n_embd) a.out[(int64_t)d.t * a.n_embd + row] = o;
+}
+
+// phase 2 on its own: XCD-aware order -- workgroup b runs on XCD b % 8, so
+// item = (b % 8) * per + b / 8 keeps the four row groups of a tile (which read
+// the same scale lines) on one L2
+__global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
+  __shared__ float red[16][16];  // [wave = slot * cd + chunk][row of the group]
+  __shared__ __align__(16) uint8_t xs[16][DC_S * XQ_STEP];  // each wave's activation terms, staged
+  __shared__ int s_slot[MAX_TOPK];
+  const int per = (int)(gridDim.x >> 3);
+  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (item >= a.T * 4 * (int)a.gdn.tiles) return;  // padding workgroups of the 8-way split
+  DownItem d;
+  down_begin(a, item, d);
+  down_end(a, d, red, xs, s_slot);
 }
 
 // ---------------------------------------------------------------------------
