@@ -1185,6 +1185,127 @@ __global__ __launch_bounds__(512) void moe_down_q4k_kernel(MoeDev a) {
   if (row < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
 }
 
+// Grouped Q4_K (several tokens per expert): the same per-(pair, row)
+// arithmetic as the kernels above, with the rows' codes and headers held in
+// registers while the work item's tokens go by one at a time (activations
+// from L2), so an expert's rows are read from HBM once per item.
+
+// gate/up: workgroup = (item, 16 rows); wave = 2 rows of gate and of up
+template <int U>
+__global__ __launch_bounds__(512) void moe_gu_q4k_grouped_kernel(MoeDev a) {
+  constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
+  int grp;
+  int4 item;
+  if (!grp_work(a, (a.n_ff + RPG - 1) / RPG, grp, item)) return;
+  const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int K = a.n_embd, nu = K / 32;
+  const uint32_t rb = (uint32_t)(K / 256) * 144u;
+  const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
+  const uint8_t* um = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
+  const int r0 = grp * RPG + wave * Q4K_GU_RPW;
+  v4u cg[Q4K_GU_RPW][U], hg[Q4K_GU_RPW][U], cu[Q4K_GU_RPW][U], hu[Q4K_GU_RPW][U];
+#pragma unroll
+  for (int j = 0; j < Q4K_GU_RPW; ++j) {
+    const int row = min(r0 + j, a.n_ff - 1);
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int u = min(lane + 64 * i, nu - 1);
+      q4k_unit_load(gm, row, rb, u, cg[j][i], hg[j][i]);
+      q4k_unit_load(um, row, rb, u, cu[j][i], hu[j][i]);
+    }
+  }
+  float gb[Q4K_GU_RPW], ub[Q4K_GU_RPW];
+#pragma unroll
+  for (int j = 0; j < Q4K_GU_RPW; ++j) {
+    const int row = min(r0 + j, a.n_ff - 1);
+    gb[j] = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + row] : 0.f;
+    ub[j] = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + row] : 0.f;
+  }
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
+#pragma nounroll
+  for (int w = 0; w < n; ++w) {
+    // decode the codes per token (hoisting the decoded weights out of the loop would need
+    // 4 x 36 registers per unit and row): the empty asm marks them as changed
+#pragma unroll
+    for (int j = 0; j < Q4K_GU_RPW; ++j)
+#pragma unroll
+      for (int i = 0; i < U; ++i) asm volatile("" : "+v"(cg[j][i]), "+v"(hg[j][i]), "+v"(cu[j][i]), "+v"(hu[j][i]));
+    const int pr = __builtin_amdgcn_readlane(my_pair, w);
+    const float* x = a.h + (int64_t)(pr / a.top_k) * K;
+    Q4kX X[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) q4k_unit_x(x, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
+#pragma unroll
+    for (int j = 0; j < Q4K_GU_RPW; ++j) {
+      float gs = 0.f, us = 0.f;
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int u = min(lane + 64 * i, nu - 1);
+        gs += q4k_unit_dot(cg[j][i], hg[j][i], u, X[i]);
+        us += q4k_unit_dot(cu[j][i], hu[j][i], u, X[i]);
+      }
+      gs = nsx_wave_sum(gs);
+      us = nsx_wave_sum(us);
+      const int row = r0 + j;
+      if (lane == 0 && row < a.n_ff)
+        a.act[(int64_t)pr * a.n_ff + row] = moe_act(a.act_kind, gs + gb[j], us + ub[j], a.alpha, a.limit);
+    }
+  }
+}
+
+// down: workgroup = (item, 16 output rows); wave = 4 rows; y[pair, rows] =
+// the expert's down rows . activation(pair) + bias (moe_combine_kernel adds
+// the pairs of a token in ascending expert id)
+constexpr int Q4K_DG_WAVES = 4, Q4K_DG_RPW = 4;
+
+template <int U>
+__global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
+  constexpr int RPG = Q4K_DG_WAVES * Q4K_DG_RPW;
+  int grp;
+  int4 item;
+  if (!grp_work(a, (a.n_embd + RPG - 1) / RPG, grp, item)) return;
+  const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int K = a.n_ff, nu = K / 32;
+  const uint32_t rb = (uint32_t)(K / 256) * 144u;
+  const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
+  const int r0 = grp * RPG + wave * Q4K_DG_RPW;
+  v4u c[Q4K_DG_RPW][U], hd[Q4K_DG_RPW][U];
+#pragma unroll
+  for (int j = 0; j < Q4K_DG_RPW; ++j) {
+    const int row = min(r0 + j, a.n_embd - 1);
+#pragma unroll
+    for (int i = 0; i < U; ++i) q4k_unit_load(dm, row, rb, min(lane + 64 * i, nu - 1), c[j][i], hd[j][i]);
+  }
+  float bias[Q4K_DG_RPW];
+#pragma unroll
+  for (int j = 0; j < Q4K_DG_RPW; ++j)
+    bias[j] = a.down_bias ? a.down_bias[(int64_t)e * a.n_embd + min(r0 + j, a.n_embd - 1)] : 0.f;
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
+#pragma nounroll
+  for (int w = 0; w < n; ++w) {
+#pragma unroll
+    for (int j = 0; j < Q4K_DG_RPW; ++j)
+#pragma unroll
+      for (int i = 0; i < U; ++i) asm volatile("" : "+v"(c[j][i]), "+v"(hd[j][i]));  // decode per token
+    const int pr = __builtin_amdgcn_readlane(my_pair, w);
+    Q4kX X[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i)
+      q4k_unit_x(a.act + (int64_t)pr * K, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
+#pragma unroll
+    for (int j = 0; j < Q4K_DG_RPW; ++j) {
+      float y = 0.f;
+#pragma unroll
+      for (int i = 0; i < U; ++i) y += q4k_unit_dot(c[j][i], hd[j][i], min(lane + 64 * i, nu - 1), X[i]);
+      y = nsx_wave_sum(y);
+      const int row = r0 + j;
+      if (lane == 0 && row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y + bias[j];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 
@@ -1199,8 +1320,20 @@ struct MoePlan {
 
 constexpr int GRP_AUTO_MIN_T = 8;  // NSX_DISPATCH_AUTO groups from this many tokens
 
+// The Q4_K kernels take K <= 4096 and 16-byte aligned expert rows.
+static bool q4k_fast(const nsx_moe_layer* L) {
+  if (L->ggml_type != NSX_Q4_K || L->n_embd > 64 * Q4K_UMAX * 32 || L->n_ff > 64 * Q4K_UMAX * 32) return false;
+  if (L->gate_base) {
+    const uintptr_t m = (uintptr_t)L->gate_base | (uintptr_t)L->up_base | (uintptr_t)L->down_base |
+                        (uintptr_t)L->gate_stride | (uintptr_t)L->up_stride | (uintptr_t)L->down_stride;
+    return (m & 15u) == 0;
+  }
+  return false;  // address tables: alignment unknown on the host
+}
+
 static bool use_grouped(const nsx_moe_layer* L, int64_t T) {
   if (L->dispatch == NSX_DISPATCH_GROUPED) return true;
+  // Q4_K groups on request only: its grouped kernels measure slower than the per-pair ones at T=32
   return L->dispatch == NSX_DISPATCH_AUTO && L->layout == NSX_LAYOUT_T64 && T >= GRP_AUTO_MIN_T;
 }
 
@@ -1288,21 +1421,12 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
   NSX_REQUIRE(L->dispatch == NSX_DISPATCH_AUTO || L->dispatch == NSX_DISPATCH_PAIRS ||
                   L->dispatch == NSX_DISPATCH_GROUPED,
               NSX_EINVAL, "dispatch %d", L->dispatch);
-  NSX_REQUIRE(!use_grouped(L, T) || L->layout == NSX_LAYOUT_T64, NSX_ENOTIMPL,
-              "grouped dispatch is implemented for the t64 layout");
+  NSX_REQUIRE(!use_grouped(L, T) || L->layout == NSX_LAYOUT_T64 || q4k_fast(L), NSX_ENOTIMPL,
+              "grouped dispatch is implemented for the t64 layout and for stacked, 16-byte aligned Q4_K "
+              "experts with K <= 4096");
   return NSX_OK;
 }
 
-// The Q4_K kernels take K <= 4096 and 16-byte aligned expert rows.
-static bool q4k_fast(const MoeDev& d, const nsx_moe_layer* L) {
-  if (L->ggml_type != NSX_Q4_K || L->n_embd > 64 * Q4K_UMAX * 32 || L->n_ff > 64 * Q4K_UMAX * 32) return false;
-  if (L->gate_base) {
-    const uintptr_t m = (uintptr_t)L->gate_base | (uintptr_t)L->up_base | (uintptr_t)L->down_base |
-                        (uintptr_t)L->gate_stride | (uintptr_t)L->up_stride | (uintptr_t)L->down_stride;
-    return (m & 15u) == 0;
-  }
-  return false;  // address tables: alignment unknown on the host
-}
 
 template <int UG, int UD>
 static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
@@ -1419,16 +1543,30 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
 
   if (p.grouped) {
     const int64_t items = (int64_t)p.max_items;
+    auto grid8 = [&](int64_t groups) { return dim3((unsigned)(8 * nsx_cdiv(items * groups, 8))); };
     if (on(NSX_PHASE_GATE_UP)) {
       if ((rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
-      if ((rc = nsx_launch(moe_gu_grouped_kernel, dim3((unsigned)(8 * nsx_cdiv(items * p.ggu.tiles, 8))),
-                           dim3(128 * p.cg), 0, st, d)))
-        return rc;
+      if (t64) {
+        rc = nsx_launch(moe_gu_grouped_kernel, grid8(p.ggu.tiles), dim3(128 * p.cg), 0, st, d);
+      } else {
+        const int64_t g = nsx_cdiv(L->n_ff, Q4K_GU_WAVES * Q4K_GU_RPW);
+        rc = L->n_embd > 64 * 32
+                 ? nsx_launch(moe_gu_q4k_grouped_kernel<2>, grid8(g), dim3(64 * Q4K_GU_WAVES), 0, st, d)
+                 : nsx_launch(moe_gu_q4k_grouped_kernel<1>, grid8(g), dim3(64 * Q4K_GU_WAVES), 0, st, d);
+      }
+      if (rc) return rc;
     }
-    if (on(NSX_PHASE_DOWN) &&
-        (rc = nsx_launch(moe_down_grouped_kernel, dim3((unsigned)(8 * nsx_cdiv(items * p.gdn.tiles, 8))),
-                         dim3(256 * p.cdg), 0, st, d)))
-      return rc;
+    if (on(NSX_PHASE_DOWN)) {
+      if (t64) {
+        rc = nsx_launch(moe_down_grouped_kernel, grid8(p.gdn.tiles), dim3(256 * p.cdg), 0, st, d);
+      } else {
+        const int64_t g = nsx_cdiv(L->n_embd, Q4K_DG_WAVES * Q4K_DG_RPW);
+        rc = L->n_ff > 64 * 32
+                 ? nsx_launch(moe_down_q4k_grouped_kernel<2>, grid8(g), dim3(64 * Q4K_DG_WAVES), 0, st, d)
+                 : nsx_launch(moe_down_q4k_grouped_kernel<1>, grid8(g), dim3(64 * Q4K_DG_WAVES), 0, st, d);
+      }
+      if (rc) return rc;
+    }
     if (on(NSX_PHASE_COMBINE) &&
         (rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
                          d)))
@@ -1448,7 +1586,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   switch (L->ggml_type) {  // the GGUF-layout down kernel also combines
     case NSX_MXFP4: return launch_raw_phases<NSX_MXFP4>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q4_K:
-      if (q4k_fast(d, L)) return launch_q4k_any(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+      if (q4k_fast(L)) return launch_q4k_any(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
       return launch_raw_phases<NSX_Q4_K>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q4_0: return launch_raw_phases<NSX_Q4_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q8_0: return launch_raw_phases<NSX_Q8_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));

@@ -85,10 +85,17 @@ def test_workspace_bytes_by_dispatch(lib):
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < w8  # no sort buffers or per-pair outputs
     L.dispatch = 9
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
-    L.dispatch = N.DISPATCH_GROUPED  # grouped needs the t64 layout
+    L.dispatch = N.DISPATCH_GROUPED  # grouped needs t64, or stacked aligned Q4_K rows
     L.layout = N.LAYOUT_GGUF
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
     assert b"grouped" in lib.nsx_last_error()
+    L.ggml_type = int(GGMLType.Q4_K)
+    L.n_embd, L.n_ff = 4096, 1536
+    L.gate_stride = L.up_stride = L.down_stride = 1536 * 2304
+    L.gate_base = L.up_base = L.down_base = 1 << 20
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) > 0
+    L.down_base = (1 << 20) + 8  # not 16-byte aligned: no Q4_K fast path, so no grouping
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
 
 
 def test_validation_errors_return_codes(lib):

@@ -109,3 +109,42 @@ def test_config3_gptoss_t128_zipf(dev):
     np.testing.assert_allclose(to_np(wg)[sub], rw, rtol=1e-5)
     err = rel_max(to_np(og)[sub], ref)
     assert err < FFN_BAR and err < MFMA_TOL, err
+
+
+def _q4k_pair_and_grouped(cfg, t):
+    return _layer(cfg, t, "gguf", dispatch="pairs"), _layer(cfg, t, "gguf", dispatch="grouped")
+
+
+@pytest.mark.parametrize("T", [1, 5, 8, 40])
+def test_grouped_q4k_equals_pairs_bitwise(dev, T):
+    """Grouped Q4_K (rows in registers, the item's tokens one at a time) keeps
+    each (pair, row)'s arithmetic: identical to the per-pair Q4_K kernels."""
+    from nurostream_amd import synth
+    cfg = _small("qwen3-small")
+    t = synth.make_layer(cfg, seed=21, device=dev)
+    lp, lg = _q4k_pair_and_grouped(cfg, t)
+    h = synth.activations(T, cfg.n_embd, seed=200 + T, device=dev)
+    op, ip, wp = lp(h)
+    og, ig, wg = lg(h)
+    assert torch.equal(ip, ig) and torch.equal(wp, wg)
+    assert torch.equal(op, og)
+    ref, _, _, _ = _oracle_layer(cfg, t, h.cpu().numpy())
+    assert rel_max(to_np(og), ref) < 1e-5
+
+
+def test_config4_qwen3_t32_grouped(dev):
+    """BASELINE config 4 at T=32: the Qwen3-235B-shaped Q4_K layer, grouped
+    == per-pair on all 32 tokens; the oracle checks 2."""
+    from nurostream_amd import synth
+    cfg = synth.QWEN3_235B
+    t = synth.make_layer(cfg, seed=0, device=dev)
+    la = _layer(cfg, t, "gguf", dispatch="grouped")
+    lp = _layer(cfg, t, "gguf", dispatch="pairs")
+    h = synth.activations(32, cfg.n_embd, seed=9, device=dev)
+    oa, ia, _ = la(h)
+    op, ip, _ = lp(h)
+    assert torch.equal(ia, ip) and torch.equal(oa, op)
+    sub = slice(0, 2)
+    ref, rid, _, _ = _oracle_layer(cfg, t, h[sub].cpu().numpy())
+    np.testing.assert_array_equal(np.sort(to_np(ia)[sub], 1), np.sort(rid, 1))
+    assert rel_max(to_np(oa)[sub], ref) < 1e-5
