@@ -62,48 +62,54 @@ __device__ __forceinline__ float key2f(uint32_t k) {
   return __builtin_bit_cast(float, k & 0x80000000u ? (k ^ 0x80000000u) : ~k);
 }
 
-constexpr int TOPK_NV = MAX_EXPERTS / 64;  // logits per lane
+constexpr int TOPK_NV = MAX_EXPERTS / 64;  // logits per lane at most
 
-// Issue the loads of one token's logits: lane l holds experts l + 64 i.
+// Issue the loads of one token's logits: lane l holds experts l + 64 i (i < NV).
 // Unpredicated (index clamped); topk_select masks experts >= E.
-__device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, float (&v)[TOPK_NV]) {
+template <int NV>
+__device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, float (&v)[NV]) {
   const int lane = __lane_id();
 #pragma unroll
-  for (int i = 0; i < TOPK_NV; ++i) {
+  for (int i = 0; i < NV; ++i) {
     const int e = lane + 64 * i;
     v[i] = lg[e < E ? e : E - 1];
   }
 }
 
-// Each round takes the wave maximum of the lanes' best keys, then the
-// minimum index holding it (DPP reductions). Results are wave-uniform.
-__device__ void topk_select(float (&v)[TOPK_NV], int E, int k, int mode, int (&sel_i)[MAX_TOPK],
-                            float (&sel_w)[MAX_TOPK]) {
+// Top-k of the E <= 64 NV logits held as by topk_load, largest first, ties to
+// the lower expert index. Each round takes the wave maximum of the lanes' best
+// remaining keys (DPP); the expert holding it with the lowest index is found
+// by ballots over the lanes' best slots in ascending order (slot s holds
+// experts 64 s .. 64 s + 63, so the first nonempty ballot has the lowest
+// index, and its lowest lane is the one). Results are wave-uniform.
+template <int NV>
+__device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mode, int (&sel_i)[MAX_TOPK],
+                                            float (&sel_w)[MAX_TOPK]) {
   const int lane = __lane_id();
-  bool ok[TOPK_NV];
+  bool ok[NV];
 #pragma unroll
-  for (int i = 0; i < TOPK_NV; ++i) ok[i] = lane + 64 * i < E;
+  for (int i = 0; i < NV; ++i) ok[i] = lane + 64 * i < E;
   if (mode == NSX_ROUTE_QWEN3) {  // probs = softmax(logits) over all experts, float32 (router.py:65)
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < TOPK_NV; ++i)
+    for (int i = 0; i < NV; ++i)
       if (ok[i]) m = fmaxf(m, v[i]);
     m = key2f(nsx_wave_max_u32(f2key(m)));
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < TOPK_NV; ++i)
+    for (int i = 0; i < NV; ++i)
       if (ok[i]) {
         v[i] = expf(v[i] - m);
         s += v[i];
       }
     s = nsx_wave_sum(s);
 #pragma unroll
-    for (int i = 0; i < TOPK_NV; ++i)
+    for (int i = 0; i < NV; ++i)
       if (ok[i]) v[i] = v[i] / s;
   }
-  uint32_t key[TOPK_NV];
+  uint32_t key[NV];
 #pragma unroll
-  for (int i = 0; i < TOPK_NV; ++i) key[i] = f2key(v[i]);
+  for (int i = 0; i < NV; ++i) key[i] = f2key(v[i]);
   float sel_v[MAX_TOPK];
 #pragma unroll
   for (int j = 0; j < MAX_TOPK; ++j) {
@@ -113,45 +119,60 @@ __device__ void topk_select(float (&v)[TOPK_NV], int E, int k, int mode, int (&s
 #pragma unroll
   for (int j = 0; j < MAX_TOPK; ++j) {
     if (j >= k) break;
-    uint32_t lk = 0, li = 0xffffu;
+    uint32_t lk = 0;
+    int ls = NV;  // this lane's best remaining slot (NV: none)
 #pragma unroll
-    for (int i = 0; i < TOPK_NV; ++i)
-      if (ok[i] && (key[i] > lk || li == 0xffffu)) {  // i ascending: ties keep the lower index
+    for (int i = 0; i < NV; ++i)
+      if (ok[i] && (ls == NV || key[i] > lk)) {  // i ascending: ties keep the lower slot
         lk = key[i];
-        li = lane + 64 * i;
+        ls = i;
       }
-    const uint32_t mk = nsx_wave_max_u32(li == 0xffffu ? 0u : lk);
-    const uint32_t wi = nsx_wave_min_u32((li != 0xffffu && lk == mk) ? li : 0xffffu);
-    sel_i[j] = wi == 0xffffu ? 0 : (int)wi;
+    const uint32_t mk = nsx_wave_max_u32(ls < NV ? lk : 0u);
+    int wi = 0;  // no expert left (E < k): index 0, as the reference's padding
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint64_t b = __builtin_amdgcn_ballot_w64(ls == i && lk == mk);
+      if (!found && b != 0) {
+        wi = 64 * i + (int)__builtin_ctzll(b);
+        found = true;
+      }
+    }
+    sel_i[j] = wi;
     sel_v[j] = key2f(mk);
 #pragma unroll
-    for (int i = 0; i < TOPK_NV; ++i)
-      if (lane + 64 * i == (int)wi) ok[i] = false;
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i == wi) ok[i] = false;
   }
   // static loop bounds (guards on k) keep sel_v / sel_w in registers
   float s = 0.f;
-  if (mode == NSX_ROUTE_GPTOSS) {  // softmax over the selected logits in float32 (gpt_oss.py:120)
 #pragma unroll
-    for (int j = 0; j < MAX_TOPK; ++j) {
-      sel_w[j] = j < k ? expf(sel_v[j] - sel_v[0]) : 0.f;
-      s += sel_w[j];
-    }
-  } else {  // renormalise the selected probabilities (router.py:68)
-#pragma unroll
-    for (int j = 0; j < MAX_TOPK; ++j) {
-      sel_w[j] = j < k ? sel_v[j] : 0.f;
+  for (int j = 0; j < MAX_TOPK; ++j) {
+    sel_w[j] = 0.f;
+    if (j < k) {
+      // GPT-OSS: softmax over the selected logits in float32 (gpt_oss.py:120);
+      // Qwen3: renormalise the selected probabilities (router.py:68)
+      sel_w[j] = mode == NSX_ROUTE_GPTOSS ? expf(sel_v[j] - sel_v[0]) : sel_v[j];
       s += sel_w[j];
     }
   }
 #pragma unroll
-  for (int j = 0; j < MAX_TOPK; ++j) sel_w[j] = sel_w[j] / s;
+  for (int j = 0; j < MAX_TOPK; ++j)
+    if (j < k) sel_w[j] = sel_w[j] / s;
 }
 
+// One token's top-k from its logits row (loads and selection), any E <= MAX_EXPERTS.
 __device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode,
                                           int (&sel_i)[MAX_TOPK], float (&sel_w)[MAX_TOPK]) {
-  float v[TOPK_NV];
-  topk_load(lg, E, v);
-  topk_select(v, E, k, mode, sel_i, sel_w);
+  if (E <= 128) {
+    float v[2];
+    topk_load<2>(lg, E, v);
+    topk_select<2>(v, E, k, mode, sel_i, sel_w);
+  } else {
+    float v[TOPK_NV];
+    topk_load<TOPK_NV>(lg, E, v);
+    topk_select<TOPK_NV>(v, E, k, mode, sel_i, sel_w);
+  }
 }
 
 // Router logits (model/gpt_oss.py:97-99,116-121; moe/router.py:59-69).
@@ -447,19 +468,6 @@ constexpr int GU_S = 3;         // K-steps per gate/up wave (one chunk)
 constexpr int DC_S = 6;         // K-steps per down wave (one chunk, one row group)
 constexpr int MAX_CHUNKS = 8;   // gate/up K-chunks (waves per matrix) of a workgroup (K <= 3072)
 
-// The pair's expert: issue the token's logit loads first (pair_logits), other
-// independent loads next, then select (pair_expert) -- waiting on the logits only.
-__device__ __forceinline__ void pair_logits(const MoeDev& a, int p, float (&v)[TOPK_NV]) {
-  topk_load(a.logits + (int64_t)(p / a.top_k) * a.E, a.E, v);
-}
-__device__ __forceinline__ int pair_expert(const MoeDev& a, int p, float (&v)[TOPK_NV]) {
-  const int j = p - (p / a.top_k) * a.top_k;
-  int si[MAX_TOPK];
-  float sw[MAX_TOPK];
-  topk_select(v, a.E, a.top_k, a.mode, si, sw);
-  return clamp_expert(si[j], a.E);
-}
-
 // Rows of D (after mx_sum_terms) for token column 0 go to dst[row] for rows < n.
 __device__ __forceinline__ void mx_store_rows(const v4f (&D)[4], int tile, int n, float* __restrict__ dst) {
   const int lane = __lane_id();
@@ -486,11 +494,9 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   // the top-k by wave 0 alone (sixteen waves selecting at once would share each SIMD four ways);
   // the token's first item also writes the ids/weights outputs, which the down phase reads
   if (wave == 0) {
-    float lg[TOPK_NV];
-    topk_load(a.logits + (int64_t)t * a.E, a.E, lg);
     int si[MAX_TOPK];
     float sw[MAX_TOPK];
-    topk_select(lg, a.E, k, a.mode, si, sw);
+    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw);
     int my_e = 0, e = 0;
     float my_w = 0.f;
 #pragma unroll
@@ -538,10 +544,25 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
 }
 
+// the arguments of the per-pair t64 kernels, loaded in one batch
+__device__ __forceinline__ void hoist_gu_args(const MoeDev& a) {
+  nsx_hoist(a.top_k, a.E, a.mode, (const void*)a.logits, (const void*)a.ids, (const void*)a.wts,
+            (const void*)a.xq_h, (const void*)a.xq_a, a.gate_base, a.up_base, (const void*)a.gate_ptrs,
+            (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias, (const void*)a.up_bias,
+            a.n_ff, a.cg, a.sg, a.ggu.nb, a.ggu.ns, a.ggu.rlast, a.ggu.tile_bytes, a.ggu.tiles, a.gdn.ns, a.act_kind,
+            a.alpha, a.limit);
+}
+__device__ __forceinline__ void hoist_down_args(const MoeDev& a) {
+  nsx_hoist(a.T, a.top_k, a.E, (const void*)a.ids, (const void*)a.wts, a.down_base, (const void*)a.down_ptrs,
+            a.down_stride, (const void*)a.down_bias, (const void*)a.xq_a, (const void*)a.out, a.n_embd, a.cd, a.sd,
+            a.gdn.nb, a.gdn.ns, a.gdn.rlast, a.gdn.tile_bytes, a.gdn.tiles, (int)gridDim.x);
+}
+
 // phase 1 on its own: workgroup = (pair, tile)
 __global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
   __shared__ float red[2][MAX_CHUNKS][64];
   __shared__ int s_e;
+  hoist_gu_args(a);
   const int tiles = (int)a.ggu.tiles;
   const int p = blockIdx.x / tiles;
   gu_item(a, p, blockIdx.x - p * tiles, red, s_e);
@@ -549,22 +570,24 @@ __global__ __launch_bounds__(1024) void moe_gu_kernel(MoeDev a) {
 
 // down and combine of one (token, 16-row group of a 64-row output tile) work
 // item, by a whole workgroup: one wave per (expert slot, K-chunk), each a
-// single pass over its steps. down_begin selects the token's top-k and
-// requests the weights and biases; down_end stages the activation terms
-// through LDS, runs the MFMAs and, in wave 0, sums each expert's chunks in a
-// fixed order (chunk 0 carries the bias) and combines the experts in
-// ascending id: out[rows] = sum of w_e * y_e. The expert ids and weights are
-// the ones the gate/up phase wrote.
+// single pass over its steps. down_begin stages the wave's activation terms
+// in LDS (they do not depend on the expert, so their loads go first), reads
+// the token's ids and weights (written by the gate/up phase) and requests the
+// weights and biases; down_end runs the MFMAs and, in wave 0, sums each
+// expert's chunks in a fixed order (chunk 0 carries the bias) and combines
+// the experts in ascending id: out[rows] = sum of w_e * y_e.
 constexpr int DC_PIECES = DC_S * XQ_STEP / 16;  // 16-byte pieces of one wave's activation terms
+constexpr int DC_STAGE = (DC_PIECES + 63) / 64;  // of them per lane
 
 struct DownItem {
   MxRegs<DC_S, 1> R;
   v4f bias;
-  int t, hh, tile, rg, p, s0, s1, my_e, my_rank;
+  int t, hh, tile, rg, p, s0, s1, my_rank;
   float my_w;
 };
 
-__device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& d) {
+__device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& d, uint8_t* xs) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int groups = 4 * (int)a.gdn.tiles;
   d.t = item / groups;
@@ -576,68 +599,52 @@ __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& 
   d.p = d.t * k + j;
   d.s0 = c * a.sd;
   d.s1 = min(a.gdn.ns, d.s0 + a.sd);
-  // the token's top-k, written by the gate/up phase: this wave's expert; in
-  // lane jj < k slot jj's expert, weight and rank in ascending expert id
-  const int32_t* tid = a.ids + (int64_t)d.t * k;
-  int idv[MAX_TOPK];
+  // this wave's activation terms (steps s0 .. s1 - 1) and the token's ids and weights, in one round trip
+  const int npc = (d.s1 - d.s0) * (XQ_STEP / 16);
+  const uint8_t* xsrc = a.xq_a + ((int64_t)d.p * a.gdn.ns + d.s0) * XQ_STEP;
+  v4u stage[DC_STAGE];
 #pragma unroll
-  for (int jj = 0; jj < MAX_TOPK; ++jj) idv[jj] = clamp_expert(tid[jj < k ? jj : k - 1], a.E);
-  const float my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
-  int e = 0, my_e = 0, my_rank = 0;
+  for (int i = 0; i < DC_STAGE; ++i) stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
+  const int id_l = clamp_expert(a.ids[(int64_t)d.t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
+  d.my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
+  const int e = __builtin_amdgcn_readlane(id_l, j);
+  // lane jj < k: slot jj's rank in ascending expert id (ties: lower slot)
+  d.my_rank = 0;
 #pragma unroll
   for (int jj = 0; jj < MAX_TOPK; ++jj) {
-    e = jj == j ? idv[jj] : e;
-    my_e = lane == jj ? idv[jj] : my_e;
+    const int ej = __builtin_amdgcn_readlane(id_l, jj < k ? jj : k - 1);
+    d.my_rank += (jj < k && (ej < id_l || (ej == id_l && jj < lane))) ? 1 : 0;
   }
-#pragma unroll
-  for (int jj = 0; jj < MAX_TOPK; ++jj)
-    my_rank += (jj < k && (idv[jj] < my_e || (idv[jj] == my_e && jj < lane))) ? 1 : 0;
-  d.my_e = my_e;
-  d.my_rank = my_rank;
-  d.my_w = my_w;
   mx_load_a<DC_S, 1>(d.R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) +
                               (int64_t)d.tile * a.gdn.tile_bytes, a.gdn, d.s0, d.s1, d.rg);
   const int r0 = d.tile * 64 + 16 * d.rg + 4 * (lane >> 4);
   d.bias = v4f{0.f, 0.f, 0.f, 0.f};  // chunk 0's bias rows, requested while the weights stream
   if (c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd)
     d.bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+#pragma unroll
+  for (int i = 0; i < DC_STAGE; ++i) {  // (clamped duplicates rewrite the same bytes)
+    const int pc = min(lane + 64 * i, npc - 1);
+    *(v4u*)(xs + pc * 16) = stage[i];
+  }
 }
 
-__device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&red)[16][16],
-                                         uint8_t (&xs)[16][DC_S * XQ_STEP], int (&s_slot)[MAX_TOPK]) {
+__device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&red)[16][16], const uint8_t* xs) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int k = a.top_k;
-  // this wave's activation terms (steps s0 .. s1 - 1), staged in LDS
-  typedef const __attribute__((address_space(1))) v4u gv4u;
-  const int npc = (d.s1 - d.s0) * (XQ_STEP / 16);
-  const uint8_t* xsrc = a.xq_a + ((int64_t)d.p * a.gdn.ns + d.s0) * XQ_STEP;
-  v4u stage[(DC_PIECES + 63) / 64];
-#pragma unroll
-  for (int i = 0; i < (DC_PIECES + 63) / 64; ++i)
-    stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
-#pragma unroll
-  for (int i = 0; i < (DC_PIECES + 63) / 64; ++i) {  // (clamped duplicates rewrite the same bytes)
-    const int pc = min(lane + 64 * i, npc - 1);
-    *(v4u*)(&xs[wave][pc * 16]) = stage[i];
-  }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes land before its reads
   __builtin_amdgcn_wave_barrier();
-  mx_load_b<DC_S, true, 1>(d.R, xs[wave], d.s0, 0, 1, d.s0, d.s1);
+  mx_load_b<DC_S, true, 1>(d.R, xs, d.s0, 0, 1, d.s0, d.s1);
   v4f D[1] = {};
   mx_compute<DC_S, 1>(d.R, a.gdn, d.s0, d.s1, D, d.rg);
   mx_sum_terms<1>(D);
-  __syncthreads();  // an earlier item's wave 0 is done with `red` and `s_slot`
   if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + d.bias;
   __syncthreads();
   if (wave != 0) return;
-  // slot order of the combine (ascending expert id), exchanged through LDS
-  if (lane < k) s_slot[d.my_rank] = lane;
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are visible to its reads
-  __builtin_amdgcn_wave_barrier();
+  // the experts in ascending id: rank jj's slot from a ballot over the slots' ranks
   const int row = d.tile * 64 + 16 * d.rg + (lane & 15);
   float o = 0.f;
   for (int jj = 0; jj < k; ++jj) {
-    const int jx = s_slot[jj];
+    const int jx = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lane < k && d.my_rank == jj));
     const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d.my_w), jx));
     float y = 0.f;
     for (int cc = 0; cc < a.cd; ++cc) y += red[jx * a.cd + cc][lane & 15];
@@ -652,13 +659,14 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
 __global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
   __shared__ float red[16][16];  // [wave = slot * cd + chunk][row of the group]
   __shared__ __align__(16) uint8_t xs[16][DC_S * XQ_STEP];  // each wave's activation terms, staged
-  __shared__ int s_slot[MAX_TOPK];
+  hoist_down_args(a);
   const int per = (int)(gridDim.x >> 3);
   const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
   if (item >= a.T * 4 * (int)a.gdn.tiles) return;  // padding workgroups of the 8-way split
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   DownItem d;
-  down_begin(a, item, d);
-  down_end(a, d, red, xs, s_slot);
+  down_begin(a, item, d, xs[wave]);
+  down_end(a, d, red, xs[wave]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1132,15 +1140,11 @@ __global__ __launch_bounds__(512) void moe_down_q4k_kernel(MoeDev a) {
   const int k = a.top_k, K = a.n_ff;
   if (wave < k) {
     const int p = t * k + wave;
-    const int e = clamp_expert(a.ids[p], a.E);
-    if (lane == 0) {  // this slot's rank in ascending expert id (ties: lower slot)
-      int rank = 0;
-      for (int jj = 0; jj < k; ++jj) {
-        const int ej = clamp_expert(a.ids[(int64_t)t * k + jj], a.E);
-        rank += (ej < e || (ej == e && jj < wave)) ? 1 : 0;
-      }
-      s_slot[rank] = wave;
-    }
+    const int id_l = clamp_expert(a.ids[(int64_t)t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
+    const int e = __builtin_amdgcn_readlane(id_l, wave);
+    // this slot's rank in ascending expert id (ties: lower slot)
+    const uint64_t before = __builtin_amdgcn_ballot_w64(lane < k && (id_l < e || (id_l == e && lane < wave)));
+    if (lane == 0) s_slot[__builtin_popcountll(before)] = wave;
     const int nu = K / 32;
     const uint32_t rb = (uint32_t)(K / 256) * 144u;
     const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);

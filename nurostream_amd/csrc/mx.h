@@ -100,7 +100,11 @@ __device__ __forceinline__ void xq_block(float r, int b, uint8_t* dst) {
     float m = fabsf(r);
     if (!(m <= 3.4028235e38f)) m = __builtin_inff();  // NaN counts as the largest
     m = nsx_row_fmax(m);
-    m = fmaxf(m, __shfl_xor(m, 16, 64));  // the block's two 16-lane rows
+    {  // the block's two 16-lane rows: permlane16_swap pairs row 2i with row 2i + 1 (no LDS)
+      const uint32_t mb = __builtin_bit_cast(uint32_t, m);
+      const auto sw = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+      m = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+    }
     uint32_t sc, code = 0;
     if (!(m <= 3.4028235e38f)) {
       sc = 255u;  // e8m0 NaN: the outputs of this token become NaN
@@ -141,8 +145,9 @@ struct MxRegs {
   uint32_t SA[S], SB[S];
 };
 
-// Weight operands of steps [s0, min(s1, s0 + S)) of a 64-row tile. Loads are
-// unpredicated so that their waits retire step by step: lanes past a partial
+// Weight operands of steps [s0, min(s1, s0 + S)) of a 64-row tile, read once
+// per call (nontemporal: streamed weights do not displace cached data). Loads
+// are unpredicated so that their waits retire step by step: lanes past a partial
 // last step read an in-bounds stand-in with scale 0 (the activation there is
 // zero). A weight e8m0 of 255 is NaN to the hardware: the row's result is
 // non-finite, as in the reference, whose fp32 dequant makes such a block
@@ -162,8 +167,8 @@ __device__ __forceinline__ void mx_load_a(MxRegs<S, G>& R, const uint8_t* __rest
       const bool alane = grp < rs;
       const int la = alane ? lane : 16 * rs - 1;
 #pragma unroll
-      for (int g = 0; g < G; ++g) R.A[u][g] = *(gv4u*)(ch + (g0 + g) * rs * 256 + la * 16);
-      R.SA[u] = *(gu32*)(ch + rs * 1024 + la * 4);  // raw: mx_compute selects (no wait in here)
+      for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
+      R.SA[u] = __builtin_nontemporal_load((gu32*)(ch + rs * 1024 + la * 4));  // raw: mx_compute selects
     }
   }
 }

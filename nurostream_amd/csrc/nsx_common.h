@@ -112,6 +112,19 @@ __device__ __forceinline__ float nsx_load_act(const void* p, int dtype, int64_t 
   return dtype == NSX_DT_F16 ? nsx_h2f(b) : nsx_bf2f(b);
 }
 
+// Kernel arguments are read through the scalar cache where first used; a
+// kernel whose first uses are spread over its prologue waits on one cache
+// miss after another. nsx_hoist ties wave-uniform values to an empty asm
+// statement, so their loads are issued together (one wait) where it stands.
+__device__ __forceinline__ void nsx_hoist1(int v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void nsx_hoist1(int64_t v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void nsx_hoist1(float v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void nsx_hoist1(const void* v) { asm volatile("" ::"s"(v)); }
+template <typename... A>
+__device__ __forceinline__ void nsx_hoist(const A&... v) {
+  (nsx_hoist1(v), ...);
+}
+
 // Wave64 reductions on DPP row rotations (within each 16-lane row, no LDS
 // round trip) plus four readlanes; the result is wave-uniform. Every lane of
 // the wave must be active.
