@@ -77,14 +77,15 @@ __device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, f
 }
 
 // Top-k of the E <= 64 NV logits held as by topk_load, largest first, ties to
-// the lower expert index. Each round takes the wave maximum of the lanes' best
-// remaining keys (DPP); the expert holding it with the lowest index is found
-// by ballots over the lanes' best slots in ascending order (slot s holds
-// experts 64 s .. 64 s + 63, so the first nonempty ballot has the lowest
-// index, and its lowest lane is the one). Results are wave-uniform.
+// the lower expert index. The lanes' remaining experts are lane masks per
+// slot (slot i holds experts 64 i .. 64 i + 63); each round takes the wave
+// maximum of the remaining keys (DPP), and the expert holding it with the
+// lowest index is the lowest set bit of the first slot's ballot of "remaining
+// and equal to the maximum". Results are wave-uniform. With weights false the
+// softmax is skipped (sel_w is left zero).
 template <int NV>
 __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mode, int (&sel_i)[MAX_TOPK],
-                                            float (&sel_w)[MAX_TOPK]) {
+                                            float (&sel_w)[MAX_TOPK], bool weights = true) {
   const int lane = __lane_id();
   bool ok[NV];
 #pragma unroll
@@ -115,24 +116,20 @@ __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mo
   for (int j = 0; j < MAX_TOPK; ++j) {
     sel_v[j] = 0.f;
     sel_i[j] = 0;
+    sel_w[j] = 0.f;
   }
 #pragma unroll
   for (int j = 0; j < MAX_TOPK; ++j) {
     if (j >= k) break;
     uint32_t lk = 0;
-    int ls = NV;  // this lane's best remaining slot (NV: none)
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (ok[i] && (ls == NV || key[i] > lk)) {  // i ascending: ties keep the lower slot
-        lk = key[i];
-        ls = i;
-      }
-    const uint32_t mk = nsx_wave_max_u32(ls < NV ? lk : 0u);
-    int wi = 0;  // no expert left (E < k): index 0, as the reference's padding
+    for (int i = 0; i < NV; ++i) lk = max(lk, ok[i] ? key[i] : 0u);
+    const uint32_t mk = nsx_wave_max_u32(lk);
+    int wi = 0;  // no expert left (E < k): index 0
     bool found = false;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const uint64_t b = __builtin_amdgcn_ballot_w64(ls == i && lk == mk);
+      const uint64_t b = __builtin_amdgcn_ballot_w64(ok[i] && key[i] == mk);
       if (!found && b != 0) {
         wi = 64 * i + (int)__builtin_ctzll(b);
         found = true;
@@ -141,14 +138,13 @@ __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mo
     sel_i[j] = wi;
     sel_v[j] = key2f(mk);
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i == wi) ok[i] = false;
+    for (int i = 0; i < NV; ++i) ok[i] = ok[i] && lane + 64 * i != wi;
   }
+  if (!weights) return;
   // static loop bounds (guards on k) keep sel_v / sel_w in registers
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < MAX_TOPK; ++j) {
-    sel_w[j] = 0.f;
     if (j < k) {
       // GPT-OSS: softmax over the selected logits in float32 (gpt_oss.py:120);
       // Qwen3: renormalise the selected probabilities (router.py:68)
@@ -163,15 +159,15 @@ __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mo
 
 // One token's top-k from its logits row (loads and selection), any E <= MAX_EXPERTS.
 __device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode,
-                                          int (&sel_i)[MAX_TOPK], float (&sel_w)[MAX_TOPK]) {
+                                          int (&sel_i)[MAX_TOPK], float (&sel_w)[MAX_TOPK], bool weights = true) {
   if (E <= 128) {
     float v[2];
     topk_load<2>(lg, E, v);
-    topk_select<2>(v, E, k, mode, sel_i, sel_w);
+    topk_select<2>(v, E, k, mode, sel_i, sel_w, weights);
   } else {
     float v[TOPK_NV];
     topk_load<TOPK_NV>(lg, E, v);
-    topk_select<TOPK_NV>(v, E, k, mode, sel_i, sel_w);
+    topk_select<TOPK_NV>(v, E, k, mode, sel_i, sel_w, weights);
   }
 }
 
@@ -496,7 +492,8 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   if (wave == 0) {
     int si[MAX_TOPK];
     float sw[MAX_TOPK];
-    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw);
+    const bool writes = j == 0 && tile == 0;  // the token's first item writes the ids and weights
+    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes);
     int my_e = 0, e = 0;
     float my_w = 0.f;
 #pragma unroll
@@ -505,7 +502,7 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
       my_e = lane == jj ? si[jj] : my_e;
       my_w = lane == jj ? sw[jj] : my_w;
     }
-    if (j == 0 && tile == 0 && lane < k) {
+    if (writes && lane < k) {
       a.ids[(int64_t)t * k + lane] = clamp_expert(my_e, a.E);
       a.wts[(int64_t)t * k + lane] = my_w;
     }
@@ -582,7 +579,7 @@ constexpr int DC_STAGE = (DC_PIECES + 63) / 64;  // of them per lane
 struct DownItem {
   MxRegs<DC_S, 1> R;
   v4f bias;
-  int t, hh, tile, rg, p, s0, s1, my_rank;
+  int t, hh, tile, rg, p, s0, s1, id_l;
   float my_w;
 };
 
@@ -605,16 +602,9 @@ __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& 
   v4u stage[DC_STAGE];
 #pragma unroll
   for (int i = 0; i < DC_STAGE; ++i) stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
-  const int id_l = clamp_expert(a.ids[(int64_t)d.t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
+  d.id_l = clamp_expert(a.ids[(int64_t)d.t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
   d.my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
-  const int e = __builtin_amdgcn_readlane(id_l, j);
-  // lane jj < k: slot jj's rank in ascending expert id (ties: lower slot)
-  d.my_rank = 0;
-#pragma unroll
-  for (int jj = 0; jj < MAX_TOPK; ++jj) {
-    const int ej = __builtin_amdgcn_readlane(id_l, jj < k ? jj : k - 1);
-    d.my_rank += (jj < k && (ej < id_l || (ej == id_l && jj < lane))) ? 1 : 0;
-  }
+  const int e = __builtin_amdgcn_readlane(d.id_l, j);
   mx_load_a<DC_S, 1>(d.R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) +
                               (int64_t)d.tile * a.gdn.tile_bytes, a.gdn, d.s0, d.s1, d.rg);
   const int r0 = d.tile * 64 + 16 * d.rg + 4 * (lane >> 4);
@@ -638,17 +628,50 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
   mx_compute<DC_S, 1>(d.R, a.gdn, d.s0, d.s1, D, d.rg);
   mx_sum_terms<1>(D);
   if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + d.bias;
+  // wave 0, while the others finish: the slots in ascending expert id (ties:
+  // lower slot) -- lane jj < k's rank, then rank r's slot jx[r] by ballot
+  int jx[MAX_TOPK];
+  if (wave == 0) {
+    int my_rank = 0;
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      const int ej = __builtin_amdgcn_readlane(d.id_l, jj < k ? jj : k - 1);
+      my_rank += (jj < k && (ej < d.id_l || (ej == d.id_l && jj < lane))) ? 1 : 0;
+    }
+#pragma unroll
+    for (int r = 0; r < MAX_TOPK; ++r) {
+      const uint64_t b = __builtin_amdgcn_ballot_w64(lane < k && my_rank == r);
+      jx[r] = b ? (int)__builtin_ctzll(b) : 0;
+    }
+  }
   __syncthreads();
   if (wave != 0) return;
-  // the experts in ascending id: rank jj's slot from a ballot over the slots' ranks
   const int row = d.tile * 64 + 16 * d.rg + (lane & 15);
   float o = 0.f;
-  for (int jj = 0; jj < k; ++jj) {
-    const int jx = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lane < k && d.my_rank == jj));
-    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d.my_w), jx));
-    float y = 0.f;
-    for (int cc = 0; cc < a.cd; ++cc) y += red[jx * a.cd + cc][lane & 15];
-    o = combine_one(o, w, y);
+  if (k <= 4 && a.cd == 4) {  // the usual shape (top-4, four K-chunks): every read issued at once
+    float v[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) v[r][cc] = red[(r < k ? jx[r] : 0) * 4 + cc][lane & 15];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (r >= k) break;
+      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d.my_w), jx[r]));
+      float y = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) y += v[r][cc];
+      o = combine_one(o, w, y);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < MAX_TOPK; ++r) {
+      if (r >= k) break;
+      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d.my_w), jx[r]));
+      float y = 0.f;
+      for (int cc = 0; cc < a.cd; ++cc) y += red[jx[r] * a.cd + cc][lane & 15];
+      o = combine_one(o, w, y);
+    }
   }
   if (lane < 16 && row < a.n_embd) a.out[(int64_t)d.t * a.n_embd + row] = o;
 }

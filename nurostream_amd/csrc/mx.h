@@ -70,65 +70,53 @@ constexpr int XQ_NT = 4;
 constexpr int XQ_CODES = 4 * XQ_NT * 32;
 constexpr int XQ_STEP = XQ_CODES + 4 * XQ_NT * 4;  // 576 B
 
-// |a| <= 448 rounded to nearest even on the E4M3 grid: returns the 7-bit
-// magnitude code and the rounded value. Normal codes have spacing 2^(e-3),
-// subnormals 2^-9; the rounding adds and removes 1.5 * 2^(k+23), which
-// leaves a multiple of 2^k (k the grid spacing) rounded by the fp32 adder.
-__device__ __forceinline__ uint32_t e4m3_code(float a, float& rq) {
-  const int e = (int)(__builtin_bit_cast(uint32_t, a) >> 23) - 127;
-  const int k = e - 3 > -9 ? e - 3 : -9;
-  const float c = __builtin_bit_cast(float, ((uint32_t)(k + 150) << 23) | 0x400000u);
-  float t = a + c;
-  asm volatile("" : "+v"(t));  // keep (a + c) - c from being folded
-  rq = t - c;
-  if (rq < 0.015625f) return (uint32_t)(rq * 512.f);  // subnormal (2^-6 itself gives code 8)
-  const uint32_t b = __builtin_bit_cast(uint32_t, rq);
-  return ((((b >> 23) & 0xffu) - 120u) << 3) | ((b >> 20) & 7u);
-}
-
 // Quantize one 32-element block into XQ_NT terms: lanes 32h .. 32h + 31 hold
-// element (lane & 31) of their block in r; dst is the token's xq base; b the
-// block index. Both 32-lane halves run in lock step (each its own block).
-__device__ __forceinline__ void xq_block(float r, int b, uint8_t* dst) {
+// element (lane & 31) of their block in r; step is the token's xq record of
+// the block's K-step and q the block's place in it (0..3). Both 32-lane
+// halves run in lock step (each its own block).
+//
+// Term 0's e8m0 scale 2^s0 comes from the block's largest |r|, so that
+// |r| / 2^s0 <= 448; term t uses 2^(s0 - 4t). v_cvt_pk_fp8_f32 rounds
+// r / 2^s to nearest even on the OCP E4M3 grid (subnormals included; checked
+// on gfx950 against a software rounding over every code, every tie and its
+// neighbours and 16M random values -- the only difference is the sign of
+// zero, so a value that rounds to zero stores +0), and the exact residual
+// r - code * 2^s is the next term's input. A residual is at most half the
+// grid spacing at the top binade, 16 * 2^s, which 2^(s - 4) still holds
+// (16 * 2^s = 256 * 2^(s - 4) <= 448 * 2^(s - 4)): every term adds 4 bits,
+// and the block's error after XQ_NT terms is at most 2^-16 of its largest
+// |r|. Only term 0 needs a reduction over the block.
+__device__ __forceinline__ void xq_block_step(float r, int q, uint8_t* step) {
   const int e = __lane_id() & 31;
-  const int s = b >> 2, q = b & 3;
   const int gp = (q & 1) * 2 + (e >> 4);
   const int j = (e & 15) + 16 * (q >> 1);
-  uint8_t* step = dst + (int64_t)s * XQ_STEP;
+  float m = fabsf(r);
+  if (!(m <= 3.4028235e38f)) m = __builtin_inff();  // NaN counts as the largest
+  m = nsx_row_max_nonneg(m);
+  {  // the block's two 16-lane rows: permlane16_swap pairs row 2i with row 2i + 1 (no LDS)
+    const uint32_t mb = __builtin_bit_cast(uint32_t, m);
+    const auto sw = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+    m = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+  }
+  const bool fin = m <= 3.4028235e38f;  // else e8m0 NaN: the outputs of this token become NaN
+  const bool nz = m != 0.f;
+  const uint32_t mb = __builtin_bit_cast(uint32_t, m);
+  const int s0 = (int)((mb >> 23) & 0xffu) - 127 - 8 + ((mb & 0x7fffffu) > 0x600000u ? 1 : 0);
+  if (!fin) r = 0.f;
 #pragma unroll
   for (int t = 0; t < XQ_NT; ++t) {
-    float m = fabsf(r);
-    if (!(m <= 3.4028235e38f)) m = __builtin_inff();  // NaN counts as the largest
-    m = nsx_row_fmax(m);
-    {  // the block's two 16-lane rows: permlane16_swap pairs row 2i with row 2i + 1 (no LDS)
-      const uint32_t mb = __builtin_bit_cast(uint32_t, m);
-      const auto sw = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
-      m = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
-    }
-    uint32_t sc, code = 0;
-    if (!(m <= 3.4028235e38f)) {
-      sc = 255u;  // e8m0 NaN: the outputs of this token become NaN
-      r = 0.f;
-    } else if (m == 0.f) {
-      sc = 0u;
-    } else {
-      const uint32_t mb = __builtin_bit_cast(uint32_t, m);
-      int sx = (int)((mb >> 23) & 0xffu) - 127 - 8 + ((mb & 0x7fffffu) > 0x600000u ? 1 : 0);
-      sx = sx < -127 ? -127 : sx;
-      sc = (uint32_t)(sx + 127);
-      float rq;
-      code = e4m3_code(__builtin_amdgcn_ldexpf(fabsf(r), -sx), rq);
-      const float back = __builtin_amdgcn_ldexpf(rq, sx);
-      if (r < 0.f) {
-        code |= code ? 0x80u : 0u;
-        r += back;
-      } else {
-        r -= back;
-      }
-    }
+    int sx = s0 - 4 * t;
+    sx = sx < -127 ? -127 : sx;
+    const uint32_t sc = !fin ? (t == 0 ? 255u : 0u) : (nz ? (uint32_t)(sx + 127) : 0u);
+    const uint32_t raw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_ldexpf(r, -sx), 0.f, 0, false) & 0xffu;
+    r -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)raw, 0), sx);  // exact
+    const uint32_t code = (raw & 0x7fu) != 0u ? raw : 0u;
     step[(gp * XQ_NT + t) * 32 + j] = (uint8_t)code;
     if (e == 0) *(uint32_t*)(step + XQ_CODES + (q * XQ_NT + t) * 4) = sc;
   }
+}
+__device__ __forceinline__ void xq_block(float r, int b, uint8_t* dst) {
+  xq_block_step(r, b & 3, dst + (int64_t)(b >> 2) * XQ_STEP);
 }
 
 // ---------------------------------------------------------------------------

@@ -131,10 +131,11 @@ __device__ __forceinline__ void nsx_hoist(const A&... v) {
 #define NSX_DPP_ROR(n) (0x120 + (n))
 template <typename Op>
 __device__ __forceinline__ uint32_t nsx_row_reduce_u32(uint32_t v, Op op) {
-  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(8), 0xf, 0xf, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(4), 0xf, 0xf, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(2), 0xf, 0xf, false));
-  v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, NSX_DPP_ROR(1), 0xf, 0xf, false));
+  // update_dpp with bound_ctrl lets the compiler fold each move into the op
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, NSX_DPP_ROR(8), 0xf, 0xf, true));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, NSX_DPP_ROR(4), 0xf, 0xf, true));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, NSX_DPP_ROR(2), 0xf, 0xf, true));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, NSX_DPP_ROR(1), 0xf, 0xf, true));
   return v;
 }
 __device__ __forceinline__ uint32_t nsx_wave_max_u32(uint32_t v) {
@@ -153,11 +154,22 @@ template <int CTRL>
 __device__ __forceinline__ float nsx_dpp_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
+// the same with bound_ctrl, so that the compiler can fold the move into its user
+template <int CTRL>
+__device__ __forceinline__ float nsx_dpp_fold(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+// max over the lane's 16-lane row of values >= 0 (or +inf): their bit patterns
+// order as unsigned integers, and the integer max folds with its DPP move
+__device__ __forceinline__ float nsx_row_max_nonneg(float v) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  return __builtin_bit_cast(float, nsx_row_reduce_u32(__builtin_bit_cast(uint32_t, v), mx));
+}
 __device__ __forceinline__ float nsx_row_fmax(float v) {  // max over the lane's 16-lane row
-  v = fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(8)>(v));
-  v = fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(4)>(v));
-  v = fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(2)>(v));
-  return fmaxf(v, nsx_dpp_f<NSX_DPP_ROR(1)>(v));
+  v = fmaxf(v, nsx_dpp_fold<NSX_DPP_ROR(8)>(v));
+  v = fmaxf(v, nsx_dpp_fold<NSX_DPP_ROR(4)>(v));
+  v = fmaxf(v, nsx_dpp_fold<NSX_DPP_ROR(2)>(v));
+  return fmaxf(v, nsx_dpp_fold<NSX_DPP_ROR(1)>(v));
 }
 // Wave64 sum (wave-uniform): rows by rotation, then rows 0 + 1 + 2 + 3.
 __device__ __forceinline__ float nsx_wave_sum(float v) {
