@@ -296,6 +296,175 @@ static int launch_topk(const float* logits, int64_t T, int64_t E, int k, int mod
   return NSX_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// Router logits for several tokens (T >= RM_MIN_T) as fp32 MFMA tiles.
+//
+// logits = h W^T is a small GEMM; the one-wave-per-expert kernel above
+// re-reads each token group's h per expert. Here a wave computes a 16-token x
+// 16-expert tile over one K-chunk of RM_KC with v_mfma_f32_16x16x4f32 (fp32
+// products, fp32 accumulation; all of the chunk's loads in flight at once),
+// and writes the tile's partial sums; router_reduce_kernel adds the chunks in
+// a fixed order, adds the bias, writes the logits and selects the top-k. A
+// workgroup is 4 waves: one token tile, 4 adjacent expert tiles (their h
+// loads hit the same lines). Extra workgroups past the tiles build h's
+// activation terms (t64 layers), as in router_logits_kernel.
+//
+// Operand layout of v_mfma_f32_16x16x4f32: A[i][k] in lane i + 16 k, B[k][j]
+// in lane j + 16 k, D[i][j] in lane j + 16 (i / 4), register i % 4. Lane
+// (i, q) loads 4 consecutive elements k0 + 4q .. k0 + 4q + 3 of its token's
+// h and of its expert's row; MFMA u (0..3) takes element u of both, so the
+// four MFMAs of a 16-wide step cover it in full.
+
+constexpr int RM_MIN_T = 16;  // tokens from which the MFMA router runs
+constexpr int RM_KC = 128;    // K per chunk (8 steps of 16)
+constexpr int RM_EW = 4;      // expert tiles (waves) per workgroup
+constexpr int RM_XQ = 2;      // h block pairs quantized per wave
+constexpr int RM_RB = 16;     // partials per expert slot loaded at once in router_reduce_kernel
+
+__device__ __forceinline__ void load4_w(const void* W, int wdt, int64_t off, float (&w)[4]) {
+  typedef const __attribute__((address_space(1))) v4f gv4f;
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  typedef const __attribute__((address_space(1))) u32x2 gu2;
+  if (wdt == NSX_F32) {
+    const v4f a = *(gv4f*)((const float*)W + off);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else {
+    const u32x2 q = *(gu2*)((const uint16_t*)W + off);
+    const uint32_t v[4] = {q.x & 0xffffu, q.x >> 16, q.y & 0xffffu, q.y >> 16};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = wdt == NSX_BF16 ? nsx_bf2f(v[i]) : nsx_h2f(v[i]);
+  }
+}
+
+__global__ __launch_bounds__(64 * RM_EW) void router_mfma_kernel(const float* __restrict__ h, int T, int K,
+                                                                 const void* __restrict__ W, int wdt, int E,
+                                                                 float* __restrict__ part, int ntile,
+                                                                 uint8_t* __restrict__ xq) {
+  typedef const __attribute__((address_space(1))) v4f gv4f;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  if ((int)blockIdx.x >= ntile) {  // activation terms of h: RM_XQ tasks (two blocks each) per wave
+    const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
+    const int64_t tasks = (int64_t)T * pairs;
+    const int64_t task0 = ((int64_t)(blockIdx.x - ntile) * RM_EW + wave) * RM_XQ;
+    float r[RM_XQ];
+#pragma unroll
+    for (int u = 0; u < RM_XQ; ++u) {  // loads first
+      const int64_t task = min(task0 + u, tasks - 1);
+      const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
+      r[u] = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
+    }
+#pragma unroll
+    for (int u = 0; u < RM_XQ; ++u) {
+      const int64_t task = task0 + u;
+      if (task >= tasks) break;
+      const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
+      xq_block(b < nb ? r[u] : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
+    }
+    return;
+  }
+  const int ET = (E + 16 * RM_EW - 1) / (16 * RM_EW), TT = (T + 15) / 16;
+  int b = (int)blockIdx.x;
+  const int eg = b % ET;
+  b /= ET;
+  const int tt = b % TT, kc = b / TT;
+  const int t0 = tt * 16, e0 = (eg * RM_EW + wave) * 16;
+  const int ti = min(t0 + (lane & 15), T - 1), ei = min(e0 + (lane & 15), E - 1);
+  const int q = lane >> 4;
+  const int k_lo = kc * RM_KC, k_hi = min(K, k_lo + RM_KC);
+  v4f a[RM_KC / 16];
+  float w[RM_KC / 16][4];
+#pragma unroll
+  for (int s = 0; s < RM_KC / 16; ++s) {
+    const int k = k_lo + 16 * s + 4 * q;
+    const int kk = k < k_hi ? k : k_hi - 4;  // (K is a multiple of 16: a chunk ends on a whole step)
+    a[s] = *(gv4f*)(h + (int64_t)ti * K + kk);
+    load4_w(W, wdt, (int64_t)ei * K + kk, w[s]);
+  }
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < RM_KC / 16; ++s) {
+    if (k_lo + 16 * s >= k_hi) break;
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].x, w[s][0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].y, w[s][1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].z, w[s][2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].w, w[s][3], acc, 0, 0, 0);
+  }
+  const int e = e0 + (lane & 15);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + 4 * q + r;
+    if (t < T && e < E) part[((int64_t)kc * T + t) * E + e] = acc[r];
+  }
+}
+
+// one wave per token: logits = sum of the K-chunk partials in chunk order +
+// bias (written out), then the top-k as topk_kernel
+template <int NV>
+__device__ __forceinline__ void router_reduce_token(const float* __restrict__ part, int nkc, int T, int E, int t,
+                                                    const float* __restrict__ bias, int k, int mode,
+                                                    float* __restrict__ logits, int32_t* __restrict__ ids,
+                                                    float* __restrict__ wts) {
+  const int lane = __lane_id();
+  float acc[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+  for (int c0 = 0; c0 < nkc; c0 += RM_RB) {  // NV x RM_RB loads in flight, then the adds in chunk order
+    float pv[NV][RM_RB];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int u = 0; u < RM_RB; ++u)
+        pv[i][u] = part[((int64_t)min(c0 + u, nkc - 1) * T + t) * E + min(lane + 64 * i, E - 1)];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int u = 0; u < RM_RB; ++u) acc[i] = c0 + u < nkc ? acc[i] + pv[i][u] : acc[i];
+  }
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = min(lane + 64 * i, E - 1);
+    v[i] = bias ? acc[i] + bias[e] : acc[i];
+    if (lane + 64 * i < E) logits[(int64_t)t * E + lane + 64 * i] = v[i];
+  }
+  int si[MAX_TOPK];
+  float sw[MAX_TOPK];
+  topk_select<NV>(v, E, k, mode, si, sw);
+  if (lane == 0)
+    for (int j = 0; j < k; ++j) {
+      ids[(int64_t)t * k + j] = si[j];
+      wts[(int64_t)t * k + j] = sw[j];
+    }
+}
+
+__global__ __launch_bounds__(256) void router_reduce_kernel(const float* __restrict__ part, int nkc, int T, int E,
+                                                            const float* __restrict__ bias, int k, int mode,
+                                                            float* __restrict__ logits, int32_t* __restrict__ ids,
+                                                            float* __restrict__ wts) {
+  const int t = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (t >= T) return;
+  if (E <= 128)
+    router_reduce_token<2>(part, nkc, T, E, t, bias, k, mode, logits, ids, wts);
+  else
+    router_reduce_token<TOPK_NV>(part, nkc, T, E, t, bias, k, mode, logits, ids, wts);
+}
+
+static int rm_chunks(int64_t K) { return (int)nsx_cdiv(K, RM_KC); }
+
+static int launch_router_mfma(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias,
+                              int64_t E, int k, int mode, float* part, float* logits, int32_t* ids, float* wts,
+                              uint8_t* xq, hipStream_t st) {
+  const int64_t ntile = nsx_cdiv(E, 16 * RM_EW) * nsx_cdiv(T, 16) * rm_chunks(K);
+  const int64_t xq_tasks = T * 2 * nsx_cdiv(K / 32, 4);
+  const int64_t grid = ntile + (xq ? nsx_cdiv(xq_tasks, (int64_t)RM_EW * RM_XQ) : 0);
+  int rc = nsx_launch(router_mfma_kernel, dim3((unsigned)grid), dim3(64 * RM_EW), 0, st, h, (int)T, (int)K, w, wdt,
+                      (int)E, part, (int)ntile, xq);
+  if (rc) return rc;
+  return nsx_launch(router_reduce_kernel, dim3((unsigned)nsx_cdiv(T, 4)), dim3(256), 0, st, (const float*)part,
+                    rm_chunks(K), (int)T, (int)E, bias, k, mode, logits, ids, wts);
+}
+
 extern "C" int nsx_router_topk(const float* h, int64_t T, int64_t K, const void* w, int w_dtype, const float* bias,
                                int64_t n_expert, int top_k, int mode, int32_t* ids, float* weights, float* logits,
                                void* stream) {
@@ -1338,7 +1507,7 @@ __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
 
 struct MoePlan {
   int64_t off_logits, off_act, off_xqh, off_xqa, total;
-  int64_t off_items, off_nitems, off_sorted, off_corder, off_y;
+  int64_t off_items, off_nitems, off_sorted, off_corder, off_y, off_rpart;
   MxGeom ggu, gdn;
   int cg, cd, sd;
   bool grouped;
@@ -1402,6 +1571,8 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   o = al(o + (p.grouped ? P * 4 : 0));
   p.off_y = o;
   o = al(o + (p.grouped ? P * L->n_embd * 4 : 0));
+  p.off_rpart = o;  // router K-chunk partials (MFMA router)
+  o = al(o + (T >= RM_MIN_T ? (int64_t)rm_chunks(L->n_embd) * T * L->n_expert * 4 : 0));
   p.total = o;
   return p;
 }
@@ -1559,12 +1730,19 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
 
   auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
   if (on(NSX_PHASE_ROUTER)) {
-    rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
-                       (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
-    if (rc) return rc;
-    if ((!t64 || p.grouped) &&  // the per-pair t64 kernels select the top-k themselves
-        (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
-      return rc;
+    if (T >= RM_MIN_T) {  // logits as MFMA tiles, then chunk sums + top-k
+      rc = launch_router_mfma(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert, L->top_k,
+                              L->router_mode, (float*)(ws + p.off_rpart), (float*)(ws + p.off_logits), ids, weights,
+                              t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
+      if (rc) return rc;
+    } else {
+      rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
+                         (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
+      if (rc) return rc;
+      if ((!t64 || p.grouped) &&  // the per-pair t64 kernels select the top-k themselves
+          (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
+        return rc;
+    }
   }
   const int64_t P = T * L->top_k;
 
