@@ -1267,15 +1267,18 @@ __device__ __forceinline__ void q4k_unit_load(const uint8_t* __restrict__ mat, i
                                               v4u& hd) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
   const uint8_t* sbp = mat + (int64_t)row * rb + (u >> 3) * 144;
-  hd = *(gv4u*)sbp;
+  hd = *(gv4u*)sbp;  // (cached: eight lanes share a header, and tokens routed alike share rows)
   c = *(gv4u*)(sbp + 16 + 16 * (u & 7));
 }
 
 // gate/up: workgroup = (pair, 16 rows), wave = 2 rows of gate and of up
-template <int U>
-__global__ __launch_bounds__(512) void moe_gu_q4k_kernel(MoeDev a) {
+template <int U>  // (4 waves per SIMD: two workgroups share a CU, VGPRs <= 128)
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void moe_gu_q4k_kernel(MoeDev a) {
   extern __shared__ __align__(16) float q4k_xs[];
   constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
+  nsx_hoist(a.n_ff, a.n_embd, a.top_k, a.E, (const void*)a.ids, (const void*)a.h, a.gate_base, a.up_base,
+            (const void*)a.gate_ptrs, (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias,
+            (const void*)a.up_bias, (const void*)a.act, a.act_kind, a.alpha, a.limit);
   const int groups = (a.n_ff + RPG - 1) / RPG;
   const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
   const int K = a.n_embd, t = p / a.top_k;
@@ -1326,6 +1329,8 @@ template <int U>
 __global__ __launch_bounds__(512) void moe_down_q4k_kernel(MoeDev a) {
   __shared__ float red[MAX_TOPK][Q4K_DN_ROWS];
   __shared__ int s_slot[MAX_TOPK];
+  nsx_hoist(a.n_embd, a.n_ff, a.top_k, a.E, (const void*)a.ids, (const void*)a.wts, (const void*)a.act,
+            a.down_base, (const void*)a.down_ptrs, a.down_stride, (const void*)a.down_bias, (const void*)a.out);
   const int groups = (a.n_embd + Q4K_DN_ROWS - 1) / Q4K_DN_ROWS;
   const int t = blockIdx.x / groups, r0 = (blockIdx.x - t * groups) * Q4K_DN_ROWS;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
