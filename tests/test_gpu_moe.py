@@ -49,6 +49,42 @@ def test_router_topk(dev, mode, T, E, K, k, wdt):
     np.testing.assert_allclose(to_np(wts)[ok], rw[ok], rtol=2e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("name,layout,T", [("gptoss-120b", "t64", 16), ("gptoss-120b", "t64", 40),
+                                           ("qwen3-235b", "gguf", 33), ("gptoss-small", "t64", 70),
+                                           ("qwen3-small", "gguf", 17)])
+def test_router_mfma_tiles(dev, name, layout, T):
+    """T >= 16: the layer's router runs as fp32 MFMA tiles over K-chunks and a
+    fixed-order chunk sum fused with the top-k. Logits (read from the
+    workspace, where the later phases read them), ids and weights of every
+    token against the oracle router; E not a multiple of 64 and T not a
+    multiple of 16 exercise the tile masks."""
+    from nurostream_amd import _native as N
+    from nurostream_amd import synth
+    cfg = {"gptoss-120b": synth.GPTOSS_120B, "qwen3-235b": synth.QWEN3_235B}.get(name) or _small(name)
+    t = synth.make_layer(cfg, seed=41, device=dev)
+    layer = _layer(cfg, t, layout)
+    h = synth.activations(T, cfg.n_embd, seed=T, device=dev)
+    E, k = cfg.n_expert, cfg.top_k
+    out = torch.empty(T, cfg.n_embd, device=dev)
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, k, device=dev)
+    ws = layer.new_workspace(T)
+    layer.phase(N.PHASE_ROUTER, h, out, ids, w, ws)
+    logits = ws[: T * E * 4].view(torch.float32).reshape(T, E)  # the workspace starts with the logits
+    hn, Wn = h.cpu().numpy(), t["router_w"].float().cpu().numpy()
+    if cfg.router_mode == "gptoss":
+        bn = t["router_b"].float().cpu().numpy()
+        rid, rw, rlog = OM.route_gptoss(hn, Wn, bn, k)
+    else:
+        bn = None
+        rid, rw, rlog = OM.route_qwen3(hn, Wn, k)
+    assert rel_max(to_np(logits), rlog) < 1e-5
+    ok = ~_near_tie_tokens(rlog, k, hn, Wn, bn)
+    assert ok.sum() >= T - 2
+    np.testing.assert_array_equal(to_np(ids)[ok], rid[ok])
+    np.testing.assert_allclose(to_np(w)[ok], rw[ok], rtol=2e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("name,layout,slabs", [("gptoss-small", "t64", False), ("gptoss-small", "t64", True),
                                                ("gptoss-small", "gguf", False), ("gptoss-small", "gguf", True),
                                                ("qwen3-small", "gguf", False), ("q4_0-small", "gguf", False)])
