@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define NSX_ABI_VERSION 2
+#define NSX_ABI_VERSION 3
 
 /* status codes; the Python shim maps them onto the reference's exceptions */
 enum {
@@ -135,6 +135,14 @@ typedef struct nsx_moe_layer {
   int64_t gate_stride;
   int64_t up_stride;
   int64_t down_stride;
+  /* t64 layout only, optional: per projection a device array of n_expert x
+   * ceil(rows / 64) tile addresses, tile t of expert e at X_tiles[e * tiles +
+   * t]; when set it takes precedence over base/ptrs. A tile may sit anywhere
+   * the device can read, pinned host memory included (see
+   * nsx_host_device_address): the kernels then read it over PCIe. */
+  const uint64_t *gate_tiles;
+  const uint64_t *up_tiles;
+  const uint64_t *down_tiles;
 } nsx_moe_layer;
 
 /* Bytes of caller-provided workspace for T tokens. The caller zeroes the
@@ -196,6 +204,11 @@ int nsx_copy_blocks_async(int64_t n, const uint64_t *src, const uint64_t *dst,
                           const int64_t *bytes, void *stream, void *event);
 int nsx_gather_copy(int64_t n, const uint64_t *src, const uint64_t *dst,
                     const int64_t *bytes, void *stream);
+
+/* The device address of pinned host memory (allocated pinned, e.g. by
+ * hipHostMalloc or torch's pin_memory), for tile tables that point into it.
+ * Fails (NSX_EHIP) if host is not device-mapped pinned memory. */
+int nsx_host_device_address(const void *host, uint64_t *device_address);
 
 #ifdef __cplusplus
 }

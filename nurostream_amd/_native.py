@@ -42,6 +42,7 @@ class MoeLayerC(C.Structure):
         ("up_ptrs", _p), ("down_ptrs", _p), ("gate_bias", _p), ("up_bias", _p),
         ("down_bias", _p), ("gate_base", _p), ("up_base", _p), ("down_base", _p),
         ("gate_stride", C.c_int64), ("up_stride", C.c_int64), ("down_stride", C.c_int64),
+        ("gate_tiles", _p), ("up_tiles", _p), ("down_tiles", _p),
     ]
 
 
@@ -62,6 +63,7 @@ _SIGS = {
     "nsx_add_rmsnorm": (_i, [_p, _p, _i64, _i64, C.c_float, _p, _p, _p, _p]),
     "nsx_copy_blocks_async": (_i, [_i64, _p, _p, _p, _p, _p]),
     "nsx_gather_copy": (_i, [_i64, _p, _p, _p, _p]),
+    "nsx_host_device_address": (_i, [_p, C.POINTER(C.c_uint64)]),
 }
 PHASE_ROUTER, PHASE_GATE_UP, PHASE_DOWN, PHASE_COMBINE = 0, 1, 2, 3
 
@@ -94,7 +96,7 @@ def load():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.nsx_abi_version() != 2:
+    if lib.nsx_abi_version() != 3:
         raise NativeError("libnsx.so ABI version mismatch")
     _lib = lib
     return lib

@@ -551,6 +551,9 @@ struct MoeDev {
   const uint64_t* gate_ptrs;
   const uint64_t* up_ptrs;
   const uint64_t* down_ptrs;
+  const uint64_t* gate_tiles;  // t64: tile t of expert e at X_tiles[e * tiles + t] (when set)
+  const uint64_t* up_tiles;
+  const uint64_t* down_tiles;
   const void* gate_base;
   const void* up_base;
   const void* down_base;
@@ -629,6 +632,15 @@ __device__ __forceinline__ const uint8_t* expert_base(const void* base, int64_t 
   return base ? (const uint8_t*)base + (int64_t)e * stride : (const uint8_t*)ptrs[e];
 }
 
+// tile `tile` of expert e's t64 matrix: from the tile table when there is one
+// (tiles may then sit anywhere the device can read, pinned host memory
+// included), else at its offset in the expert
+__device__ __forceinline__ const uint8_t* tile_base(const void* base, int64_t stride, const uint64_t* ptrs,
+                                                    const uint64_t* tiles, const MxGeom& G, int e, int tile) {
+  if (tiles) return (const uint8_t*)tiles[(int64_t)e * G.tiles + tile];
+  return expert_base(base, stride, ptrs, e) + (int64_t)tile * G.tile_bytes;
+}
+
 constexpr int GU_S = 3;         // K-steps per gate/up wave (one chunk)
 constexpr int DC_S = 6;         // K-steps per down wave (one chunk, one row group)
 constexpr int MAX_CHUNKS = 8;   // gate/up K-chunks (waves per matrix) of a workgroup (K <= 3072)
@@ -679,9 +691,9 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   }
   __syncthreads();
   const int e = s_e;
-  const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
-                              : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
-  mx_load_a<GU_S>(R, mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1);
+  const uint8_t* mat = m == 0 ? tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile)
+                              : tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
+  mx_load_a<GU_S>(R, mat, a.ggu, s0, s1);
   const int row = tile * 64 + lane;
   const int rowc = min(row, a.n_ff - 1);
   float gb = 0.f, ub = 0.f;  // wave 0's biases, requested while the weights stream
@@ -714,12 +726,14 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
 __device__ __forceinline__ void hoist_gu_args(const MoeDev& a) {
   nsx_hoist(a.top_k, a.E, a.mode, (const void*)a.logits, (const void*)a.ids, (const void*)a.wts,
             (const void*)a.xq_h, (const void*)a.xq_a, a.gate_base, a.up_base, (const void*)a.gate_ptrs,
-            (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias, (const void*)a.up_bias,
+            (const void*)a.up_ptrs, (const void*)a.gate_tiles, (const void*)a.up_tiles, a.gate_stride, a.up_stride,
+            (const void*)a.gate_bias, (const void*)a.up_bias,
             a.n_ff, a.cg, a.sg, a.ggu.nb, a.ggu.ns, a.ggu.rlast, a.ggu.tile_bytes, a.ggu.tiles, a.gdn.ns, a.act_kind,
             a.alpha, a.limit);
 }
 __device__ __forceinline__ void hoist_down_args(const MoeDev& a) {
   nsx_hoist(a.T, a.top_k, a.E, (const void*)a.ids, (const void*)a.wts, a.down_base, (const void*)a.down_ptrs,
+            (const void*)a.down_tiles,
             a.down_stride, (const void*)a.down_bias, (const void*)a.xq_a, (const void*)a.out, a.n_embd, a.cd, a.sd,
             a.gdn.nb, a.gdn.ns, a.gdn.rlast, a.gdn.tile_bytes, a.gdn.tiles, (int)gridDim.x);
 }
@@ -774,8 +788,8 @@ __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& 
   d.id_l = clamp_expert(a.ids[(int64_t)d.t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
   d.my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
   const int e = __builtin_amdgcn_readlane(d.id_l, j);
-  mx_load_a<DC_S, 1>(d.R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) +
-                              (int64_t)d.tile * a.gdn.tile_bytes, a.gdn, d.s0, d.s1, d.rg);
+  mx_load_a<DC_S, 1>(d.R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, d.tile), a.gdn,
+                     d.s0, d.s1, d.rg);
   const int r0 = d.tile * 64 + 16 * d.rg + 4 * (lane >> 4);
   d.bias = v4f{0.f, 0.f, 0.f, 0.f};  // chunk 0's bias rows, requested while the weights stream
   if (c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd)
@@ -997,10 +1011,10 @@ __global__ __launch_bounds__(1024) void moe_gu_grouped_kernel(MoeDev a) {
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
   const int m = wave / a.cg, c = wave - m * a.cg;
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
-  const uint8_t* mat = m == 0 ? expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e)
-                              : expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
+  const uint8_t* mat = m == 0 ? tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile)
+                              : tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
   MxRegs<GU_S> R;
-  mx_load_a<GU_S>(R, mat + (int64_t)tile * a.ggu.tile_bytes, a.ggu, s0, s1);
+  mx_load_a<GU_S>(R, mat, a.ggu, s0, s1);
   const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
   const int64_t xs = (int64_t)a.ggu.ns * XQ_STEP;
   for (int tg = 0; tg * 4 < n; ++tg) {
@@ -1048,8 +1062,8 @@ __global__ __launch_bounds__(1024) void moe_down_grouped_kernel(MoeDev a) {
   const int c = wave >> 2, rg = wave & 3;
   const int s0 = c * a.sdg, s1 = min(a.gdn.ns, s0 + a.sdg);
   MxRegs<DC_S, 1> R;
-  mx_load_a<DC_S, 1>(R, expert_base(a.down_base, a.down_stride, a.down_ptrs, e) + (int64_t)tile * a.gdn.tile_bytes,
-                     a.gdn, s0, s1, rg);
+  mx_load_a<DC_S, 1>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, tile), a.gdn, s0,
+                     s1, rg);
   const int r0 = tile * 64 + 16 * rg + 4 * (lane >> 4);
   v4f bias = {0.f, 0.f, 0.f, 0.f};  // chunk 0 carries the bias, as in moe_down_kernel
   if (c == 0 && a.down_bias && r0 < a.n_embd) bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
@@ -1602,9 +1616,11 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
   NSX_REQUIRE(L->n_embd > 0 && L->n_ff > 0 && L->n_embd % be == 0 && L->n_ff % be == 0, NSX_EINVAL,
               "n_embd=%d n_ff=%d must be multiples of %d", L->n_embd, L->n_ff, be);
   NSX_REQUIRE(L->act == NSX_ACT_CLAMPED_SWIGLU || L->act == NSX_ACT_SILU_MUL, NSX_EINVAL, "act %d", L->act);
-  NSX_REQUIRE(L->router_w && (L->gate_ptrs || L->gate_base) && (L->up_ptrs || L->up_base) &&
-                  (L->down_ptrs || L->down_base),
+  NSX_REQUIRE(L->router_w && (L->gate_ptrs || L->gate_base || L->gate_tiles) &&
+                  (L->up_ptrs || L->up_base || L->up_tiles) && (L->down_ptrs || L->down_base || L->down_tiles),
               NSX_EINVAL, "null weights");
+  NSX_REQUIRE(L->layout == NSX_LAYOUT_T64 || !(L->gate_tiles || L->up_tiles || L->down_tiles), NSX_EINVAL,
+              "tile tables need the t64 layout");
   const int64_t mx = std::max(L->n_embd, L->n_ff);
   NSX_REQUIRE((int64_t)raw_row_bytes<NSX_Q8_0>((int)mx) * mx < (1ll << 31), NSX_EINVAL, "expert matrix above 2 GiB");
   if (L->layout == NSX_LAYOUT_GGUF) {
@@ -1699,6 +1715,9 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.gate_ptrs = L->gate_ptrs;
   d.up_ptrs = L->up_ptrs;
   d.down_ptrs = L->down_ptrs;
+  d.gate_tiles = L->gate_tiles;
+  d.up_tiles = L->up_tiles;
+  d.down_tiles = L->down_tiles;
   d.gate_base = L->gate_base;
   d.up_base = L->up_base;
   d.down_base = L->down_base;
@@ -1968,5 +1987,17 @@ extern "C" int nsx_gather_copy(int64_t n, const uint64_t* src, const uint64_t* d
     int rc = nsx_launch(gather_copy_kernel, dim3((unsigned)max_chunks, (unsigned)L.n), dim3(256), 0, S(stream), L);
     if (rc) return rc;
   }
+  return NSX_OK;
+}
+
+extern "C" int nsx_host_device_address(const void* host, uint64_t* device_address) {
+  NSX_REQUIRE(host && device_address, NSX_EINVAL, "null pointer");
+  void* d = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&d, const_cast<void*>(host), 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // reported here: do not leave it for the caller's next HIP call
+    return nsx_fail(NSX_EHIP, "hipHostGetDevicePointer: %s (not device-mapped pinned memory?)", hipGetErrorString(e));
+  }
+  *device_address = (uint64_t)(uintptr_t)d;
   return NSX_OK;
 }

@@ -155,6 +155,7 @@ class _HostBlockStore:
         self.kinds = tuple(full)
         import numpy as np
         self.per, self.blocks, self.dev, self.host, self.where, self.whole = {}, {}, {}, {}, {}, {}
+        self.tiles, self.block_bytes = {}, {}
         self.segs = {}
         self.host_bytes = 0
         for kind in self.kinds:
@@ -183,6 +184,8 @@ class _HostBlockStore:
                         where[(e, i)] = ("dev", od, b0, n)
                         od += n
             self.per[kind], self.blocks[kind] = per, len(spans)
+            self.tiles[kind] = -(-rows[kind] // 64)
+            self.block_bytes[kind] = block_rows * rb  # every block but the last spans this many bytes
             self.dev[kind], self.host[kind], self.where[kind] = dev, hst, where
             self.whole[kind] = [not host[e].any() for e in range(n_expert)]
             self.host_bytes += nh
@@ -207,23 +210,63 @@ class _HostBlockStore:
             return None
         return self.dev[kind].data_ptr() + self.where[kind][(e, 0)][1]
 
+    def tile_table(self, kind: str, device) -> torch.Tensor:
+        """int64 device tensor: the address of every 64-row tile of every
+        expert, in HBM or (device-mapped) in the pinned host blocks."""
+        from .. import _native as N
+        import ctypes as C
+        lib = N.load()
+        hdev = C.c_uint64(0)
+        N.check(lib.nsx_host_device_address(self.host[kind].data_ptr(), C.byref(hdev)), "host device address")
+        per, n_expert = self.per[kind], len(self.whole[kind])
+        tiles = self.tiles[kind]
+        tb = per // tiles
+        dbase, hbase = self.dev[kind].data_ptr(), int(hdev.value)
+        tab = []
+        for e in range(n_expert):
+            for t in range(tiles):
+                loc, off, b0, n = self.where[kind][(e, (t * tb) // self.block_bytes[kind])]
+                assert b0 <= t * tb and t * tb + tb <= b0 + n
+                tab.append((dbase if loc == "dev" else hbase) + off + t * tb - b0)
+        return torch.tensor(tab, dtype=torch.int64, device=device)
+
+    def host_bytes_of(self, kind: str, e: int) -> int:
+        """Bytes of expert e's matrix held in pinned host RAM."""
+        return sum(n for (ee, _), (loc, _, _, n) in self.where[kind].items() if ee == e and loc == "host")
+
 
 class GptOssHostStreamedStack(GptOssFFNStack):
     """BASELINE config 5b: the FFN stack with a seeded share (25%) of the
-    experts' row blocks in pinned host RAM.
+    experts' row blocks in pinned host RAM. Two ways to reach them:
 
-    Per layer and step: the router runs on the device and its ids come to the
-    host (model/gpt_oss.py:121 does the same to pick its windows); every
-    chosen expert matrix with host blocks is assembled in a staging slot --
-    its host blocks as DMA copies from pinned RAM (nsx_copy_blocks_async, all
-    of the layer's blocks queued at once), its HBM blocks as one gather kernel
+    mode "read": every layer gets tile tables (MoELayer.set_tile_tables) that
+    point each 64-row tile at HBM or at its pinned host block; the expert
+    kernels read the host tiles over PCIe themselves. A step needs no host
+    synchronisation and no staging copy, so it is one graph like the
+    resident stack.
+
+    mode "stage": per layer and step the router's ids come to the host
+    (model/gpt_oss.py:121 does the same to pick its windows); every chosen
+    expert matrix with host blocks is assembled in a staging slot -- its host
+    blocks as DMA copies from pinned RAM (nsx_copy_blocks_async, all of the
+    layer's blocks queued at once), its HBM blocks as one gather kernel
     (nsx_gather_copy) -- and the layer's expert address table points at the
-    slots for this step. The experts then run in the same fused kernels as
-    the resident stack: outputs are identical to it."""
+    slots for this step.
 
-    def __init__(self, layers, stores, eps: float = 1e-5) -> None:
+    Either way the experts run in the same fused kernels as the resident
+    stack, with the same arithmetic: outputs are identical to it."""
+
+    def __init__(self, layers, stores, eps: float = 1e-5, mode: str = "stage") -> None:
         super().__init__(layers, eps=eps)
+        if mode not in ("stage", "read"):
+            raise ValueError(f"mode {mode!r}: 'stage' or 'read'")
         self.stores = stores
+        self.mode = mode
+        self.bytes_from_host = 0
+        if mode == "read":
+            for layer, st in zip(layers, stores):
+                layer.set_tile_tables(*(st.tile_table(k, self.device) for k in ("gate", "up", "down")))
+            return
         n_slots = min(self.cfg.n_expert, 64)
         self._slots = {k: torch.empty(n_slots * stores[0].per[k], dtype=torch.uint8, device=self.device)
                        for k in stores[0].kinds}
@@ -233,7 +276,6 @@ class GptOssHostStreamedStack(GptOssFFNStack):
         self._default = [{k: torch.tensor([st.address(k, e) or self._slots[k].data_ptr()
                                            for e in range(self.cfg.n_expert)], dtype=torch.int64)
                           for k in st.kinds} for st in stores]
-        self.bytes_from_host = 0
         # host blocks spread over several copy streams (default priority), so
         # several DMA engines share the PCIe link
         self._copy_streams = [torch.cuda.Stream(self.device) for _ in range(self.COPY_STREAMS)]
@@ -284,8 +326,20 @@ class GptOssHostStreamedStack(GptOssFFNStack):
                 dev_table.copy_(self._tables[li][kind], non_blocking=True)
         self.bytes_from_host += int(H[:, 2].sum()) if len(H) else 0
 
+    def host_bytes_of_routing(self, ids) -> int:
+        """Bytes read from pinned host RAM for a step routed as `ids` (per layer
+        (T, k) expert ids): every chosen expert's host blocks, once per layer."""
+        total = 0
+        for li, st in enumerate(self.stores):
+            for e in torch.unique(ids[li]).tolist():
+                total += sum(st.host_bytes_of(k, e) for k in st.kinds)
+        return total
+
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-        """As GptOssFFNStack.forward; one host synchronisation per layer (routing)."""
+        """As GptOssFFNStack.forward; in "stage" mode one host synchronisation
+        per layer (routing)."""
+        if self.mode == "read":
+            return GptOssFFNStack.forward(self, x, out)
         from ..moe.fused import router_topk
         x = x.reshape(-1, self.cfg.n_embd)
         T = x.shape[0]
@@ -308,7 +362,7 @@ class GptOssHostStreamedStack(GptOssFFNStack):
 
     @classmethod
     def synthetic(cls, cfg, n_layers: int, seed: int, device, host_fraction: float = 0.25, block_rows: int = 512,
-                  dispatch: str = "auto"):
+                  dispatch: str = "auto", mode: str = "stage"):
         """BASELINE config 5b: the layers of GptOssFFNStack.synthetic with a
         seeded host_fraction of their block_rows-row blocks in pinned RAM."""
         import numpy as np
@@ -339,7 +393,7 @@ class GptOssHostStreamedStack(GptOssFFNStack):
                                    router_mode=cfg.router_mode, act=cfg.act, dispatch=dispatch))
             stores.append(st)
             del t
-        return cls(layers, stores)
+        return cls(layers, stores, mode=mode)
 
 
 @dataclass

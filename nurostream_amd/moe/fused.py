@@ -98,6 +98,22 @@ class MoELayer:
         self._c = L
         self._ws: dict[int, torch.Tensor] = {}
 
+    def set_tile_tables(self, gate, up, down) -> None:
+        """t64 layers: per projection an int64 device tensor of n_expert x
+        ceil(rows / 64) tile addresses (tile t of expert e at [e * tiles + t];
+        a tile may sit in device-mapped pinned host memory, read over PCIe),
+        or None to use the stacked/slab addresses again."""
+        if self.layout != "t64":
+            raise ValueError("tile tables need the t64 layout")
+        tabs = (gate, up, down)
+        for name, rows, t in (("gate", self.n_ff, gate), ("up", self.n_ff, up), ("down", self.n_embd, down)):
+            if t is not None:
+                N.require_device(t)
+                if t.dtype != torch.int64 or t.numel() != self.n_expert * (-(-rows // 64)):
+                    raise ValueError(f"{name} tile table: int64 with {self.n_expert} x {-(-rows // 64)} entries")
+            setattr(self._c, name + "_tiles", None if t is None else t.data_ptr())
+        self._tiles = tabs  # keep the tables alive with the layer
+
     def workspace(self, T: int) -> torch.Tensor:
         ws = self._ws.get(T)
         if ws is None:

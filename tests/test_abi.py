@@ -39,7 +39,7 @@ def test_exported_symbols_are_the_header_set(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.nsx_abi_version() == 2
+    assert lib.nsx_abi_version() == 3
     assert isinstance(lib.nsx_last_error(), bytes)
 
 

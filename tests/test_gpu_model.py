@@ -101,16 +101,19 @@ def test_qwen3_moe_ffn_over_cache(dev, T):
     assert cache.stats.slab_hits > 0
 
 
+@pytest.mark.parametrize("mode", ["stage", "read"])
 @pytest.mark.parametrize("T,frac", [(1, 0.5), (5, 0.25), (9, 1.0)])
-def test_host_streamed_stack_equals_resident(dev, T, frac):
+def test_host_streamed_stack_equals_resident(dev, T, frac, mode):
     """BASELINE config 5b on a small stack: with a share of the row blocks in
-    pinned host RAM, staged per step, the outputs equal the resident stack's."""
+    pinned host RAM -- staged per step, or read over PCIe by the kernels
+    through tile tables -- the outputs equal the resident stack's."""
     from nurostream_amd import synth
     from nurostream_amd.model.gpt_oss import GptOssFFNStack, GptOssHostStreamedStack
     cfg = _small("gptoss-small")
     L = 3
     res = GptOssFFNStack.synthetic(cfg, L, seed=31, device=dev)
-    hs = GptOssHostStreamedStack.synthetic(cfg, L, seed=31, device=dev, host_fraction=frac, block_rows=64)
+    hs = GptOssHostStreamedStack.synthetic(cfg, L, seed=31, device=dev, host_fraction=frac, block_rows=64,
+                                           mode=mode)
     assert sum(st.host_bytes for st in hs.stores) > 0
     x = synth.activations(T, cfg.n_embd, seed=40 + T, device=dev)
     for _ in range(2):  # a second step reuses the slots and tables
@@ -118,7 +121,41 @@ def test_host_streamed_stack_equals_resident(dev, T, frac):
         y_hs = hs(x)
         torch.cuda.synchronize()
         assert torch.equal(y_res, y_hs)
-    assert hs.bytes_from_host > 0
+    if mode == "stage":
+        assert hs.bytes_from_host > 0
+        return
+    ids, _ = hs.last_routing(T)
+    assert hs.host_bytes_of_routing(ids.cpu()) > 0
+    # read mode has no host synchronisation: a step is one graph
+    x_in = x.clone()
+    y_g = torch.empty_like(y_res)
+    hs(x_in, out=y_g)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            hs(x_in, out=y_g)
+    torch.cuda.synchronize()
+    for i in range(4):
+        xi = synth.activations(T, cfg.n_embd, seed=60 + i, device=dev)
+        x_in.copy_(xi)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_g, res(xi)), i
+
+
+def test_host_device_address(dev):
+    """Pinned host memory maps to a device address; pageable memory is refused."""
+    import ctypes as C
+    from nurostream_amd import _native as N
+    lib = N.load()
+    out = C.c_uint64(0)
+    pinned = torch.zeros(4096, dtype=torch.uint8).pin_memory()
+    assert lib.nsx_host_device_address(pinned.data_ptr(), C.byref(out)) == N.OK and out.value != 0
+    pageable = torch.zeros(4096, dtype=torch.uint8)
+    assert lib.nsx_host_device_address(pageable.data_ptr(), C.byref(out)) == N.EHIP
 
 
 def test_gather_and_block_copies_check_ranges(dev):
