@@ -34,7 +34,7 @@ enum {
 /* ggml type ids (format/gguf.py:19-35) */
 enum {
   NSX_F32 = 0, NSX_F16 = 1, NSX_Q4_0 = 2, NSX_Q8_0 = 8, NSX_Q4_K = 12,
-  NSX_BF16 = 30, NSX_MXFP4 = 39
+  NSX_Q6_K = 14, NSX_BF16 = 30, NSX_MXFP4 = 39
 };
 
 /* activation / output element types */
@@ -65,15 +65,17 @@ int nsx_selftest(uint32_t *scratch, void *stream);
 
 /* compute/quant.py:153-184 dequantize(raw, dtype, n_elements, out_dtype).
  * raw: `raw_bytes` bytes of ggml blocks (any alignment); out: n_elements of
- * out_dtype. Bit-exact with the reference for Q4_0, Q8_0, Q4_K, MXFP4. */
+ * out_dtype. Bit-exact with the reference for Q4_0, Q8_0, Q4_K, Q6_K, MXFP4
+ * (Q6_K: compute/quant.py:84-107). */
 int nsx_dequantize(int ggml_type, const void *raw, int64_t raw_bytes,
                    int64_t n_elements, void *out, int out_dtype, void *stream);
 
 /* compute/triton_kernels.py:199-228 fused_gemv(raw, dtype, x, n_rows, K).
  * y[t, r] = sum_k x[t, k] * dequant(raw)[r, k] for t < T, fp32 accumulate.
- * raw: n_rows * row_bytes GGUF bytes (any alignment for 32-element formats,
- * 4-byte aligned for Q4_K); x: (T, K) row-major in x_dtype; y: (T, n_rows)
- * fp32. The reference fuses only T == 1; here T <= 16. */
+ * raw: n_rows * row_bytes GGUF bytes (any alignment for Q4_0, Q8_0, Q6_K and
+ * MXFP4, 4-byte aligned for Q4_K); x: (T, K) row-major in x_dtype; y:
+ * (T, n_rows) fp32. The reference fuses only T == 1 (Q6_K:
+ * triton_kernels.py:97-143); here T <= 16. */
 int nsx_fused_gemv(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
                    const void *x, int x_dtype, int64_t T, float *y, void *stream);
 

@@ -23,7 +23,7 @@ ROUTE_GPTOSS, ROUTE_QWEN3 = 0, 1
 DISPATCH_AUTO, DISPATCH_PAIRS, DISPATCH_GROUPED = 0, 1, 2
 ACT_CLAMPED_SWIGLU, ACT_SILU_MUL = 0, 1
 
-BLOCK_TYPES = frozenset({GGMLType.Q4_0, GGMLType.Q8_0, GGMLType.Q4_K, GGMLType.MXFP4})
+BLOCK_TYPES = frozenset({GGMLType.Q4_0, GGMLType.Q8_0, GGMLType.Q4_K, GGMLType.Q6_K, GGMLType.MXFP4})
 
 _p = C.c_void_p
 _i64 = C.c_int64

@@ -4,7 +4,7 @@
 (neurostream/compute/quant.py:153-184): uint8 input or TypeError, F32/F16/BF16
 are views plus a cast, unknown types raise NotImplementedError, the output is
 truncated to `n_elements` and cast to `out_dtype`. Block formats (Q4_0, Q8_0,
-Q4_K, MXFP4) expand in one HIP kernel, bit-exact with the reference; they need
+Q4_K, Q6_K, MXFP4) expand in one HIP kernel, bit-exact with the reference; they need
 the tensor on the GPU.
 """
 from __future__ import annotations

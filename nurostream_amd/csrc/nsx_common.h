@@ -50,7 +50,7 @@ static inline int64_t nsx_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline int nsx_block_elems(int t) {
   switch (t) {
     case NSX_Q4_0: case NSX_Q8_0: case NSX_MXFP4: return 32;
-    case NSX_Q4_K: return 256;
+    case NSX_Q4_K: case NSX_Q6_K: return 256;
     default: return 0;
   }
 }
@@ -60,6 +60,7 @@ static inline int nsx_block_bytes(int t) {
     case NSX_Q8_0: return 34;
     case NSX_MXFP4: return 17;
     case NSX_Q4_K: return 144;
+    case NSX_Q6_K: return 210;
     default: return 0;
   }
 }

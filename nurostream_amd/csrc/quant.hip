@@ -59,7 +59,7 @@ extern "C" int nsx_selftest(uint32_t* scratch, void* stream) {
 }
 
 // ---------------------------------------------------------------------------
-// dequantize (quant.py:118-140, 24-56, 110-115)
+// dequantize (quant.py:118-140, 24-56, 84-107, 110-115)
 //
 // A workgroup stages BPW consecutive blocks into LDS with range-checked dword
 // buffer loads (the source may start at any byte), then each thread expands
@@ -73,6 +73,7 @@ template <> struct Fmt<NSX_MXFP4> { static constexpr int BE = 32, BB = 17, BPW =
 template <> struct Fmt<NSX_Q4_0> { static constexpr int BE = 32, BB = 18, BPW = 32; };
 template <> struct Fmt<NSX_Q8_0> { static constexpr int BE = 32, BB = 34, BPW = 32; };
 template <> struct Fmt<NSX_Q4_K> { static constexpr int BE = 256, BB = 144, BPW = 4; };
+template <> struct Fmt<NSX_Q6_K> { static constexpr int BE = 256, BB = 210, BPW = 4; };
 
 template <int FMT>
 __device__ __forceinline__ float dq_elem(const uint8_t* B, int blk, int j) {
@@ -92,6 +93,17 @@ __device__ __forceinline__ float dq_elem(const uint8_t* B, int blk, int j) {
     const float d = nsx_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
     const int v = (int)(int8_t)p[2 + j];
     return __fmul_rn(d, (float)v);
+  } else if constexpr (FMT == NSX_Q6_K) {
+    // element j = 128 h + 32 L + l: low 4 bits from ql[64 h + 32 (L & 1) + l]
+    // (nibble L >> 1), high 2 bits from qh[32 h + l] >> 2L, scale int8
+    // sc[j / 16], d fp16 at byte 208. d * sc * (q - 32) is exact in fp32
+    // (11 + 7 + 5 significant bits), so the product order does not matter.
+    const int h = j >> 7, L = (j >> 5) & 3, l = j & 31;
+    const uint32_t lo = (p[64 * h + 32 * (L & 1) + l] >> (4 * (L >> 1))) & 15u;
+    const uint32_t hi = (p[128 + 32 * h + l] >> (2 * L)) & 3u;
+    const float d = nsx_h2f((uint32_t)p[208] | ((uint32_t)p[209] << 8));
+    const float sc = (float)(int8_t)p[192 + (j >> 4)];
+    return __fmul_rn(__fmul_rn(d, sc), (float)((int)(lo | (hi << 4)) - 32));
   } else {  // Q4_K
     const float d = nsx_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
     const float dmin = nsx_h2f((uint32_t)p[2] | ((uint32_t)p[3] << 8));
@@ -195,7 +207,7 @@ static int dequant_fmt(const void* raw, int64_t nb, int64_t ne, void* out, int o
 extern "C" int nsx_dequantize(int t, const void* raw, int64_t raw_bytes, int64_t n_elements,
                               void* out, int out_dtype, void* stream) {
   const int BE = nsx_block_elems(t), BB = nsx_block_bytes(t);
-  NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no dequant kernel for ggml type %d; supported: Q4_0 Q8_0 Q4_K MXFP4", t);
+  NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no dequant kernel for ggml type %d; supported: Q4_0 Q8_0 Q4_K Q6_K MXFP4", t);
   NSX_REQUIRE(raw_bytes >= 0 && n_elements >= 0, NSX_EINVAL, "negative size");
   const int64_t nb = raw_bytes / BB;
   NSX_REQUIRE(n_elements <= nb * BE, NSX_EINVAL, "%lld elements requested from %lld blocks",
@@ -209,6 +221,7 @@ extern "C" int nsx_dequantize(int t, const void* raw, int64_t raw_bytes, int64_t
     case NSX_Q4_0: return dequant_fmt<NSX_Q4_0>(raw, need, n_elements, out, out_dtype, st);
     case NSX_Q8_0: return dequant_fmt<NSX_Q8_0>(raw, need, n_elements, out, out_dtype, st);
     case NSX_Q4_K: return dequant_fmt<NSX_Q4_K>(raw, need, n_elements, out, out_dtype, st);
+    case NSX_Q6_K: return dequant_fmt<NSX_Q6_K>(raw, need, n_elements, out, out_dtype, st);
   }
   return nsx_fail(NSX_ENOTIMPL, "ggml type %d", t);
 }
@@ -315,6 +328,7 @@ extern "C" int nsx_fused_gemv(int t, const void* raw, int64_t n_rows, int64_t K,
       case NSX_Q4_0: rc = gemv_raw_fmt<NSX_Q4_0>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
       case NSX_Q8_0: rc = gemv_raw_fmt<NSX_Q8_0>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
       case NSX_Q4_K: rc = gemv_raw_fmt<NSX_Q4_K>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
+      case NSX_Q6_K: rc = gemv_raw_fmt<NSX_Q6_K>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
     }
     if (rc) return rc;
   }

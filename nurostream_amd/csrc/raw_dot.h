@@ -1,7 +1,7 @@
 // Row dot products over raw GGUF rows, shared by the fused GEMV seam and the
 // raw-layout MoE kernels. One wave computes one row for NT tokens: lanes take
 // 32-element units (a whole block for MXFP4/Q4_0/Q8_0, one sub-block for
-// Q4_K), fetch them with range-checked dword buffer loads from the aligned
+// Q4_K, an eighth of a block for Q6_K), fetch them with range-checked dword buffer loads from the aligned
 // address below and realign in registers, then the wave reduces.
 //
 // Activations come from LDS as fp32, token stride K, together with per-32
@@ -109,6 +109,71 @@ __device__ __forceinline__ void raw_unit_dot(__amdgpu_buffer_rsrc_t rs, uint32_t
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = fmaf(d, part[t], acc[t]);
+  } else if constexpr (FMT == NSX_Q6_K) {
+    // Unit u = block b (u / 8), part j (u % 8): half h = j / 4 of the block,
+    // positions l0 .. l0 + 7 (l0 = 8 (j % 4)) of its four 32-element lanes
+    // L = 0..3, i.e. elements 128 h + 32 L + l0 + i. The part's 8 bytes of
+    // ql[64 h + l0 ..] (lanes 0, 2), ql[64 h + 32 + l0 ..] (lanes 1, 3) and
+    // qh[32 h + l0 ..] are each read once; its four int8 scales are
+    // sc[8 h + l0 / 16 + 2 L]. Every field offset is a multiple of 4 from the
+    // block start, so one byte shift realigns them all (any row alignment).
+    const int b = u >> 3, j = u & 7, h = j >> 2, l0 = (j & 3) * 8;
+    const uint32_t o = o_row + (uint32_t)b * 210u;
+    const uint32_t sft = o & 3u, oa = o & ~3u;
+    auto ld8 = [&](uint32_t off, uint32_t& w0, uint32_t& w1) {
+      const uint32_t D0 = nsx_bload32(rs, oa + off), D1 = nsx_bload32(rs, oa + off + 4),
+                     D2 = nsx_bload32(rs, oa + off + 8);
+      w0 = nsx_alignbyte(D1, D0, sft);
+      w1 = nsx_alignbyte(D2, D1, sft);
+    };
+    uint32_t A[2], B[2], C[2], S[2], dw, dw1;
+    ld8(64u * h + l0, A[0], A[1]);
+    ld8(64u * h + 32u + l0, B[0], B[1]);
+    ld8(128u + 32u * h + l0, C[0], C[1]);
+    ld8(192u + 8u * h, S[0], S[1]);
+    dw = nsx_bload32(rs, oa + 208u);
+    dw1 = nsx_bload32(rs, oa + 212u);
+    const float d = nsx_h2f(nsx_alignbyte(dw1, dw, sft) & 0xffffu);
+    const int is = l0 >> 4;
+    float dsc[4];
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+      const int k = is + 2 * L;  // scale byte within the half's 8
+      dsc[L] = d * (float)(int8_t)((S[k >> 2] >> (8 * (k & 3))) & 0xffu);  // exact
+    }
+    const float* xb0 = xs + b * 256 + h * 128 + l0;
+    float part[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int L = 0; L < 4; ++L) part[t][L] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // 4 positions per dword
+      const uint32_t qa = A[i], qb = B[i], qc = C[i];
+      const uint32_t q[4] = {(qa & 0x0f0f0f0fu) | ((qc << 4) & 0x30303030u),
+                             (qb & 0x0f0f0f0fu) | ((qc << 2) & 0x30303030u),
+                             ((qa >> 4) & 0x0f0f0f0fu) | (qc & 0x30303030u),
+                             ((qb >> 4) & 0x0f0f0f0fu) | ((qc >> 2) & 0x30303030u)};
+#pragma unroll
+      for (int L = 0; L < 4; ++L) {
+        const float q0 = nsx_ub<0>(q[L]) - 32.f, q1 = nsx_ub<1>(q[L]) - 32.f;  // exact
+        const float q2 = nsx_ub<2>(q[L]) - 32.f, q3 = nsx_ub<3>(q[L]) - 32.f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const v4f xa = *(const v4f*)(xb0 + t * K + 32 * L + 4 * i);
+          float p = part[t][L];
+          p = fmaf(q0, xa.x, p); p = fmaf(q1, xa.y, p); p = fmaf(q2, xa.z, p); p = fmaf(q3, xa.w, p);
+          part[t][L] = p;
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float a = acc[t];
+#pragma unroll
+      for (int L = 0; L < 4; ++L) a = fmaf(dsc[L], part[t][L], a);
+      acc[t] = a;
+    }
   } else {  // Q4_K sub-block unit: block b = u/8, sub-block s = u%8 (rows 4-byte aligned)
     const int b = u >> 3, s = u & 7;
     const uint32_t o = o_row + (uint32_t)b * 144u;
@@ -180,7 +245,7 @@ __device__ __forceinline__ void stage_x(float* __restrict__ xs, const void* __re
 
 template <int FMT>
 __device__ __host__ constexpr int raw_units(int K) {
-  return K / 32;  // 32-element units; Q4_K sub-blocks are 32 elements too
+  return K / 32;  // 32-element units; Q4_K sub-blocks and Q6_K parts are 32 elements too
 }
 
 template <int FMT>
@@ -188,5 +253,6 @@ __device__ __host__ constexpr uint32_t raw_row_bytes(int K) {
   return FMT == NSX_MXFP4 ? (uint32_t)(K / 32) * 17u
        : FMT == NSX_Q4_0  ? (uint32_t)(K / 32) * 18u
        : FMT == NSX_Q8_0  ? (uint32_t)(K / 32) * 34u
+       : FMT == NSX_Q6_K  ? (uint32_t)(K / 256) * 210u
                           : (uint32_t)(K / 256) * 144u;
 }

@@ -86,6 +86,9 @@ def block_bytes(dtype: GGMLType, n_blocks: int, gen: torch.Generator, device, *,
         s = 2.0 ** -8 if d_std is None else d_std
         b[:, 0:2] = _f16_abs_normal(n_blocks, s, gen, device)
         b[:, 2:4] = _f16_abs_normal(n_blocks, s, gen, device)
+    elif dtype == GGMLType.Q6_K:
+        # random int8 sub-block scales (bytes 192:208) and 6-bit codes; d small
+        b[:, 208:210] = _f16_abs_normal(n_blocks, 2.0 ** -10 if d_std is None else d_std, gen, device)
     else:
         raise NotImplementedError(dtype)
     return b.reshape(-1)

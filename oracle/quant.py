@@ -10,6 +10,7 @@ reference root, neurostream/compute/):
   dequant_q4_k   quant.py:24-56  (+ get_scale_min_k4 index maths, triton_kernels.py:52-88)
   dequant_mxfp4  quant.py:129-140
   dequant_q8_0   quant.py:110-115
+  dequant_q6_k   quant.py:84-107 (layout as in the Triton kernel, triton_kernels.py:97-143)
   dequantize     quant.py:153-184
   gemv           triton_kernels.py:199-228 semantics, computed the way the
                  reference's non-fused branch does it: dequantize, then x @ w.T
@@ -20,10 +21,14 @@ Pinning (see tests/test_oracle_quant.py):
     (OCP e2m1 table x 2^(e-127), the convention of transformers'
     integrations/mxfp4.py:29-45,271-275) and against the reference's own
     known-answer input (tests/test_gpt_oss.py:103-109);
-  * Q4_0 / Q4_K / Q8_0: round trips through independent encoders that pack
-    chosen (d, dmin, sub-scale, min, code) values into bytes, exhaustive over
-    every 6-bit scale/min pattern of the Q4_K 12-byte field, plus the
-    reference's Q8_0 known answer arange(1, 33) (tests/test_tuning.py:104-133);
+  * Q4_0 / Q4_K / Q8_0 / Q6_K: round trips through independent encoders that
+    pack chosen (d, dmin, sub-scale, min, code) values into bytes, exhaustive
+    over every 6-bit scale/min pattern of the Q4_K 12-byte field and over
+    every 6-bit Q6_K code and int8 Q6_K scale, plus the reference's Q8_0 known
+    answer arange(1, 33) (tests/test_tuning.py:104-133). The reference's tests
+    hold no Q6_K vector; the Q6_K encoder follows ggml's published
+    quantize_row_q6_K packing (ggml-quants.c, MIT), with scale index
+    element // 16;
   * gemv: against float64 x @ dequant.T and brute force on tiny inputs.
 """
 from __future__ import annotations
@@ -31,10 +36,10 @@ from __future__ import annotations
 import numpy as np
 
 # ggml type ids (format/gguf.py:19-35)
-F32, F16, Q4_0, Q8_0, Q4_K, BF16, MXFP4 = 0, 1, 2, 8, 12, 30, 39
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16, MXFP4 = 0, 1, 2, 8, 12, 14, 30, 39
 
 LAYOUT = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34),
-          Q4_K: (256, 144), MXFP4: (32, 17)}
+          Q4_K: (256, 144), Q6_K: (256, 210), MXFP4: (32, 17)}
 
 # quant.py:137-139 -- ggml's doubled e2m1 table; code 8 is +0.0
 MXFP4_LUT2 = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12],
@@ -86,6 +91,30 @@ def dequant_q8_0(blocks: np.ndarray) -> np.ndarray:
     return (d * q).astype(np.float32)
 
 
+def dequant_q6_k(blocks: np.ndarray) -> np.ndarray:
+    """Q6_K: ql[128] | qh[64] | int8 scales[16] | d (quant.py:84-107).
+
+    Each 128-element half h has four 32-wide lanes L; element l of lane L takes
+    its low 4 bits from ql[64h + 32(L % 2) + l] (low nibble for L < 2, high
+    for L >= 2), its high 2 bits from qh[32h + l] >> 2L, and is scaled by
+    d * scales[8h + l // 16 + 2L]; value = d * sc * (q - 32).
+    """
+    nb = blocks.shape[0]
+    ql = blocks[:, 0:128].reshape(nb, 2, 64).astype(np.int32)
+    qh = blocks[:, 128:192].reshape(nb, 2, 32).astype(np.int32)
+    sc = np.ascontiguousarray(blocks[:, 192:208]).view(np.int8).reshape(nb, 2, 8).astype(np.float32)
+    d = _f16_field(blocks, 208)[:, :, None]  # (nb, 1, 1)
+    half_of_lane = np.arange(32) // 16
+    out = np.empty((nb, 2, 128), np.float32)
+    for L in range(4):
+        src = ql[:, :, 32 * (L % 2):32 * (L % 2) + 32]
+        low = (src & 0x0F) if L < 2 else (src >> 4)
+        q = low | (((qh >> (2 * L)) & 3) << 4)
+        s = sc[:, :, half_of_lane + 2 * L]
+        out[:, :, 32 * L:32 * L + 32] = (d * s) * (q - 32).astype(np.float32)
+    return out.reshape(nb, 256)
+
+
 def mxfp4_scale(e: np.ndarray) -> np.ndarray:
     """2^(e-128) built from raw float bits; e=0,1 are denormals, e=255 -> 2^127 (quant.py:131-134)."""
     e = e.astype(np.int64)
@@ -101,7 +130,8 @@ def dequant_mxfp4(blocks: np.ndarray) -> np.ndarray:
     return (scale * MXFP4_LUT2[codes]).astype(np.float32)
 
 
-_KERNELS = {MXFP4: dequant_mxfp4, Q4_K: dequant_q4_k, Q8_0: dequant_q8_0, Q4_0: dequant_q4_0}
+_KERNELS = {MXFP4: dequant_mxfp4, Q4_K: dequant_q4_k, Q6_K: dequant_q6_k, Q8_0: dequant_q8_0,
+            Q4_0: dequant_q4_0}
 
 
 def dequantize(raw: np.ndarray, dtype: int, n_elements: int) -> np.ndarray:

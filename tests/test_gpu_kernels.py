@@ -35,7 +35,7 @@ def _q_special_d(rng, nb, bb):
     return raw
 
 
-@pytest.mark.parametrize("fmt", ["MXFP4", "Q4_0", "Q8_0", "Q4_K"])
+@pytest.mark.parametrize("fmt", ["MXFP4", "Q4_0", "Q8_0", "Q4_K", "Q6_K"])
 @pytest.mark.parametrize("offset", [0, 1, 3])
 def test_dequant_bit_exact(dev, fmt, offset):
     from nurostream_amd.compute.quant import dequantize
@@ -47,6 +47,9 @@ def test_dequant_bit_exact(dev, fmt, offset):
     elif fmt == "Q4_K":
         raw = rng.integers(0, 256, (300, bb), dtype=np.uint8)
         raw[:150, 0:4] = _q_special_d(rng, 150, 4)[:, 0:4]
+    elif fmt == "Q6_K":  # d sits at bytes 208:210
+        raw = rng.integers(0, 256, (300, bb), dtype=np.uint8)
+        raw[:150, 208:210] = _q_special_d(rng, 150, 2)
     else:
         raw = _q_special_d(rng, 777, bb)
     flat = raw.reshape(-1)
@@ -95,7 +98,8 @@ def _gemv_case(fmt, rows, K, seed, e_lo=117, e_hi=123):
 
 @pytest.mark.parametrize("fmt,rows,K", [("MXFP4", 19, 2880), ("Q8_0", 19, 2880), ("MXFP4", 2880, 2880),
                                         ("Q4_0", 512, 4096), ("Q4_K", 1536, 4096), ("Q4_K", 96, 1536),
-                                        ("Q4_0", 7, 64), ("MXFP4", 1, 32)])
+                                        ("Q4_0", 7, 64), ("MXFP4", 1, 32), ("Q6_K", 300, 4096),
+                                        ("Q6_K", 33, 2816), ("Q6_K", 5, 256)])
 @pytest.mark.parametrize("T", [1, 3, 16])
 def test_fused_gemv_matches_oracle(dev, fmt, rows, K, T):
     from nurostream_amd.compute.kernels import can_fuse, fused_gemv
@@ -112,6 +116,22 @@ def test_fused_gemv_matches_oracle(dev, fmt, rows, K, T):
     err = rel_max(y, ref)
     assert err < GEMV_TIGHT, err
     np.testing.assert_allclose(y, ref, atol=1e-4 * np.abs(ref).max() + 1e-6, rtol=1e-4)
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_fused_gemv_q6k_any_alignment(dev, offset):
+    """Q6_K rows are 210 B per block, so rows start at any byte: the kernel's
+    arithmetic does not depend on where the bytes sit (bitwise equal)."""
+    from nurostream_amd.compute.kernels import fused_gemv
+    rows, K = 77, 2816
+    raw = _gemv_case("Q6_K", rows, K, seed=5)
+    x = torch.from_numpy(np.random.default_rng(2).standard_normal((3, K)).astype(np.float32)).to(dev)
+    base = torch.from_numpy(raw).to(dev)
+    buf = torch.zeros(raw.size + 8, dtype=torch.uint8, device=dev)
+    buf[offset:offset + raw.size] = base
+    y0 = fused_gemv(base, OQ.Q6_K, x, rows, K, out_dtype=torch.float32)
+    y1 = fused_gemv(buf[offset:offset + raw.size], OQ.Q6_K, x, rows, K, out_dtype=torch.float32)
+    assert torch.equal(y0, y1)
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])

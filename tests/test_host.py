@@ -184,8 +184,10 @@ def test_quantized_compute_never_falls_back_to_cpu():
         fused_gemv(raw, GGMLType.Q8_0, x, 4, 32)
     with pytest.raises(TypeError):
         dequantize(raw.view(torch.int8), GGMLType.Q8_0, 128)
+    with pytest.raises(N.NativeError):
+        dequantize(torch.zeros(210, dtype=torch.uint8), GGMLType.Q6_K, 256)
     with pytest.raises(NotImplementedError):
-        dequantize(raw, GGMLType.Q6_K, 128)
+        dequantize(raw, GGMLType.Q5_K, 128)
 
 
 def test_router_stats_contract():

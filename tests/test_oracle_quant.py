@@ -166,29 +166,91 @@ def test_q4_k_values_from_encoder(seed):
     np.testing.assert_array_equal(got, np.stack(want))
 
 
+def _q6k_block(dbits: int, scales: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    """Pack 256 6-bit codes and 16 int8 scales the way ggml's quantize_row_q6_K
+    writes them: per 128-element half, element l, l+32, l+64, l+96 (l < 32)
+    share qh[l] (2 bits each, in that order from bit 0) and element l / l+64
+    (l+32 / l+96) share ql[l] (ql[l+32]) as low / high nibble. Scale s covers
+    elements 16s .. 16s+15."""
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for half in range(2):
+        c = codes[128 * half:128 * half + 128].astype(np.int64)
+        for l in range(32):
+            ql[64 * half + l] = (c[l] & 15) | ((c[l + 64] & 15) << 4)
+            ql[64 * half + l + 32] = (c[l + 32] & 15) | ((c[l + 96] & 15) << 4)
+            qh[32 * half + l] = ((c[l] >> 4) | ((c[l + 32] >> 4) << 2) | ((c[l + 64] >> 4) << 4)
+                                 | ((c[l + 96] >> 4) << 6))
+    return np.concatenate([ql, qh, scales.astype(np.int8).view(np.uint8),
+                           np.array([dbits], np.uint16).view(np.uint8)])
+
+
+def _q6k_expected(dbits: int, scales: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    d = float(np.array([dbits], np.uint16).view(np.float16)[0])
+    s = scales.astype(np.float64)[np.arange(256) // 16]
+    return (d * s * (codes.astype(np.float64) - 32)).astype(np.float32)  # exact: <= 23 significant bits
+
+
+def test_q6_k_every_code_and_scale():
+    """Every 6-bit code at every position class and every int8 scale value, against the
+    independent packer and value = d * scales[e // 16] * (code - 32)."""
+    rng = np.random.default_rng(11)
+    all_scales = np.arange(-128, 128)
+    blocks, want = [], []
+    for i in range(16):  # 16 blocks x 16 scales = all 256 int8 values
+        sc = all_scales[16 * i:16 * i + 16][rng.permutation(16)]
+        # lane offsets 13 (e // 32): elements 32 or 64 apart (which share ql / qh bytes) get
+        # different nibbles; over the 16 blocks every code lands in every (half, lane) class
+        e = np.arange(256)
+        codes = (e + 13 * (e // 32) + 17 * i) % 64
+        dbits = int(_F16_SPECIAL[i % len(_F16_SPECIAL)])
+        blocks.append(_q6k_block(dbits, sc, codes))
+        want.append(_q6k_expected(dbits, sc, codes))
+    got = OQ.dequantize(np.concatenate(blocks), OQ.Q6_K, 16 * 256).reshape(16, 256)
+    np.testing.assert_array_equal(got, np.stack(want))
+    # the sign of zero follows the float32 product order d * sc * 0 (as in the reference)
+    assert np.array_equal(np.signbit(got), np.signbit(np.stack(want)))
+
+
+def test_q6_k_random_blocks_round_trip():
+    """Random codes, scales and d: decode(pack(c, s, d)) == d * s[e // 16] * (c - 32)."""
+    rng = np.random.default_rng(12)
+    blocks, want = [], []
+    for _ in range(40):
+        codes = rng.integers(0, 64, 256)
+        sc = rng.integers(-128, 128, 16)
+        dbits = int(np.array([abs(rng.normal(0, 2 ** -10))], np.float16).view(np.uint16)[0])
+        blocks.append(_q6k_block(dbits, sc, codes))
+        want.append(_q6k_expected(dbits, sc, codes))
+    got = OQ.dequantize(np.concatenate(blocks), OQ.Q6_K, 40 * 256 - 3)
+    np.testing.assert_array_equal(got, np.concatenate(want)[:40 * 256 - 3])
+
+
 def test_dequantize_dispatch_errors():
     """The reference dispatcher's error contract (quant.py:153-184)."""
     with pytest.raises(TypeError):
         OQ.dequantize(np.zeros(34, np.int8), OQ.Q8_0, 32)
     with pytest.raises(NotImplementedError):
-        OQ.dequantize(np.zeros(34, np.uint8), 14, 32)  # Q6_K: no kernel on this path
+        OQ.dequantize(np.zeros(176, np.uint8), 13, 256)  # Q5_K: no kernel on this path
     # truncation to n_elements
     assert OQ.dequantize(np.zeros(34 * 2, np.uint8), OQ.Q8_0, 40).shape == (40,)
 
 
-@pytest.mark.parametrize("fmt", ["MXFP4", "Q4_0", "Q8_0", "Q4_K"])
+@pytest.mark.parametrize("fmt", ["MXFP4", "Q4_0", "Q8_0", "Q4_K", "Q6_K"])
 def test_gemv_matches_float64_closed_form(fmt):
     """oracle.gemv (float32, the reference's non-fused torch path) within fp32 accumulation of
     float64 x @ W^T over independently decoded W."""
     t = getattr(OQ, fmt)
     be, bb = OQ.LAYOUT[t]
-    rows, K = 19, 512 if fmt != "Q4_K" else 1024
+    rows, K = 19, 512 if fmt not in ("Q4_K", "Q6_K") else 1024
     rng = np.random.default_rng(3)
     raw = rng.integers(0, 256, rows * (K // be) * bb, dtype=np.uint8).reshape(-1, bb)
     if fmt == "MXFP4":
         raw[:, 0] = rng.integers(117, 124, raw.shape[0])
     elif fmt in ("Q4_0", "Q8_0"):
         raw[:, 0:2] = np.abs(rng.normal(0, 0.02, raw.shape[0])).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    elif fmt == "Q6_K":
+        raw[:, 208:210] = np.abs(rng.normal(0, 2 ** -10, raw.shape[0])).astype(np.float16).view(np.uint8).reshape(-1, 2)
     else:
         raw[:, 0:4] = np.abs(rng.normal(0, 2 ** -8, (raw.shape[0], 2))).astype(np.float16).view(np.uint8).reshape(-1, 4)
     x = np.linspace(-1, 1, K, dtype=np.float32)[None, :]  # the reference's test input
