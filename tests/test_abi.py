@@ -100,8 +100,10 @@ def test_workspace_bytes_by_dispatch(lib):
 
 def test_validation_errors_return_codes(lib):
     # unsupported block type: NotImplemented, with a message
-    rc = lib.nsx_dequantize(14, None, 210, 256, None, N.DT_F32, None)
-    assert rc == N.ENOTIMPL and b"Q4_K" in lib.nsx_last_error()
+    rc = lib.nsx_dequantize(13, None, 176, 256, None, N.DT_F32, None)  # Q5_K
+    assert rc == N.ENOTIMPL and b"Q6_K" in lib.nsx_last_error()
+    rc = lib.nsx_fused_gemv(13, None, 1, 256, None, N.DT_F32, 1, None, None)
+    assert rc == N.ENOTIMPL
     rc = lib.nsx_dequantize(int(GGMLType.Q8_0), None, 34, 64, None, N.DT_F32, None)
     assert rc == N.EINVAL  # more elements than blocks
     # router: top_k above n_expert
