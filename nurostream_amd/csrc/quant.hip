@@ -9,6 +9,7 @@
 #include "raw_dot.h"
 
 #include <algorithm>
+#include <mutex>
 #include <string.h>
 
 // ---------------------------------------------------------------------------
@@ -229,37 +230,192 @@ extern "C" int nsx_dequantize(int t, const void* raw, int64_t raw_bytes, int64_t
 // ---------------------------------------------------------------------------
 // fused GEMV on raw GGUF rows (triton_kernels.py:199-228 seam)
 //
-// One wave per row (grid-stride); lanes take the row's 32-element units and
-// the wave reduces (raw_dot.h). x is staged once per workgroup in LDS.
+// One wave per row; lanes take the row's 32-element units (raw_dot.h) and the
+// wave reduces. A row is processed in chunks of up to 128 units (4096
+// elements). Each chunk's bytes are read with coalesced 16-byte buffer loads
+// (lane i takes bytes 16 i .., so one load instruction covers 1 KiB of
+// consecutive bytes) into registers, written to a wave-private LDS buffer,
+// and the lanes then read their units' fields from LDS: unit-per-lane global
+// loads would touch many cache lines per instruction and revisit each line
+// once per field. The loads of the wave's next chunk are issued before the
+// arithmetic of the current one, so they overlap it. The grid is persistent
+// (as many workgroups as fit at once): x is staged into LDS once per
+// workgroup.
 
 constexpr int GV_THREADS = 256;
+constexpr int GV_WAVES = GV_THREADS / 64;
 constexpr int GV_MAXT = 16;
+constexpr int GV_CHUNK_UNITS = 128;
+#ifndef GV_DEPTH_OVERRIDE
+constexpr int GV_DEPTH = 2;  // chunks whose loads are in flight per wave
+#else
+constexpr int GV_DEPTH = GV_DEPTH_OVERRIDE;
+#endif
 
-template <int FMT, int NT>
+template <int FMT>
+struct GvChunk {
+  static constexpr int BLOCKS = GV_CHUNK_UNITS * 32 / RawBlock<FMT>::BE;  // blocks per chunk
+  static constexpr int BYTES = BLOCKS * RawBlock<FMT>::BB;
+  static constexpr int LOADS = (BYTES + 3 + 1023) / 1024;  // 16-byte loads per lane
+  // wave buffer: the loaded span plus the fetch's reads past the last unit
+  static constexpr int WAVE_BYTES = LOADS * 1024 + 64;
+};
+
+template <int NT>
+__host__ __device__ constexpr int gv_x_bytes(int K) {
+  return ((NT * (K + K / 32) * 4) + 15) & ~15;
+}
+
+// Activations of one unit held in registers (unit order), one token.
+struct RawXReg {
+  const float (&x)[32];
+  __device__ __forceinline__ v4f operator()(int, int k4) const {
+    return v4f{x[4 * k4], x[4 * k4 + 1], x[4 * k4 + 2], x[4 * k4 + 3]};
+  }
+};
+struct RawXSumReg {
+  float s;
+  __device__ __forceinline__ float operator()(int) const { return s; }
+};
+
+// XREG (one token, K <= 4096, so one chunk per row): each lane's two units
+// are the same for every row, so their activations are read from LDS once
+// into registers instead of once per row.
+template <int FMT, int NT, bool XREG>
 __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
     const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int n_rows, int K,
     const void* __restrict__ x, int x_dtype, int T, float* __restrict__ y, int64_t ystride) {
-  extern __shared__ float xs[];  // [NT][K] then [NT][K/32] block sums
+  using C = GvChunk<FMT>;
+  constexpr int BE = RawBlock<FMT>::BE, BB = RawBlock<FMT>::BB;
+  extern __shared__ __align__(16) uint8_t gv_smem[];
+  float* xs = (float*)gv_smem;  // [NT][K] then [NT][K/32] block sums
   stage_x<NT>(xs, x, x_dtype, K, T, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
   const float* xsum = xs + NT * K;
-  const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
   const int lane = __lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nwaves = gridDim.x * (GV_THREADS / 64);
-  const uint32_t rb = raw_row_bytes<FMT>(K);
-  const int nu = raw_units<FMT>(K);
-  for (int r = blockIdx.x * (GV_THREADS / 64) + wave; r < n_rows; r += nwaves) {
-    float acc[NT];
+  uint8_t* wbuf = gv_smem + gv_x_bytes<NT>(K) + wave * C::WAVE_BYTES;
+  constexpr bool SUMS = FMT == NSX_Q4_0 || FMT == NSX_Q4_K;
+  float xra[XREG ? 32 : 1], xrb[XREG ? 32 : 1], xsa = 0.f, xsb = 0.f;
+  if constexpr (XREG) {
+    const int nu0 = K / 32;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.f;
-    const uint32_t o_row = head + (uint32_t)r * rb;
-    for (int u = lane; u < nu; u += 64) raw_unit_dot<FMT, NT>(rs, o_row, u, xs, K, xsum, acc);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const float v = nsx_wave_sum(acc[t]);
-      if (lane == 0 && t < T) y[(int64_t)t * ystride + r] = v;
+    for (int k = 0; k < 32; ++k) {
+      xra[k] = lane < nu0 ? xs[raw_unit_elem<FMT>(lane, k)] : 0.f;
+      xrb[k] = lane + 64 < nu0 ? xs[raw_unit_elem<FMT>(lane + 64, k)] : 0.f;
+    }
+    if (SUMS) {
+      xsa = lane < nu0 ? xsum[lane] : 0.f;
+      xsb = lane + 64 < nu0 ? xsum[lane + 64] : 0.f;
     }
   }
+  const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
+  const int nwaves = gridDim.x * GV_WAVES;
+  const uint32_t rb = raw_row_bytes<FMT>(K);
+  const int nblk = K / BE;                        // blocks per row
+  const int nch = (nblk + C::BLOCKS - 1) / C::BLOCKS;  // chunks per row
+
+  // Work items of this wave: (row r0 + (k / nch) * nwaves, chunk k % nch).
+  const int r0 = blockIdx.x * GV_WAVES + wave;
+  if (r0 >= n_rows) return;
+  const int nitems = ((n_rows - 1 - r0) / nwaves + 1) * nch;
+  auto item_row = [&](int k) { return r0 + (k / nch) * nwaves; };
+  auto chunk_start = [&](int k) {
+    return head + (uint32_t)item_row(k) * rb + (uint32_t)((k % nch) * C::BLOCKS * BB);
+  };
+  auto chunk_loads = [&](int k) {  // 16-byte loads covering the chunk from its aligned start
+    const int nb = min(C::BLOCKS, nblk - (k % nch) * C::BLOCKS);
+    return (int)((nb * BB + 3 + 15) >> 4);
+  };
+  // Every 16-byte load lies inside the range: slots past the chunk repeat its
+  // last slot, and a slot that would cross the range's end (the final row's
+  // tail) is moved back to end there. Such a slot lands in LDS at its own
+  // (4-byte aligned) position, so repeated bytes are written with their own
+  // values. The range is at least one block (>= 17 bytes) long.
+  const uint32_t rend = (range + 3u) & ~3u;
+  struct Slot { v4u V[C::LOADS]; uint32_t D[C::LOADS]; };  // loaded bytes, LDS byte offsets
+  auto issue = [&](int k, Slot& S) {
+    const uint32_t s0 = chunk_start(k) & ~3u;
+    const int n16 = chunk_loads(k);
+#pragma unroll
+    for (int g = 0; g < C::LOADS; ++g) {
+      const uint32_t i = (uint32_t)min(lane + 64 * g, n16 - 1);
+      const uint32_t off = min(s0 + 16u * i, rend - 16u);
+      S.V[g] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+      S.D[g] = off - s0;
+    }
+  };
+  float acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = 0.f;
+  // Item k: its bytes (slot k % GV_DEPTH, loaded GV_DEPTH items earlier) ->
+  // LDS, the loads of item k + GV_DEPTH into the freed slot, then item k's
+  // arithmetic.
+  auto step = [&](int k, Slot& S) {
+#pragma unroll
+    for (int g = 0; g < C::LOADS; ++g) {  // in order with this wave's earlier LDS reads
+      uint32_t* w = (uint32_t*)(wbuf + S.D[g]);
+      w[0] = S.V[g].x; w[1] = S.V[g].y; w[2] = S.V[g].z; w[3] = S.V[g].w;
+    }
+    const uint32_t rel = chunk_start(k) & 3u;  // offset of the chunk's first byte in wbuf
+    if (k + GV_DEPTH < nitems) issue(k + GV_DEPTH, S);
+    const int c = k % nch;
+    const int nu = min(GV_CHUNK_UNITS, (nblk - c * C::BLOCKS) * BE / 32);
+    const int u0 = c * GV_CHUNK_UNITS;
+    const RawLdsSrc src{wbuf};
+    const RawUnit<FMT> A = raw_unit_fetch<FMT>(src, rel, lane);
+    const RawUnit<FMT> B = raw_unit_fetch<FMT>(src, rel, lane + 64);
+    if constexpr (XREG) {
+      if (lane < nu) raw_unit_math<FMT, NT>(A, u0 + lane, RawXReg{xra}, RawXSumReg{xsa}, acc);
+      if (lane + 64 < nu) raw_unit_math<FMT, NT>(B, u0 + lane + 64, RawXReg{xrb}, RawXSumReg{xsb}, acc);
+    } else {
+      const int ua = u0 + lane, ub = ua + 64;
+      if (lane < nu) raw_unit_math<FMT, NT>(A, ua, RawXLds<FMT>{xs, K, ua}, RawXSumLds{xsum, K >> 5, ua}, acc);
+      if (lane + 64 < nu) raw_unit_math<FMT, NT>(B, ub, RawXLds<FMT>{xs, K, ub}, RawXSumLds{xsum, K >> 5, ub}, acc);
+    }
+    if (c == nch - 1) {
+      const int r = item_row(k);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const float v = nsx_wave_sum(acc[t]);
+        if (lane == 0 && t < T) y[(int64_t)t * ystride + r] = v;
+        acc[t] = 0.f;
+      }
+    }
+  };
+  if constexpr (GV_DEPTH == 1) {
+    Slot S0;
+    issue(0, S0);
+    for (int k = 0; k < nitems; ++k) step(k, S0);
+  } else {
+    Slot S0, S1;
+    issue(0, S0);
+    if (nitems > 1) issue(1, S1);
+    for (int k = 0; k < nitems; k += 2) {
+      step(k, S0);
+      if (k + 1 < nitems) step(k + 1, S1);
+    }
+  }
+}
+
+// Workgroups of `kernel` (GV_THREADS threads, `lds` bytes) resident on the
+// current device at once: CUs x blocks per CU, cached per kernel and LDS size.
+static int resident_workgroups(const void* kernel, size_t lds) {
+  struct Entry { const void* k; size_t lds; int dev; int n; };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == kernel && cache[i].lds == lds && cache[i].dev == dev) return cache[i].n;
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GV_THREADS, lds) != hipSuccess || per <= 0) per = 1;
+  (void)hipGetLastError();
+  const int n = cus * per;
+  if (used < 64) cache[used++] = Entry{kernel, lds, dev, n};
+  return n;
 }
 
 template <int FMT, int NT>
@@ -267,20 +423,25 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
                            int64_t T, float* y, hipStream_t st) {
   const int64_t row_bytes = raw_row_bytes<FMT>((int)K);
   const int64_t rows_per_launch = std::max<int64_t>(1, ((int64_t)1 << 31) / row_bytes);
-  const size_t lds = (size_t)NT * (K + K / 32) * sizeof(float);
-  if (lds > 64 * 1024)
-    NSX_HIP(hipFuncSetAttribute((const void*)gemv_raw_kernel<FMT, NT>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  const size_t lds = (size_t)gv_x_bytes<NT>((int)K) + (size_t)GV_WAVES * GvChunk<FMT>::WAVE_BYTES;
+  constexpr bool XR = NT == 1;  // the register path exists for one token only
+  const bool xreg = XR && K <= GV_CHUNK_UNITS * 32;
+  const void* kern = xreg ? (const void*)gemv_raw_kernel<FMT, NT, XR> : (const void*)gemv_raw_kernel<FMT, NT, false>;
+  if (lds > 64 * 1024) NSX_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  const int64_t resident = resident_workgroups(kern, lds);
   for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_launch) {
     const int64_t nr = std::min(rows_per_launch, n_rows - r0);
     const uint8_t* p = (const uint8_t*)raw + r0 * row_bytes;
     const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
     const uint32_t head = (uint32_t)((uintptr_t)p - a);
     const uint32_t range = head + (uint32_t)(nr * row_bytes);
-    const int waves = GV_THREADS / 64;
-    const unsigned grid = (unsigned)std::min<int64_t>(nsx_cdiv(nr, waves), 8192);
-    hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT>), dim3(grid), dim3(GV_THREADS), lds, st,
-                       (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows);
+    const unsigned grid = (unsigned)std::min<int64_t>(nsx_cdiv(nr, GV_WAVES), resident);
+    if (xreg)
+      hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, XR>), dim3(grid), dim3(GV_THREADS), lds, st,
+                         (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows);
+    else
+      hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, false>), dim3(grid), dim3(GV_THREADS), lds, st,
+                         (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows);
     NSX_LAUNCHED();
   }
   return NSX_OK;
