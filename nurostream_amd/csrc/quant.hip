@@ -266,12 +266,18 @@ __host__ __device__ constexpr int gv_x_bytes(int K) {
   return ((NT * (K + K / 32) * 4) + 15) & ~15;
 }
 
-// Activations of one unit held in registers (unit order), one token.
+// Activations of one unit held in registers (unit order), one token, with
+// the unit's sum and its four 8-element group sums.
 struct RawXReg {
+  static constexpr bool kRegSums = true;
   const float (&x)[32];
+  float s;
+  const float (&g)[4];
   __device__ __forceinline__ v4f operator()(int, int k4) const {
     return v4f{x[4 * k4], x[4 * k4 + 1], x[4 * k4 + 2], x[4 * k4 + 3]};
   }
+  __device__ __forceinline__ float sum() const { return s; }
+  __device__ __forceinline__ float gsum(int L) const { return g[L]; }
 };
 struct RawXSumReg {
   float s;
@@ -288,25 +294,52 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
   using C = GvChunk<FMT>;
   constexpr int BE = RawBlock<FMT>::BE, BB = RawBlock<FMT>::BB;
   extern __shared__ __align__(16) uint8_t gv_smem[];
-  float* xs = (float*)gv_smem;  // [NT][K] then [NT][K/32] block sums
-  stage_x<NT>(xs, x, x_dtype, K, T, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
+  // LDS: [NT][K] activations and [NT][K/32] block sums (not with XREG), then
+  // one chunk buffer per wave
+  float* xs = (float*)gv_smem;
+  constexpr bool SUMS = FMT == NSX_Q4_0 || FMT == NSX_Q4_K;
+  if constexpr (!XREG) stage_x<NT>(xs, x, x_dtype, K, T, K, SUMS);
   const float* xsum = xs + NT * K;
   const int lane = __lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* wbuf = gv_smem + gv_x_bytes<NT>(K) + wave * C::WAVE_BYTES;
-  constexpr bool SUMS = FMT == NSX_Q4_0 || FMT == NSX_Q4_K;
-  float xra[XREG ? 32 : 1], xrb[XREG ? 32 : 1], xsa = 0.f, xsb = 0.f;
+  uint8_t* wbuf = gv_smem + (XREG ? 0 : gv_x_bytes<NT>(K)) + wave * C::WAVE_BYTES;
+  float xra[XREG ? 32 : 1], xrb[XREG ? 32 : 1], xsa = 0.f, xsb = 0.f, xga[4], xgb[4];
   if constexpr (XREG) {
+    // The lane's two units of x straight from global memory (L2-resident
+    // after the first waves), four elements per load; sums in the same
+    // sequential order as stage_x.
     const int nu0 = K / 32;
+    const uint32_t align = x_dtype == NSX_DT_F32 ? 15u : 7u;
+    const bool vec = ((uintptr_t)x & align) == 0;
+    auto gather = [&](int u, float (&xr)[32], float& sum, float (&gs)[4]) {
+      const bool on = u < nu0;
+      const int uu = on ? u : 0;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-      xra[k] = lane < nu0 ? xs[raw_unit_elem<FMT>(lane, k)] : 0.f;
-      xrb[k] = lane + 64 < nu0 ? xs[raw_unit_elem<FMT>(lane + 64, k)] : 0.f;
-    }
-    if (SUMS) {
-      xsa = lane < nu0 ? xsum[lane] : 0.f;
-      xsb = lane + 64 < nu0 ? xsum[lane + 64] : 0.f;
-    }
+      for (int k4 = 0; k4 < 8; ++k4) {
+        const v4f v = nsx_load_act4(x, x_dtype, raw_unit_elem<FMT>(uu, 4 * k4), vec);
+        xr[4 * k4] = on ? v.x : 0.f;
+        xr[4 * k4 + 1] = on ? v.y : 0.f;
+        xr[4 * k4 + 2] = on ? v.z : 0.f;
+        xr[4 * k4 + 3] = on ? v.w : 0.f;
+      }
+      if constexpr (SUMS || FMT == NSX_Q8_0) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) a += xr[k];
+        sum = a;
+      }
+      if constexpr (FMT == NSX_Q6_K) {
+#pragma unroll
+        for (int L = 0; L < 4; ++L) {
+          float a = 0.f;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) a += xr[8 * L + k];
+          gs[L] = a;
+        }
+      }
+    };
+    gather(lane, xra, xsa, xga);
+    gather(lane + 64, xrb, xsb, xgb);
   }
   const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
   const int nwaves = gridDim.x * GV_WAVES;
@@ -365,8 +398,8 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
     const RawUnit<FMT> A = raw_unit_fetch<FMT>(src, rel, lane);
     const RawUnit<FMT> B = raw_unit_fetch<FMT>(src, rel, lane + 64);
     if constexpr (XREG) {
-      if (lane < nu) raw_unit_math<FMT, NT>(A, u0 + lane, RawXReg{xra}, RawXSumReg{xsa}, acc);
-      if (lane + 64 < nu) raw_unit_math<FMT, NT>(B, u0 + lane + 64, RawXReg{xrb}, RawXSumReg{xsb}, acc);
+      if (lane < nu) raw_unit_math<FMT, NT>(A, u0 + lane, RawXReg{xra, xsa, xga}, RawXSumReg{xsa}, acc);
+      if (lane + 64 < nu) raw_unit_math<FMT, NT>(B, u0 + lane + 64, RawXReg{xrb, xsb, xgb}, RawXSumReg{xsb}, acc);
     } else {
       const int ua = u0 + lane, ub = ua + 64;
       if (lane < nu) raw_unit_math<FMT, NT>(A, ua, RawXLds<FMT>{xs, K, ua}, RawXSumLds{xsum, K >> 5, ua}, acc);
@@ -423,9 +456,9 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
                            int64_t T, float* y, hipStream_t st) {
   const int64_t row_bytes = raw_row_bytes<FMT>((int)K);
   const int64_t rows_per_launch = std::max<int64_t>(1, ((int64_t)1 << 31) / row_bytes);
-  const size_t lds = (size_t)gv_x_bytes<NT>((int)K) + (size_t)GV_WAVES * GvChunk<FMT>::WAVE_BYTES;
   constexpr bool XR = NT == 1;  // the register path exists for one token only
   const bool xreg = XR && K <= GV_CHUNK_UNITS * 32;
+  const size_t lds = (xreg ? 0 : (size_t)gv_x_bytes<NT>((int)K)) + (size_t)GV_WAVES * GvChunk<FMT>::WAVE_BYTES;
   const void* kern = xreg ? (const void*)gemv_raw_kernel<FMT, NT, XR> : (const void*)gemv_raw_kernel<FMT, NT, false>;
   if (lds > 64 * 1024) NSX_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   const int64_t resident = resident_workgroups(kern, lds);

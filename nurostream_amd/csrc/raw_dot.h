@@ -88,9 +88,13 @@ __device__ __forceinline__ RawUnit<FMT> raw_unit_fetch(const Src& ld, uint32_t o
 }
 
 // acc[t] += dot(unit u, x[t]) for the fetched unit. The unit's activations
-// come through `xa(t, k4)`: elements 4 k4 .. 4 k4 + 3 of the unit, in unit
+// come through `xa4(t, k4)`: elements 4 k4 .. 4 k4 + 3 of the unit, in unit
 // order (raw_unit_elem), of token t; `xsum(t)` is the sum of the unit's 32
-// activations of token t (used by Q4_0 and Q4_K only).
+// activations of token t (used by Q4_0 and Q4_K only). An accessor with
+// kRegSums (one token, held in registers) also gives the unit's sum and its
+// four 8-element group sums, so Q8_0 and Q6_K convert unsigned codes
+// (q + 128, q) and take the offset off per unit / group instead of per
+// element.
 template <int FMT, int NT, class XA, class XS>
 __device__ __forceinline__ void raw_unit_math(const RawUnit<FMT>& r, int u, const XA& xa4, const XS& xsum,
                                               float (&acc)[NT]) {
@@ -129,7 +133,10 @@ __device__ __forceinline__ void raw_unit_math(const RawUnit<FMT>& r, int u, cons
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t w = nsx_alignbyte(E[i + 1], E[i], 2);
-        const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+        uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+        // keep the masked dwords: the compiler would otherwise extract every
+        // nibble with its own bit-field op ahead of the byte conversion
+        asm volatile("" : "+v"(lo), "+v"(hi));
         const float l0 = nsx_ub<0>(lo), l1 = nsx_ub<1>(lo);
         const float l2 = nsx_ub<2>(lo), l3 = nsx_ub<3>(lo);
         const float h0 = nsx_ub<0>(hi), h1 = nsx_ub<1>(hi);
@@ -160,18 +167,37 @@ __device__ __forceinline__ void raw_unit_math(const RawUnit<FMT>& r, int u, cons
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t w = nsx_alignbyte(E[i + 1], E[i], 2);
-      const float q0 = (float)(int8_t)(w & 0xffu), q1 = (float)(int8_t)((w >> 8) & 0xffu);
-      const float q2 = (float)(int8_t)((w >> 16) & 0xffu), q3 = (float)(int8_t)(w >> 24);
+      if constexpr (XA::kRegSums) {
+        // q + 128 as unsigned bytes (one conversion each); the 128 comes off
+        // through the unit's activation sum below
+        const uint32_t wu = w ^ 0x80808080u;
+        const float q0 = nsx_ub<0>(wu), q1 = nsx_ub<1>(wu), q2 = nsx_ub<2>(wu), q3 = nsx_ub<3>(wu);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const v4f xa = xa4(t, i);
-        float p = part[t];
-        p = fmaf(q0, xa.x, p); p = fmaf(q1, xa.y, p); p = fmaf(q2, xa.z, p); p = fmaf(q3, xa.w, p);
-        part[t] = p;
+        for (int t = 0; t < NT; ++t) {
+          const v4f xa = xa4(t, i);
+          float p = part[t];
+          p = fmaf(q0, xa.x, p); p = fmaf(q1, xa.y, p); p = fmaf(q2, xa.z, p); p = fmaf(q3, xa.w, p);
+          part[t] = p;
+        }
+      } else {
+        const float q0 = (float)(int8_t)(w & 0xffu), q1 = (float)(int8_t)((w >> 8) & 0xffu);
+        const float q2 = (float)(int8_t)((w >> 16) & 0xffu), q3 = (float)(int8_t)(w >> 24);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const v4f xa = xa4(t, i);
+          float p = part[t];
+          p = fmaf(q0, xa.x, p); p = fmaf(q1, xa.y, p); p = fmaf(q2, xa.z, p); p = fmaf(q3, xa.w, p);
+          part[t] = p;
+        }
       }
     }
+    if constexpr (XA::kRegSums) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = fmaf(d, part[t], acc[t]);
+      for (int t = 0; t < NT; ++t) acc[t] = fmaf(d, fmaf(-128.f, xa4.sum(), part[t]), acc[t]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] = fmaf(d, part[t], acc[t]);
+    }
   } else if constexpr (FMT == NSX_Q6_K) {
     // Element 128 h + 32 L + l0 + i takes its low 4 bits from ql[64 h + 32 (L & 1)
     // + l0 + i] (nibble L >> 1), its high 2 bits from qh[32 h + l0 + i] >> 2L,
@@ -205,8 +231,10 @@ __device__ __forceinline__ void raw_unit_math(const RawUnit<FMT>& r, int u, cons
                              ((qb >> 4) & 0x0f0f0f0fu) | ((qc >> 2) & 0x30303030u)};
 #pragma unroll
       for (int L = 0; L < 4; ++L) {
-        const float q0 = nsx_ub<0>(q[L]) - 32.f, q1 = nsx_ub<1>(q[L]) - 32.f;  // exact
-        const float q2 = nsx_ub<2>(q[L]) - 32.f, q3 = nsx_ub<3>(q[L]) - 32.f;
+        // with register sums the 32 comes off per 8-element group below
+        constexpr float off = XA::kRegSums ? 0.f : 32.f;
+        const float q0 = nsx_ub<0>(q[L]) - off, q1 = nsx_ub<1>(q[L]) - off;  // exact
+        const float q2 = nsx_ub<2>(q[L]) - off, q3 = nsx_ub<3>(q[L]) - off;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const v4f xa = xa4(t, 2 * L + i);  // elements 32 L + 4 i .. of the part
@@ -220,7 +248,10 @@ __device__ __forceinline__ void raw_unit_math(const RawUnit<FMT>& r, int u, cons
     for (int t = 0; t < NT; ++t) {
       float a = acc[t];
 #pragma unroll
-      for (int L = 0; L < 4; ++L) a = fmaf(dsc[L], part[t][L], a);
+      for (int L = 0; L < 4; ++L) {
+        if constexpr (XA::kRegSums) a = fmaf(dsc[L], fmaf(-32.f, xa4.gsum(L), part[t][L]), a);
+        else a = fmaf(dsc[L], part[t][L], a);
+      }
       acc[t] = a;
     }
   } else {  // Q4_K sub-block unit: block b = u/8, sub-block s = u%8
@@ -243,7 +274,8 @@ __device__ __forceinline__ void raw_unit_math(const RawUnit<FMT>& r, int u, cons
     for (int t = 0; t < NT; ++t) part[t] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t q = (r.Q[i] >> sh) & 0x0f0f0f0fu;
+      uint32_t q = (r.Q[i] >> sh) & 0x0f0f0f0fu;
+      asm volatile("" : "+v"(q));  // one mask per dword, not one bit-field op per nibble
       const float q0 = nsx_ub<0>(q), q1 = nsx_ub<1>(q);
       const float q2 = nsx_ub<2>(q), q3 = nsx_ub<3>(q);
 #pragma unroll
@@ -278,6 +310,7 @@ __device__ __forceinline__ int raw_unit_elem(int u, int k) {
 // sums).
 template <int FMT>
 struct RawXLds {
+  static constexpr bool kRegSums = false;  // no per-unit / per-8 sums on hand
   const float* xs;
   int K, u;
   __device__ __forceinline__ v4f operator()(int t, int k4) const {
