@@ -31,6 +31,11 @@ Other workloads (`--workload`, one JSON line each, for the design notes):
                 BASELINE config 5b: the same stack with a seeded 25% of the
                 512-row expert blocks in pinned host RAM, staged per step
                 (eager: one host synchronisation per layer for the routing)
+  lmhead-q6k    the fused raw-GGUF GEMV (nsx_fused_gemv) at T=1 over a
+                Qwen3-235B-shaped Q6_K LM head, 151936 x 4096 (the Q6_K
+                tensor of Q4_K_M files); two weight copies alternate
+  lmhead-q8     the same over a GPT-OSS-120B-shaped Q8_0 LM head,
+                201088 x 2880
 
 Prints one JSON line (the driver's contract) with a `roofline` object for the
 dominant kernel (the gate/up dequant-GEMV) and a `cpu_baseline` object: the
@@ -47,7 +52,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8", "stack-t1-host25",
-             "stack-t8-host25")
+             "stack-t8-host25", "lmhead-q6k", "lmhead-q8")
 
 # per workload: (config name, T, steps, warmup, rotating layers or stack depth, profile steps)
 _DEFAULTS = {
@@ -59,7 +64,11 @@ _DEFAULTS = {
     "stack-t8": ("GPTOSS_120B", 8, 20, 2, 36, 0),
     "stack-t1-host25": ("GPTOSS_120B", 1, 20, 3, 36, 0),
     "stack-t8-host25": ("GPTOSS_120B", 8, 10, 2, 36, 0),
+    "lmhead-q6k": ("Q6_K", 1, 200, 20, 2, 0),
+    "lmhead-q8": ("Q8_0", 1, 200, 20, 2, 0),
 }
+# LM-head GEMV shapes: (rows = vocabulary, K = hidden, model)
+_LMHEAD = {"lmhead-q6k": (151936, 4096, "qwen3-235b-a22b"), "lmhead-q8": (201088, 2880, "gpt-oss-120b")}
 
 
 def _parse():
@@ -405,6 +414,98 @@ def stack_workload(args, torch, N, synth, dev):
     }
 
 
+def _gemv_cpu_baseline(raw_cpu, t, x, rows, K, budget_s):
+    """The reference's CPU path for a quantized linear (compute/quant.py
+    dequantize, then x @ w.T in float32; compute/blockffn.py:202-207) as the
+    numpy oracle, over row blocks of the same matrix for about budget_s."""
+    from oracle import quant as OQ
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    ncores = min(16, len(os.sched_getaffinity(0)))
+    rb = OQ.row_bytes(int(t), K)
+    blk = 4096
+    ctx = threadpool_limits(ncores) if threadpool_limits else None
+    done = 0
+    try:
+        if ctx:
+            ctx.__enter__()
+        OQ.gemv(raw_cpu[:blk * rb], int(t), x, blk, K)  # warm-up
+        t0 = time.perf_counter()
+        while True:
+            r0 = (done % rows) // blk * blk
+            n = min(blk, rows - r0)
+            OQ.gemv(raw_cpu[r0 * rb:(r0 + n) * rb], int(t), x, n, K)
+            done += n
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        dt = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return {"value": round(done / rows / dt, 3), "unit": "tok/s", "cores": ncores, "kind": "port",
+            "sample": f"{done} of the {rows} rows ({done / rows:.2f} LM-head passes) in {blk}-row blocks "
+                      f"(oracle.quant.gemv: numpy dequantize single-threaded, BLAS GEMV with {ncores} threads) "
+                      f"in {dt:.1f} s"}
+
+
+def gemv_workload(args, torch, N, synth, dev):
+    """One token through an LM-head-shaped raw GGUF matrix per step (nsx_fused_gemv, T=1)."""
+    name = args.workload
+    fmt_name, T, K0, W0, L0, _ = _DEFAULTS[name]
+    rows, K, model = _LMHEAD[name]
+    K_steps = args.steps if args.steps is not None else K0
+    W = args.warmup if args.warmup is not None else W0
+    n_copies = max(1, args.layers if args.layers is not None else L0)
+    t = getattr(synth.GGMLType, fmt_name)
+    raws = [synth.matrix_bytes(t, rows, K, synth.generator(synth.layer_seed(args.seed, i), dev), dev)
+            for i in range(n_copies)]
+    nbytes = raws[0].numel()
+    xs = synth.activations(W + K_steps, K, seed=args.seed + 1, device=dev)
+    ys = torch.empty((W + K_steps, rows), dtype=torch.float32, device=dev)
+    lib = N.load()
+
+    def run_steps(rng):
+        s = N.stream_ptr(dev)
+        for i in rng:
+            N.check(lib.nsx_fused_gemv(int(t), raws[i % n_copies].data_ptr(), rows, K, xs[i].data_ptr(), N.DT_F32,
+                                       1, ys[i].data_ptr(), s), "fused_gemv")
+
+    ms, wall_s, _ = _graph_time(torch, run_steps, W, K_steps)
+    us = ms * 1e3 / K_steps
+    # parity spot check of the timed outputs against the oracle (a row block)
+    from oracle import quant as OQ
+    rb = OQ.row_bytes(int(t), K)
+    i = W + K_steps - 1
+    raw_i = raws[i % n_copies][:512 * rb].cpu().numpy()
+    ref = OQ.gemv(raw_i, int(t), xs[i:i + 1].cpu().numpy(), 512, K, f64=True)[0]
+    got = ys[i, :512].cpu().numpy()
+    import numpy as np
+    err = float(np.max(np.abs(got - ref)) / max(1e-30, float(np.max(np.abs(ref)))))
+    if err > 1e-3:
+        raise RuntimeError(f"{name}: timed outputs differ from the oracle (max rel err {err:.3g})")
+    cpu = None
+    if not args.no_cpu:
+        cpu = _gemv_cpu_baseline(raws[0].cpu().numpy(), t, xs[0:1].cpu().numpy(), rows, K, args.cpu_seconds)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    kname = f"gemv_raw_kernel<{int(t)}, 1, true>"
+    return {
+        "metric": f"LM-head decode tok/s ({model} shape, {fmt_name} raw GGUF rows, fused GEMV)",
+        "value": round(1e6 / us, 1), "unit": "tok/s", "n_gpus": 1, "steps": K_steps, "warmup": W,
+        "ms_per_step": round(us * 1e-3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": f"{fmt_name.lower()} weights x fp32 activations, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": f"{model} LM head {rows} x {K} {fmt_name}, T=1 ({n_copies} alternating copies)",
+                   "rows": rows, "K": K, "T": 1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname),
+                     "kernel": kname, "algorithmic_bytes": nbytes},
+        "parity_max_rel_err": err,
+        "wall_s": round(wall_s, 4),
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -424,6 +525,8 @@ def main():
     N.ensure_selftest(dev)
     if args.workload.startswith("stack"):
         result = stack_workload(args, torch, N, synth, dev)
+    elif args.workload.startswith("lmhead"):
+        result = gemv_workload(args, torch, N, synth, dev)
     else:
         result = layer_workload(args, torch, N, synth, dev)
     if args.copy_probe_mib > 0:  # a plain copy of known size for the counter calibration
