@@ -28,7 +28,9 @@ enum {
   NSX_ETYPE = 2,    /* TypeError: wrong buffer element type */
   NSX_ENOTIMPL = 3, /* NotImplementedError: unsupported ggml type */
   NSX_EHIP = 4,     /* RuntimeError: HIP runtime failure */
-  NSX_EKERNEL = 5   /* RuntimeError: a kernel's own bounded check failed */
+  NSX_EKERNEL = 5,  /* RuntimeError: a kernel's own bounded check failed */
+  NSX_EIO = 6,      /* OSError (EOFError for a short read): a file read failed */
+  NSX_ETIMEDOUT = 7 /* TimeoutError: a wait ran out of time */
 };
 
 /* ggml type ids (format/gguf.py:19-35) */
@@ -211,6 +213,60 @@ int nsx_gather_copy(int64_t n, const uint64_t *src, const uint64_t *dst,
  * hipHostMalloc or torch's pin_memory), for tile tables that point into it.
  * Fails (NSX_EHIP) if host is not device-mapped pinned memory. */
 int nsx_host_device_address(const void *host, uint64_t *device_address);
+
+/* ---- disk reader: GGUF bytes from a file into device (or host) memory ----
+ * Replaces the reference's thread-pool reader and the disk side of its
+ * streaming source (io/reader.py AsyncReader, io/stream.py StreamingSource):
+ * n_workers threads issue positional reads (O_DIRECT where the file system
+ * allows it) into staging buffers, and a read into device memory is copied
+ * from its pinned staging buffer on the reader's copy stream as soon as it
+ * lands, with no host thread in between. Reads larger than a staging buffer
+ * are split across buffers and workers. */
+typedef struct nsx_reader nsx_reader;
+
+enum { NSX_READ_DIRECT = 1 }; /* try O_DIRECT (page-cache bypass); buffered where refused */
+
+typedef struct {
+  int64_t requests;     /* reads submitted */
+  int64_t bytes_read;   /* bytes delivered */
+  double read_seconds;  /* time spent inside reads, summed over the workers */
+  double first_read;    /* CLOCK_MONOTONIC seconds: start of the first read */
+  double last_read;     /* end of the latest read */
+  int32_t direct;       /* 1 while reads bypass the page cache */
+  int32_t n_workers;
+} nsx_reader_stats;
+
+/* io/reader.py:72-92 AsyncReader(path, n_workers). n_slots staging buffers
+ * of slot_bytes each (>= 3 x 4096); pinned host memory when device >= 0 (the
+ * device whose memory reads land in, copied on copy_stream, a hipStream_t of
+ * that device), plain host memory when device < 0 (host destinations only).
+ * n_workers == 0 gives a reader that never reads: a wait can only time out
+ * (for tests of that path). */
+int nsx_reader_open(const char *path, int n_workers, int flags, int n_slots, int64_t slot_bytes,
+                    int device, void *copy_stream, nsx_reader **out);
+/* io/reader.py:116-118 submit(offset, nbytes), the read under
+ * io/stream.py:200-216 submit_rows: queue file bytes [offset, offset +
+ * nbytes) into dst -- device memory when dst_on_device (the copy stream
+ * first waits for the work already queued on `stream`, the stream dst was
+ * allocated on), else host memory. A read past the end of the file fails
+ * at wait. */
+int nsx_reader_submit(nsx_reader *r, int64_t offset, int64_t nbytes, void *dst, int dst_on_device,
+                      void *stream, uint64_t *ticket);
+/* 1 once the ticket's bytes are read and their copies queued, 0 while
+ * pending (the fut.done() of io/reader.py:129); NSX_EINVAL (< 0 as
+ * -NSX_EINVAL) for an unknown ticket. */
+int nsx_reader_poll(nsx_reader *r, uint64_t ticket);
+/* io/reader.py:127-139 wait(fut): block up to timeout_us (< 0: no limit)
+ * until the ticket's reads are done, then order `stream` after their device
+ * copies (host destinations are complete on return), and retire the ticket.
+ * NSX_EIO if a read failed or came up short (the ticket is retired),
+ * NSX_ETIMEDOUT if the time ran out (the ticket stays pending). */
+int nsx_reader_wait(nsx_reader *r, uint64_t ticket, int64_t timeout_us, void *stream);
+/* io/reader.py:31-69 IOStats (the reader-side counters). */
+int nsx_reader_get_stats(nsx_reader *r, nsx_reader_stats *out);
+/* io/reader.py:141-148 close(): drop queued reads (their tickets fail), join
+ * the workers, wait for copies out of staging, free everything. */
+int nsx_reader_close(nsx_reader *r);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libnsx.so"
 HEADER = Path(__file__).resolve().parents[1] / "include" / "nurostream_amd.h"
 
 # status codes (nurostream_amd.h)
-OK, EINVAL, ETYPE, ENOTIMPL, EHIP, EKERNEL = 0, 1, 2, 3, 4, 5
+OK, EINVAL, ETYPE, ENOTIMPL, EHIP, EKERNEL, EIO, ETIMEDOUT = 0, 1, 2, 3, 4, 5, 6, 7
+READ_DIRECT = 1
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 LAYOUT_GGUF, LAYOUT_T64 = 0, 1
 ROUTE_GPTOSS, ROUTE_QWEN3 = 0, 1
@@ -46,6 +47,14 @@ class MoeLayerC(C.Structure):
     ]
 
 
+class ReaderStatsC(C.Structure):
+    """nsx_reader_stats."""
+
+    _fields_ = [("requests", C.c_int64), ("bytes_read", C.c_int64), ("read_seconds", C.c_double),
+                ("first_read", C.c_double), ("last_read", C.c_double), ("direct", C.c_int32),
+                ("n_workers", C.c_int32)]
+
+
 _SIGS = {
     "nsx_last_error": (C.c_char_p, []),
     "nsx_abi_version": (_i, []),
@@ -64,6 +73,12 @@ _SIGS = {
     "nsx_copy_blocks_async": (_i, [_i64, _p, _p, _p, _p, _p]),
     "nsx_gather_copy": (_i, [_i64, _p, _p, _p, _p]),
     "nsx_host_device_address": (_i, [_p, C.POINTER(C.c_uint64)]),
+    "nsx_reader_open": (_i, [C.c_char_p, _i, _i, _i, _i64, _i, _p, C.POINTER(_p)]),
+    "nsx_reader_submit": (_i, [_p, _i64, _i64, _p, _i, _p, C.POINTER(C.c_uint64)]),
+    "nsx_reader_poll": (_i, [_p, C.c_uint64]),
+    "nsx_reader_wait": (_i, [_p, C.c_uint64, _i64, _p]),
+    "nsx_reader_get_stats": (_i, [_p, C.POINTER(ReaderStatsC)]),
+    "nsx_reader_close": (_i, [_p]),
 }
 PHASE_ROUTER, PHASE_GATE_UP, PHASE_DOWN, PHASE_COMBINE = 0, 1, 2, 3
 
@@ -114,6 +129,10 @@ def check(rc: int, what: str = "") -> None:
         raise TypeError(msg)
     if rc == ENOTIMPL:
         raise NotImplementedError(msg)
+    if rc == EIO:
+        raise (EOFError if "short read" in msg else OSError)(msg)
+    if rc == ETIMEDOUT:
+        raise TimeoutError(msg)
     raise NativeError(msg)
 
 

@@ -23,7 +23,7 @@ import torch
 from .compute.blockffn import DEFAULT_BLOCK_ROWS, DEFAULT_LOOKAHEAD
 from .format.gguf import FLOAT_TYPES, row_geometry
 from .io.arena import Arena
-from .io.source import GGUFSource
+from .io.stream import DiskSource
 from .residency.cache import TieredCache
 
 _SIZE_RE = re.compile(r"^\s*([\d.]+)\s*([KMGT]?)B?\s*$", re.I)
@@ -68,10 +68,12 @@ class NeuroStream:
         self.dtype = compute_dtype or torch.float32
         self.verbose = verbose
         self.arena = Arena(parse_size(mem_budget))
-        self.source = GGUFSource(path, self.arena, device=device)
+        # weights stream from the file through n_workers reader threads (api.py:96-101)
+        self.source = DiskSource(path, self.arena, n_workers=n_workers, device=device)
         self.gguf = self.source.gguf
         arch = self.gguf.arch()
         if arch != "gpt-oss":
+            self.source.close()
             raise ValueError(f"unsupported architecture: {arch} (this build runs GPT-OSS MoE FFN stacks; "
                              "Qwen3 MoE layers run through nurostream_amd.model.qwen3 / moe.router.moe_ffn)")
         self.cfg = MoEModelConfig.from_gguf(self.gguf)

@@ -16,7 +16,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libnsx.so"
-SOURCES = ("quant.hip", "moe.hip")
+SOURCES = ("quant.hip", "moe.hip", "reader.hip")
 HEADERS = ("nsx_common.h", "raw_dot.h")
 
 HIPCC_FLAGS = [
@@ -25,6 +25,7 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-shared",
+    "-pthread",
     # never let the compiler emit packed fp32 arithmetic (v_pk_fma_f32 & co.)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
