@@ -36,6 +36,12 @@ Other workloads (`--workload`, one JSON line each, for the design notes):
                 tensor of Q4_K_M files); two weight copies alternate
   lmhead-q8     the same over a GPT-OSS-120B-shaped Q8_0 LM head,
                 201088 x 2880
+  disk-stream   expert weights from a GGUF file on the box's disk: one
+                GPT-OSS-120B-shaped layer's MXFP4 expert tensors (1.7 GB)
+                are written, then read into HBM in 512-row blocks by the
+                native reader (O_DIRECT, then buffered), and decode tokens
+                run through the layer with every expert block streamed from
+                the file (DiskSource + BlockPrefetcher + stream_expert_ffn)
 
 Prints one JSON line (the driver's contract) with a `roofline` object for the
 dominant kernel (the gate/up dequant-GEMV) and a `cpu_baseline` object: the
@@ -52,7 +58,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8", "stack-t1-host25",
-             "stack-t8-host25", "lmhead-q6k", "lmhead-q8")
+             "stack-t8-host25", "lmhead-q6k", "lmhead-q8", "disk-stream")
 
 # per workload: (config name, T, steps, warmup, rotating layers or stack depth, profile steps)
 _DEFAULTS = {
@@ -66,6 +72,7 @@ _DEFAULTS = {
     "stack-t8-host25": ("GPTOSS_120B", 8, 10, 2, 36, 0),
     "lmhead-q6k": ("Q6_K", 1, 200, 20, 2, 0),
     "lmhead-q8": ("Q8_0", 1, 200, 20, 2, 0),
+    "disk-stream": ("GPTOSS_120B", 1, 12, 2, 1, 0),
 }
 # LM-head GEMV shapes: (rows = vocabulary, K = hidden, model)
 _LMHEAD = {"lmhead-q6k": (151936, 4096, "qwen3-235b-a22b"), "lmhead-q8": (201088, 2880, "gpt-oss-120b")}
@@ -506,6 +513,144 @@ def gemv_workload(args, torch, N, synth, dev):
     }
 
 
+def _fs_of(path):
+    """(mount point, file system type) holding `path`, from /proc/mounts."""
+    best = ("", "?")
+    try:
+        with open("/proc/mounts") as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 3 and str(path).startswith(parts[1]) and len(parts[1]) >= len(best[0]):
+                    best = (parts[1], parts[2])
+    except OSError:
+        pass
+    return best
+
+
+def disk_workload(args, torch, N, synth, dev):
+    """Expert blocks from a GGUF on disk into HBM: the reader's raw rate, then decode tokens."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from nurostream_amd.compute.blockffn import BlockPrefetcher, stream_expert_ffn
+    from nurostream_amd.format.gguf import GGUFWriter, row_geometry, tensor_info
+    from nurostream_amd.io.arena import Arena
+    from nurostream_amd.io.reader import DiskReader
+    from nurostream_amd.io.stream import DiskSource
+    from oracle import moe as OM
+    from oracle import quant as OQ
+    cfg = synth.GPTOSS_120B
+    K_steps = args.steps if args.steps is not None else _DEFAULTS["disk-stream"][2]
+    W = args.warmup if args.warmup is not None else _DEFAULTS["disk-stream"][3]
+    block_rows = 512
+    tmp = tempfile.mkdtemp(prefix="nsx_disk_", dir=os.environ.get("NSX_DISK_DIR") or None)
+    path = os.path.join(tmp, "layer.gguf")
+    try:
+        t = synth.make_layer(cfg, seed=args.seed, device="cpu")
+        gw = GGUFWriter(path, "gpt-oss")
+        names = {}
+        for kind in ("gate", "up", "down"):
+            rows, K = cfg.rows_K(kind)
+            nm = f"blk.0.ffn_{kind}_exps.weight"
+            gw.add_tensor(nm, (cfg.n_expert, rows, K), synth.GGMLType.MXFP4, t[kind].numpy())
+            gw.add_tensor(f"blk.0.ffn_{kind}_exps.bias", (cfg.n_expert, rows), synth.GGMLType.F32,
+                          t[kind + "_b"].reshape(-1).numpy().view(np.uint8))
+            names[kind] = nm
+        gw.write()
+        del gw
+        mount, fstype = _fs_of(os.path.realpath(path))
+        src0 = DiskSource(path, Arena(1 << 30), n_workers=1, device="cpu")
+        infos = {k: src0.gguf.tensors[names[k]] for k in names}
+        spans = []
+        for info in infos.values():
+            n_rows, _, rb = row_geometry(info)
+            off = src0.gguf.file_offset(info)
+            spans += [(off + r0 * rb, min(block_rows, n_rows - r0) * rb) for r0 in range(0, n_rows, block_rows)]
+        src0.close()
+        total = sum(n for _, n in spans)
+
+        def raw_rate(direct):
+            with DiskReader(path, n_workers=16, device=dev, direct=direct) as r:
+                window, futs, t0 = 64, [], time.perf_counter()
+                for span in spans:
+                    futs.append(r.submit(*span))
+                    if len(futs) >= window:
+                        r.wait(futs.pop(0))
+                for f in futs:
+                    r.wait(f)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                return {"GBps": round(total / dt / 1e9, 3), "seconds": round(dt, 3), "direct": r.direct,
+                        "blocks": len(spans), "bytes": total}
+
+        rates = {"o_direct": raw_rate(True), "buffered": raw_rate(False)}
+
+        # decode tokens through the layer, every expert block from the file
+        src = DiskSource(path, Arena(256 << 20), n_workers=16, device=dev)
+        xs = synth.activations(W + K_steps, cfg.n_embd, seed=args.seed + 7, device="cpu")
+        rng = np.random.default_rng(args.seed)
+
+        def act_t(g, u):
+            gc = torch.clamp(g, max=7.0)
+            uc = torch.clamp(u, -7.0, 7.0)
+            return (uc + 1) * (gc * torch.sigmoid(1.702 * gc))
+
+        def step(i):
+            experts = sorted(rng.choice(cfg.n_expert, cfg.top_k, replace=False).tolist())
+            plan = [(names[k], e * r, (e + 1) * r) for e in experts
+                    for k, r in (("gate", cfg.n_ff), ("up", cfg.n_ff), ("down", cfg.n_embd))]
+            x = xs[i:i + 1].to(dev)
+            with BlockPrefetcher(src, plan, block_rows=block_rows, depth=24) as pf:
+                ys = [stream_expert_ffn(src, "blk.0.", e, x, cfg.n_ff, cfg.n_embd, act_t, block_rows=block_rows,
+                                        device=dev, bias=True, lookahead=2, prefetcher=pf) for e in experts]
+            return experts, ys
+
+        for i in range(W):
+            step(i)
+        torch.cuda.synchronize()
+        st0 = src.stats
+        t0 = time.perf_counter()
+        last = None
+        for i in range(W, W + K_steps):
+            last = (i, step(i))
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        st1 = src.stats
+        # parity of the last token's expert outputs against the oracle
+        i, (experts, ys) = last
+        ex = OM.ExpertSet(OQ.MXFP4, cfg.n_embd, cfg.n_ff, {k: t[k].numpy() for k in ("gate", "up", "down")},
+                          {k: t[k + "_b"].numpy() for k in ("gate", "up", "down")})
+        err = 0.0
+        for e, y in zip(experts, ys):
+            ref = OM.expert_ffn(ex, e, xs[i:i + 1].numpy(), lambda g, u: OM.clamped_swiglu(g, u),
+                                block_rows=block_rows)
+            err = max(err, float(np.max(np.abs(y.cpu().numpy() - ref)) / max(1e-30, float(np.max(np.abs(ref))))))
+        if err > 1e-3:
+            raise RuntimeError(f"disk-stream: expert outputs differ from the oracle (max rel err {err:.3g})")
+        direct = src.reader.direct
+        src.close()
+        tok_bytes = cfg.top_k * sum(cfg.expert_bytes(k) for k in ("gate", "up", "down"))
+        ms = dt * 1e3 / K_steps
+        return {
+            "metric": "MoE-FFN decode tok/s with every expert block read from disk (GPT-OSS-120B shape, MXFP4)",
+            "value": round(K_steps / dt, 3), "unit": "tok/s", "n_gpus": 1, "steps": K_steps, "warmup": W,
+            "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "mxfp4 weights x fp32 activations", "data": "synthetic (a GGUF written to the box's disk)",
+            "config": {"workload": "gpt-oss-120b MoE layer experts from a GGUF file on disk, T=1, 512-row blocks",
+                       "block_rows": block_rows, "prefetch_depth": 24, "n_workers": 16, "file_bytes":
+                       os.path.getsize(path), "fs": fstype, "mount": mount, "o_direct": direct},
+            "expert_bytes_per_token": tok_bytes,
+            "disk_GBps_during_decode": round((st1.bytes_read - st0.bytes_read) / dt / 1e9, 3),
+            "reader_raw": rates,
+            "stall_seconds": round(st1.stall_seconds - st0.stall_seconds, 4),
+            "parity_max_rel_err": err,
+            "roofline": None,
+            "cpu_baseline": None,
+        }
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -527,6 +672,8 @@ def main():
         result = stack_workload(args, torch, N, synth, dev)
     elif args.workload.startswith("lmhead"):
         result = gemv_workload(args, torch, N, synth, dev)
+    elif args.workload == "disk-stream":
+        result = disk_workload(args, torch, N, synth, dev)
     else:
         result = layer_workload(args, torch, N, synth, dev)
     if args.copy_probe_mib > 0:  # a plain copy of known size for the counter calibration
