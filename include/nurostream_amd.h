@@ -214,6 +214,40 @@ int nsx_gather_copy(int64_t n, const uint64_t *src, const uint64_t *dst,
  * Fails (NSX_EHIP) if host is not device-mapped pinned memory. */
 int nsx_host_device_address(const void *host, uint64_t *device_address);
 
+/* ---- the step either side of the FFN in a GPT-OSS decode token ----
+ * The token's position is read from device memory (`pos`, an int32), so a
+ * captured graph of a whole decode token replays token after token;
+ * nsx_pos_advance moves it on. KV cache: K and V each
+ * [n_kv][ctx_max][head_dim] fp32. head_dim is 64 (GPT-OSS). */
+
+/* compute/blockffn.py:470-487 gather_embeddings: out[i] = dequant(row
+ * ids[i]) as fp32 (K elements), ids in device memory; an id outside
+ * [0, n_rows) gives zeros. Types: F32, F16, BF16 and the block types. */
+int nsx_dequantize_rows(int ggml_type, const void *raw, int64_t n_rows, int64_t K, const int32_t *ids,
+                        int64_t n_ids, float *out, void *stream);
+
+/* model/gpt_oss.py:42-58 (yarn_tables), 101-110 (q/k/v bias, rotary,
+ * KVCache.append) for one token: qkv holds the q (n_head rows), k and v
+ * (n_kv rows each) projections, head_dim each; biases are added (NULL:
+ * none); q and k rows are rotated by angle pos * inv_freq[i] (fp32) with
+ * cos and sin scaled by amplitude, q in place; k and v go into the caches at
+ * row pos. Nothing is written unless 0 <= pos < ctx_max. */
+int nsx_rope_kv_append(float *qkv, const float *q_bias, const float *k_bias, const float *v_bias, int n_head,
+                       int n_kv, int head_dim, const float *inv_freq, float amplitude, const int32_t *pos,
+                       float *k_cache, float *v_cache, int64_t ctx_max, void *stream);
+/* Workspace bytes of nsx_attn_decode for this cache length. */
+int64_t nsx_attn_workspace_bytes(int n_head, int head_dim, int64_t ctx_max);
+/* model/gpt_oss.py:73-85 sink_attention for the query token at position
+ * pos: keys 0..pos (the last `window` of them when window > 0), query head h
+ * reading kv head h / (n_head / n_kv), scores times `scale`, softmax over
+ * [scores, sinks[h]] with the sink column dropped (sinks NULL: no sink).
+ * out: [n_head][head_dim] fp32. */
+int nsx_attn_decode(const float *q, const float *k_cache, const float *v_cache, const float *sinks, int n_head,
+                    int n_kv, int head_dim, const int32_t *pos, int64_t ctx_max, int window, float scale,
+                    void *workspace, float *out, void *stream);
+/* *pos += n on the stream (one thread). */
+int nsx_pos_advance(int32_t *pos, int32_t n, void *stream);
+
 /* ---- disk reader: GGUF bytes from a file into device (or host) memory ----
  * Replaces the reference's thread-pool reader and the disk side of its
  * streaming source (io/reader.py AsyncReader, io/stream.py StreamingSource):

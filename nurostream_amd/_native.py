@@ -73,6 +73,11 @@ _SIGS = {
     "nsx_copy_blocks_async": (_i, [_i64, _p, _p, _p, _p, _p]),
     "nsx_gather_copy": (_i, [_i64, _p, _p, _p, _p]),
     "nsx_host_device_address": (_i, [_p, C.POINTER(C.c_uint64)]),
+    "nsx_dequantize_rows": (_i, [_i, _p, _i64, _i64, _p, _i64, _p, _p]),
+    "nsx_rope_kv_append": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, C.c_float, _p, _p, _p, _i64, _p]),
+    "nsx_attn_workspace_bytes": (_i64, [_i, _i, _i64]),
+    "nsx_attn_decode": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _i64, _i, C.c_float, _p, _p, _p]),
+    "nsx_pos_advance": (_i, [_p, C.c_int32, _p]),
     "nsx_reader_open": (_i, [C.c_char_p, _i, _i, _i, _i64, _i, _p, C.POINTER(_p)]),
     "nsx_reader_submit": (_i, [_p, _i64, _i64, _p, _i, _p, C.POINTER(C.c_uint64)]),
     "nsx_reader_poll": (_i, [_p, C.c_uint64]),

@@ -80,6 +80,8 @@ class NeuroStream:
         self.cache = TieredCache(self.source, device=device, compute_dtype=self.dtype,
                                  vram_budget=parse_size(vram_budget), ram_budget=parse_size(ram_budget))
         self.cache.slab_budget = parse_size(slab_budget)
+        if self.cache.vram_budget:
+            self._admit_dense()
         if self.cache.slab_budget:
             self._admit_experts()
         self.model = GptOssModel(self.cache, self.cfg, device, self.dtype, block_rows=block_rows,
@@ -105,6 +107,18 @@ class NeuroStream:
                 continue
             out.append((name, lo, hi, rpe * row_geometry(info)[2]))
         return out
+
+    def _admit_dense(self) -> int:
+        """The non-expert tensors into HBM (TieredCache VRAM-Q: quantized ones
+        stay raw for the fused GEMV), in file order while the VRAM budget lasts."""
+        n = 0
+        for name in self.gguf.tensors:
+            if "_exps." in name:
+                continue
+            n += bool(self.cache.admit_vram(name))
+        if self.verbose:
+            print(f"  {n} dense tensors resident ({self.cache.stats.vram_bytes / 1e9:.2f}GB)", flush=True)
+        return n
 
     def _admit(self, slabs) -> bool:
         """All of an expert's slabs or none (api.py:364-386: a partial expert
@@ -139,9 +153,67 @@ class NeuroStream:
             print(f"  pinned {pinned} expert slabs ({self.cache.slab_bytes / 1e9:.2f}GB)", flush=True)
         return pinned
 
+    # -- generation (api.py:179-237) -----------------------------------------
+
+    @staticmethod
+    def _sample(logits: torch.Tensor, temperature: float, top_p: float) -> int:
+        """Greedy at temperature <= 0, else softmax sampling with a top-p cut (api.py:179-191)."""
+        if temperature <= 0:
+            return int(logits.argmax())
+        probs = torch.softmax(logits.float() / temperature, dim=-1)
+        if 0 < top_p < 1:
+            srt, idx = torch.sort(probs, descending=True)
+            keep = (torch.cumsum(srt, 0) - srt) < top_p
+            srt = srt * keep
+            srt = srt / srt.sum()
+            return int(idx[torch.multinomial(srt, 1)])
+        return int(torch.multinomial(probs, 1))
+
+    def _piece(self, token: int) -> str:
+        """The token's entry in the GGUF vocabulary (tokenizer.ggml.tokens), or <id> without one."""
+        vocab = self.gguf.metadata.get("tokenizer.ggml.tokens")
+        if vocab is not None and 0 <= token < len(vocab):
+            return str(vocab[token])
+        return f"<{token}>"
+
     def generate(self, prompt, max_tokens: int = 128, temperature: float = 0.0, top_p: float = 0.95,
                  stop_on_eos: bool = True):
-        raise NotImplementedError(
-            "generate() needs the token embedding, attention (sink attention with YaRN RoPE), the output norm, "
-            "the LM head and the tokenizer; this build implements the MoE expert path only "
-            "(NeuroStream.model.ffn_stack / _ffn_block)")
+        """Yield one text piece per generated token (api.py:193-237).
+
+        The prompt is a list of token ids: the GGUF tokenizer (text to ids) is
+        outside this build, so a str prompt raises NotImplementedError. The
+        prompt runs through the model token by token, then each sampled token
+        is decoded the same way (embedding, every layer's attention and MoE
+        FFN, LM head, on the GPU). A piece is the token's vocabulary entry when
+        the GGUF has one, else "<id>"."""
+        import time
+        from .model.decode import DeviceKV
+        if isinstance(prompt, str):
+            raise NotImplementedError("text prompts need the GGUF tokenizer, which is outside this build; "
+                                      "pass a list of token ids")
+        ids = [int(t) for t in prompt]
+        if not ids:
+            raise ValueError("empty prompt")
+        c = self.model.attn_config()
+        kv = DeviceKV(self.cfg.n_layer, c, min(c.context_length, len(ids) + max_tokens), self.device)
+        self.stats = GenerationStats(prompt_tokens=len(ids))
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            logits = self.model.forward(ids, kv, start_pos=0)
+        self.stats.prefill_seconds = time.perf_counter() - t0
+        eos_id = self.gguf.metadata.get("tokenizer.ggml.eos_token_id")
+        eos = set() if eos_id is None else {int(eos_id)}
+        pos = len(ids)
+        t0 = time.perf_counter()
+        for _ in range(max_tokens):
+            nxt = self._sample(logits[-1], temperature, top_p)
+            if stop_on_eos and nxt in eos:
+                break
+            self.stats.generated_tokens += 1
+            yield self._piece(nxt)
+            if self.stats.generated_tokens >= max_tokens or pos >= kv.ctx_max:
+                break
+            with torch.no_grad():
+                logits = self.model.forward([nxt], kv, start_pos=pos)
+            pos += 1
+        self.stats.decode_seconds = time.perf_counter() - t0

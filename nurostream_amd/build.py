@@ -16,7 +16,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libnsx.so"
-SOURCES = ("quant.hip", "moe.hip", "reader.hip")
+SOURCES = ("quant.hip", "moe.hip", "attn.hip", "reader.hip")
 HEADERS = ("nsx_common.h", "raw_dot.h")
 
 HIPCC_FLAGS = [

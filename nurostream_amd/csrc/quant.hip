@@ -228,6 +228,73 @@ extern "C" int nsx_dequantize(int t, const void* raw, int64_t raw_bytes, int64_t
 }
 
 // ---------------------------------------------------------------------------
+// row gather + dequantize (compute/blockffn.py:470-487 gather_embeddings):
+// one workgroup per requested row, the row id read from device memory so a
+// captured decode step can take the next token from a device buffer. An id
+// outside [0, n_rows) gives a row of zeros.
+
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ raw, int64_t row_bytes,
+                                                           int64_t n_rows, const int32_t* __restrict__ ids, int K,
+                                                           float* __restrict__ out) {
+  const int64_t i = blockIdx.x;
+  const int id = ids[i];
+  const bool valid = id >= 0 && id < n_rows;
+  const uint8_t* p = raw + (valid ? (int64_t)id : 0) * row_bytes;
+  for (int j = threadIdx.x; j < K; j += blockDim.x) {
+    float v = 0.f;
+    if (valid) {
+      if constexpr (FMT == NSX_F32) {
+        v = ((const float*)p)[j];
+      } else if constexpr (FMT == NSX_F16) {
+        v = nsx_h2f(((const uint16_t*)p)[j]);
+      } else if constexpr (FMT == NSX_BF16) {
+        v = nsx_bf2f(((const uint16_t*)p)[j]);
+      } else {
+        constexpr int BE = Fmt<FMT>::BE;
+        v = dq_elem<FMT>(p, j / BE, j % BE);
+      }
+    }
+    out[i * K + j] = v;
+  }
+}
+
+extern "C" int nsx_dequantize_rows(int t, const void* raw, int64_t n_rows, int64_t K, const int32_t* ids,
+                                   int64_t n_ids, float* out, void* stream) {
+  NSX_REQUIRE(n_rows >= 0 && K > 0 && n_ids >= 0 && n_ids < (1ll << 31) && K < (1ll << 30), NSX_EINVAL,
+              "bad shape");
+  int64_t row_bytes = 0;
+  if (t == NSX_F32) row_bytes = K * 4;
+  else if (t == NSX_F16 || t == NSX_BF16) row_bytes = K * 2;
+  else {
+    const int BE = nsx_block_elems(t), BB = nsx_block_bytes(t);
+    NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no dequant kernel for ggml type %d", t);
+    NSX_REQUIRE(K % BE == 0, NSX_EINVAL, "K=%lld is not a multiple of the %d-element block", (long long)K, BE);
+    row_bytes = K / BE * BB;
+  }
+  if (n_ids == 0) return NSX_OK;
+  NSX_REQUIRE(raw && ids && out, NSX_EINVAL, "null buffer");
+  if ((t == NSX_F32 && ((uintptr_t)raw & 3)) || ((t == NSX_F16 || t == NSX_BF16) && ((uintptr_t)raw & 1)))
+    return nsx_fail(NSX_EINVAL, "float rows must be aligned to their element size");
+  const dim3 g((unsigned)n_ids), b(256);
+  const uint8_t* r = (const uint8_t*)raw;
+  hipStream_t st = S(stream);
+  switch (t) {
+    case NSX_F32: hipLaunchKernelGGL(dequant_rows_kernel<NSX_F32>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_F16: hipLaunchKernelGGL(dequant_rows_kernel<NSX_F16>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_BF16: hipLaunchKernelGGL(dequant_rows_kernel<NSX_BF16>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_MXFP4: hipLaunchKernelGGL(dequant_rows_kernel<NSX_MXFP4>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_Q4_0: hipLaunchKernelGGL(dequant_rows_kernel<NSX_Q4_0>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_Q8_0: hipLaunchKernelGGL(dequant_rows_kernel<NSX_Q8_0>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_Q4_K: hipLaunchKernelGGL(dequant_rows_kernel<NSX_Q4_K>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    case NSX_Q6_K: hipLaunchKernelGGL(dequant_rows_kernel<NSX_Q6_K>, g, b, 0, st, r, row_bytes, n_rows, ids, (int)K, out); break;
+    default: return nsx_fail(NSX_ENOTIMPL, "ggml type %d", t);
+  }
+  NSX_LAUNCHED();
+  return NSX_OK;
+}
+
+// ---------------------------------------------------------------------------
 // fused GEMV on raw GGUF rows (triton_kernels.py:199-228 seam)
 //
 // One wave per row; lanes take the row's 32-element units (raw_dot.h) and the

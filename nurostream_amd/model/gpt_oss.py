@@ -442,6 +442,8 @@ class GptOssModel:
         self.neuron_callback = None
         self._w: dict[str, torch.Tensor] = {}
         self._fused: dict[int, MoELayer] = {}
+        self._acfg = None
+        self._capturing: list | None = None
 
     def w(self, name: str) -> torch.Tensor:
         t = self._w.get(name)
@@ -496,7 +498,10 @@ class GptOssModel:
         fused = self._fused_layer(layer)
         if fused is not None:
             out, ids, _ = fused.forward(h)
-            self.router_stats.record(layer, ids)
+            if self._capturing is not None:  # no host copy inside a graph capture: recorded after each replay
+                self._capturing.append((layer, ids))
+            else:
+                self.router_stats.record(layer, ids)
             return x + out
         chosen, ids, weights = self._route(h, layer)
         stats = self.router_stats
@@ -528,3 +533,168 @@ class GptOssModel:
         for layer in range(self.cfg.n_layer):
             x = self._ffn_block(x, layer)
         return x
+
+    # -- the step either side of the FFN (model/gpt_oss.py:97-114, 207-228) --
+
+    def attn_config(self):
+        from .decode import AttnConfig, yarn_inv_freq
+        if self._acfg is None:
+            need = ["token_embd.weight", "output_norm.weight"] + [
+                f"blk.{li}.{n}" for li in range(self.cfg.n_layer)
+                for n in ("attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight")]
+            missing = [n for n in need if not self.has(n)]
+            if missing or self.gguf.cfg("attention.head_count") is None:
+                raise NotImplementedError(
+                    f"a decode token needs the embedding, attention and output tensors; this GGUF lacks "
+                    f"{missing[:3] or ['attention.head_count']}{' ...' if len(missing) > 3 else ''}")
+            self._acfg = AttnConfig.from_gguf(self.gguf)
+            self._inv_freq, self._amp = yarn_inv_freq(self._acfg, self.device)
+        return self._acfg
+
+    def _resident_raw(self, name: str):
+        """(raw device bytes, dtype) of a quantized tensor held whole in HBM, or None."""
+        hit = self.cache.raw_quantized(name)
+        if hit is None or not hit[0].is_cuda:
+            return None
+        return hit
+
+    def _linear(self, name: str, x: torch.Tensor) -> torch.Tensor:
+        """x @ W.T in fp32 (model/qwen3.py:169-194): the fused GEMV on HBM-resident
+        raw rows, else stream_linear by row blocks; float tensors by matmul."""
+        from ..compute.blockffn import stream_linear
+        from ..compute.kernels import can_fuse, fused_gemv
+        from ..format.gguf import FLOAT_TYPES, row_geometry
+        info = self.gguf.tensors[name]
+        n_rows, K, _ = row_geometry(info)
+        if info.dtype in FLOAT_TYPES:
+            return x @ self.w(name).T
+        hit = self._resident_raw(name)
+        if hit is not None and can_fuse(hit[1], x):
+            return fused_gemv(hit[0], hit[1], x, n_rows, K, out_dtype=torch.float32)
+        return stream_linear(self.cache, name, x, self.block_rows, self.device, torch.float32)
+
+    def _biased_linear(self, name: str, x: torch.Tensor) -> torch.Tensor:
+        out = self._linear(name + ".weight", x)
+        return out + self.w(name + ".bias") if self.has(name + ".bias") else out
+
+    def embed(self, ids: torch.Tensor) -> torch.Tensor:
+        """Rows of token_embd for device int32 ids -> (T, n_embd) fp32 (gather_embeddings, blockffn.py:470-487)."""
+        from ..format.gguf import FLOAT_TYPES, row_geometry
+        from .decode import dequantize_rows
+        name = "token_embd.weight"
+        info = self.gguf.tensors[name]
+        n_rows, K, _ = row_geometry(info)
+        if info.dtype in FLOAT_TYPES:
+            return self.w(name).reshape(n_rows, K)[ids.long()]
+        hit = self._resident_raw(name)
+        if hit is not None:
+            return dequantize_rows(hit[0], hit[1], n_rows, K, ids)
+        return torch.stack([self.cache.fetch_rows(name, t, t + 1, device=self.device, dtype=torch.float32)[0]
+                            for t in ids.tolist()])
+
+    def _attention_block(self, x: torch.Tensor, layer: int, kv) -> torch.Tensor:
+        """x + o_proj(sink_attention(...)) for the one token at kv.pos (gpt_oss.py:101-114):
+        rms_norm, q/k/v projections, then bias + rotary + cache append and the
+        sink attention (sliding window on even layers) as kernels."""
+        from .decode import attn_decode, rope_kv_append
+        c, p = self.attn_config(), f"blk.{layer}."
+        h = add_rms_norm(x, None, self.w(p + "attn_norm.weight"), self.cfg.rms_eps)
+        q = self._linear(p + "attn_q.weight", h)
+        k = self._linear(p + "attn_k.weight", h)
+        v = self._linear(p + "attn_v.weight", h)
+        qkv = torch.cat([q.reshape(-1), k.reshape(-1), v.reshape(-1)])
+        b = lambda n: self.w(p + n + ".bias") if self.has(p + n + ".bias") else None  # noqa: E731
+        rope_kv_append(qkv, b("attn_q"), b("attn_k"), b("attn_v"), c, self._inv_freq, self._amp, kv, layer)
+        sinks = self.w(p + "attn_sinks.weight") if self.has(p + "attn_sinks.weight") else None
+        att = attn_decode(qkv[:c.n_head * c.head_dim], kv, layer, sinks, c.sliding_window if layer % 2 == 0 else 0, c)
+        return x + self._biased_linear(p + "attn_output", att.reshape(1, -1))
+
+    def _head(self, x: torch.Tensor) -> torch.Tensor:
+        """Logits of the last hidden state: output_norm, then output.weight (or the tied embedding)."""
+        h = add_rms_norm(x.contiguous(), None, self.w("output_norm.weight"), self.cfg.rms_eps)
+        return self._linear("output.weight" if self.has("output.weight") else "token_embd.weight", h)
+
+    def _decode_one(self, ids: torch.Tensor, kv) -> torch.Tensor:
+        """One token (device int32 id) through every layer at kv.pos; kv.pos += 1 on the device."""
+        from .decode import advance
+        x = self.embed(ids).reshape(1, -1).contiguous()
+        for layer in range(self.cfg.n_layer):
+            x = self._attention_block(x, layer, kv)
+            x = self._ffn_block(x, layer)
+        logits = self._head(x)
+        advance(kv)
+        return logits
+
+    def forward(self, tokens, kv=None, start_pos: int = 0, last_only: bool = True) -> torch.Tensor:
+        """Logits (model/gpt_oss.py:207-228): (1, vocab), or (T, vocab) when not
+        last_only. Tokens go through one at a time at positions start_pos..;
+        kv is a DeviceKV whose length must be start_pos (a new one sized for
+        these tokens when None)."""
+        from .decode import DeviceKV
+        c = self.attn_config()
+        ids = torch.as_tensor(tokens, dtype=torch.int32).reshape(-1).to(self.device)
+        T = ids.numel()
+        if start_pos + T > c.context_length:
+            raise ValueError("prompt and continuation exceed model context length")
+        if kv is None:
+            kv = DeviceKV(self.cfg.n_layer, c, start_pos + T, self.device)
+            if start_pos:
+                kv.pos.fill_(start_pos)
+                kv.length = start_pos
+        if kv.length != start_pos:
+            raise ValueError(f"start_pos {start_pos} does not follow the cache's {kv.length} positions")
+        if start_pos + T > kv.ctx_max:
+            raise ValueError(f"{start_pos + T} positions exceed the cache's capacity of {kv.ctx_max}")
+        outs = [self._decode_one(ids[i:i + 1], kv) for i in range(T)]
+        return outs[-1] if last_only else torch.cat(outs)
+
+
+class GptOssDecodeGraph:
+    """One decode token of a GptOssModel -- embedding, every layer's attention
+    and fused MoE FFN, output norm, LM head and the position step -- captured
+    as one HIP graph over a DeviceKV, replayed once per token.
+
+    Needs every quantized dense tensor whole in HBM and every layer's experts
+    as t64 slabs (no host synchronisation inside a token)."""
+
+    def __init__(self, model: GptOssModel, kv) -> None:
+        from ..format.gguf import FLOAT_TYPES
+        from .decode import DeviceKV
+        self.model, self.kv = model, kv
+        c = model.attn_config()
+        for name, info in model.gguf.tensors.items():
+            if ".ffn_" in name and "_exps." in name:
+                continue
+            if info.dtype not in FLOAT_TYPES and model._resident_raw(name) is None:
+                raise ValueError(f"{name} is not resident in HBM: a decode graph reads every dense tensor in place")
+        for layer in range(model.cfg.n_layer):
+            if model._fused_layer(layer) is None:
+                raise ValueError(f"layer {layer}: experts are not all t64 slabs in HBM")
+        self.ids = torch.zeros(1, dtype=torch.int32, device=model.device)
+        # one eager token on a scratch cache runs every lazy setup step before capture
+        scratch = DeviceKV(model.cfg.n_layer, c, 1, model.device)
+        model._capturing = []
+        try:
+            model._decode_one(self.ids, scratch)
+            torch.cuda.synchronize(model.device)
+            model._capturing = []
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.logits = model._decode_one(self.ids, kv)
+            kv.length -= 1  # the capture did not run the step
+            self._routing = model._capturing
+        finally:
+            model._capturing = None
+        del scratch
+
+    def step(self, token: int, record: bool = True) -> torch.Tensor:
+        """Logits (1, vocab) of `token` at the cache's next position (the graph's own buffer)."""
+        if self.kv.length >= self.kv.ctx_max:
+            raise ValueError(f"the cache's {self.kv.ctx_max} positions are used up")
+        self.ids.fill_(int(token))
+        self.graph.replay()
+        self.kv.length += 1
+        if record:
+            for layer, ids in self._routing:
+                self.model.router_stats.record(layer, ids)
+        return self.logits

@@ -5,9 +5,26 @@ import numpy as np
 import torch
 
 
-def write_gptoss_gguf(path, cfg, n_layers: int, seed: int):
+# attention geometry of the tiny model: 8 query heads, 2 kv heads of 64, vocab 300
+ATTN = dict(n_head=8, n_head_kv=2, head_dim=64, vocab=300, rope_base=150000.0, context=4096, window=4,
+            rope_factor=32.0, original_context=4096, beta_fast=32.0, beta_slow=1.0)
+
+
+def _q8(rows, K, g):
+    from nurostream_amd import synth
+    from nurostream_amd.format.gguf import GGMLType
+    return synth.matrix_bytes(GGMLType.Q8_0, rows, K, g, "cpu", d_std=0.02)
+
+
+def write_gptoss_gguf(path, cfg, n_layers: int, seed: int, attention: bool = False):
     """Write n_layers MoE FFN blocks of `cfg` (synth.make_layer tensors) plus a
-    post-attention norm weight per layer; returns {layer: tensors} (CPU)."""
+    post-attention norm weight per layer; returns {layer: tensors} (CPU).
+
+    attention=True adds what a decode token needs around the FFN (the
+    reference's GPT-OSS tensor names): token_embd / output (Q8_0),
+    output_norm, and per layer attn_norm, attn_q/k/v/output (Q8_0) with
+    biases, attn_sinks, plus the attention and rope metadata (ATTN); those
+    tensors come back under layers["model"]."""
     from nurostream_amd import synth
     from nurostream_amd.format.gguf import GGMLType, GGUFWriter
     wr = GGUFWriter(path, "gpt-oss")
@@ -34,6 +51,41 @@ def write_gptoss_gguf(path, cfg, n_layers: int, seed: int):
                           t[kind + "_b"].numpy().astype(np.float32).tobytes())
         wr.add_tensor(p + "post_attention_norm.weight", (cfg.n_embd,), GGMLType.F32, t["norm"].numpy().tobytes())
         layers[li] = t
+    if attention:
+        a = ATTN
+        wr.add("gpt-oss.attention.head_count", a["n_head"])
+        wr.add("gpt-oss.attention.head_count_kv", a["n_head_kv"])
+        wr.add("gpt-oss.attention.key_length", a["head_dim"])
+        wr.add("gpt-oss.rope.freq_base", a["rope_base"])
+        wr.add("gpt-oss.context_length", a["context"])
+        wr.add("gpt-oss.attention.sliding_window", a["window"])
+        wr.add("gpt-oss.rope.scaling.factor", a["rope_factor"])
+        wr.add("gpt-oss.rope.scaling.original_context_length", a["original_context"])
+        wr.add("gpt-oss.rope.scaling.yarn_beta_fast", a["beta_fast"])
+        wr.add("gpt-oss.rope.scaling.yarn_beta_slow", a["beta_slow"])
+        g = torch.Generator().manual_seed(seed * 7 + 3)
+        nq, nkv = a["n_head"] * a["head_dim"], a["n_head_kv"] * a["head_dim"]
+        m = {"token_embd.weight": _q8(a["vocab"], cfg.n_embd, g), "output.weight": _q8(a["vocab"], cfg.n_embd, g),
+             "output_norm.weight": torch.rand(cfg.n_embd, generator=g) + 0.5}
+        for li in range(n_layers):
+            p = f"blk.{li}."
+            m[p + "attn_norm.weight"] = torch.rand(cfg.n_embd, generator=g) + 0.5
+            for nm, rows, K in (("attn_q", nq, cfg.n_embd), ("attn_k", nkv, cfg.n_embd), ("attn_v", nkv, cfg.n_embd),
+                                ("attn_output", cfg.n_embd, nq)):
+                m[p + nm + ".weight"] = _q8(rows, K, g)
+                m[p + nm + ".bias"] = torch.randn(rows, generator=g) * 0.1
+            m[p + "attn_sinks.weight"] = torch.randn(a["n_head"], generator=g)
+        for name, tnsr in m.items():
+            if tnsr.dtype == torch.uint8:
+                rows = a["vocab"] if name in ("token_embd.weight", "output.weight") else None
+                if rows is None:
+                    nm = name.split(".")[2]
+                    rows = {"attn_q": nq, "attn_k": nkv, "attn_v": nkv, "attn_output": cfg.n_embd}[nm]
+                K = len(tnsr) // rows // 34 * 32
+                wr.add_tensor(name, (rows, K), GGMLType.Q8_0, tnsr.numpy().tobytes())
+            else:
+                wr.add_tensor(name, tuple(tnsr.shape), GGMLType.F32, tnsr.float().numpy().tobytes())
+        layers["model"] = m
     wr.write()
     return layers
 

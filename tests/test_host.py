@@ -222,7 +222,9 @@ def test_parse_size_and_api_on_cpu(tmp_path):
     write_gptoss_gguf(path, cfg, n_layers=1, seed=1)
     ns = NeuroStream.load(path, device="cpu")
     assert (ns.cfg.n_layer, ns.cfg.n_embd, ns.cfg.n_expert, ns.cfg.n_expert_used, ns.cfg.n_ffn_expert) == (1, 64, 8, 2, 64)
-    with pytest.raises(NotImplementedError):
-        ns.generate([1, 2, 3])
+    with pytest.raises(NotImplementedError):  # no attention tensors in this GGUF
+        next(ns.generate([1, 2, 3]))
+    with pytest.raises(NotImplementedError):  # text prompts need the tokenizer
+        next(ns.generate("hello"))
     with pytest.raises(N.NativeError):
         ns.model._ffn_block(torch.randn(1, 64), 0)
