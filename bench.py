@@ -36,6 +36,11 @@ Other workloads (`--workload`, one JSON line each, for the design notes):
                 tensor of Q4_K_M files); two weight copies alternate
   lmhead-q8     the same over a GPT-OSS-120B-shaped Q8_0 LM head,
                 201088 x 2880
+  gptoss-token  a whole GPT-OSS-120B decode token as one HIP graph: token
+                embedding, 36 x (rms_norm, q/k/v, YaRN rotary + KV append,
+                sink attention, o-proj, MoE FFN), output norm, LM head, with
+                `--context` positions already in the KV cache (synthetic);
+                dense tensors Q8_0, experts MXFP4 t64 slabs, all in HBM
   disk-stream   expert weights from a GGUF file on the box's disk: one
                 GPT-OSS-120B-shaped layer's MXFP4 expert tensors (1.7 GB)
                 are written, then read into HBM in 512-row blocks by the
@@ -58,7 +63,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8", "stack-t1-host25",
-             "stack-t8-host25", "lmhead-q6k", "lmhead-q8", "disk-stream")
+             "stack-t8-host25", "lmhead-q6k", "lmhead-q8", "disk-stream", "gptoss-token")
 
 # per workload: (config name, T, steps, warmup, rotating layers or stack depth, profile steps)
 _DEFAULTS = {
@@ -73,6 +78,7 @@ _DEFAULTS = {
     "lmhead-q6k": ("Q6_K", 1, 200, 20, 2, 0),
     "lmhead-q8": ("Q8_0", 1, 200, 20, 2, 0),
     "disk-stream": ("GPTOSS_120B", 1, 12, 2, 1, 0),
+    "gptoss-token": ("GPTOSS_120B", 1, 200, 20, 36, 0),
 }
 # LM-head GEMV shapes: (rows = vocabulary, K = hidden, model)
 _LMHEAD = {"lmhead-q6k": (151936, 4096, "qwen3-235b-a22b"), "lmhead-q8": (201088, 2880, "gpt-oss-120b")}
@@ -93,6 +99,8 @@ def _parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--host-mode", choices=("read", "stage"), default="read",
                    help="config 5b: kernels read pinned host tiles over PCIe (read) or DMA-stage them per layer")
+    p.add_argument("--context", type=int, default=1024,
+                   help="gptoss-token: positions already in the KV cache when the timed tokens start")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after the run, copy a buffer of this size 3 times (calibrates rocprofv3 byte counters)")
     return p.parse_args()
@@ -651,6 +659,126 @@ def disk_workload(args, torch, N, synth, dev):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+class _ModelIndex:
+    """A GGUF-like index (tensors + metadata) for a model built in memory."""
+
+    def __init__(self, tensors, metadata):
+        self.tensors, self.metadata = tensors, metadata
+
+    def arch(self):
+        return "gpt-oss"
+
+    def cfg(self, suffix, default=None):
+        return self.metadata.get(f"gpt-oss.{suffix}", default)
+
+
+def token_workload(args, torch, N, synth, dev):
+    """One GPT-OSS-120B decode token (every layer's attention and MoE FFN, LM head) per graph replay."""
+    import math
+    from nurostream_amd.format.gguf import GGMLType, tensor_info
+    from nurostream_amd.io.arena import Arena
+    from nurostream_amd.io.source import HostSource
+    from nurostream_amd.model.decode import DeviceKV
+    from nurostream_amd.model.gpt_oss import GptOssDecodeGraph, GptOssFFNStack, GptOssModel, MoEModelConfig
+    from nurostream_amd.residency.cache import TieredCache
+    cfg = synth.GPTOSS_120B
+    K_steps = args.steps if args.steps is not None else _DEFAULTS["gptoss-token"][2]
+    W = args.warmup if args.warmup is not None else _DEFAULTS["gptoss-token"][3]
+    n_layers = args.layers if args.layers is not None else _DEFAULTS["gptoss-token"][4]
+    n_head, n_kv, hd, vocab, window = 64, 8, 64, 201088, 128
+    ctx0 = max(0, int(args.context))
+    meta = {"gpt-oss.embedding_length": cfg.n_embd, "gpt-oss.block_count": n_layers,
+            "gpt-oss.attention.head_count": n_head, "gpt-oss.attention.head_count_kv": n_kv,
+            "gpt-oss.attention.key_length": hd, "gpt-oss.rope.freq_base": 150000.0,
+            "gpt-oss.context_length": 131072, "gpt-oss.attention.sliding_window": window,
+            "gpt-oss.rope.scaling.factor": 32.0, "gpt-oss.rope.scaling.original_context_length": 4096,
+            "gpt-oss.rope.scaling.yarn_beta_fast": 32.0, "gpt-oss.rope.scaling.yarn_beta_slow": 1.0}
+    g = synth.generator(synth.layer_seed(args.seed, 999), dev)
+    infos, tensors = {}, {}
+
+    def add(name, shape, dtype, data):
+        infos[name] = tensor_info(name, shape, dtype)
+        tensors[name] = (infos[name], data.reshape(-1).view(torch.uint8))
+
+    def q8(rows, K):
+        return synth.matrix_bytes(GGMLType.Q8_0, rows, K, g, dev, d_std=0.02)
+
+    def f32(n, scale=0.1, base=0.0):
+        return (torch.randn(n, generator=g, device=dev) * scale + base).float()
+
+    add("token_embd.weight", (vocab, cfg.n_embd), GGMLType.Q8_0, q8(vocab, cfg.n_embd))
+    add("output.weight", (vocab, cfg.n_embd), GGMLType.Q8_0, q8(vocab, cfg.n_embd))
+    add("output_norm.weight", (cfg.n_embd,), GGMLType.F32, f32(cfg.n_embd, 0.05, 1.0))
+    for li in range(n_layers):
+        p = f"blk.{li}."
+        add(p + "attn_norm.weight", (cfg.n_embd,), GGMLType.F32, f32(cfg.n_embd, 0.05, 1.0))
+        add(p + "post_attention_norm.weight", (cfg.n_embd,), GGMLType.F32, f32(cfg.n_embd, 0.05, 1.0))
+        for nm, rows, K in (("attn_q", n_head * hd, cfg.n_embd), ("attn_k", n_kv * hd, cfg.n_embd),
+                            ("attn_v", n_kv * hd, cfg.n_embd), ("attn_output", cfg.n_embd, n_head * hd)):
+            add(p + nm + ".weight", (rows, K), GGMLType.Q8_0, q8(rows, K))
+            add(p + nm + ".bias", (rows,), GGMLType.F32, f32(rows))
+        add(p + "attn_sinks.weight", (n_head,), GGMLType.F32, f32(n_head, 1.0))
+    src = HostSource(tensors, Arena(1 << 30), device=dev, pin=False)
+    src.gguf = _ModelIndex(infos, meta)
+    cache = TieredCache(src, device=dev, vram_budget=1 << 40)
+    for name in infos:
+        assert cache.admit_vram(name), name
+    dense_bytes = sum(i.nbytes for i in infos.values())
+    mcfg = MoEModelConfig(n_layer=n_layers, n_embd=cfg.n_embd, n_expert=cfg.n_expert, n_expert_used=cfg.top_k,
+                          n_ffn_expert=cfg.n_ff, rms_eps=1e-5)
+    model = GptOssModel(cache, mcfg, dev)
+    stack = GptOssFFNStack.synthetic(cfg, n_layers, seed=args.seed, device=dev)
+    model._fused = dict(enumerate(stack.layers))
+    del tensors
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    acfg = model.attn_config()
+    kv = DeviceKV(n_layers, acfg, ctx0 + W + K_steps + 2, dev)
+    for t in (*kv.k, *kv.v):  # a synthetic history of ctx0 positions
+        t[:, :ctx0].normal_(0.0, 0.5, generator=g)
+    kv.pos.fill_(ctx0)
+    kv.length = ctx0
+    graph = GptOssDecodeGraph(model, kv)
+    toks = torch.randint(0, vocab, (W + K_steps,), generator=torch.Generator().manual_seed(args.seed)).tolist()
+    for i in range(W):
+        graph.step(toks[i], record=False)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    ev0.record()
+    for i in range(W, W + K_steps):
+        logits = graph.step(toks[i], record=False)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t_wall
+    ms = ev0.elapsed_time(ev1) / K_steps
+    if not bool(torch.isfinite(logits).all()):
+        raise RuntimeError("gptoss-token: non-finite logits")
+    # bytes a token must read: 4 experts per layer (+ router, biases), attention weights, the KV history
+    # (full-attention odd layers read every position, sliding even layers the last 128), the LM head
+    ctx_mid = ctx0 + W + K_steps // 2
+    full_layers, sliding_layers = n_layers // 2, n_layers - n_layers // 2
+    kv_bytes = (full_layers * (ctx_mid + 1) + sliding_layers * min(window, ctx_mid + 1)) * n_kv * hd * 4 * 2
+    attn_bytes = sum(i.nbytes for n, i in infos.items() if n.startswith("blk."))
+    token_bytes = n_layers * cfg.layer_bytes_per_token() + attn_bytes + infos["output.weight"].nbytes + kv_bytes
+    achieved = token_bytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "GPT-OSS-120B decode tok/s, whole token on the device as one graph (T=1)",
+        "value": round(1e3 / ms, 1), "unit": "tok/s", "n_gpus": 1, "steps": K_steps, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4 experts, q8_0 dense weights, fp32 activations and KV", "data": "synthetic",
+        "config": {"workload": f"gpt-oss-120b decode token, {n_layers} layers, {ctx0} positions in the KV cache",
+                   "n_layers": n_layers, "context": ctx0, "n_head": n_head, "n_kv": n_kv, "head_dim": hd,
+                   "vocab": vocab, "sliding_window": window, "dense_type": "Q8_0",
+                   "dense_bytes": dense_bytes, "kv_cache_bytes": kv.nbytes()},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "whole token",
+                     "algorithmic_bytes": int(token_bytes)},
+        "wall_s": round(wall_s, 4),
+        "cpu_baseline": None,
+    }
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -674,6 +802,8 @@ def main():
         result = gemv_workload(args, torch, N, synth, dev)
     elif args.workload == "disk-stream":
         result = disk_workload(args, torch, N, synth, dev)
+    elif args.workload == "gptoss-token":
+        result = token_workload(args, torch, N, synth, dev)
     else:
         result = layer_workload(args, torch, N, synth, dev)
     if args.copy_probe_mib > 0:  # a plain copy of known size for the counter calibration
