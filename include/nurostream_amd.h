@@ -80,6 +80,12 @@ int nsx_dequantize(int ggml_type, const void *raw, int64_t raw_bytes,
  * triton_kernels.py:97-143); here T <= 16. */
 int nsx_fused_gemv(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
                    const void *x, int x_dtype, int64_t T, float *y, void *stream);
+/* nsx_fused_gemv with the epilogue of model/gpt_oss.py:97-99,114
+ * (x + _biased_linear(...)): y[t, r] = resid[t, r] + (dot + bias[r]);
+ * bias (n_rows) and resid ((T, n_rows), may be y) are optional (NULL). */
+int nsx_fused_gemv_ex(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
+                      const void *x, int x_dtype, int64_t T, float *y, const float *bias,
+                      const float *resid, void *stream);
 
 /* 64-row interleaved tiles for VRAM-resident expert slabs. No reference
  * counterpart: residency/cache.py:369-389 admit_slab keeps the raw bytes;

@@ -117,8 +117,12 @@ def can_fuse(dtype, x: torch.Tensor) -> bool:
 
 def fused_gemv(raw, dtype, x: torch.Tensor, n_rows: int, K: int,
                out_dtype: torch.dtype = torch.float16, block_n: int = 16,
-               num_warps: int = 2) -> torch.Tensor:
-    """y = x @ dequant(raw).T without materialising the weights -> (T, n_rows)."""
+               num_warps: int = 2, bias: torch.Tensor | None = None,
+               resid: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ dequant(raw).T without materialising the weights -> (T, n_rows).
+
+    bias (n_rows) and resid (T, n_rows) fp32, both optional and raw rows only,
+    are added in the kernel's epilogue as resid + (y + bias)."""
     dtype = GGMLType(dtype)
     x2 = x.reshape(-1, K)
     T = x2.shape[0]
@@ -130,6 +134,8 @@ def fused_gemv(raw, dtype, x: torch.Tensor, n_rows: int, K: int,
     with torch.cuda.device(x2.device):
         s = N.stream_ptr(x2.device)
         if isinstance(raw, T64Rows):
+            if bias is not None or resid is not None:
+                raise NotImplementedError("bias / resid epilogue on t64 windows")
             if raw.hi - raw.lo != n_rows or raw.K != K:
                 raise ValueError(f"t64 window [{raw.lo}, {raw.hi}) x {raw.K} does not match {n_rows} x {K}")
             xf = x2.float().contiguous()
@@ -152,6 +158,12 @@ def fused_gemv(raw, dtype, x: torch.Tensor, n_rows: int, K: int,
             if not flat.is_contiguous():
                 flat = flat.contiguous()
             xc = x2 if x2.is_contiguous() else x2.contiguous()
-            N.check(lib.nsx_fused_gemv(int(dtype), flat.data_ptr(), n_rows, K, xc.data_ptr(),
-                                       N.act_dtype_code(xc.dtype), T, y.data_ptr(), s), "fused_gemv")
+            for name, t, n in (("bias", bias, n_rows), ("resid", resid, T * n_rows)):
+                if t is not None and (not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous()
+                                      or t.numel() != n):
+                    raise ValueError(f"{name} must be a contiguous fp32 device tensor of {n} elements")
+            N.check(lib.nsx_fused_gemv_ex(int(dtype), flat.data_ptr(), n_rows, K, xc.data_ptr(),
+                                          N.act_dtype_code(xc.dtype), T, y.data_ptr(),
+                                          None if bias is None else bias.data_ptr(),
+                                          None if resid is None else resid.data_ptr(), s), "fused_gemv")
     return y if out_dtype == torch.float32 else y.to(out_dtype)

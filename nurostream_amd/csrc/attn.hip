@@ -11,18 +11,21 @@
 // KV cache layout: K and V each [n_kv][ctx_max][head_dim] fp32.
 // Attention is split over chunks of ATTN_CHUNK keys (one workgroup per kv
 // head and chunk, each handling the kv head's n_rep query heads), and a
-// combine kernel merges the chunks in chunk order together with the sink.
+// combine kernel merges the chunks in chunk order together with the sink; a
+// layer whose keys always fit one chunk (a 128-key sliding window) finishes
+// in the chunk kernel.
 // Both grids are sized for ctx_max, so their shape does not depend on the
 // position; chunks past the current length return at once.
 #include "nsx_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <math.h>
 
 namespace {
 
 constexpr int ATTN_D = 64;        // head_dim (GPT-OSS)
-constexpr int ATTN_CHUNK = 256;   // keys per attention workgroup
+constexpr int ATTN_CHUNK = 128;   // keys per attention workgroup (two rounds of 64)
 constexpr int ATTN_THREADS = 256;
 constexpr int ATTN_MAX_REP = 16;  // query heads per kv head
 
@@ -80,16 +83,26 @@ __device__ __forceinline__ void attn_span(int p, int window, int& lo, int& total
   total = p + 1 - lo;
 }
 
-// Workgroup (kv head g, chunk c): scores of its n_rep query heads against
-// the chunk's keys, the chunk's softmax statistics, and the value sums.
+// Workgroup (kv head g, chunk c of ATTN_CHUNK keys): the chunk's attention
+// for the kv head's n_rep query heads. Wave w takes query heads w, w + 4,
+// ... (HPW = ceil(n_rep / 4) of them) and walks the chunk in rounds of 64
+// keys: the scores with one key per lane, a running softmax per head in
+// registers (wave max / sum), then the value sums with lane = (key group
+// kg = lane / 16, dimensions 4 * (lane % 16) ..+3) over keys kg, kg + 4, ...,
+// so a round's 64 value rows are 16 coalesced 16-byte loads per lane. The
+// four key groups are summed with two shuffles at the end.
 // part[(h * nchunk + c) * (D + 2)] = {m, l, acc[D]} for query head h.
+// FINAL (only ever one chunk: a sliding window or a cache of at most
+// ATTN_CHUNK keys): the workgroup also merges the sink and writes out[h].
+template <bool FINAL, int HPW>
 __global__ __launch_bounds__(ATTN_THREADS) void attn_chunk_kernel(
     const float* __restrict__ q, const float* __restrict__ k_cache, const float* __restrict__ v_cache,
     const int32_t* __restrict__ pos_ptr, int64_t ctx_max, int window, float scale, int n_rep, int nchunk,
-    float* __restrict__ part) {
+    float* __restrict__ part, const float* __restrict__ sinks, float* __restrict__ out) {
+  constexpr int NW = ATTN_THREADS / 64;
   __shared__ float qs[ATTN_MAX_REP][ATTN_D];
-  __shared__ float sc[ATTN_MAX_REP][ATTN_CHUNK];
-  __shared__ float ml[ATTN_MAX_REP][2];
+  // each wave's key weights, key j at (j % 4) * 16 + j / 4: key group kg reads its 16 as 4 vectors
+  __shared__ float wl[NW][HPW][64];
   const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
   const int p = *pos_ptr;
   if (p < 0 || p >= ctx_max) return;
@@ -101,61 +114,98 @@ __global__ __launch_bounds__(ATTN_THREADS) void attn_chunk_kernel(
   for (int i = t; i < n_rep * ATTN_D; i += ATTN_THREADS)
     qs[i / ATTN_D][i % ATTN_D] = q[((int64_t)g * n_rep + i / ATTN_D) * ATTN_D + i % ATTN_D];
   __syncthreads();
-  // scores: one key per thread, all of its query heads
-  {
-    float acc[ATTN_MAX_REP];
+  const int wave = t >> 6, lane = t & 63, kg = lane >> 4, dq = lane & 15;
+  const float* kb = k_cache + ((int64_t)g * ctx_max + lo + k0) * ATTN_D;
+  const float* vb = v_cache + ((int64_t)g * ctx_max + lo + k0) * ATTN_D + 4 * dq;
+  float m[HPW], l[HPW];
+  v4f acc[HPW];
 #pragma unroll
-    for (int h = 0; h < ATTN_MAX_REP; ++h) acc[h] = 0.f;
-    if (t < nk) {
-      const v4f* kr = (const v4f*)(k_cache + ((int64_t)g * ctx_max + lo + k0 + t) * ATTN_D);
-#pragma unroll 4
-      for (int d4 = 0; d4 < ATTN_D / 4; ++d4) {
-        const v4f kv = kr[d4];
+  for (int i = 0; i < HPW; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+    acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int r0 = 0; r0 < nk; r0 += 64) {
+    const int n = min(64, nk - r0);
+    const bool valid = lane < n;
+    // All of the round's loads go out together; rows past the round's keys
+    // are clamped to its last key and get weight 0.
+    const v4f* kr = (const v4f*)(kb + (int64_t)(r0 + (valid ? lane : n - 1)) * ATTN_D);
+    v4f kv[ATTN_D / 4];
 #pragma unroll
-        for (int h = 0; h < ATTN_MAX_REP; ++h) {
-          if (h < n_rep) {
-            const v4f qv = *(const v4f*)&qs[h][4 * d4];
-            float a = acc[h];
-            a = fmaf(qv.x, kv.x, a); a = fmaf(qv.y, kv.y, a); a = fmaf(qv.z, kv.z, a); a = fmaf(qv.w, kv.w, a);
-            acc[h] = a;
-          }
+    for (int d4 = 0; d4 < ATTN_D / 4; ++d4) kv[d4] = kr[d4];
+    v4f vd[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) vd[u] = *(const v4f*)(vb + (int64_t)(r0 + min(kg + 4 * u, n - 1)) * ATTN_D);
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const int h = wave + i * NW;
+      float e = 0.f, corr = 1.f;
+      if (h < n_rep) {
+        float a = 0.f;
+#pragma unroll
+        for (int d4 = 0; d4 < ATTN_D / 4; ++d4) {
+          const v4f qv = *(const v4f*)&qs[h][4 * d4];
+          a = fmaf(qv.x, kv[d4].x, a); a = fmaf(qv.y, kv[d4].y, a);
+          a = fmaf(qv.z, kv[d4].z, a); a = fmaf(qv.w, kv[d4].w, a);
         }
+        const float sc = valid ? a * scale : -INFINITY;
+        const float mn = fmaxf(m[i], wave_max(sc));  // finite: lane 0 holds a key
+        e = valid ? expf(sc - mn) : 0.f;
+        corr = expf(m[i] - mn);  // 0 on the first round (m = -inf)
+        l[i] = fmaf(l[i], corr, wave_sum(e));
+        m[i] = mn;
+      }
+      acc[i] *= corr;
+      wl[wave][i][(lane & 3) * 16 + (lane >> 2)] = e;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4) {
+        const v4f e = *(const v4f*)&wl[wave][i][kg * 16 + 4 * u4];  // keys kg + 4 * (4 * u4 + 0..3)
+        acc[i] += e.x * vd[4 * u4];
+        acc[i] += e.y * vd[4 * u4 + 1];
+        acc[i] += e.z * vd[4 * u4 + 2];
+        acc[i] += e.w * vd[4 * u4 + 3];
       }
     }
-    for (int h = 0; h < n_rep; ++h) sc[h][t] = t < nk ? acc[h] * scale : -INFINITY;
+    __builtin_amdgcn_wave_barrier();  // reads done before the next round's writes
   }
-  __syncthreads();
-  // softmax statistics of the chunk: wave w takes heads w, w + 4, ...
-  const int wave = t >> 6, lane = t & 63;
-  for (int h = wave; h < n_rep; h += ATTN_THREADS / 64) {
-    float m = -INFINITY;
-    for (int j = lane; j < ATTN_CHUNK; j += 64) m = fmaxf(m, sc[h][j]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int j = lane; j < ATTN_CHUNK; j += 64) {
-      const float e = j < nk ? expf(sc[h][j] - m) : 0.f;
-      sc[h][j] = e;
-      l += e;
+#pragma unroll
+  for (int i = 0; i < HPW; ++i) {
+    const int h = wave + i * NW;
+    if (h >= n_rep) continue;
+    v4f a = acc[i];
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {
+      a.x += __shfl_xor(a.x, o, 64);
+      a.y += __shfl_xor(a.y, o, 64);
+      a.z += __shfl_xor(a.z, o, 64);
+      a.w += __shfl_xor(a.w, o, 64);
     }
-    l = wave_sum(l);
-    if (lane == 0) {
-      ml[h][0] = m;
-      ml[h][1] = l;
+    if (kg != 0) continue;
+    const int hq = g * n_rep + h;
+    if constexpr (FINAL) {  // the combine kernel's arithmetic for a single chunk
+      const float sink = sinks ? sinks[hq] : -INFINITY;
+      const float M = fmaxf(sink, m[i]);
+      const float w = expf(m[i] - M);
+      const float Z = fmaf(w, l[i], sinks ? expf(sink - M) : 0.f);
+      *(v4f*)(out + (int64_t)hq * ATTN_D + 4 * dq) =
+          v4f{(w * a.x) / Z, (w * a.y) / Z, (w * a.z) / Z, (w * a.w) / Z};
+    } else {
+      float* o = part + ((int64_t)hq * nchunk + c) * (ATTN_D + 2);
+      if (dq == 0) {
+        o[0] = m[i];
+        o[1] = l[i];
+      }
+      float* od = o + 2 + 4 * dq;  // 8-byte aligned only: scalar stores
+      od[0] = a.x;
+      od[1] = a.y;
+      od[2] = a.z;
+      od[3] = a.w;
     }
-  }
-  __syncthreads();
-  // value sums: thread (head slot, d), keys in order
-  const int d = t & (ATTN_D - 1);
-  for (int h = t / ATTN_D; h < n_rep; h += ATTN_THREADS / ATTN_D) {
-    float a = 0.f;
-    const float* vr = v_cache + ((int64_t)g * ctx_max + lo + k0) * ATTN_D + d;
-    for (int j = 0; j < nk; ++j) a = fmaf(sc[h][j], vr[(int64_t)j * ATTN_D], a);
-    float* o = part + ((int64_t)(g * n_rep + h) * nchunk + c) * (ATTN_D + 2);
-    if (d == 0) {
-      o[0] = ml[h][0];
-      o[1] = ml[h][1];
-    }
-    o[2 + d] = a;
   }
 }
 
@@ -224,12 +274,33 @@ extern "C" int nsx_attn_decode(const float* q, const float* k_cache, const float
   NSX_REQUIRE(ctx_max > 0 && ctx_max < (1ll << 31) && window >= 0, NSX_EINVAL, "ctx_max=%lld window=%d",
               (long long)ctx_max, window);
   NSX_REQUIRE(q && k_cache && v_cache && pos && workspace && out, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE(((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) % 16 == 0, NSX_EINVAL,
+              "q, the caches and out must be 16-byte aligned");
   const int nchunk = (int)nsx_cdiv(ctx_max, ATTN_CHUNK);
   // a sliding window bounds the keys: only its chunks can be live
   const int live = window > 0 ? (int)std::min<int64_t>(nchunk, nsx_cdiv(window, ATTN_CHUNK)) : nchunk;
   const int n_rep = n_head / n_kv;
-  hipLaunchKernelGGL(attn_chunk_kernel, dim3(n_kv, live), dim3(ATTN_THREADS), 0, S(stream), q, k_cache, v_cache,
-                     pos, ctx_max, window, scale, n_rep, nchunk, (float*)workspace);
+  const int hpw = (n_rep + ATTN_THREADS / 64 - 1) / (ATTN_THREADS / 64);
+  auto chunks = [&](auto final_tag, auto hpw_tag) {
+    constexpr bool F = decltype(final_tag)::value;
+    hipLaunchKernelGGL((attn_chunk_kernel<F, decltype(hpw_tag)::value>), dim3(n_kv, F ? 1 : live),
+                       dim3(ATTN_THREADS), 0, S(stream), q, k_cache, v_cache, pos, ctx_max, window, scale, n_rep,
+                       nchunk, (float*)workspace, sinks, out);
+  };
+  auto by_hpw = [&](auto final_tag) {
+    switch (hpw) {
+      case 1: chunks(final_tag, std::integral_constant<int, 1>{}); break;
+      case 2: chunks(final_tag, std::integral_constant<int, 2>{}); break;
+      case 3: chunks(final_tag, std::integral_constant<int, 3>{}); break;
+      default: chunks(final_tag, std::integral_constant<int, 4>{}); break;
+    }
+  };
+  if (live == 1) {  // one chunk at any position: no partials, no combine launch
+    by_hpw(std::true_type{});
+    NSX_LAUNCHED();
+    return NSX_OK;
+  }
+  by_hpw(std::false_type{});
   NSX_LAUNCHED();
   hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head), dim3(64), 0, S(stream), (const float*)workspace, sinks, pos,
                      ctx_max, window, nchunk, out);

@@ -1865,16 +1865,25 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(const float* 
   const int64_t row = blockIdx.x;
   const float* xr = x + row * n;
   const float* rr = r ? r + row * n : nullptr;
-  float v[NORM_MAXV];
+  // Every load is issued unconditionally (addresses clamped into the row,
+  // tails zeroed at use), so all of them are in flight together: predicated
+  // loads would each wait behind the last.
+  float v[NORM_MAXV], wv[NORM_MAXV];
+#pragma unroll
+  for (int i = 0; i < NORM_MAXV; ++i) {
+    const int c = min((int)threadIdx.x + i * NORM_THREADS, n - 1);
+    v[i] = xr[c];
+    wv[i] = w ? w[c] : 1.f;
+  }
+  if (rr) {
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) v[i] += rr[min((int)threadIdx.x + i * NORM_THREADS, n - 1)];
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NORM_MAXV; ++i) {
-    const int c = threadIdx.x + i * NORM_THREADS;
-    v[i] = 0.f;
-    if (c < n) {
-      v[i] = rr ? xr[c] + rr[c] : xr[c];
-      ss = fmaf(v[i], v[i], ss);
-    }
+    if ((int)threadIdx.x + i * NORM_THREADS >= n) v[i] = 0.f;
+    ss = fmaf(v[i], v[i], ss);
   }
   ss = nsx_wave_sum(ss);
   if (__lane_id() == 0) part[threadIdx.x >> 6] = ss;
@@ -1888,7 +1897,7 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(const float* 
     const int c = threadIdx.x + i * NORM_THREADS;
     if (c < n) {
       if (sum) sum[row * n + c] = v[i];
-      if (y) y[row * n + c] = w ? (v[i] * inv) * w[c] : v[i] * inv;
+      if (y) y[row * n + c] = w ? (v[i] * inv) * wv[i] : v[i] * inv;
     }
   }
 }

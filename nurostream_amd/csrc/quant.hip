@@ -357,7 +357,8 @@ struct RawXSumReg {
 template <int FMT, int NT, bool XREG>
 __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
     const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int n_rows, int K,
-    const void* __restrict__ x, int x_dtype, int T, float* __restrict__ y, int64_t ystride) {
+    const void* __restrict__ x, int x_dtype, int T, float* __restrict__ y, int64_t ystride,
+    const float* __restrict__ bias, const float* resid) {  // resid may be y (read, then written, per element)
   using C = GvChunk<FMT>;
   constexpr int BE = RawBlock<FMT>::BE, BB = RawBlock<FMT>::BB;
   extern __shared__ __align__(16) uint8_t gv_smem[];
@@ -476,8 +477,13 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
       const int r = item_row(k);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const float v = nsx_wave_sum(acc[t]);
-        if (lane == 0 && t < T) y[(int64_t)t * ystride + r] = v;
+        float v = nsx_wave_sum(acc[t]);
+        if (lane == 0 && t < T) {
+          // epilogue in the reference's order: resid + (x @ W.T + bias)
+          if (bias) v += bias[r];
+          if (resid) v = resid[(int64_t)t * ystride + r] + v;
+          y[(int64_t)t * ystride + r] = v;
+        }
         acc[t] = 0.f;
       }
     }
@@ -520,7 +526,7 @@ static int resident_workgroups(const void* kernel, size_t lds) {
 
 template <int FMT, int NT>
 static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const void* x, int xdt,
-                           int64_t T, float* y, hipStream_t st) {
+                           int64_t T, float* y, const float* bias, const float* resid, hipStream_t st) {
   const int64_t row_bytes = raw_row_bytes<FMT>((int)K);
   const int64_t rows_per_launch = std::max<int64_t>(1, ((int64_t)1 << 31) / row_bytes);
   constexpr bool XR = NT == 1;  // the register path exists for one token only
@@ -536,12 +542,14 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
     const uint32_t head = (uint32_t)((uintptr_t)p - a);
     const uint32_t range = head + (uint32_t)(nr * row_bytes);
     const unsigned grid = (unsigned)std::min<int64_t>(nsx_cdiv(nr, GV_WAVES), resident);
+    const float* b = bias ? bias + r0 : nullptr;
+    const float* rr = resid ? resid + r0 : nullptr;
     if (xreg)
       hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, XR>), dim3(grid), dim3(GV_THREADS), lds, st,
-                         (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows);
+                         (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows, b, rr);
     else
       hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, false>), dim3(grid), dim3(GV_THREADS), lds, st,
-                         (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows);
+                         (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows, b, rr);
     NSX_LAUNCHED();
   }
   return NSX_OK;
@@ -549,18 +557,28 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
 
 template <int FMT>
 static int gemv_raw_fmt(const void* raw, int64_t n_rows, int64_t K, const void* x, int xdt, int64_t T,
-                        float* y, hipStream_t st) {
-  if (T == 1) return launch_gemv_raw<FMT, 1>(raw, n_rows, K, x, xdt, T, y, st);
-  if (T == 2) return launch_gemv_raw<FMT, 2>(raw, n_rows, K, x, xdt, T, y, st);
-  if (T <= 4) return launch_gemv_raw<FMT, 4>(raw, n_rows, K, x, xdt, T, y, st);
-  if (T <= 8) return launch_gemv_raw<FMT, 8>(raw, n_rows, K, x, xdt, T, y, st);
-  return launch_gemv_raw<FMT, 16>(raw, n_rows, K, x, xdt, T, y, st);
+                        float* y, const float* bias, const float* resid, hipStream_t st) {
+  if (T == 1) return launch_gemv_raw<FMT, 1>(raw, n_rows, K, x, xdt, T, y, bias, resid, st);
+  if (T == 2) return launch_gemv_raw<FMT, 2>(raw, n_rows, K, x, xdt, T, y, bias, resid, st);
+  if (T <= 4) return launch_gemv_raw<FMT, 4>(raw, n_rows, K, x, xdt, T, y, bias, resid, st);
+  if (T <= 8) return launch_gemv_raw<FMT, 8>(raw, n_rows, K, x, xdt, T, y, bias, resid, st);
+  return launch_gemv_raw<FMT, 16>(raw, n_rows, K, x, xdt, T, y, bias, resid, st);
 }
 
 static inline int64_t pad_tokens(int64_t T) { return T == 1 ? 1 : T == 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16; }
 
+extern "C" int nsx_fused_gemv_ex(int t, const void* raw, int64_t n_rows, int64_t K, const void* x,
+                                 int x_dtype, int64_t T, float* y, const float* bias, const float* resid,
+                                 void* stream);
+
 extern "C" int nsx_fused_gemv(int t, const void* raw, int64_t n_rows, int64_t K, const void* x,
                               int x_dtype, int64_t T, float* y, void* stream) {
+  return nsx_fused_gemv_ex(t, raw, n_rows, K, x, x_dtype, T, y, nullptr, nullptr, stream);
+}
+
+extern "C" int nsx_fused_gemv_ex(int t, const void* raw, int64_t n_rows, int64_t K, const void* x,
+                                 int x_dtype, int64_t T, float* y, const float* bias, const float* resid,
+                                 void* stream) {
   const int BE = nsx_block_elems(t), BB = nsx_block_bytes(t);
   NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no fused kernel for ggml type %d", t);
   NSX_REQUIRE(n_rows >= 0 && K > 0 && K % BE == 0, NSX_EINVAL,
@@ -583,13 +601,14 @@ extern "C" int nsx_fused_gemv(int t, const void* raw, int64_t n_rows, int64_t K,
     const int64_t nt = std::min(chunk, T - t0);
     const void* xc = (const char*)x + t0 * K * xsz;
     float* yc = y + t0 * n_rows;
+    const float* rc_ = resid ? resid + t0 * n_rows : nullptr;
     int rc = NSX_ENOTIMPL;
     switch (t) {
-      case NSX_MXFP4: rc = gemv_raw_fmt<NSX_MXFP4>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
-      case NSX_Q4_0: rc = gemv_raw_fmt<NSX_Q4_0>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
-      case NSX_Q8_0: rc = gemv_raw_fmt<NSX_Q8_0>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
-      case NSX_Q4_K: rc = gemv_raw_fmt<NSX_Q4_K>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
-      case NSX_Q6_K: rc = gemv_raw_fmt<NSX_Q6_K>(raw, n_rows, K, xc, x_dtype, nt, yc, st); break;
+      case NSX_MXFP4: rc = gemv_raw_fmt<NSX_MXFP4>(raw, n_rows, K, xc, x_dtype, nt, yc, bias, rc_, st); break;
+      case NSX_Q4_0: rc = gemv_raw_fmt<NSX_Q4_0>(raw, n_rows, K, xc, x_dtype, nt, yc, bias, rc_, st); break;
+      case NSX_Q8_0: rc = gemv_raw_fmt<NSX_Q8_0>(raw, n_rows, K, xc, x_dtype, nt, yc, bias, rc_, st); break;
+      case NSX_Q4_K: rc = gemv_raw_fmt<NSX_Q4_K>(raw, n_rows, K, xc, x_dtype, nt, yc, bias, rc_, st); break;
+      case NSX_Q6_K: rc = gemv_raw_fmt<NSX_Q6_K>(raw, n_rows, K, xc, x_dtype, nt, yc, bias, rc_, st); break;
     }
     if (rc) return rc;
   }

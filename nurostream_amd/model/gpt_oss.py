@@ -444,6 +444,7 @@ class GptOssModel:
         self._fused: dict[int, MoELayer] = {}
         self._acfg = None
         self._capturing: list | None = None
+        self._qkv: dict[int, tuple | None] = {}
 
     def w(self, name: str) -> torch.Tensor:
         t = self._w.get(name)
@@ -592,36 +593,85 @@ class GptOssModel:
         return torch.stack([self.cache.fetch_rows(name, t, t + 1, device=self.device, dtype=torch.float32)[0]
                             for t in ids.tolist()])
 
-    def _attention_block(self, x: torch.Tensor, layer: int, kv) -> torch.Tensor:
-        """x + o_proj(sink_attention(...)) for the one token at kv.pos (gpt_oss.py:101-114):
-        rms_norm, q/k/v projections, then bias + rotary + cache append and the
-        sink attention (sliding window on even layers) as kernels."""
+    def _qkv_raw(self, layer: int):
+        """(raw bytes, dtype, rows) of the layer's q, k and v weights concatenated
+        once in HBM -- one GEMV then writes the q | k | v block -- or None when
+        they are not all resident quantized rows of one type."""
+        from ..format.gguf import row_geometry
+        if layer in self._qkv:
+            return self._qkv[layer]
+        p = f"blk.{layer}."
+        names = [p + n + ".weight" for n in ("attn_q", "attn_k", "attn_v")]
+        hits = [self._resident_raw(n) for n in names]
+        got = None
+        if all(h is not None for h in hits) and len({h[1] for h in hits}) == 1:
+            rows = sum(row_geometry(self.gguf.tensors[n])[0] for n in names)
+            got = (torch.cat([h[0].reshape(-1) for h in hits]), hits[0][1], rows)
+        self._qkv[layer] = got
+        return got
+
+    def _attention_block(self, x: torch.Tensor, layer: int, kv, pending: torch.Tensor | None = None) -> torch.Tensor:
+        """x + o_proj(sink_attention(...)) for the one token at kv.pos (gpt_oss.py:101-114).
+
+        `pending` (the previous FFN output) is added to x first, inside the
+        attention norm's kernel (x is updated in place). Then one GEMV for q|k|v,
+        one kernel for bias + rotary + cache append, the sink attention
+        (sliding window on even layers), and one GEMV for the output projection
+        with its bias and the residual."""
+        from ..compute.kernels import can_fuse, fused_gemv
+        from ..format.gguf import row_geometry
         from .decode import attn_decode, rope_kv_append
         c, p = self.attn_config(), f"blk.{layer}."
-        h = add_rms_norm(x, None, self.w(p + "attn_norm.weight"), self.cfg.rms_eps)
-        q = self._linear(p + "attn_q.weight", h)
-        k = self._linear(p + "attn_k.weight", h)
-        v = self._linear(p + "attn_v.weight", h)
-        qkv = torch.cat([q.reshape(-1), k.reshape(-1), v.reshape(-1)])
+        h = add_rms_norm(x, pending, self.w(p + "attn_norm.weight"), self.cfg.rms_eps,
+                         sum_out=x if pending is not None else None)
+        cat = self._qkv_raw(layer)
+        if cat is not None and can_fuse(cat[1], h):
+            qkv = fused_gemv(cat[0], cat[1], h, cat[2], h.shape[-1], out_dtype=torch.float32).reshape(-1)
+        else:
+            qkv = torch.cat([self._linear(p + n + ".weight", h).reshape(-1) for n in ("attn_q", "attn_k", "attn_v")])
         b = lambda n: self.w(p + n + ".bias") if self.has(p + n + ".bias") else None  # noqa: E731
         rope_kv_append(qkv, b("attn_q"), b("attn_k"), b("attn_v"), c, self._inv_freq, self._amp, kv, layer)
         sinks = self.w(p + "attn_sinks.weight") if self.has(p + "attn_sinks.weight") else None
-        att = attn_decode(qkv[:c.n_head * c.head_dim], kv, layer, sinks, c.sliding_window if layer % 2 == 0 else 0, c)
-        return x + self._biased_linear(p + "attn_output", att.reshape(1, -1))
+        att = attn_decode(qkv[:c.n_head * c.head_dim], kv, layer, sinks, c.sliding_window if layer % 2 == 0 else 0,
+                          c).reshape(1, -1)
+        o_name = p + "attn_output.weight"
+        hit = self._resident_raw(o_name)
+        if hit is not None and can_fuse(hit[1], att):
+            n_rows, K, _ = row_geometry(self.gguf.tensors[o_name])
+            return fused_gemv(hit[0], hit[1], att, n_rows, K, out_dtype=torch.float32, bias=b("attn_output"),
+                              resid=x)
+        return x + self._biased_linear(p + "attn_output", att)
 
-    def _head(self, x: torch.Tensor) -> torch.Tensor:
-        """Logits of the last hidden state: output_norm, then output.weight (or the tied embedding)."""
-        h = add_rms_norm(x.contiguous(), None, self.w("output_norm.weight"), self.cfg.rms_eps)
+    def _ffn_pending(self, x: torch.Tensor, layer: int):
+        """(x, moe output) for a fused layer -- the residual add is left to the
+        next norm kernel -- or (x + ffn(x), None) on the streamed path."""
+        fused = self._fused_layer(layer)
+        if fused is None:
+            return self._ffn_block(x, layer), None
+        p = f"blk.{layer}."
+        norm = p + "post_attention_norm.weight"
+        h = add_rms_norm(x, None, self.w(norm) if self.has(norm) else None, self.cfg.rms_eps)
+        out, ids, _ = fused.forward(h)
+        if self._capturing is not None:  # no host copy inside a graph capture: recorded after each replay
+            self._capturing.append((layer, ids))
+        else:
+            self.router_stats.record(layer, ids)
+        return x, out
+
+    def _head(self, x: torch.Tensor, pending: torch.Tensor | None = None) -> torch.Tensor:
+        """Logits of the last hidden state (+ pending): output_norm, then output.weight (or the tied embedding)."""
+        h = add_rms_norm(x.contiguous(), pending, self.w("output_norm.weight"), self.cfg.rms_eps)
         return self._linear("output.weight" if self.has("output.weight") else "token_embd.weight", h)
 
     def _decode_one(self, ids: torch.Tensor, kv) -> torch.Tensor:
         """One token (device int32 id) through every layer at kv.pos; kv.pos += 1 on the device."""
         from .decode import advance
         x = self.embed(ids).reshape(1, -1).contiguous()
+        pending = None
         for layer in range(self.cfg.n_layer):
-            x = self._attention_block(x, layer, kv)
-            x = self._ffn_block(x, layer)
-        logits = self._head(x)
+            x = self._attention_block(x, layer, kv, pending)
+            x, pending = self._ffn_pending(x, layer)
+        logits = self._head(x, pending)
         advance(kv)
         return logits
 

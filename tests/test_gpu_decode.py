@@ -23,11 +23,13 @@ def _cfg(n_head=16, n_kv=2, window=128, ctx=4096):
 
 
 @pytest.mark.parametrize("window", [0, 128])
-def test_attention_kernels_match_oracle(dev, window):
-    """300 decode steps (past the 256-key chunk): bias + YaRN rotary + append, then sink attention
-    (16 query heads on 2 kv heads) against the oracle with the caches built the reference's way."""
+@pytest.mark.parametrize("heads", [(16, 2), (4, 4), (6, 2), (32, 2)], ids=["rep8", "rep1", "rep3", "rep16"])
+def test_attention_kernels_match_oracle(dev, window, heads):
+    """300 decode steps (past two 128-key chunks, each two 64-key rounds): bias + YaRN rotary +
+    append, then sink attention against the oracle with the caches built the reference's way;
+    1, 3, 8 and 16 query heads per kv head (one to four heads per wave)."""
     from nurostream_amd.model.decode import DeviceKV, advance, attn_decode, rope_kv_append, yarn_inv_freq
-    c = _cfg()
+    c = _cfg(n_head=heads[0], n_kv=heads[1])
     L = 300
     rng = np.random.default_rng(5)
     kv = DeviceKV(1, c, L, dev)
@@ -43,7 +45,7 @@ def test_attention_kernels_match_oracle(dev, window):
     sinks = torch.from_numpy(rng.standard_normal(c.n_head).astype(np.float32)).to(dev)
     Kref = np.zeros((c.n_head_kv, 0, 64))
     Vref = np.zeros((c.n_head_kv, 0, 64))
-    checks = {0, 1, 2, 127, 128, 129, 255, 256, 257, L - 1}
+    checks = {0, 1, 2, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 257, L - 1}
     worst = 0.0
     for p in range(L):
         rows = rng.standard_normal((c.n_head + 2 * c.n_head_kv, 64)).astype(np.float32)
@@ -54,8 +56,9 @@ def test_attention_kernels_match_oracle(dev, window):
         cos, sin = OA.yarn_tables(64, c.rope_base, c.rope_factor, c.original_context, c.beta_fast, c.beta_slow, [p])
         x = rows.astype(np.float64)
         q = OA.apply_rope((x[:c.n_head] + bq.cpu().numpy().reshape(c.n_head, 64))[:, None], cos, sin)
-        k = OA.apply_rope((x[c.n_head:c.n_head + 2] + bk.cpu().numpy().reshape(2, 64))[:, None], cos, sin)
-        v = (x[c.n_head + 2:] + bv.cpu().numpy().reshape(2, 64))[:, None]
+        nkv = c.n_head_kv
+        k = OA.apply_rope((x[c.n_head:c.n_head + nkv] + bk.cpu().numpy().reshape(nkv, 64))[:, None], cos, sin)
+        v = (x[c.n_head + nkv:] + bv.cpu().numpy().reshape(nkv, 64))[:, None]
         Kref = np.concatenate([Kref, k], axis=1)
         Vref = np.concatenate([Vref, v], axis=1)
         if p in checks:

@@ -134,6 +134,28 @@ def test_fused_gemv_q6k_any_alignment(dev, offset):
     assert torch.equal(y0, y1)
 
 
+@pytest.mark.parametrize("fmt,T", [("Q8_0", 1), ("Q6_K", 1), ("MXFP4", 3), ("Q4_K", 2)])
+def test_fused_gemv_bias_residual_epilogue(dev, fmt, T):
+    """nsx_fused_gemv_ex: resid + (x @ W.T + bias), also with resid being the output itself."""
+    from nurostream_amd.compute.kernels import fused_gemv
+    rows, K = 300, 1024
+    t = getattr(OQ, fmt)
+    raw = _gemv_case(fmt, rows, K, seed=9)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    b = rng.standard_normal(rows).astype(np.float32)
+    r = rng.standard_normal((T, rows)).astype(np.float32)
+    raw_t, xt = torch.from_numpy(raw).to(dev), torch.from_numpy(x).to(dev)
+    bt, rt = torch.from_numpy(b).to(dev), torch.from_numpy(r).to(dev)
+    ref = r + (OQ.gemv(raw, t, x, rows, K, f64=True) + b)
+    y = fused_gemv(raw_t, t, xt, rows, K, out_dtype=torch.float32, bias=bt, resid=rt)
+    assert rel_max(to_np(y), ref) < GEMV_TIGHT
+    plain = fused_gemv(raw_t, t, xt, rows, K, out_dtype=torch.float32)
+    torch.testing.assert_close(y, rt + (plain + bt), rtol=0, atol=0)  # the same fp32 operations
+    with pytest.raises(ValueError):
+        fused_gemv(raw_t, t, xt, rows, K, out_dtype=torch.float32, bias=bt[:-1])
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_fused_gemv_half_activations(dev, xdt):
     from nurostream_amd.compute.kernels import fused_gemv
