@@ -251,6 +251,17 @@ int64_t nsx_attn_workspace_bytes(int n_head, int head_dim, int64_t ctx_max);
 int nsx_attn_decode(const float *q, const float *k_cache, const float *v_cache, const float *sinks, int n_head,
                     int n_kv, int head_dim, const int32_t *pos, int64_t ctx_max, int window, float scale,
                     void *workspace, float *out, void *stream);
+/* nsx_rope_kv_append followed by nsx_attn_decode in one launch (two with the
+ * chunk combine): qkv is the token's raw [n_head + 2 n_kv][head_dim] block
+ * (the QKV projection without its bias), left unchanged; the token's k (with
+ * bias and rotary) and v (with bias) rows are appended to the caches at pos,
+ * and out is the attention of the rotated q. Results are bit-identical to the
+ * two calls. Replaces the same reference lines: model/gpt_oss.py:42-58,
+ * 73-85, 101-114. */
+int nsx_attn_decode_qkv(const float *qkv, const float *q_bias, const float *k_bias, const float *v_bias,
+                        const float *inv_freq, float amplitude, const float *sinks, int n_head, int n_kv,
+                        int head_dim, const int32_t *pos, float *k_cache, float *v_cache, int64_t ctx_max,
+                        int window, float scale, void *workspace, float *out, void *stream);
 /* *pos += n on the stream (one thread). */
 int nsx_pos_advance(int32_t *pos, int32_t n, void *stream);
 

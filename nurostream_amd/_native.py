@@ -78,6 +78,8 @@ _SIGS = {
     "nsx_rope_kv_append": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, C.c_float, _p, _p, _p, _i64, _p]),
     "nsx_attn_workspace_bytes": (_i64, [_i, _i, _i64]),
     "nsx_attn_decode": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _i64, _i, C.c_float, _p, _p, _p]),
+    "nsx_attn_decode_qkv": (_i, [_p, _p, _p, _p, _p, C.c_float, _p, _i, _i, _i, _p, _p, _p, _i64, _i, C.c_float,
+                                 _p, _p, _p]),
     "nsx_pos_advance": (_i, [_p, C.c_int32, _p]),
     "nsx_reader_open": (_i, [C.c_char_p, _i, _i, _i, _i64, _i, _p, C.POINTER(_p)]),
     "nsx_reader_submit": (_i, [_p, _i64, _i64, _p, _i, _p, C.POINTER(C.c_uint64)]),

@@ -40,6 +40,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Rotary of element d of a 64-element head row at position p: x = the
+// element, partner = element d ^ 32 (both with bias), rotate_half pairing
+// (gpt_oss.py:42-58, ops.py:95-104). Explicit fmaf so that every kernel that
+// applies it rounds the same way.
+__device__ __forceinline__ float rope_elem(float x, float partner, int d, int p, const float* __restrict__ inv_freq,
+                                           float amp) {
+  const float ang = (float)p * inv_freq[d & (ATTN_D / 2 - 1)];  // fp32, as positions.float() * inv
+  float s, c;
+  sincosf(ang, &s, &c);
+  c *= amp;
+  s *= amp;
+  const float ps = partner * s;
+  return d < ATTN_D / 2 ? fmaf(x, c, -ps) : fmaf(x, c, ps);
+}
+
 // One wave per row of the q | k | v block: bias, then rotary for q and k
 // rows; k and v rows go into the cache at the token's position.
 __global__ __launch_bounds__(64) void rope_kv_append_kernel(
@@ -61,15 +76,7 @@ __global__ __launch_bounds__(64) void rope_kv_append_kernel(
     v_cache[((int64_t)g * ctx_max + p) * ATTN_D + lane] = x;
     return;
   }
-  // rotate_half pairing: element i with i + D/2 (gpt_oss.py:42-58, ops.py:95-104)
-  const int i = lane & (ATTN_D / 2 - 1);
-  const float ang = (float)p * inv_freq[i];  // fp32, as positions.float() * inv
-  float s, c;
-  sincosf(ang, &s, &c);
-  c *= amp;
-  s *= amp;
-  const float partner = __shfl_xor(x, ATTN_D / 2, 64);
-  const float y = lane < ATTN_D / 2 ? x * c - partner * s : x * c + partner * s;
+  const float y = rope_elem(x, __shfl_xor(x, ATTN_D / 2, 64), lane, p, inv_freq, amp);
   if (r < n_head) {
     qkv[(int64_t)r * ATTN_D + lane] = y;
   } else {
@@ -94,11 +101,20 @@ __device__ __forceinline__ void attn_span(int p, int window, int& lo, int& total
 // part[(h * nchunk + c) * (D + 2)] = {m, l, acc[D]} for query head h.
 // FINAL (only ever one chunk: a sliding window or a cache of at most
 // ATTN_CHUNK keys): the workgroup also merges the sink and writes out[h].
-template <bool FINAL, int HPW>
+// ROPE: q is the token's raw q | k | v block; each workgroup adds the bias
+// and applies the rotary to its query heads itself, and the workgroup whose
+// chunk holds the token's position does the same for the token's k row, adds
+// v's bias and appends both to the cache before it reads any key (no other
+// workgroup reads that row), so no separate rotary + append launch is needed.
+struct RopeArgs {
+  const float *bq, *bk, *bv, *inv_freq;
+  float amp;
+};
+template <bool FINAL, int HPW, bool ROPE>
 __global__ __launch_bounds__(ATTN_THREADS) void attn_chunk_kernel(
-    const float* __restrict__ q, const float* __restrict__ k_cache, const float* __restrict__ v_cache,
-    const int32_t* __restrict__ pos_ptr, int64_t ctx_max, int window, float scale, int n_rep, int nchunk,
-    float* __restrict__ part, const float* __restrict__ sinks, float* __restrict__ out) {
+    const float* __restrict__ q, float* k_cache, float* v_cache, const int32_t* __restrict__ pos_ptr,
+    int64_t ctx_max, int window, float scale, int n_rep, int n_head, int nchunk, float* __restrict__ part,
+    const float* __restrict__ sinks, float* __restrict__ out, RopeArgs ra) {
   constexpr int NW = ATTN_THREADS / 64;
   __shared__ float qs[ATTN_MAX_REP][ATTN_D];
   // each wave's key weights, key j at (j % 4) * 16 + j / 4: key group kg reads its 16 as 4 vectors
@@ -111,9 +127,40 @@ __global__ __launch_bounds__(ATTN_THREADS) void attn_chunk_kernel(
   const int k0 = c * ATTN_CHUNK;
   if (k0 >= total) return;  // past the current length
   const int nk = min(ATTN_CHUNK, total - k0);
-  for (int i = t; i < n_rep * ATTN_D; i += ATTN_THREADS)
-    qs[i / ATTN_D][i % ATTN_D] = q[((int64_t)g * n_rep + i / ATTN_D) * ATTN_D + i % ATTN_D];
-  __syncthreads();
+  if constexpr (ROPE) {
+    for (int i = t; i < n_rep * ATTN_D; i += ATTN_THREADS) {
+      const int64_t r = (int64_t)g * n_rep + i / ATTN_D;
+      const int d = i % ATTN_D, dp = d ^ (ATTN_D / 2);
+      float x = q[r * ATTN_D + d], xp = q[r * ATTN_D + dp];
+      if (ra.bq) {
+        x += ra.bq[r * ATTN_D + d];
+        xp += ra.bq[r * ATTN_D + dp];
+      }
+      qs[i / ATTN_D][d] = rope_elem(x, xp, d, p, ra.inv_freq, ra.amp);
+    }
+    if (c == (total - 1) / ATTN_CHUNK && t < 2 * ATTN_D) {  // this chunk holds the token's own key
+      const int d = t & (ATTN_D - 1);
+      const int64_t at = ((int64_t)g * ctx_max + p) * ATTN_D + d;
+      if (t < ATTN_D) {
+        const float* kr = q + ((int64_t)n_head + g) * ATTN_D;
+        const int dp = d ^ (ATTN_D / 2);
+        float x = kr[d], xp = kr[dp];
+        if (ra.bk) {
+          x += ra.bk[(int64_t)g * ATTN_D + d];
+          xp += ra.bk[(int64_t)g * ATTN_D + dp];
+        }
+        k_cache[at] = rope_elem(x, xp, d, p, ra.inv_freq, ra.amp);
+      } else {
+        float x = q[((int64_t)n_head + n_head / n_rep + g) * ATTN_D + d];  // v rows follow the n_kv k rows
+        if (ra.bv) x += ra.bv[(int64_t)g * ATTN_D + d];
+        v_cache[at] = x;
+      }
+    }
+  } else {
+    for (int i = t; i < n_rep * ATTN_D; i += ATTN_THREADS)
+      qs[i / ATTN_D][i % ATTN_D] = q[((int64_t)g * n_rep + i / ATTN_D) * ATTN_D + i % ATTN_D];
+  }
+  __syncthreads();  // q staged; the appended k / v rows visible to the workgroup's loads
   const int wave = t >> 6, lane = t & 63, kg = lane >> 4, dq = lane & 15;
   const float* kb = k_cache + ((int64_t)g * ctx_max + lo + k0) * ATTN_D;
   const float* vb = v_cache + ((int64_t)g * ctx_max + lo + k0) * ATTN_D + 4 * dq;
@@ -264,9 +311,11 @@ extern "C" int64_t nsx_attn_workspace_bytes(int n_head, int head_dim, int64_t ct
   return (int64_t)n_head * nchunk * (ATTN_D + 2) * (int64_t)sizeof(float);
 }
 
-extern "C" int nsx_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* sinks,
-                               int n_head, int n_kv, int head_dim, const int32_t* pos, int64_t ctx_max,
-                               int window, float scale, void* workspace, float* out, void* stream) {
+// Checks shared by both attention entry points, then the chunk launches
+// (and the combine unless one chunk covers every position).
+static int attn_launch(const float* q, float* k_cache, float* v_cache, const float* sinks, int n_head, int n_kv,
+                       int head_dim, const int32_t* pos, int64_t ctx_max, int window, float scale,
+                       void* workspace, float* out, bool rope, const RopeArgs& ra, hipStream_t st) {
   NSX_REQUIRE(head_dim == ATTN_D, NSX_ENOTIMPL, "head_dim %d (the kernels are written for 64)", head_dim);
   NSX_REQUIRE(n_head > 0 && n_kv > 0 && n_head % n_kv == 0 && n_head / n_kv <= ATTN_MAX_REP, NSX_EINVAL,
               "n_head=%d, n_kv=%d: n_head must be a multiple of n_kv, at most %d per kv head", n_head, n_kv,
@@ -281,18 +330,22 @@ extern "C" int nsx_attn_decode(const float* q, const float* k_cache, const float
   const int live = window > 0 ? (int)std::min<int64_t>(nchunk, nsx_cdiv(window, ATTN_CHUNK)) : nchunk;
   const int n_rep = n_head / n_kv;
   const int hpw = (n_rep + ATTN_THREADS / 64 - 1) / (ATTN_THREADS / 64);
-  auto chunks = [&](auto final_tag, auto hpw_tag) {
+  auto chunks = [&](auto final_tag, auto hpw_tag, auto rope_tag) {
     constexpr bool F = decltype(final_tag)::value;
-    hipLaunchKernelGGL((attn_chunk_kernel<F, decltype(hpw_tag)::value>), dim3(n_kv, F ? 1 : live),
-                       dim3(ATTN_THREADS), 0, S(stream), q, k_cache, v_cache, pos, ctx_max, window, scale, n_rep,
-                       nchunk, (float*)workspace, sinks, out);
+    hipLaunchKernelGGL((attn_chunk_kernel<F, decltype(hpw_tag)::value, decltype(rope_tag)::value>),
+                       dim3(n_kv, F ? 1 : live), dim3(ATTN_THREADS), 0, st, q, k_cache, v_cache, pos, ctx_max,
+                       window, scale, n_rep, n_head, nchunk, (float*)workspace, sinks, out, ra);
+  };
+  auto by_rope = [&](auto final_tag, auto hpw_tag) {
+    if (rope) chunks(final_tag, hpw_tag, std::true_type{});
+    else chunks(final_tag, hpw_tag, std::false_type{});
   };
   auto by_hpw = [&](auto final_tag) {
     switch (hpw) {
-      case 1: chunks(final_tag, std::integral_constant<int, 1>{}); break;
-      case 2: chunks(final_tag, std::integral_constant<int, 2>{}); break;
-      case 3: chunks(final_tag, std::integral_constant<int, 3>{}); break;
-      default: chunks(final_tag, std::integral_constant<int, 4>{}); break;
+      case 1: by_rope(final_tag, std::integral_constant<int, 1>{}); break;
+      case 2: by_rope(final_tag, std::integral_constant<int, 2>{}); break;
+      case 3: by_rope(final_tag, std::integral_constant<int, 3>{}); break;
+      default: by_rope(final_tag, std::integral_constant<int, 4>{}); break;
     }
   };
   if (live == 1) {  // one chunk at any position: no partials, no combine launch
@@ -302,10 +355,28 @@ extern "C" int nsx_attn_decode(const float* q, const float* k_cache, const float
   }
   by_hpw(std::false_type{});
   NSX_LAUNCHED();
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head), dim3(64), 0, S(stream), (const float*)workspace, sinks, pos,
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head), dim3(64), 0, st, (const float*)workspace, sinks, pos,
                      ctx_max, window, nchunk, out);
   NSX_LAUNCHED();
   return NSX_OK;
+}
+
+extern "C" int nsx_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* sinks,
+                               int n_head, int n_kv, int head_dim, const int32_t* pos, int64_t ctx_max,
+                               int window, float scale, void* workspace, float* out, void* stream) {
+  // the caches are only read on this path
+  return attn_launch(q, const_cast<float*>(k_cache), const_cast<float*>(v_cache), sinks, n_head, n_kv, head_dim,
+                     pos, ctx_max, window, scale, workspace, out, false, RopeArgs{}, S(stream));
+}
+
+extern "C" int nsx_attn_decode_qkv(const float* qkv, const float* q_bias, const float* k_bias, const float* v_bias,
+                                   const float* inv_freq, float amplitude, const float* sinks, int n_head, int n_kv,
+                                   int head_dim, const int32_t* pos, float* k_cache, float* v_cache,
+                                   int64_t ctx_max, int window, float scale, void* workspace, float* out,
+                                   void* stream) {
+  NSX_REQUIRE(inv_freq, NSX_EINVAL, "null inv_freq");
+  return attn_launch(qkv, k_cache, v_cache, sinks, n_head, n_kv, head_dim, pos, ctx_max, window, scale, workspace,
+                     out, true, RopeArgs{q_bias, k_bias, v_bias, inv_freq, amplitude}, S(stream));
 }
 
 extern "C" int nsx_pos_advance(int32_t* pos, int32_t n, void* stream) {

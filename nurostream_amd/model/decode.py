@@ -10,7 +10,8 @@ Python seams over libnsx (model/gpt_oss.py of the reference):
 - `DeviceKV`: KVCache (model/qwen3.py:79-106) with a fixed capacity in HBM
   and the token position in device memory, so one decode token can be
   captured as a graph and replayed.
-- `rope_kv_append`, `attn_decode`, `dequantize_rows`: the kernels.
+- `rope_kv_append`, `attn_decode`, `dequantize_rows`: the kernels;
+  `attn_decode_qkv` does the first two in one launch.
 """
 from __future__ import annotations
 
@@ -124,6 +125,21 @@ def attn_decode(q: torch.Tensor, kv: DeviceKV, layer: int, sinks: torch.Tensor |
     return y
 
 
+def attn_decode_qkv(qkv: torch.Tensor, bq, bk, bv, cfg: AttnConfig, inv_freq: torch.Tensor, amp: float,
+                    kv: DeviceKV, layer: int, sinks: torch.Tensor | None, window: int,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """rope_kv_append + attn_decode as one launch (two with the chunk combine); qkv (the raw
+    projection, no bias) is left unchanged. Bit-identical to the two calls."""
+    y = torch.empty((cfg.n_head, cfg.head_dim), dtype=torch.float32, device=qkv.device) if out is None else out
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    N.check(N.load().nsx_attn_decode_qkv(qkv.data_ptr(), ptr(bq), ptr(bk), ptr(bv), inv_freq.data_ptr(), float(amp),
+                                         ptr(sinks), cfg.n_head, cfg.n_head_kv, cfg.head_dim, kv.pos.data_ptr(),
+                                         kv.k[layer].data_ptr(), kv.v[layer].data_ptr(), kv.ctx_max, int(window),
+                                         1.0 / math.sqrt(cfg.head_dim), kv.workspace.data_ptr(), y.data_ptr(),
+                                         N.stream_ptr(qkv.device)), "attn_decode_qkv")
+    return y
+
+
 def advance(kv: DeviceKV, n: int = 1) -> None:
     N.check(N.load().nsx_pos_advance(kv.pos.data_ptr(), int(n), N.stream_ptr(kv.pos.device)), "pos_advance")
     kv.length += n
@@ -141,5 +157,5 @@ def dequantize_rows(raw: torch.Tensor, dtype, n_rows: int, K: int, ids: torch.Te
     return y
 
 
-__all__ = ["AttnConfig", "DeviceKV", "yarn_inv_freq", "rope_kv_append", "attn_decode", "advance",
+__all__ = ["AttnConfig", "DeviceKV", "yarn_inv_freq", "rope_kv_append", "attn_decode", "attn_decode_qkv", "advance",
            "dequantize_rows", "FLOAT_TYPES"]

@@ -615,12 +615,13 @@ class GptOssModel:
 
         `pending` (the previous FFN output) is added to x first, inside the
         attention norm's kernel (x is updated in place). Then one GEMV for q|k|v,
-        one kernel for bias + rotary + cache append, the sink attention
-        (sliding window on even layers), and one GEMV for the output projection
-        with its bias and the residual."""
+        the sink attention (sliding window on even layers) with the bias,
+        rotary and cache append of the token's q / k / v in the same launch,
+        and one GEMV for the output projection with its bias and the
+        residual."""
         from ..compute.kernels import can_fuse, fused_gemv
         from ..format.gguf import row_geometry
-        from .decode import attn_decode, rope_kv_append
+        from .decode import attn_decode_qkv
         c, p = self.attn_config(), f"blk.{layer}."
         h = add_rms_norm(x, pending, self.w(p + "attn_norm.weight"), self.cfg.rms_eps,
                          sum_out=x if pending is not None else None)
@@ -630,10 +631,9 @@ class GptOssModel:
         else:
             qkv = torch.cat([self._linear(p + n + ".weight", h).reshape(-1) for n in ("attn_q", "attn_k", "attn_v")])
         b = lambda n: self.w(p + n + ".bias") if self.has(p + n + ".bias") else None  # noqa: E731
-        rope_kv_append(qkv, b("attn_q"), b("attn_k"), b("attn_v"), c, self._inv_freq, self._amp, kv, layer)
         sinks = self.w(p + "attn_sinks.weight") if self.has(p + "attn_sinks.weight") else None
-        att = attn_decode(qkv[:c.n_head * c.head_dim], kv, layer, sinks, c.sliding_window if layer % 2 == 0 else 0,
-                          c).reshape(1, -1)
+        att = attn_decode_qkv(qkv, b("attn_q"), b("attn_k"), b("attn_v"), c, self._inv_freq, self._amp, kv, layer,
+                              sinks, c.sliding_window if layer % 2 == 0 else 0).reshape(1, -1)
         o_name = p + "attn_output.weight"
         hit = self._resident_raw(o_name)
         if hit is not None and can_fuse(hit[1], att):

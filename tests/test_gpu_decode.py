@@ -73,9 +73,48 @@ def test_attention_kernels_match_oracle(dev, window, heads):
     np.testing.assert_allclose(to_np(kv.v[0]), Vref, rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("window", [0, 128])
+@pytest.mark.parametrize("heads", [(16, 2), (6, 2)], ids=["rep8", "rep3"])
+def test_fused_attention_equals_two_calls(dev, window, heads):
+    """attn_decode_qkv (bias + rotary + append inside the attention launch) against rope_kv_append
+    followed by attn_decode: outputs and both caches bit-identical over 300 positions, the raw
+    q | k | v block left unchanged."""
+    from nurostream_amd.model.decode import (DeviceKV, advance, attn_decode, attn_decode_qkv, rope_kv_append,
+                                             yarn_inv_freq)
+    c = _cfg(n_head=heads[0], n_kv=heads[1])
+    L = 300
+    g = torch.Generator(device="cpu").manual_seed(11)
+    kv1, kv2 = DeviceKV(1, c, L, dev), DeviceKV(1, c, L, dev)
+    inv, amp = yarn_inv_freq(c, dev)
+    bq, bk, bv = (torch.randn(n * 64, generator=g).to(dev) for n in (c.n_head, c.n_head_kv, c.n_head_kv))
+    sinks = torch.randn(c.n_head, generator=g).to(dev)
+    rows = c.n_head + 2 * c.n_head_kv
+    for p in range(L):
+        raw = torch.randn(rows * 64, generator=g).to(dev)
+        qkv = raw.clone()
+        rope_kv_append(qkv, bq, bk, bv, c, inv, amp, kv1, 0)
+        a1 = attn_decode(qkv[:c.n_head * 64], kv1, 0, sinks, window, c)
+        keep = raw.clone()
+        a2 = attn_decode_qkv(raw, bq, bk, bv, c, inv, amp, kv2, 0, sinks, window)
+        advance(kv1)
+        advance(kv2)
+        if p in (0, 1, 63, 64, 127, 128, 129, 255, 256, L - 1):
+            assert torch.equal(a1, a2), p
+            assert torch.equal(raw, keep), p
+    torch.cuda.synchronize()
+    assert torch.equal(kv1.k[0], kv2.k[0]) and torch.equal(kv1.v[0], kv2.v[0])
+    # no bias: the same identity
+    q0 = torch.randn(rows * 64, generator=g).to(dev)
+    kv1.reset(), kv2.reset()
+    q1 = q0.clone()
+    rope_kv_append(q1, None, None, None, c, inv, amp, kv1, 0)
+    assert torch.equal(attn_decode(q1[:c.n_head * 64], kv1, 0, None, window, c),
+                       attn_decode_qkv(q0, None, None, None, c, inv, amp, kv2, 0, None, window))
+
+
 def test_attention_position_outside_cache_writes_nothing(dev):
     """A position at or past the cache capacity leaves the caches and the output untouched."""
-    from nurostream_amd.model.decode import DeviceKV, attn_decode, rope_kv_append, yarn_inv_freq
+    from nurostream_amd.model.decode import DeviceKV, attn_decode, attn_decode_qkv, rope_kv_append, yarn_inv_freq
     c = _cfg(n_head=8, n_kv=8, window=0)
     kv = DeviceKV(1, c, 4, dev)
     kv.pos.fill_(4)
@@ -84,6 +123,7 @@ def test_attention_position_outside_cache_writes_nothing(dev):
     rope_kv_append(qkv, None, None, None, c, inv, amp, kv, 0)
     out = torch.full((c.n_head, 64), 7.0, device=dev)
     attn_decode(qkv[:c.n_head * 64], kv, 0, None, 0, c, out=out)
+    attn_decode_qkv(qkv, None, None, None, c, inv, amp, kv, 0, None, 0, out=out)
     torch.cuda.synchronize()
     assert float(kv.k[0].abs().sum()) == 0.0 and float(kv.v[0].abs().sum()) == 0.0
     assert bool((out == 7.0).all())
