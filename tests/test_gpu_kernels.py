@@ -134,11 +134,13 @@ def test_fused_gemv_q6k_any_alignment(dev, offset):
     assert torch.equal(y0, y1)
 
 
-@pytest.mark.parametrize("fmt,T", [("Q8_0", 1), ("Q6_K", 1), ("MXFP4", 3), ("Q4_K", 2)])
-def test_fused_gemv_bias_residual_epilogue(dev, fmt, T):
-    """nsx_fused_gemv_ex: resid + (x @ W.T + bias), also with resid being the output itself."""
+@pytest.mark.parametrize("fmt,T,rows,K", [("Q8_0", 1, 300, 1024), ("Q6_K", 1, 300, 1024), ("MXFP4", 3, 300, 1024),
+                                         ("Q4_K", 2, 300, 1024), ("Q8_0", 1, 40000, 256), ("Q6_K", 1, 20000, 256)])
+def test_fused_gemv_bias_residual_epilogue(dev, fmt, T, rows, K):
+    """nsx_fused_gemv_ex: resid + (x @ W.T + bias). The 20000 / 40000-row cases give every wave
+    of the persistent grid several rows, so each row's bias and residual (loaded with its weights)
+    must reach that row's epilogue."""
     from nurostream_amd.compute.kernels import fused_gemv
-    rows, K = 300, 1024
     t = getattr(OQ, fmt)
     raw = _gemv_case(fmt, rows, K, seed=9)
     rng = np.random.default_rng(4)
