@@ -92,7 +92,7 @@ def _parse():
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default per workload)")
     p.add_argument("--layers", type=int, default=None, help="rotating weight copies, or the stack depth")
     p.add_argument("--layout", choices=["t64", "gguf"], default="t64")
-    p.add_argument("--dispatch", choices=["auto", "pairs", "grouped"], default="auto")
+    p.add_argument("--dispatch", choices=["auto", "pairs", "grouped", "mfma"], default="auto")
     p.add_argument("--profile-steps", type=int, default=None, help="steps timed per phase graph")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -289,7 +289,13 @@ def layer_workload(args, torch, N, synth, dev):
     ids_cpu = ids[W:W + K + R].cpu()
     distinct = [len(torch.unique(ids_cpu[s])) for s in range(ids_cpu.shape[0])]
     mean_distinct = sum(distinct) / len(distinct)
-    gu_kernel = ("moe_gu_grouped_kernel" if grouped else "moe_gu_kernel") if layout == "t64" else "moe_gu_raw_kernel"
+    if layout == "t64":
+        gu_kernel = "moe_gu_grouped_kernel" if grouped else "moe_gu_kernel"
+    elif cfg.ggml_type == synth.GGMLType.Q4_K:  # stacked 16-byte aligned Q4_K experts take the Q4_K kernels
+        gu_kernel = {"mfma": "moe_q4k_mfma_kernel<true>", "grouped": "moe_gu_q4k_grouped_kernel"}.get(
+            args.dispatch, "moe_gu_q4k_kernel")
+    else:
+        gu_kernel = "moe_gu_raw_kernel"
     gu_bytes, dn_bytes = _expert_bytes(cfg, mean_distinct)
     roofline = None
     if R > 0:

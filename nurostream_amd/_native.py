@@ -21,7 +21,7 @@ READ_DIRECT = 1
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 LAYOUT_GGUF, LAYOUT_T64 = 0, 1
 ROUTE_GPTOSS, ROUTE_QWEN3 = 0, 1
-DISPATCH_AUTO, DISPATCH_PAIRS, DISPATCH_GROUPED = 0, 1, 2
+DISPATCH_AUTO, DISPATCH_PAIRS, DISPATCH_GROUPED, DISPATCH_MFMA = 0, 1, 2, 3
 ACT_CLAMPED_SWIGLU, ACT_SILU_MUL = 0, 1
 
 BLOCK_TYPES = frozenset({GGMLType.Q4_0, GGMLType.Q8_0, GGMLType.Q4_K, GGMLType.Q6_K, GGMLType.MXFP4})

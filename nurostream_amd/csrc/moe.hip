@@ -1522,6 +1522,249 @@ __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
 }
 
 // ---------------------------------------------------------------------------
+// Grouped Q4_K on the matrix cores (NSX_DISPATCH_MFMA). For an expert's work
+// item (up to 16 tokens) a wave computes 16 rows x the item's tokens with
+// v_mfma_f32_16x16x32_f16, one 32-element sub-block per instruction:
+//   A (16 rows x 32 k) = sc * q: integers <= 945, exact in f16, built from the
+//     nibbles as the f16 bit patterns 0x6400 | q (= 1024 + q) and one packed
+//     fma (x sc - 1024 sc, exact);
+//   B (32 k x 16 tokens) = the activations as two f16 terms (hi + lo) of a
+//     copy scaled by a power of two per token (mq_terms_kernel): about 22
+//     significant bits per element, every product exact in the fp32 sum;
+//   per 256-element super-block: y += d * acc - dmin * acc_min, where acc_min
+//     = m (the sub-block mins) x the sub-blocks' activation sums, a second
+//     MFMA over k = the super-block's 8 sub-blocks.
+// The decode of each weight is shared by the item's tokens (the per-pair
+// kernels decode an expert once per routed token) and the products run on
+// the matrix cores, so the kernels are bound by the expert bytes.
+// Operand layouts (16x16x32 f16): A lane l = row l % 16, k = 8 (l / 16) + v;
+// B lane l = column l % 16, same k; D lane l = column l % 16, rows
+// 4 (l / 16) + i.
+
+constexpr int MQ_ROWS = 16;  // rows per wave (one MFMA tile)
+constexpr int MQ_WG_ROWS = 64;
+
+typedef _Float16 mq_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mq_h2 __attribute__((ext_vector_type(2)));
+typedef float mq_f4 __attribute__((ext_vector_type(4)));
+
+// Bytes of one row of activation terms for K columns (K a multiple of 256):
+// hi[K], lo[K] (f16), sub-block sums hi[K/32], lo[K/32] (f16), 2^e (f32),
+// padding to 16 bytes.
+__host__ __device__ constexpr int64_t mq_row_bytes(int64_t K) { return 4 * K + K / 8 + 16; }
+
+// One workgroup per row of x (K columns): x' = x * 2^-e with max |x'| < 512,
+// hi = f16(x'), lo = f16(x' - hi); the 32-element sums of x' likewise (< 2^14,
+// inside f16's range); then 2^e.
+__global__ __launch_bounds__(256) void mq_terms_kernel(const float* __restrict__ x, int K,
+                                                       uint8_t* __restrict__ terms) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const float* xr = x + r * K;
+  _Float16* hi = (_Float16*)(terms + r * mq_row_bytes(K));
+  _Float16* lo = hi + K;
+  _Float16* shi = lo + K;
+  _Float16* slo = shi + K / 32;
+  float mx = 0.f;
+  for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  if (mx > 0.f && mx <= 3.4e38f) (void)frexpf(mx, &ex);  // mx < 2^ex
+  const int e = ex - 9;
+  for (int k = threadIdx.x; k < K; k += 256) {
+    const float v = ldexpf(xr[k], -e);
+    const _Float16 h = (_Float16)v;
+    hi[k] = h;
+    lo[k] = (_Float16)(v - (float)h);
+  }
+  for (int sidx = threadIdx.x; sidx < K / 32; sidx += 256) {
+    float acc = 0.f;
+    for (int i = 0; i < 32; ++i) acc += ldexpf(xr[32 * sidx + i], -e);
+    const _Float16 h = (_Float16)acc;
+    shi[sidx] = h;
+    slo[sidx] = (_Float16)(acc - (float)h);
+  }
+  if (threadIdx.x == 0) *(float*)(slo + K / 32) = ldexpf(1.f, e);
+}
+
+// A operands of one sub-block pair from its 8 code bytes (elements
+// 8 g .. 8 g + 7): low nibbles -> sub-block 2j (x sc_lo), high nibbles ->
+// sub-block 2j + 1 (x sc_hi). Each code byte b becomes the f16 bit pattern
+// 0x64 : b (v_perm against a register of 0x64 bytes) after masking one
+// nibble: 1024 + q for the low one; 1024 + 16 q for the high one, left in
+// place, so its multiplier is sc / 16 (exact in f16).
+__device__ __forceinline__ void mq_a_pair(uint2 q, int sc_lo, int sc_hi, mq_h8& alo, mq_h8& ahi) {
+  const _Float16 fl = (_Float16)sc_lo, fh = (_Float16)((float)sc_hi * 0.0625f);
+  const mq_h2 ml = {fl, fl}, mh = {fh, fh};
+  const _Float16 cl0 = (_Float16)(-1024.f * (float)sc_lo), ch0 = (_Float16)(-64.f * (float)sc_hi);
+  const mq_h2 cl = {cl0, cl0}, ch = {ch0, ch0};
+  const uint32_t w[2] = {q.x, q.y};
+  uint32_t lo[4], hi[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t wl = w[h] & 0x0F0F0F0Fu, wh = w[h] & 0xF0F0F0F0u;
+    // selector bytes 0-3 pick the second operand's bytes, 4 the first's (0x64)
+    const uint32_t l01 = __builtin_amdgcn_perm(0x64646464u, wl, 0x04010400u);
+    const uint32_t l23 = __builtin_amdgcn_perm(0x64646464u, wl, 0x04030402u);
+    const uint32_t h01 = __builtin_amdgcn_perm(0x64646464u, wh, 0x04010400u);
+    const uint32_t h23 = __builtin_amdgcn_perm(0x64646464u, wh, 0x04030402u);
+    lo[2 * h] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(mq_h2, l01), ml, cl));
+    lo[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(mq_h2, l23), ml, cl));
+    hi[2 * h] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(mq_h2, h01), mh, ch));
+    hi[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(mq_h2, h23), mh, ch));
+  }
+  alo = __builtin_bit_cast(mq_h8, v4u{lo[0], lo[1], lo[2], lo[3]});
+  ahi = __builtin_bit_cast(mq_h8, v4u{hi[0], hi[1], hi[2], hi[3]});
+}
+
+// One super-block of one matrix: header H (d | dmin, scales[12]) and the
+// lane's code bytes Q[j] (sub-block pair j) -> y (rows 4 g + i, the lane's
+// token) += d * (sc q . x) - dmin * (m . xsum).
+__device__ __forceinline__ void mq_superblock(const v4u& H, const uint2 (&Q)[4], const mq_h8 (&BH)[8],
+                                              const mq_h8 (&BL)[8], const mq_h8& SH, const mq_h8& SL, int g,
+                                              mq_f4& y) {
+  auto byte = [&](int i) {  // scales[i] = header byte 4 + i
+    const uint32_t w = i < 4 ? H.y : (i < 8 ? H.z : H.w);
+    return (int)((w >> (8 * (i & 3))) & 0xFFu);
+  };
+  int sc[8], mn[8];  // get_scale_min_k4
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = byte(j) & 63;
+    mn[j] = byte(j + 4) & 63;
+    sc[j + 4] = (byte(j + 8) & 0xF) | ((byte(j) >> 6) << 4);
+    mn[j + 4] = (byte(j + 8) >> 4) | ((byte(j + 4) >> 6) << 4);
+  }
+  mq_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    mq_h8 alo, ahi;
+    mq_a_pair(Q[j], sc[2 * j], sc[2 * j + 1], alo, ahi);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[2 * j], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[2 * j], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[2 * j + 1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BL[2 * j + 1], acc, 0, 0, 0);
+  }
+  mq_h8 A2;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) A2[j] = g == 0 ? (_Float16)mn[j] : (_Float16)0.f;
+  mq_f4 am = {0.f, 0.f, 0.f, 0.f};
+  am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, SH, am, 0, 0, 0);
+  am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, SL, am, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // d, dmin of row 4 g + i: the header lane (4 g + i) loaded
+    const uint32_t dw = (uint32_t)__shfl((int)H.x, 4 * g + i, 64);
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(dw >> 16));
+    y[i] = fmaf(d, acc[i], y[i]);
+    y[i] = fmaf(-dmin, am[i], y[i]);
+  }
+}
+
+// GU: gate and up rows (n_ff) over h's terms, then the activation into act;
+// else: down rows (n_embd) over the pairs' activation terms, plus the bias,
+// into y (moe_combine_kernel adds a token's pairs in ascending expert id).
+// Workgroup = (item, 64 rows), wave = 16 rows over all of K.
+template <bool GU>
+__global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
+  const int NR = GU ? a.n_ff : a.n_embd, K = GU ? a.n_embd : a.n_ff;
+  int tile;
+  int4 item;
+  if (!grp_work(a, (NR + MQ_WG_ROWS - 1) / MQ_WG_ROWS, tile, item)) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int lr = lane & 15, g = lane >> 4;
+  const int r0 = tile * MQ_WG_ROWS + wave * MQ_ROWS;
+  if (r0 >= NR) return;  // no barriers below
+  const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
+  const int nsb = K / 256;
+  const int64_t rb = (int64_t)nsb * 144;
+  // weights through buffer loads (an expert matrix: NR rows of rb bytes), so
+  // they are tracked by the vector-memory counter alone
+  const uint32_t arow_off = (uint32_t)(min(r0 + lr, NR - 1) * rb);
+  const __amdgpu_buffer_rsrc_t rs0 = nsx_rsrc(expert_base(GU ? a.gate_base : a.down_base, GU ? a.gate_stride : a.down_stride,
+                                                          GU ? a.gate_ptrs : a.down_ptrs, e),
+                                              (uint32_t)(NR * rb));
+  const __amdgpu_buffer_rsrc_t rs1 =
+      GU ? nsx_rsrc(expert_base(a.up_base, a.up_stride, a.up_ptrs, e), (uint32_t)(NR * rb)) : rs0;
+  // Columns past the item's tokens load the last token's terms (valid
+  // memory); their results are never stored, and MFMA columns are independent.
+  const bool tv = lr < n;
+  const int pr = a.sorted[pos0 + min(lr, n - 1)];
+  const int64_t brow = GU ? pr / a.top_k : pr;
+  const int64_t tb = mq_row_bytes(K);
+  const uint8_t* tbase = GU ? a.xq_h : (const uint8_t*)a.xq_a;
+  // terms rows: GU one per token (T), else one per pair (T * top_k)
+  const __amdgpu_buffer_rsrc_t rt = nsx_rsrc(tbase, (uint32_t)((int64_t)(GU ? a.T : a.T * a.top_k) * tb));
+  const uint32_t tv_off = (uint32_t)(brow * tb) + 16u * (uint32_t)g;  // the lane's token row, k-group g
+  const uint32_t ts_off = (uint32_t)(brow * tb);
+  // Weights are double-buffered: a super-block's activation terms (L2) are
+  // loaded first, then the next super-block's weights (HBM), so waiting for
+  // the terms does not wait for the prefetch (loads complete in order).
+  struct W {
+    v4u H0, H1;
+    uint2 Q0[4], Q1[4];
+  };
+  auto load_w = [&](int sb, W& o) {
+    const uint32_t b = arow_off + (uint32_t)sb * 144u;
+    o.H0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, b, 0, 0));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o.Q0[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs0, b + 16u + 32u * j + 8u * g, 0, 0));
+    if constexpr (GU) {
+      o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, b, 0, 0));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o.Q1[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs1, b + 16u + 32u * j + 8u * g, 0, 0));
+    }
+  };
+  mq_f4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
+  auto step = [&](int sb, const W& cur, W& nxt) {
+    mq_h8 BH[8], BL[8];
+    const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + 64u * s8, sh_off, 0));
+      BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + 64u * s8, sl_off, 0));
+    }
+    // sub-block sums after the terms; the min term's A operand is zero outside
+    // k < 8 (g == 0), so every group may load the same sums
+    const mq_h8 SH = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + 16 * sb, 0));
+    const mq_h8 SL =
+        __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
+    if (sb + 1 < nsb) load_w(sb + 1, nxt);
+    mq_superblock(cur.H0, cur.Q0, BH, BL, SH, SL, g, y0);
+    if constexpr (GU) mq_superblock(cur.H1, cur.Q1, BH, BL, SH, SL, g, y1);
+  };
+  W wa, wb;
+  load_w(0, wa);
+  int sb = 0;
+  for (; sb + 1 < nsb; sb += 2) {
+    step(sb, wa, wb);
+    step(sb + 1, wb, wa);
+  }
+  if (sb < nsb) step(sb, wa, wb);
+  const float scale = *(const float*)(tbase + brow * tb + 4 * K + K / 8);  // 2^e of this column's terms
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = r0 + 4 * g + i;
+    if (!tv || row >= NR) continue;
+    if constexpr (GU) {
+      float gv = y0[i] * scale, uv = y1[i] * scale;
+      if (a.gate_bias) gv += a.gate_bias[(int64_t)e * a.n_ff + row];
+      if (a.up_bias) uv += a.up_bias[(int64_t)e * a.n_ff + row];
+      a.act[(int64_t)pr * a.n_ff + row] = moe_act(a.act_kind, gv, uv, a.alpha, a.limit);
+    } else {
+      float v = y0[i] * scale;
+      if (a.down_bias) v += a.down_bias[(int64_t)e * a.n_embd + row];
+      a.y[(int64_t)pr * a.n_embd + row] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 struct MoePlan {
@@ -1531,6 +1774,7 @@ struct MoePlan {
   int cg, cd, sd;
   bool grouped;
   int max_items, cdg, sdg;
+  bool mq;  // grouped Q4_K on the matrix cores: xqh / xqa hold activation terms (mq_row_bytes per row)
 };
 
 constexpr int GRP_AUTO_MIN_T = 8;  // NSX_DISPATCH_AUTO groups from this many tokens
@@ -1546,8 +1790,13 @@ static bool q4k_fast(const nsx_moe_layer* L) {
   return false;  // address tables: alignment unknown on the host
 }
 
+// Grouped Q4_K on the matrix cores (moe_q4k_mfma_kernel).
+static bool use_mq(const nsx_moe_layer* L, int64_t) {
+  return L->dispatch == NSX_DISPATCH_MFMA && L->layout == NSX_LAYOUT_GGUF && q4k_fast(L);
+}
+
 static bool use_grouped(const nsx_moe_layer* L, int64_t T) {
-  if (L->dispatch == NSX_DISPATCH_GROUPED) return true;
+  if (L->dispatch == NSX_DISPATCH_GROUPED || use_mq(L, T)) return true;
   // Q4_K groups on request only: its grouped kernels measure slower than the per-pair ones at T=32
   return L->dispatch == NSX_DISPATCH_AUTO && L->layout == NSX_LAYOUT_T64 && T >= GRP_AUTO_MIN_T;
 }
@@ -1558,6 +1807,7 @@ static int64_t grp_chunk_tokens(const nsx_moe_layer* L) { return GRP_MAX_PAIRS /
 static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   MoePlan p{};
   p.grouped = use_grouped(L, T);
+  p.mq = use_mq(L, T);
   if (p.grouped) T = std::min(T, grp_chunk_tokens(L));
   const int64_t P = T * L->top_k;
   const bool t64 = L->layout == NSX_LAYOUT_T64;
@@ -1577,9 +1827,9 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.off_act = o;
   o = al(o + (t64 ? 0 : P * L->n_ff * 4));
   p.off_xqh = o;
-  o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP : 0));
+  o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP : (p.mq ? T * mq_row_bytes(L->n_embd) : 0)));
   p.off_xqa = o;
-  o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : 0));
+  o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : (p.mq ? P * mq_row_bytes(L->n_ff) : 0)));
   p.off_items = o;
   o = al(o + (int64_t)p.max_items * 16);
   p.off_nitems = o;
@@ -1638,8 +1888,10 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
     }
   }
   NSX_REQUIRE(L->dispatch == NSX_DISPATCH_AUTO || L->dispatch == NSX_DISPATCH_PAIRS ||
-                  L->dispatch == NSX_DISPATCH_GROUPED,
+                  L->dispatch == NSX_DISPATCH_GROUPED || L->dispatch == NSX_DISPATCH_MFMA,
               NSX_EINVAL, "dispatch %d", L->dispatch);
+  NSX_REQUIRE(L->dispatch != NSX_DISPATCH_MFMA || (L->layout == NSX_LAYOUT_GGUF && q4k_fast(L)), NSX_ENOTIMPL,
+              "NSX_DISPATCH_MFMA is implemented for stacked, 16-byte aligned Q4_K experts with K <= 4096");
   NSX_REQUIRE(!use_grouped(L, T) || L->layout == NSX_LAYOUT_T64 || q4k_fast(L), NSX_ENOTIMPL,
               "grouped dispatch is implemented for the t64 layout and for stacked, 16-byte aligned Q4_K "
               "experts with K <= 4096");
@@ -1777,6 +2029,11 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
       if ((rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
       if (t64) {
         rc = nsx_launch(moe_gu_grouped_kernel, grid8(p.ggu.tiles), dim3(128 * p.cg), 0, st, d);
+      } else if (p.mq) {
+        if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
+                             (uint8_t*)(ws + p.off_xqh))))
+          return rc;
+        rc = nsx_launch(moe_q4k_mfma_kernel<true>, grid8(nsx_cdiv(L->n_ff, MQ_WG_ROWS)), dim3(256), 0, st, d);
       } else {
         const int64_t g = nsx_cdiv(L->n_ff, Q4K_GU_WAVES * Q4K_GU_RPW);
         rc = L->n_embd > 64 * 32
@@ -1788,6 +2045,11 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     if (on(NSX_PHASE_DOWN)) {
       if (t64) {
         rc = nsx_launch(moe_down_grouped_kernel, grid8(p.gdn.tiles), dim3(256 * p.cdg), 0, st, d);
+      } else if (p.mq) {
+        if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
+                             (int)L->n_ff, d.xq_a)))
+          return rc;
+        rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, MQ_WG_ROWS)), dim3(256), 0, st, d);
       } else {
         const int64_t g = nsx_cdiv(L->n_embd, Q4K_DG_WAVES * Q4K_DG_RPW);
         rc = L->n_ff > 64 * 32

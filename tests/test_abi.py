@@ -94,7 +94,14 @@ def test_workspace_bytes_by_dispatch(lib):
     L.gate_stride = L.up_stride = L.down_stride = 1536 * 2304
     L.gate_base = L.up_base = L.down_base = 1 << 20
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) > 0
+    wq = lib.nsx_moe_workspace_bytes(C.byref(L), 8)
+    L.dispatch = N.DISPATCH_MFMA  # plus the activation terms: 8 tokens of h, 32 pairs of activations
+    terms = 8 * (4 * 4096 + 4096 // 8 + 16) + 32 * (4 * 1536 + 1536 // 8 + 16)
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) >= wq + terms
     L.down_base = (1 << 20) + 8  # not 16-byte aligned: no Q4_K fast path, so no grouping
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
+    assert b"MFMA" in lib.nsx_last_error()
+    L.dispatch = N.DISPATCH_GROUPED
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
 
 

@@ -148,3 +148,43 @@ def test_config4_qwen3_t32_grouped(dev):
     ref, rid, _, _ = _oracle_layer(cfg, t, h[sub].cpu().numpy())
     np.testing.assert_array_equal(np.sort(to_np(ia)[sub], 1), np.sort(rid, 1))
     assert rel_max(to_np(oa)[sub], ref) < 1e-5
+
+
+@pytest.mark.parametrize("T,scale", [(1, 1.0), (5, 1.0), (8, 1.0), (40, 1.0), (5, 1e3), (5, 1e-3)])
+def test_mfma_q4k_matches_oracle_and_pairs(dev, T, scale):
+    """NSX_DISPATCH_MFMA (grouped Q4_K on the matrix cores: f16 products of the exact sc * q
+    codes with a two-term split of power-of-two-scaled activations): the same routing as the
+    per-pair kernels, outputs within 1e-5 of theirs and of the float64 oracle, also for
+    activations scaled far from 1 (T=40 splits busy experts over several work items)."""
+    from nurostream_amd import synth
+    cfg = _small("qwen3-small")
+    t = synth.make_layer(cfg, seed=21, device=dev)
+    lp = _layer(cfg, t, "gguf", dispatch="pairs")
+    lm = _layer(cfg, t, "gguf", dispatch="mfma")
+    h = synth.activations(T, cfg.n_embd, seed=300 + T, device=dev) * scale
+    op, ip, wp = lp(h)
+    om, im, wm = lm(h)
+    assert torch.equal(ip, im) and torch.equal(wp, wm)
+    assert bool(torch.isfinite(om).all())
+    assert rel_max(to_np(om), to_np(op)) < 1e-5
+    ref, _, _, _ = _oracle_layer(cfg, t, h.cpu().numpy())
+    assert rel_max(to_np(om), ref) < 1e-5
+
+
+def test_config4_qwen3_t32_mfma(dev):
+    """BASELINE config 4 at T=32 on the matrix cores: within 1e-5 of the per-pair kernels on all
+    32 tokens; the oracle checks 2."""
+    from nurostream_amd import synth
+    cfg = synth.QWEN3_235B
+    t = synth.make_layer(cfg, seed=0, device=dev)
+    lm = _layer(cfg, t, "gguf", dispatch="mfma")
+    lp = _layer(cfg, t, "gguf", dispatch="pairs")
+    h = synth.activations(32, cfg.n_embd, seed=9, device=dev)
+    om, im, _ = lm(h)
+    op, ip, _ = lp(h)
+    assert torch.equal(im, ip)
+    assert rel_max(to_np(om), to_np(op)) < 1e-5
+    sub = slice(0, 2)
+    ref, rid, _, _ = _oracle_layer(cfg, t, h[sub].cpu().numpy())
+    np.testing.assert_array_equal(np.sort(to_np(im)[sub], 1), np.sort(rid, 1))
+    assert rel_max(to_np(om)[sub], ref) < 1e-5
