@@ -292,8 +292,9 @@ def layer_workload(args, torch, N, synth, dev):
     if layout == "t64":
         gu_kernel = "moe_gu_grouped_kernel" if grouped else "moe_gu_kernel"
     elif cfg.ggml_type == synth.GGMLType.Q4_K:  # stacked 16-byte aligned Q4_K experts take the Q4_K kernels
-        gu_kernel = {"mfma": "moe_q4k_mfma_kernel<true>", "grouped": "moe_gu_q4k_grouped_kernel"}.get(
-            args.dispatch, "moe_gu_q4k_kernel")
+        mq = args.dispatch == "mfma" or (args.dispatch == "auto" and T >= 8)
+        gu_kernel = "moe_q4k_mfma_kernel<true>" if mq else (
+            "moe_gu_q4k_grouped_kernel" if args.dispatch == "grouped" else "moe_gu_q4k_kernel")
     else:
         gu_kernel = "moe_gu_raw_kernel"
     gu_bytes, dn_bytes = _expert_bytes(cfg, mean_distinct)

@@ -54,10 +54,11 @@ enum { NSX_ACT_CLAMPED_SWIGLU = 0, NSX_ACT_SILU_MUL = 1 };
 /* How nsx_moe_forward runs the routed experts: per (token, expert) pair, or
  * grouped (pairs sorted by expert; each active expert's weights read once per
  * work item of up to 16 of its tokens; t64 MXFP4 layers, and stacked 16-byte
- * aligned Q4_K rows with K <= 4096). AUTO groups t64 layers from T >= 8.
- * MFMA: grouped stacked Q4_K on the matrix cores (f16 products of the exact
- * sc * q codes and a two-term split of the activations; outputs within 1e-5
- * of the per-pair kernels' rather than identical to them). */
+ * aligned Q4_K rows with K <= 4096). MFMA: grouped stacked Q4_K on the
+ * matrix cores (f16 products of the exact sc * q codes and a two-term split
+ * of the activations; outputs within 1e-5 of the per-pair kernels' rather
+ * than identical to them). AUTO groups t64 layers, and takes MFMA for
+ * stacked aligned Q4_K layers, from T >= 8; below that it runs pairs. */
 enum { NSX_DISPATCH_AUTO = 0, NSX_DISPATCH_PAIRS = 1, NSX_DISPATCH_GROUPED = 2, NSX_DISPATCH_MFMA = 3 };
 
 const char *nsx_last_error(void);

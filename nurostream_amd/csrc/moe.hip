@@ -1596,11 +1596,8 @@ __global__ __launch_bounds__(256) void mq_terms_kernel(const float* __restrict__
 // 0x64 : b (v_perm against a register of 0x64 bytes) after masking one
 // nibble: 1024 + q for the low one; 1024 + 16 q for the high one, left in
 // place, so its multiplier is sc / 16 (exact in f16).
-__device__ __forceinline__ void mq_a_pair(uint2 q, int sc_lo, int sc_hi, mq_h8& alo, mq_h8& ahi) {
-  const _Float16 fl = (_Float16)sc_lo, fh = (_Float16)((float)sc_hi * 0.0625f);
-  const mq_h2 ml = {fl, fl}, mh = {fh, fh};
-  const _Float16 cl0 = (_Float16)(-1024.f * (float)sc_lo), ch0 = (_Float16)(-64.f * (float)sc_hi);
-  const mq_h2 cl = {cl0, cl0}, ch = {ch0, ch0};
+// ml = (sc_lo, sc_lo), cl = -1024 ml, mh = (sc_hi / 16, sc_hi / 16), ch = -1024 mh.
+__device__ __forceinline__ void mq_a_pair(uint2 q, mq_h2 ml, mq_h2 cl, mq_h2 mh, mq_h2 ch, mq_h8& alo, mq_h8& ahi) {
   const uint32_t w[2] = {q.x, q.y};
   uint32_t lo[4], hi[4];
 #pragma unroll
@@ -1626,31 +1623,35 @@ __device__ __forceinline__ void mq_a_pair(uint2 q, int sc_lo, int sc_hi, mq_h8& 
 __device__ __forceinline__ void mq_superblock(const v4u& H, const uint2 (&Q)[4], const mq_h8 (&BH)[8],
                                               const mq_h8 (&BL)[8], const mq_h8& SH, const mq_h8& SL, int g,
                                               mq_f4& y) {
-  auto byte = [&](int i) {  // scales[i] = header byte 4 + i
-    const uint32_t w = i < 4 ? H.y : (i < 8 ? H.z : H.w);
-    return (int)((w >> (8 * (i & 3))) & 0xFFu);
-  };
-  int sc[8], mn[8];  // get_scale_min_k4
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sc[j] = byte(j) & 63;
-    mn[j] = byte(j + 4) & 63;
-    sc[j + 4] = (byte(j + 8) & 0xF) | ((byte(j) >> 6) << 4);
-    mn[j + 4] = (byte(j + 8) >> 4) | ((byte(j + 4) >> 6) << 4);
-  }
+  // get_scale_min_k4 for all 8 sub-blocks at once: byte s of SC / MN (scales
+  // bytes 0-3 = H.y, 4-7 = H.z, 8-11 = H.w)
+  const uint32_t SC03 = H.y & 0x3F3F3F3Fu, MN03 = H.z & 0x3F3F3F3Fu;
+  const uint32_t SC47 = (H.w & 0x0F0F0F0Fu) | ((H.y >> 2) & 0x30303030u);
+  const uint32_t MN47 = ((H.w >> 4) & 0x0F0F0F0Fu) | ((H.z >> 2) & 0x30303030u);
+  // a byte b under 0x64 is the f16 1024 + b
+  auto biased = [](uint32_t w, uint32_t sel) { return __builtin_bit_cast(mq_h2, __builtin_amdgcn_perm(0x64646464u, w, sel)); };
+  const mq_h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f}, km1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+  const mq_h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, km64 = {(_Float16)-64.f, (_Float16)-64.f};
   mq_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    const uint32_t SCW = j < 2 ? SC03 : SC47;
+    const uint32_t blo = 2u * (j & 1), bhi = blo + 1u;  // bytes of sub-blocks 2j, 2j + 1
+    const mq_h2 ml = biased(SCW, 0x04000400u | (blo << 16) | blo) - k1024;
+    const mq_h2 mh = __builtin_elementwise_fma(biased(SCW, 0x04000400u | (bhi << 16) | bhi), k16, km64);
     mq_h8 alo, ahi;
-    mq_a_pair(Q[j], sc[2 * j], sc[2 * j + 1], alo, ahi);
+    mq_a_pair(Q[j], ml, ml * km1024, mh, mh * km1024, alo, ahi);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[2 * j], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[2 * j], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[2 * j + 1], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BL[2 * j + 1], acc, 0, 0, 0);
   }
-  mq_h8 A2;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) A2[j] = g == 0 ? (_Float16)mn[j] : (_Float16)0.f;
+  // A2 row = the 8 sub-block mins at k 0..7 (group 0), zero elsewhere
+  const uint32_t m01 = __builtin_bit_cast(uint32_t, biased(MN03, 0x04010400u) - k1024);
+  const uint32_t m23 = __builtin_bit_cast(uint32_t, biased(MN03, 0x04030402u) - k1024);
+  const uint32_t m45 = __builtin_bit_cast(uint32_t, biased(MN47, 0x04010400u) - k1024);
+  const uint32_t m67 = __builtin_bit_cast(uint32_t, biased(MN47, 0x04030402u) - k1024);
+  const mq_h8 A2 = __builtin_bit_cast(mq_h8, g == 0 ? v4u{m01, m23, m45, m67} : v4u{0u, 0u, 0u, 0u});
   mq_f4 am = {0.f, 0.f, 0.f, 0.f};
   am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, SH, am, 0, 0, 0);
   am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, SL, am, 0, 0, 0);
@@ -1790,14 +1791,16 @@ static bool q4k_fast(const nsx_moe_layer* L) {
   return false;  // address tables: alignment unknown on the host
 }
 
-// Grouped Q4_K on the matrix cores (moe_q4k_mfma_kernel).
-static bool use_mq(const nsx_moe_layer* L, int64_t) {
-  return L->dispatch == NSX_DISPATCH_MFMA && L->layout == NSX_LAYOUT_GGUF && q4k_fast(L);
+// Grouped Q4_K on the matrix cores (moe_q4k_mfma_kernel): on request, and by
+// AUTO from GRP_AUTO_MIN_T tokens (config 4, T=32: 0.58 ms against 0.92 ms per pair).
+static bool use_mq(const nsx_moe_layer* L, int64_t T) {
+  const bool want = L->dispatch == NSX_DISPATCH_MFMA || (L->dispatch == NSX_DISPATCH_AUTO && T >= GRP_AUTO_MIN_T);
+  return want && L->layout == NSX_LAYOUT_GGUF && q4k_fast(L);
 }
 
 static bool use_grouped(const nsx_moe_layer* L, int64_t T) {
   if (L->dispatch == NSX_DISPATCH_GROUPED || use_mq(L, T)) return true;
-  // Q4_K groups on request only: its grouped kernels measure slower than the per-pair ones at T=32
+  // Q4_K: AUTO groups through use_mq (the VALU grouped kernels measure slower than the per-pair ones)
   return L->dispatch == NSX_DISPATCH_AUTO && L->layout == NSX_LAYOUT_T64 && T >= GRP_AUTO_MIN_T;
 }
 

@@ -44,7 +44,8 @@ class MoELayer:
         active expert once per work item of up to 16 tokens (t64 layout),
         "auto" groups from 8 tokens on (t64). These give identical outputs.
         "mfma" groups stacked Q4_K experts and runs them on the matrix cores
-        (within 1e-5 of the others, not identical)."""
+        (within 1e-5 of the others, not identical); "auto" takes it for such
+        layers from 8 tokens on."""
         if dispatch not in _DISPATCH:
             raise ValueError(f"dispatch {dispatch!r} not in {sorted(_DISPATCH)}")
         self.device = router_w.device
