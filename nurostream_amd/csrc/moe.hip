@@ -1620,7 +1620,7 @@ __device__ __forceinline__ void mq_a_pair(uint2 q, mq_h2 ml, mq_h2 cl, mq_h2 mh,
 // One super-block of one matrix: header H (d | dmin, scales[12]) and the
 // lane's code bytes Q[j] (sub-block pair j) -> y (rows 4 g + i, the lane's
 // token) += d * (sc q . x) - dmin * (m . xsum).
-__device__ __forceinline__ void mq_superblock(const v4u& H, const uint2 (&Q)[4], const mq_h8 (&BH)[8],
+__device__ __forceinline__ void mq_superblock(const v4u& H, const v4u& QA, const v4u& QB, const mq_h8 (&BH)[8],
                                               const mq_h8 (&BL)[8], const mq_h8& SH, const mq_h8& SL, int g,
                                               mq_f4& y) {
   // get_scale_min_k4 for all 8 sub-blocks at once: byte s of SC / MN (scales
@@ -1632,19 +1632,23 @@ __device__ __forceinline__ void mq_superblock(const v4u& H, const uint2 (&Q)[4],
   auto biased = [](uint32_t w, uint32_t sel) { return __builtin_bit_cast(mq_h2, __builtin_amdgcn_perm(0x64646464u, w, sel)); };
   const mq_h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f}, km1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
   const mq_h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, km64 = {(_Float16)-64.f, (_Float16)-64.f};
+  // lane group g holds sub-block pair g (sub-blocks 2g, 2g + 1): its two scales
+  const uint32_t SCW = g < 2 ? SC03 : SC47;
+  const uint32_t blo = 2u * (uint32_t)(g & 1), bhi = blo + 1u;
+  const mq_h2 ml = biased(SCW, 0x04000400u | (blo << 16) | blo) - k1024;
+  const mq_h2 mh = __builtin_elementwise_fma(biased(SCW, 0x04000400u | (bhi << 16) | bhi), k16, km64);
+  const mq_h2 cl = ml * km1024, ch = mh * km1024;
   mq_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t SCW = j < 2 ? SC03 : SC47;
-    const uint32_t blo = 2u * (j & 1), bhi = blo + 1u;  // bytes of sub-blocks 2j, 2j + 1
-    const mq_h2 ml = biased(SCW, 0x04000400u | (blo << 16) | blo) - k1024;
-    const mq_h2 mh = __builtin_elementwise_fma(biased(SCW, 0x04000400u | (bhi << 16) | bhi), k16, km64);
+  for (int t = 0; t < 4; ++t) {  // code bytes 8t .. 8t + 7 of the pair
+    const uint2 q8 = t == 0 ? uint2{QA.x, QA.y} : t == 1 ? uint2{QA.z, QA.w} : t == 2 ? uint2{QB.x, QB.y}
+                                                                                     : uint2{QB.z, QB.w};
     mq_h8 alo, ahi;
-    mq_a_pair(Q[j], ml, ml * km1024, mh, mh * km1024, alo, ahi);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[2 * j], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[2 * j], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[2 * j + 1], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BL[2 * j + 1], acc, 0, 0, 0);
+    mq_a_pair(q8, ml, cl, mh, ch, alo, ahi);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[t], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[t], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[4 + t], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BL[4 + t], acc, 0, 0, 0);
   }
   // A2 row = the 8 sub-block mins at k 0..7 (group 0), zero elsewhere
   const uint32_t m01 = __builtin_bit_cast(uint32_t, biased(MN03, 0x04010400u) - k1024);
@@ -1699,26 +1703,25 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   const uint8_t* tbase = GU ? a.xq_h : (const uint8_t*)a.xq_a;
   // terms rows: GU one per token (T), else one per pair (T * top_k)
   const __amdgpu_buffer_rsrc_t rt = nsx_rsrc(tbase, (uint32_t)((int64_t)(GU ? a.T : a.T * a.top_k) * tb));
-  const uint32_t tv_off = (uint32_t)(brow * tb) + 16u * (uint32_t)g;  // the lane's token row, k-group g
+  // the lane's token row; lane group g takes elements 64 g .. 64 g + 63 of each super-block
+  const uint32_t tv_off = (uint32_t)(brow * tb) + 128u * (uint32_t)g;
   const uint32_t ts_off = (uint32_t)(brow * tb);
   // Weights are double-buffered: a super-block's activation terms (L2) are
   // loaded first, then the next super-block's weights (HBM), so waiting for
   // the terms does not wait for the prefetch (loads complete in order).
+  // lane group g reads code bytes 32 g .. 32 g + 31 (sub-block pair g) as two 16-byte loads
   struct W {
-    v4u H0, H1;
-    uint2 Q0[4], Q1[4];
+    v4u H0, H1, A0, B0, A1, B1;
   };
   auto load_w = [&](int sb, W& o) {
-    const uint32_t b = arow_off + (uint32_t)sb * 144u;
+    const uint32_t b = arow_off + (uint32_t)sb * 144u, q = b + 16u + 32u * (uint32_t)g;
     o.H0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, b, 0, 0));
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o.Q0[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs0, b + 16u + 32u * j + 8u * g, 0, 0));
+    o.A0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q, 0, 0));
+    o.B0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q + 16u, 0, 0));
     if constexpr (GU) {
       o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, b, 0, 0));
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        o.Q1[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs1, b + 16u + 32u * j + 8u * g, 0, 0));
+      o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q, 0, 0));
+      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q + 16u, 0, 0));
     }
   };
   mq_f4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
@@ -1726,9 +1729,10 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
     mq_h8 BH[8], BL[8];
     const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {
-      BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + 64u * s8, sh_off, 0));
-      BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + 64u * s8, sl_off, 0));
+    for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: elements 64 g + 32 hi + 8 t .. + 7
+      const uint32_t o = tv_off + 64u * (uint32_t)(s8 >> 2) + 16u * (uint32_t)(s8 & 3);
+      BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, o, sh_off, 0));
+      BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, o, sl_off, 0));
     }
     // sub-block sums after the terms; the min term's A operand is zero outside
     // k < 8 (g == 0), so every group may load the same sums
@@ -1736,8 +1740,8 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
     const mq_h8 SL =
         __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
     if (sb + 1 < nsb) load_w(sb + 1, nxt);
-    mq_superblock(cur.H0, cur.Q0, BH, BL, SH, SL, g, y0);
-    if constexpr (GU) mq_superblock(cur.H1, cur.Q1, BH, BL, SH, SL, g, y1);
+    mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
+    if constexpr (GU) mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
   };
   W wa, wb;
   load_w(0, wa);
