@@ -1632,19 +1632,27 @@ __device__ __forceinline__ void mq_superblock(const v4u& H, const v4u& QA, const
   auto biased = [](uint32_t w, uint32_t sel) { return __builtin_bit_cast(mq_h2, __builtin_amdgcn_perm(0x64646464u, w, sel)); };
   const mq_h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f}, km1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
   const mq_h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, km64 = {(_Float16)-64.f, (_Float16)-64.f};
-  // lane group g holds sub-block pair g (sub-blocks 2g, 2g + 1): its two scales
-  const uint32_t SCW = g < 2 ? SC03 : SC47;
-  const uint32_t blo = 2u * (uint32_t)(g & 1), bhi = blo + 1u;
-  const mq_h2 ml = biased(SCW, 0x04000400u | (blo << 16) | blo) - k1024;
-  const mq_h2 mh = __builtin_elementwise_fma(biased(SCW, 0x04000400u | (bhi << 16) | bhi), k16, km64);
-  const mq_h2 cl = ml * km1024, ch = mh * km1024;
+  // lane group g holds half (g & 1) of sub-block pairs g / 2 (QA) and
+  // 2 + g / 2 (QB): their scales (pair p = sub-blocks 2p, 2p + 1)
+  const uint32_t blo = 2u * (uint32_t)(g >> 1), bhi = blo + 1u;  // bytes of pair g / 2 in SC03, of pair 2 + g / 2 in SC47
+  const uint32_t sel_lo = 0x04000400u | (blo << 16) | blo, sel_hi = 0x04000400u | (bhi << 16) | bhi;
+  mq_h2 ml[2], mh[2], cl[2], ch[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const uint32_t SCW = u == 0 ? SC03 : SC47;
+    ml[u] = biased(SCW, sel_lo) - k1024;
+    mh[u] = __builtin_elementwise_fma(biased(SCW, sel_hi), k16, km64);
+    cl[u] = ml[u] * km1024;
+    ch[u] = mh[u] * km1024;
+  }
   mq_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {  // code bytes 8t .. 8t + 7 of the pair
+  for (int t = 0; t < 4; ++t) {  // t < 2: QA's bytes 8t .., t >= 2: QB's bytes 8 (t - 2) ..
     const uint2 q8 = t == 0 ? uint2{QA.x, QA.y} : t == 1 ? uint2{QA.z, QA.w} : t == 2 ? uint2{QB.x, QB.y}
                                                                                      : uint2{QB.z, QB.w};
+    const int u = t >> 1;
     mq_h8 alo, ahi;
-    mq_a_pair(q8, ml, cl, mh, ch, alo, ahi);
+    mq_a_pair(q8, ml[u], cl[u], mh[u], ch[u], alo, ahi);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[t], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[t], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[4 + t], acc, 0, 0, 0);
@@ -1703,25 +1711,27 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   const uint8_t* tbase = GU ? a.xq_h : (const uint8_t*)a.xq_a;
   // terms rows: GU one per token (T), else one per pair (T * top_k)
   const __amdgpu_buffer_rsrc_t rt = nsx_rsrc(tbase, (uint32_t)((int64_t)(GU ? a.T : a.T * a.top_k) * tb));
-  // the lane's token row; lane group g takes elements 64 g .. 64 g + 63 of each super-block
-  const uint32_t tv_off = (uint32_t)(brow * tb) + 128u * (uint32_t)g;
+  // the lane's token row; lane group g takes, in each super-block, elements
+  // 64 p + 32 hi + 16 (g & 1) + 0..15 of pairs p = g / 2 and 2 + g / 2
+  const uint32_t tv_off = (uint32_t)(brow * tb) + 2u * (64u * (uint32_t)(g >> 1) + 16u * (uint32_t)(g & 1));
   const uint32_t ts_off = (uint32_t)(brow * tb);
   // Weights are double-buffered: a super-block's activation terms (L2) are
   // loaded first, then the next super-block's weights (HBM), so waiting for
   // the terms does not wait for the prefetch (loads complete in order).
-  // lane group g reads code bytes 32 g .. 32 g + 31 (sub-block pair g) as two 16-byte loads
+  // lane group g reads code bytes 16 g .. + 15 and 64 + 16 g .. + 15, so each
+  // load instruction covers 64 contiguous bytes of a row
   struct W {
     v4u H0, H1, A0, B0, A1, B1;
   };
   auto load_w = [&](int sb, W& o) {
-    const uint32_t b = arow_off + (uint32_t)sb * 144u, q = b + 16u + 32u * (uint32_t)g;
+    const uint32_t b = arow_off + (uint32_t)sb * 144u, q = b + 16u + 16u * (uint32_t)g;
     o.H0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, b, 0, 0));
     o.A0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q, 0, 0));
-    o.B0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q + 16u, 0, 0));
+    o.B0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q + 64u, 0, 0));
     if constexpr (GU) {
       o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, b, 0, 0));
       o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q, 0, 0));
-      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q + 16u, 0, 0));
+      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q + 64u, 0, 0));
     }
   };
   mq_f4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
@@ -1729,8 +1739,9 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
     mq_h8 BH[8], BL[8];
     const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: elements 64 g + 32 hi + 8 t .. + 7
-      const uint32_t o = tv_off + 64u * (uint32_t)(s8 >> 2) + 16u * (uint32_t)(s8 & 3);
+    for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: pair (t >> 1) * 2 + g / 2, elements + 32 hi + 8 (t & 1)
+      const int t = s8 & 3;
+      const uint32_t o = tv_off + 2u * (128u * (uint32_t)(t >> 1) + 32u * (uint32_t)(s8 >> 2) + 8u * (uint32_t)(t & 1));
       BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, o, sh_off, 0));
       BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, o, sl_off, 0));
     }
