@@ -580,6 +580,7 @@ struct MoeDev {
   float* y;              // (pairs, n_embd) expert outputs, bias included
   int max_items;
   int cdg, sdg;          // grouped down: K-chunks and K-steps per chunk
+  int topk_in_gu;        // per-pair Q4_K: the gate/up kernel selects the top-k (no top-k launch)
 };
 
 __device__ __forceinline__ float moe_act(int kind, float g, float u, float alpha, float limit) {
@@ -1293,13 +1294,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void m
   nsx_hoist(a.n_ff, a.n_embd, a.top_k, a.E, (const void*)a.ids, (const void*)a.h, a.gate_base, a.up_base,
             (const void*)a.gate_ptrs, (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias,
             (const void*)a.up_bias, (const void*)a.act, a.act_kind, a.alpha, a.limit);
+  __shared__ int s_e;
   const int groups = (a.n_ff + RPG - 1) / RPG;
   const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
   const int K = a.n_embd, t = p / a.top_k;
-  const int e = clamp_expert(a.ids[p], a.E);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  if (a.topk_in_gu && wave == 0) {
+    // the top-k from the router's logits by wave 0 (as moe_gu_kernel); the
+    // token's first workgroup also writes the ids / weights the down phase reads
+    const int k = a.top_k, j = p - t * k;
+    int si[MAX_TOPK];
+    float sw[MAX_TOPK];
+    const bool writes = j == 0 && r0 == 0;
+    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes);
+    int my_e = 0, ej = 0;
+    float my_w = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      ej = jj == j ? si[jj] : ej;
+      my_e = lane == jj ? si[jj] : my_e;
+      my_w = lane == jj ? sw[jj] : my_w;
+    }
+    if (writes && lane < k) {
+      a.ids[(int64_t)t * k + lane] = clamp_expert(my_e, a.E);
+      a.wts[(int64_t)t * k + lane] = my_w;
+    }
+    if (lane == 0) s_e = clamp_expert(ej, a.E);
+  }
   for (int i = threadIdx.x; i < K / 4; i += blockDim.x) ((v4f*)q4k_xs)[i] = ((const v4f*)(a.h + (int64_t)t * K))[i];
   __syncthreads();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int e = a.topk_in_gu ? s_e : clamp_expert(a.ids[p], a.E);
   const int nu = K / 32;
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
   const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
@@ -2021,6 +2045,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.max_items = p.max_items;
   d.cdg = p.cdg;
   d.sdg = p.sdg;
+  d.topk_in_gu = !t64 && !p.grouped && q4k_fast(L) && T < RM_MIN_T;  // the MFMA router selects in its reduce
 
   auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
   if (on(NSX_PHASE_ROUTER)) {
@@ -2033,7 +2058,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
       rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
                          (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
       if (rc) return rc;
-      if ((!t64 || p.grouped) &&  // the per-pair t64 kernels select the top-k themselves
+      if ((!t64 || p.grouped) && !d.topk_in_gu &&  // the per-pair t64 and Q4_K kernels select the top-k themselves
           (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
         return rc;
     }
