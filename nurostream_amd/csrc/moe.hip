@@ -1710,10 +1710,14 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   const int NR = GU ? a.n_ff : a.n_embd, K = GU ? a.n_embd : a.n_ff;
   int tile;
   int4 item;
-  if (!grp_work(a, (NR + MQ_WG_ROWS - 1) / MQ_WG_ROWS, tile, item)) return;
+  // down: two 16-row tiles per wave (the second in the H1/A1/B1, y1 slots
+  // that gate/up uses for the up matrix), so a wave's activation-term loads
+  // serve twice the weight bytes
+  constexpr int TILES = GU ? 1 : 2;
+  if (!grp_work(a, (NR + TILES * MQ_WG_ROWS - 1) / (TILES * MQ_WG_ROWS), tile, item)) return;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int lr = lane & 15, g = lane >> 4;
-  const int r0 = tile * MQ_WG_ROWS + wave * MQ_ROWS;
+  const int r0 = (tile * MQ_WG_ROWS + wave * MQ_ROWS) * TILES;
   if (r0 >= NR) return;  // no barriers below
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
   const int nsb = K / 256;
@@ -1721,6 +1725,7 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   // weights through buffer loads (an expert matrix: NR rows of rb bytes), so
   // they are tracked by the vector-memory counter alone
   const uint32_t arow_off = (uint32_t)(min(r0 + lr, NR - 1) * rb);
+  const uint32_t arow1_off = GU ? arow_off : (uint32_t)(min(r0 + MQ_ROWS + lr, NR - 1) * rb);
   const __amdgpu_buffer_rsrc_t rs0 = nsx_rsrc(expert_base(GU ? a.gate_base : a.down_base, GU ? a.gate_stride : a.down_stride,
                                                           GU ? a.gate_ptrs : a.down_ptrs, e),
                                               (uint32_t)(NR * rb));
@@ -1756,6 +1761,11 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
       o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, b, 0, 0));
       o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q, 0, 0));
       o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q + 64u, 0, 0));
+    } else {  // the second row tile
+      const uint32_t b1 = arow1_off + (uint32_t)sb * 144u, q1 = b1 + 16u + 16u * (uint32_t)g;
+      o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, b1, 0, 0));
+      o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q1, 0, 0));
+      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q1 + 64u, 0, 0));
     }
   };
   mq_f4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
@@ -1776,7 +1786,7 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
         __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
     if (sb + 1 < nsb) load_w(sb + 1, nxt);
     mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
-    if constexpr (GU) mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
+    mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
   };
   W wa, wb;
   load_w(0, wa);
@@ -1798,6 +1808,16 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
       a.act[(int64_t)pr * a.n_ff + row] = moe_act(a.act_kind, gv, uv, a.alpha, a.limit);
     } else {
       float v = y0[i] * scale;
+      if (a.down_bias) v += a.down_bias[(int64_t)e * a.n_embd + row];
+      a.y[(int64_t)pr * a.n_embd + row] = v;
+    }
+  }
+  if constexpr (!GU) {  // the second row tile
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = r0 + MQ_ROWS + 4 * g + i;
+      if (!tv || row >= NR) continue;
+      float v = y1[i] * scale;
       if (a.down_bias) v += a.down_bias[(int64_t)e * a.n_embd + row];
       a.y[(int64_t)pr * a.n_embd + row] = v;
     }
@@ -2092,7 +2112,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
                              (int)L->n_ff, d.xq_a)))
           return rc;
-        rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, MQ_WG_ROWS)), dim3(256), 0, st, d);
+        rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, 2 * MQ_WG_ROWS)), dim3(256), 0, st, d);
       } else {
         const int64_t g = nsx_cdiv(L->n_embd, Q4K_DG_WAVES * Q4K_DG_RPW);
         rc = L->n_ff > 64 * 32
