@@ -69,6 +69,15 @@ int nsx_abi_version(void);
  * one device uint32. No reference counterpart (a load-time self test). */
 int nsx_selftest(uint32_t *scratch, void *stream);
 
+/* No reference counterpart: a read-bandwidth probe, the same-box denominator
+ * the expert kernels' HBM fractions are set beside. `workgroups` workgroups of
+ * `threads` threads (a multiple of 64, <= 1024) read `bytes` (a multiple of
+ * 16, src 16-byte aligned) in equal contiguous shares with 16-byte
+ * nontemporal loads, 8 per thread in flight; nothing is written unless the
+ * bytes fold to one fixed word (then one word of sink). */
+int nsx_read_probe(const void *src, int64_t bytes, int workgroups, int threads,
+                   uint32_t *sink, void *stream);
+
 /* compute/quant.py:153-184 dequantize(raw, dtype, n_elements, out_dtype).
  * raw: `raw_bytes` bytes of ggml blocks (any alignment); out: n_elements of
  * out_dtype. Bit-exact with the reference for Q4_0, Q8_0, Q4_K, Q6_K, MXFP4
@@ -170,18 +179,20 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
                     float *out, int32_t *ids, float *weights, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
-/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits; the top-k and the
- * ids/weights outputs except for the per-pair t64 kernels, which select it
- * themselves; in the t64 layout also the activation terms of h),
- * NSX_PHASE_GATE_UP (grouped dispatch: the sort by expert; expert gate/up
- * GEMVs + activation; the per-pair t64 kernel also selects the top-k and
- * writes ids/weights), NSX_PHASE_DOWN (expert down GEMVs; per-pair dispatch
- * also the weighted combine into out)
+/* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, the top-k and the
+ * ids/weights outputs, for every layout and dispatch; in the t64 layout also
+ * the activation terms of h), NSX_PHASE_GATE_UP (grouped dispatch: the sort
+ * by expert; expert gate/up GEMVs + activation; the per-pair t64 kernel
+ * selects the top-k again from the logits and rewrites the same ids/weights),
+ * NSX_PHASE_DOWN (expert down GEMVs; per-pair dispatch also the weighted
+ * combine into out)
  * and NSX_PHASE_COMBINE (grouped dispatch: the ascending-expert combine;
  * otherwise nothing). A phase reads what the earlier phases of the same call
  * sequence left in the workspace; running the four in order is
- * nsx_moe_forward. Callers use it to interleave other work (block reads,
- * another layer's router) between phases or to time one phase; the
+ * nsx_moe_forward (which skips the top-k launch where a gate/up kernel selects
+ * the top-k itself: per-pair t64, and per-pair Q4_K below 16 tokens). Callers
+ * use it to interleave other work (block reads, another layer's router)
+ * between phases or to time one phase; the
  * reference runs these steps as separate torch calls
  * (model/gpt_oss.py:123-177). */
 #define NSX_PHASE_ROUTER 0

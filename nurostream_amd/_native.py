@@ -59,6 +59,7 @@ _SIGS = {
     "nsx_last_error": (C.c_char_p, []),
     "nsx_abi_version": (_i, []),
     "nsx_selftest": (_i, [_p, _p]),
+    "nsx_read_probe": (_i, [_p, _i64, _i, _i, _p, _p]),
     "nsx_dequantize": (_i, [_i, _p, _i64, _i64, _p, _i, _p]),
     "nsx_fused_gemv": (_i, [_i, _p, _i64, _i64, _p, _i, _i64, _p, _p]),
     "nsx_fused_gemv_ex": (_i, [_i, _p, _i64, _i64, _p, _i, _i64, _p, _p, _p, _p]),

@@ -2065,7 +2065,13 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.max_items = p.max_items;
   d.cdg = p.cdg;
   d.sdg = p.sdg;
-  d.topk_in_gu = !t64 && !p.grouped && q4k_fast(L) && T < RM_MIN_T;  // the MFMA router selects in its reduce
+  // Per-pair Q4_K below RM_MIN_T tokens: the gate/up kernel selects the top-k itself (no top-k launch), but only
+  // when this call runs both phases -- a router phase run on its own always leaves the ids and weights written.
+  d.topk_in_gu = !t64 && !p.grouped && q4k_fast(L) && T < RM_MIN_T && ph0 <= NSX_PHASE_ROUTER &&
+                 ph1 >= NSX_PHASE_GATE_UP;
+  // The per-pair t64 gate/up kernel always selects the top-k itself; a router phase that ends the call launches
+  // the top-k too, so that phase-by-phase callers read the ids after it.
+  const bool router_alone = ph1 == NSX_PHASE_ROUTER;
 
   auto on = [&](int ph) { return ph0 <= ph && ph <= ph1; };
   if (on(NSX_PHASE_ROUTER)) {
@@ -2078,7 +2084,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
       rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
                          (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
       if (rc) return rc;
-      if ((!t64 || p.grouped) && !d.topk_in_gu &&  // the per-pair t64 and Q4_K kernels select the top-k themselves
+      if ((!t64 || p.grouped || router_alone) && !d.topk_in_gu &&  // else the gate/up kernel selects it
           (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
         return rc;
     }

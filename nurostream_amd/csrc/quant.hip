@@ -60,6 +60,50 @@ extern "C" int nsx_selftest(uint32_t* scratch, void* stream) {
 }
 
 // ---------------------------------------------------------------------------
+// Read-bandwidth probe: the denominator the expert kernels' HBM fractions are
+// read against on the same box. Workgroup b reads bytes [b * per, (b + 1) *
+// per) of src with 16-byte nontemporal loads, PROBE_U per thread in flight
+// at once (as the expert kernels issue their weight loads), and folds them
+// into one word that is stored only if it equals a constant no input of
+// interest produces -- so the loads cannot be dropped and nothing is written.
+
+constexpr int PROBE_U = 8;
+
+__global__ __launch_bounds__(1024) void read_probe_kernel(const v4u* __restrict__ src, int64_t n16, int64_t per16,
+                                                          uint32_t* __restrict__ sink) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  const int64_t lo = (int64_t)blockIdx.x * per16;
+  const int64_t hi = min(lo + per16, n16);
+  const int64_t step = (int64_t)blockDim.x * PROBE_U;
+  uint32_t acc = 0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += step) {
+    v4u v[PROBE_U];
+#pragma unroll
+    for (int u = 0; u < PROBE_U; ++u) {
+      const int64_t j = min(i + (int64_t)u * blockDim.x, hi - 1);  // in bounds; duplicates past hi are discarded
+      v[u] = __builtin_nontemporal_load((gv4u*)(src + j));
+    }
+#pragma unroll
+    for (int u = 0; u < PROBE_U; ++u)
+      acc ^= i + (int64_t)u * blockDim.x < hi ? (v[u].x ^ v[u].y ^ v[u].z ^ v[u].w) : 0u;
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+extern "C" int nsx_read_probe(const void* src, int64_t bytes, int workgroups, int threads, uint32_t* sink,
+                              void* stream) {
+  NSX_REQUIRE(src && sink, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE(bytes >= 16 && bytes % 16 == 0 && ((uintptr_t)src & 15u) == 0, NSX_EINVAL,
+              "the probe reads 16-byte aligned whole 16-byte units (%lld bytes)", (long long)bytes);
+  NSX_REQUIRE(workgroups >= 1 && workgroups <= (1 << 20), NSX_EINVAL, "workgroups=%d", workgroups);
+  NSX_REQUIRE(threads >= 64 && threads <= 1024 && threads % 64 == 0, NSX_EINVAL, "threads=%d", threads);
+  const int64_t n16 = bytes / 16;
+  const int64_t per16 = nsx_cdiv(n16, workgroups);
+  return nsx_launch(read_probe_kernel, dim3((unsigned)workgroups), dim3((unsigned)threads), 0, S(stream),
+                    (const v4u*)src, n16, per16, sink);
+}
+
+// ---------------------------------------------------------------------------
 // dequantize (quant.py:118-140, 24-56, 84-107, 110-115)
 //
 // A workgroup stages BPW consecutive blocks into LDS with range-checked dword

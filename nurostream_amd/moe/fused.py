@@ -128,14 +128,29 @@ class MoELayer:
             self._ws[T] = ws
         return ws
 
-    def forward(self, h: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
-                weights: torch.Tensor | None = None):
-        """h: (T, n_embd) fp32 -> (out (T, n_embd) fp32, ids (T, k) int32, weights (T, k) fp32)."""
+    def _check_buffers(self, T: int, out: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor) -> None:
+        """The native call writes through raw pointers: each output must be a
+        contiguous tensor of exactly the expected shape and dtype on this
+        layer's device, or a ValueError is raised before anything runs."""
+        for name, t, shape, dtype in (("out", out, (T, self.n_embd), torch.float32),
+                                      ("ids", ids, (T, self.top_k), torch.int32),
+                                      ("weights", weights, (T, self.top_k), torch.float32)):
+            if not isinstance(t, torch.Tensor):
+                raise ValueError(f"{name} must be a tensor")
+            if t.device != self.device:
+                raise ValueError(f"{name} is on {t.device}, the layer on {self.device}")
+            if t.dtype != dtype or tuple(t.shape) != shape or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous {dtype} tensor of shape {shape}, got "
+                                 f"{t.dtype} {tuple(t.shape)}{'' if t.is_contiguous() else ' (strided)'}")
+
+    def _prepare(self, h: torch.Tensor, out, ids, weights):
         N.require_device(h)
         h = h.reshape(-1, self.n_embd)
         if h.dtype != torch.float32:
             h = h.float()
         h = h.contiguous()
+        if h.device != self.device:
+            raise ValueError(f"h is on {h.device}, the layer on {self.device}")
         T = h.shape[0]
         if out is None:
             out = torch.empty((T, self.n_embd), dtype=torch.float32, device=self.device)
@@ -143,6 +158,13 @@ class MoELayer:
             ids = torch.empty((T, self.top_k), dtype=torch.int32, device=self.device)
         if weights is None:
             weights = torch.empty((T, self.top_k), dtype=torch.float32, device=self.device)
+        self._check_buffers(T, out, ids, weights)
+        return h, T, out, ids, weights
+
+    def forward(self, h: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                weights: torch.Tensor | None = None):
+        """h: (T, n_embd) fp32 -> (out (T, n_embd) fp32, ids (T, k) int32, weights (T, k) fp32)."""
+        h, T, out, ids, weights = self._prepare(h, out, ids, weights)
         ws = self.workspace(T)
         with torch.cuda.device(self.device):
             N.check(N.load().nsx_moe_forward(C.byref(self._c), h.data_ptr(), T, out.data_ptr(), ids.data_ptr(),
@@ -161,7 +183,11 @@ class MoELayer:
         if h.dtype != torch.float32 or not h.is_contiguous():
             raise TypeError("phase() takes a contiguous fp32 h")
         T = h.shape[0]
+        self._check_buffers(T, out, ids, weights)
         ws = self.workspace(T) if workspace is None else workspace
+        need = N.load().nsx_moe_workspace_bytes(C.byref(self._c), T)
+        if ws.device != self.device or ws.dtype != torch.uint8 or not ws.is_contiguous() or ws.numel() < need:
+            raise ValueError(f"workspace must be a contiguous uint8 tensor of >= {need} bytes on {self.device}")
         with torch.cuda.device(self.device):
             N.check(N.load().nsx_moe_phase(C.byref(self._c), int(phase), h.data_ptr(), T, out.data_ptr(),
                                            ids.data_ptr(), weights.data_ptr(), ws.data_ptr(), ws.numel(),

@@ -122,3 +122,23 @@ def test_validation_errors_return_codes(lib):
     assert rc == N.EINVAL
     with pytest.raises(ValueError):
         N.check(rc)
+
+
+def test_moe_layer_rejects_bad_outputs():
+    """MoELayer checks out / ids / weights before the native call writes
+    through their pointers (shape, dtype, contiguity, device)."""
+    import torch
+
+    from nurostream_amd.moe.fused import MoELayer
+    lay = MoELayer.__new__(MoELayer)
+    lay.device, lay.n_embd, lay.top_k = torch.device("cpu"), 16, 2
+    good = (torch.empty(3, 16), torch.empty(3, 2, dtype=torch.int32), torch.empty(3, 2))
+    lay._check_buffers(3, *good)
+    bad = [(torch.empty(3, 17), good[1], good[2]),
+           (good[0], torch.empty(3, 2, dtype=torch.int64), good[2]),
+           (good[0], good[1], torch.empty(2, 3).t()),
+           (torch.empty(16, 3).t(), good[1], good[2]),
+           (good[0], good[1], torch.empty(3, 2, dtype=torch.float16))]
+    for out, ids, w in bad:
+        with pytest.raises(ValueError):
+            lay._check_buffers(3, out, ids, w)

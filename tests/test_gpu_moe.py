@@ -132,3 +132,36 @@ def test_qwen3_layer_decode(dev):
     ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
     np.testing.assert_array_equal(to_np(ids), rid)
     assert rel_max(to_np(out), ref) < 1e-5
+
+
+@pytest.mark.parametrize("name,layout,T,dispatch", [("gptoss-small", "t64", 3, "auto"),
+                                                    ("gptoss-small", "t64", 20, "auto"),
+                                                    ("gptoss-small", "t64", 5, "grouped"),
+                                                    ("qwen3-small", "gguf", 2, "auto"),
+                                                    ("qwen3-small", "gguf", 17, "auto"),
+                                                    ("qwen3-small", "gguf", 3, "mfma"),
+                                                    ("q4_0-small", "gguf", 3, "auto")])
+def test_router_phase_alone_writes_ids(dev, name, layout, T, dispatch):
+    """NSX_PHASE_ROUTER run on its own leaves the ids and weights written for
+    every layout and dispatch (a caller reads them to queue expert block reads
+    before the gate/up phase), equal to what the whole forward writes; the
+    later phases then give the forward's output."""
+    from nurostream_amd import _native as N
+    from nurostream_amd import synth
+    cfg = _small(name)
+    t = synth.make_layer(cfg, seed=41, device=dev)
+    layer = _layer(cfg, t, layout, dispatch=dispatch)
+    h = synth.activations(T, cfg.n_embd, seed=42, device=dev)
+    ref_out, ref_ids, ref_w = layer.forward(h)
+    ws = layer.new_workspace(T)
+    out = torch.full_like(ref_out, float("nan"))
+    ids = torch.full_like(ref_ids, -1)
+    wts = torch.full_like(ref_w, float("nan"))
+    layer.phase(N.PHASE_ROUTER, h, out, ids, wts, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ref_ids)
+    assert torch.equal(wts, ref_w)
+    for ph in (N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE):
+        layer.phase(ph, h, out, ids, wts, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out)
