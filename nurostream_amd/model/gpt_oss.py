@@ -444,7 +444,6 @@ class GptOssModel:
         self._fused: dict[int, MoELayer] = {}
         self._acfg = None
         self._capturing: list | None = None
-        self._qkv: dict[int, tuple | None] = {}
 
     def w(self, name: str) -> torch.Tensor:
         t = self._w.get(name)
@@ -553,11 +552,9 @@ class GptOssModel:
         return self._acfg
 
     def _resident_raw(self, name: str):
-        """(raw device bytes, dtype) of a quantized tensor held whole in HBM, or None."""
-        hit = self.cache.raw_quantized(name)
-        if hit is None or not hit[0].is_cuda:
-            return None
-        return hit
+        """(raw device bytes, dtype) of a quantized tensor held whole in the HBM
+        tier, or None (a RAM-tier tensor is not: it takes the streamed paths)."""
+        return self.cache.vram_raw(name)
 
     def _linear(self, name: str, x: torch.Tensor) -> torch.Tensor:
         """x @ W.T in fp32 (model/qwen3.py:169-194): the fused GEMV on HBM-resident
@@ -594,21 +591,19 @@ class GptOssModel:
                             for t in ids.tolist()])
 
     def _qkv_raw(self, layer: int):
-        """(raw bytes, dtype, rows) of the layer's q, k and v weights concatenated
-        once in HBM -- one GEMV then writes the q | k | v block -- or None when
-        they are not all resident quantized rows of one type."""
+        """(raw bytes, dtype, rows) of the layer's q, k and v weights laid out
+        back to back in HBM by the cache (TieredCache.fuse_vram: the three
+        residents become views of one buffer, no extra bytes) -- one GEMV then
+        writes the q | k | v block -- or None when they are not all HBM-tier
+        quantized rows of one type."""
         from ..format.gguf import row_geometry
-        if layer in self._qkv:
-            return self._qkv[layer]
         p = f"blk.{layer}."
         names = [p + n + ".weight" for n in ("attn_q", "attn_k", "attn_v")]
-        hits = [self._resident_raw(n) for n in names]
-        got = None
-        if all(h is not None for h in hits) and len({h[1] for h in hits}) == 1:
-            rows = sum(row_geometry(self.gguf.tensors[n])[0] for n in names)
-            got = (torch.cat([h[0].reshape(-1) for h in hits]), hits[0][1], rows)
-        self._qkv[layer] = got
-        return got
+        got = self.cache.fuse_vram(names)
+        if got is None:
+            return None
+        rows = sum(row_geometry(self.gguf.tensors[n])[0] for n in names)
+        return got[0], got[1], rows
 
     def _attention_block(self, x: torch.Tensor, layer: int, kv, pending: torch.Tensor | None = None) -> torch.Tensor:
         """x + o_proj(sink_attention(...)) for the one token at kv.pos (gpt_oss.py:101-114).
