@@ -1,20 +1,24 @@
-"""Public surface of the reference (api.py:30-237, 342-388) over this build's MoE path.
+"""Public surface of the reference (api.py:30-237, 336-441) over this build's MoE path.
 
     ns = NeuroStream.load("model.gguf", mem_budget="2GB", slab_budget="60GB")
     y = ns.model.ffn_stack(x)          # every layer's routed-expert FFN block
+    for piece in ns.generate([1, 2, 3], max_tokens=16): ...
     ns.pin_hot_experts()
+    print(ns.report())
+    ns.close()                         # or: with NeuroStream.load(...) as ns:
 
 `NeuroStream.load` keeps the reference's keyword arguments and their meaning
 for the parts this build covers: the arena budget (`mem_budget`), VRAM/RAM
 tiers, expert slabs in HBM (`slab_budget`, admitted in layer order as t64
 tiles), `block_rows` and `expert_lookahead` for the streamed neuron path.
-`generate` needs the token embedding, attention (sink attention with YaRN
-RoPE), the output norm, the LM head and the tokenizer, which this build does
-not implement: it raises NotImplementedError instead of producing tokens.
+`generate` runs a GPT-OSS GGUF token by token on the device (embedding,
+attention with YaRN rotary and sinks, the MoE FFN, the LM head) and takes
+the prompt as token ids: the GGUF tokenizer is outside this build, so a str
+prompt raises NotImplementedError. `report()` gathers the arena, reader,
+cache, router and generation counters.
 """
 from __future__ import annotations
 
-import re
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -26,18 +30,31 @@ from .io.arena import Arena
 from .io.stream import DiskSource
 from .residency.cache import TieredCache
 
-_SIZE_RE = re.compile(r"^\s*([\d.]+)\s*([KMGT]?)B?\s*$", re.I)
-_MULT = {"": 1, "K": 1 << 10, "M": 1 << 20, "G": 1 << 30, "T": 1 << 40}
+_UNIT_SHIFT = {"": 0, "K": 10, "M": 20, "G": 30, "T": 40}
 
 
 def parse_size(v: int | str) -> int:
-    """api.py:30-37: ints pass through; "2GB", "1.5G", "512M", "64K" (powers of 1024)."""
+    """A byte count from an int (returned as is) or a string such as "2GB",
+    "1.5G", "512MiB", "64K" or "4096": K / M / G / T are powers of 1024, the
+    trailing "B" / "iB" optional (api.py:30-37 accepts the same forms)."""
+    if isinstance(v, bool):
+        raise ValueError(f"cannot parse size: {v!r}")
     if isinstance(v, int):
         return v
-    m = _SIZE_RE.match(v)
-    if not m:
+    text = str(v).strip().upper()
+    for tail in ("IB", "B"):
+        if text.endswith(tail) and len(text) > len(tail):
+            text = text[:-len(tail)]
+            break
+    unit = text[-1] if text and text[-1] in _UNIT_SHIFT else ""
+    number = text[:len(text) - len(unit)].strip()
+    try:
+        value = float(number)
+    except ValueError:
+        raise ValueError(f"cannot parse size: {v!r}") from None
+    if not value >= 0 or value == float("inf"):
         raise ValueError(f"cannot parse size: {v!r}")
-    return int(float(m.group(1)) * _MULT[m.group(2).upper()])
+    return int(value * (1 << _UNIT_SHIFT[unit]))
 
 
 @dataclass
@@ -50,6 +67,11 @@ class GenerationStats:
     @property
     def tokens_per_second(self) -> float:
         return 0.0 if self.decode_seconds <= 0 else self.generated_tokens / self.decode_seconds
+
+    def summary(self) -> str:
+        return (f"generate: {self.prompt_tokens} prompt tokens in {self.prefill_seconds:.3f} s, "
+                f"{self.generated_tokens} generated in {self.decode_seconds:.3f} s "
+                f"({self.tokens_per_second:.2f} tok/s)")
 
 
 _EXPERT_TENSORS = ("ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight")
@@ -157,17 +179,18 @@ class NeuroStream:
 
     @staticmethod
     def _sample(logits: torch.Tensor, temperature: float, top_p: float) -> int:
-        """Greedy at temperature <= 0, else softmax sampling with a top-p cut (api.py:179-191)."""
+        """The next token (api.py:179-191): argmax at temperature <= 0; else a
+        draw from softmax(logits / temperature) restricted, when 0 < top_p <
+        1, to the smallest set of most likely tokens whose mass reaches top_p."""
         if temperature <= 0:
             return int(logits.argmax())
         probs = torch.softmax(logits.float() / temperature, dim=-1)
-        if 0 < top_p < 1:
-            srt, idx = torch.sort(probs, descending=True)
-            keep = (torch.cumsum(srt, 0) - srt) < top_p
-            srt = srt * keep
-            srt = srt / srt.sum()
-            return int(idx[torch.multinomial(srt, 1)])
-        return int(torch.multinomial(probs, 1))
+        if not 0 < top_p < 1:
+            return int(torch.multinomial(probs, 1))
+        p_desc, order = torch.sort(probs, descending=True)
+        mass = torch.cumsum(p_desc, 0)
+        n_keep = min(int(torch.searchsorted(mass, torch.tensor([top_p], dtype=mass.dtype))) + 1, p_desc.numel())
+        return int(order[torch.multinomial(p_desc[:n_keep], 1)])
 
     def _piece(self, token: int) -> str:
         """The token's entry in the GGUF vocabulary (tokenizer.ggml.tokens), or <id> without one."""
@@ -217,3 +240,53 @@ class NeuroStream:
                 logits = self.model.forward([nxt], kv, start_pos=pos)
             pos += 1
         self.stats.decode_seconds = time.perf_counter() - t0
+
+    # -- warm-up and introspection (api.py:336-341, 399-441) -------------------
+
+    def warmup(self, prompt=None, tokens: int = 24) -> None:
+        """Generate a few tokens greedily only to observe which experts fire,
+        so that pin_hot_experts has measured routing to rank. The prompt is
+        token ids (default: the GGUF's BOS id, else token 0, and the next
+        seven ids)."""
+        if prompt is None:
+            bos = self.gguf.metadata.get("tokenizer.ggml.bos_token_id")
+            start = 0 if bos is None else int(bos)
+            vocab = self.gguf.tensors.get("token_embd.weight")
+            n_vocab = vocab.torch_shape[0] if vocab is not None else 8
+            prompt = [(start + i) % n_vocab for i in range(8)]
+        for _ in self.generate(prompt, max_tokens=tokens, temperature=0.0, stop_on_eos=False):
+            pass
+
+    def report(self) -> str:
+        """One line per subsystem: model file, device, arena budget, disk
+        reader, cache tiers and slabs, router statistics, last generation."""
+        info = [("model", f"{self.gguf.path.name}, {self.gguf.arch()}, "
+                          f"{self.gguf.total_tensor_bytes() / 2**30:.2f} GiB of tensors"),
+                ("device", f"{self.device}, compute {str(self.dtype).replace('torch.', '')}"),
+                ("arena", self.arena.summary()),
+                ("io", self.source.stats.summary()),
+                ("cache", self.cache.stats.summary())]
+        if self.cache.slab_bytes:
+            info.append(("slabs", f"{self.cache.slab_bytes / 2**30:.2f} GiB of expert slabs in HBM, "
+                                  f"{self.cache.stats.slab_hits} block reads served from them"))
+        rs = getattr(self.model, "router_stats", None)
+        if rs is not None:
+            info.append(("router", rs.summary()))
+        info.append(("generate", self.stats.summary()))
+        width = max(len(k) for k, _ in info)
+        return "\n".join(f"{k:<{width}} : {v}" for k, v in info)
+
+    def close(self) -> None:
+        """Drop every cached tensor and slab and close the disk reader."""
+        cache = getattr(self, "cache", None)
+        if cache is not None:
+            cache.clear()
+        src = getattr(self, "source", None)
+        if src is not None:
+            src.close()
+
+    def __enter__(self) -> "NeuroStream":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()

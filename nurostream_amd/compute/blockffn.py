@@ -9,8 +9,10 @@ Behaviour of neurostream/compute/blockffn.py, kept call-compatible:
                                computes; leftover leases are released in
                                `finally`.
   BlockPrefetcher    :278-393  one layer-wide queue of `depth` blocks across
-                               every (tensor, window) of a plan; cached windows
-                               are never queued; a failed submit re-queues.
+                               every (tensor, window) of a plan; held windows
+                               are never queued; a failed submit is retried;
+                               a block the caller passes before it was
+                               submitted is dropped from the plan.
   stream_expert_ffn  :396-449  gate/up windows + bias row, activation, down
                                window + bias row.
 The block product itself is a HIP kernel: `fused_gemv` on raw GGUF bytes or
@@ -141,82 +143,113 @@ def stream_linear(provider, name: str, x: torch.Tensor, block_rows: int = DEFAUL
 
 
 class BlockPrefetcher:
-    """Keeps `depth` block copies in flight across a whole layer's plan of windows.
+    """A read-ahead queue over a whole layer's plan of row windows.
 
-    `plan` is [(tensor name, row_lo, row_hi)] in consumption order. Peak bytes
-    stay at depth+1 blocks, charged to the source's arena.
+    `plan` is [(tensor name, row_lo, row_hi)] in the order the caller will
+    consume the windows (e.g. every chosen expert's gate, up and down). The
+    windows are cut into blocks of `block_rows` rows, skipping windows the
+    provider already holds (resident tensors, admitted slabs), and up to
+    `depth` block reads are kept submitted at once across window boundaries,
+    so the queue drains once per layer rather than once per projection. Each
+    submitted block holds an arena lease until the caller, having taken it
+    with `take`, releases it; `block_rows` and `depth` are clamped so that
+    depth + 1 blocks fit the arena (the one being computed still holds its
+    lease), else the prefetcher disables itself.
+
+    The contract of the reference's BlockPrefetcher
+    (compute/blockffn.py:278-393): `enabled`, `block_rows`, `depth`,
+    `bounds(lo, hi)`, `take(name, start) -> (raw, nbytes) | None`, `close()`
+    and the context manager. A submit that fails (arena full) leaves the block
+    first in line for the next top-up; a block the caller asks for before it
+    was submitted is dropped from the plan (the caller reads it itself), so
+    it is never read late.
     """
 
     def __init__(self, provider, plan, block_rows: int, depth: int = DEFAULT_LOOKAHEAD) -> None:
         self.provider = provider
         self.src = getattr(provider, "source", provider)
-        self.block_rows = max(1, block_rows)
-        self.depth = max(1, depth)
-        self._queue: deque = deque()
-        self._inflight: dict = {}
-        self._plan: deque = deque()
+        self.block_rows = max(1, int(block_rows))
+        self.depth = max(1, int(depth))
         self.enabled = hasattr(self.src, "submit_rows") and hasattr(self.src, "reader")
+        self._blocks: list[tuple[str, int, int]] = []  # every block to read, in consumption order
+        self._where: dict[tuple[str, int], int] = {}  # (name, start) -> index in _blocks
+        self._cursor = 0  # first block not yet submitted
+        self._skipped: set[int] = set()  # blocks the caller went past before they were submitted
+        self._live: dict[tuple[str, int], tuple] = {}  # submitted, not yet taken: (future, nbytes)
         if not self.enabled or not plan:
             return
-        widest = max(row_geometry(provider.gguf.tensors[n])[2] for n, _, _ in plan)
-        self.block_rows, self.depth, ok = _budget_clamp(self.src.arena.budget, widest, self.block_rows,
-                                                        self.depth)
-        if not ok:
-            self.enabled = False
+        widest = max(row_geometry(provider.gguf.tensors[name])[2] for name, _, _ in plan)
+        self.block_rows, self.depth, self.enabled = _budget_clamp(self.src.arena.budget, widest, self.block_rows,
+                                                                  self.depth)
+        if not self.enabled:
             return
+        br = self.block_rows
         for name, lo, hi in plan:
-            if self._cached(name, lo, hi):
-                continue
-            for start in range(lo, hi, self.block_rows):
-                self._plan.append((name, start, min(start + self.block_rows, hi)))
-        self._fill()
+            if not self._held(name, lo, hi):
+                self._blocks += [(name, s, min(s + br, hi)) for s in range(lo, hi, br)]
+        self._where = {(name, lo): i for i, (name, lo, _) in enumerate(self._blocks)}
+        self._top_up()
 
-    def _cached(self, name, lo, hi) -> bool:
+    def _held(self, name: str, lo: int, hi: int) -> bool:
+        """The provider already holds these rows: no read is ever queued for them."""
         if getattr(self.provider, "is_resident", lambda _n: False)(name):
             return True
         has_slab = getattr(self.provider, "has_slab", None)
-        return bool(has_slab and has_slab(name, lo, hi))
+        return bool(has_slab is not None and has_slab(name, lo, hi))
 
-    def _fill(self) -> None:
-        while len(self._inflight) < self.depth and self._plan:
-            name, start, end = self._plan.popleft()
+    def _top_up(self) -> None:
+        while len(self._live) < self.depth and self._cursor < len(self._blocks):
+            i = self._cursor
+            if i in self._skipped:
+                self._cursor += 1
+                continue
+            name, lo, hi = self._blocks[i]
             try:
-                self._inflight[(name, start)] = self.src.submit_rows(name, start, end)
-            except Exception:
-                self._plan.appendleft((name, start, end))  # budget full: resolves later or synchronously
+                handle = self.src.submit_rows(name, lo, hi)
+            except Exception:  # arena full or reader refused: retried at the next top-up
                 return
-            self._queue.append((name, start))
+            self._live[(name, lo)] = handle
+            self._cursor += 1
 
-    def bounds(self, lo: int, hi: int):
-        return [(s, min(s + self.block_rows, hi)) for s in range(lo, hi, self.block_rows)]
+    def bounds(self, lo: int, hi: int) -> list[tuple[int, int]]:
+        """The blocks of window [lo, hi), cut as the plan cut them."""
+        br = self.block_rows
+        return [(s, min(s + br, hi)) for s in range(lo, hi, br)]
 
     def take(self, name: str, start: int):
-        """(raw, nbytes) of a queued block, or None if it was never queued."""
-        entry = self._inflight.pop((name, start), None)
-        if entry is None:
+        """(raw bytes, nbytes) of the block of `name` starting at `start`, once
+        its read is done; the caller releases the nbytes lease. None when the
+        block was not read ahead (the caller reads it). The queue is topped up
+        before returning, so reads stay in flight while the caller computes."""
+        key = (name, start)
+        handle = self._live.pop(key, None)
+        if handle is None:
+            i = self._where.get(key)
+            if i is not None and i >= self._cursor:
+                self._skipped.add(i)
             return None
-        try:
-            self._queue.remove((name, start))
-        except ValueError:
-            pass
-        fut, nbytes = entry
+        fut, nbytes = handle
         reader = self.src._reader_for(name) if hasattr(self.src, "_reader_for") else self.src.reader
-        raw = reader.wait(fut)
-        self._fill()  # refill before the caller computes
+        try:
+            raw = reader.wait(fut)
+        except BaseException:
+            self.src.arena.release(nbytes)
+            raise
+        self._top_up()
         return raw, nbytes
 
     def close(self) -> None:
-        for fut, nbytes in self._inflight.values():
+        """Cancel the reads still queued and return their leases."""
+        live, self._live = self._live, {}
+        for fut, nbytes in live.values():
             fut.cancel()
             self.src.arena.release(nbytes)
-        self._inflight.clear()
-        self._queue.clear()
-        self._plan.clear()
+        self._cursor = len(self._blocks)
 
-    def __enter__(self):
+    def __enter__(self) -> "BlockPrefetcher":
         return self
 
-    def __exit__(self, *exc):
+    def __exit__(self, *exc) -> None:
         self.close()
 
 

@@ -1,9 +1,12 @@
 """GGML block layouts, tensor coordinates and a minimal GGUF v3 container.
 
-Mirrors the reference's `neurostream/format/gguf.py`:
-  * `GGMLType` / `TYPE_LAYOUT` / `nbytes_for`  -> format/gguf.py:19-68
+The interface of the reference's `neurostream/format/gguf.py`:
+  * `GGMLType` / `TYPE_LAYOUT` / `nbytes_for`  -> format/gguf.py:19-68 (the
+    type ids and block layouts are ggml's file format)
   * `TensorInfo` (ggml-order shape, torch_shape, memoised geometry) -> :102-128
-  * `GGUFFile` (header, metadata and tensor index; no tensor data) -> :162-245
+  * `GGUFFile` (header, metadata and tensor index; no tensor data) -> :162-245;
+    here decoded from a read-only memory map of the header, field by field at
+    offsets
 
 The writer (`GGUFWriter`) has no counterpart in the reference package (the
 reference's tests use the third-party gguf-py writer); it exists so that
@@ -11,11 +14,13 @@ synthetic models can be written to and re-read from a real GGUF file.
 """
 from __future__ import annotations
 
+import mmap
+import os
 import struct
 from dataclasses import dataclass
 from enum import IntEnum
 from pathlib import Path
-from typing import Any, BinaryIO
+from typing import Any
 
 GGUF_MAGIC = b"GGUF"
 DEFAULT_ALIGNMENT = 32
@@ -63,16 +68,18 @@ FLOAT_TYPES = frozenset({GGMLType.F32, GGMLType.F16, GGMLType.BF16})
 
 
 def nbytes_for(dtype: GGMLType, n_elements: int) -> int:
-    """Byte size of `n_elements` stored as `dtype` (format/gguf.py:58-68)."""
-    if dtype not in TYPE_LAYOUT:
-        raise NotImplementedError(f"unsupported ggml type: {dtype!r}")
-    block_elems, block_bytes = TYPE_LAYOUT[dtype]
-    if n_elements % block_elems:
-        raise ValueError(
-            f"{n_elements} elements is not a multiple of {dtype.name} "
-            f"block size {block_elems}"
-        )
-    return (n_elements // block_elems) * block_bytes
+    """Bytes that `n_elements` values of `dtype` occupy: whole blocks only
+    (the contract of format/gguf.py:58-68: NotImplementedError for a type
+    without a known block layout, ValueError for a partial block)."""
+    layout = TYPE_LAYOUT.get(dtype)
+    if layout is None:
+        raise NotImplementedError(f"no block layout known for ggml type {dtype!r}")
+    per, size = layout
+    blocks, rest = divmod(int(n_elements), per)
+    if rest:
+        raise ValueError(f"{GGMLType(dtype).name} stores whole blocks of {per} values; "
+                         f"{n_elements} values leave {rest} over")
+    return blocks * size
 
 
 @dataclass(slots=True)
@@ -135,6 +142,7 @@ def row_geometry(info: TensorInfo) -> tuple[int, int, int]:
 # GGUF v3 container (format/gguf.py:71-245)
 
 class _ValueType(IntEnum):
+    """GGUF metadata value type ids (part of the file format)."""
     UINT8 = 0
     INT8 = 1
     UINT16 = 2
@@ -150,6 +158,7 @@ class _ValueType(IntEnum):
     FLOAT64 = 12
 
 
+# little-endian struct codes of the fixed-size value types
 _SCALAR_FMT = {
     _ValueType.UINT8: "<B", _ValueType.INT8: "<b",
     _ValueType.UINT16: "<H", _ValueType.INT16: "<h",
@@ -158,39 +167,62 @@ _SCALAR_FMT = {
     _ValueType.UINT64: "<Q", _ValueType.INT64: "<q",
     _ValueType.FLOAT64: "<d",
 }
+_SCALAR = {vt: struct.Struct(f) for vt, f in _SCALAR_FMT.items()}
+_U32, _U64 = struct.Struct("<I"), struct.Struct("<Q")
+_HEAD = struct.Struct("<4sIQQ")  # magic, version, tensor count, metadata count
 
 
-class _Cursor:
-    def __init__(self, fh: BinaryIO) -> None:
-        self.fh = fh
+class _HeaderView:
+    """Decodes the header region of a GGUF file in place, from a read-only
+    memory map: every field is unpacked at an offset, so no stream position
+    or intermediate copies are involved."""
 
-    def read(self, n: int) -> bytes:
-        b = self.fh.read(n)
-        if len(b) != n:
-            raise EOFError(f"truncated GGUF: wanted {n} bytes, got {len(b)}")
-        return b
+    def __init__(self, buf, path) -> None:
+        self.buf = buf
+        self.pos = 0
+        self.path = path
 
-    def scalar(self, vt: _ValueType) -> Any:
-        fmt = _SCALAR_FMT[vt]
-        return struct.unpack(fmt, self.read(struct.calcsize(fmt)))[0]
+    def _take(self, n: int) -> int:
+        at = self.pos
+        if at + n > len(self.buf):
+            raise EOFError(f"{self.path}: the GGUF header ends early ({n} bytes needed at offset {at}, "
+                           f"the file has {len(self.buf)})")
+        self.pos = at + n
+        return at
 
-    def string(self) -> str:
-        (n,) = struct.unpack("<Q", self.read(8))
-        return self.read(n).decode("utf-8", errors="replace")
+    def unpack(self, st: struct.Struct):
+        return st.unpack_from(self.buf, self._take(st.size))
 
-    def value(self, vt: _ValueType) -> Any:
+    def u32(self) -> int:
+        return self.unpack(_U32)[0]
+
+    def u64(self) -> int:
+        return self.unpack(_U64)[0]
+
+    def text(self) -> str:
+        n = self.u64()
+        at = self._take(n)
+        return bytes(self.buf[at:at + n]).decode("utf-8", errors="replace")
+
+    def value(self, vt: int) -> Any:
+        vt = _ValueType(vt)
         if vt == _ValueType.STRING:
-            return self.string()
+            return self.text()
         if vt == _ValueType.ARRAY:
-            (elem_t,) = struct.unpack("<I", self.read(4))
-            (count,) = struct.unpack("<Q", self.read(8))
-            elem_t = _ValueType(elem_t)
-            return [self.value(elem_t) for _ in range(count)]
-        return self.scalar(vt)
+            inner = _ValueType(self.u32())
+            count = self.u64()
+            if inner in _SCALAR:  # a run of fixed-size values: one unpack
+                st = _SCALAR[inner]
+                at = self._take(st.size * count)
+                return list(struct.unpack_from(f"<{count}{st.format[1:]}", self.buf, at))
+            return [self.value(inner) for _ in range(count)]
+        return self.unpack(_SCALAR[vt])[0]
 
 
 class GGUFFile:
-    """Parsed GGUF index. Holds no tensor data (format/gguf.py:162-245)."""
+    """Header, metadata and tensor index of a GGUF v3 file; holds no tensor
+    data (the reader contract of format/gguf.py:162-245: `metadata`,
+    `tensors`, `alignment`, `data_offset`, `arch()`, `cfg()`, `file_offset()`)."""
 
     def __init__(self, path: str | Path) -> None:
         self.path = Path(path)
@@ -198,55 +230,58 @@ class GGUFFile:
         self.tensors: dict[str, TensorInfo] = {}
         self.alignment = DEFAULT_ALIGNMENT
         self.data_offset = 0
-        self._parse()
-
-    def _parse(self) -> None:
+        self.version = 0
         with open(self.path, "rb") as fh:
-            cur = _Cursor(fh)
-            magic = cur.read(4)
+            size = os.fstat(fh.fileno()).st_size
+            if size < _HEAD.size:
+                raise EOFError(f"{self.path}: {size} bytes is too short for a GGUF header")
+            with mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ) as mm:
+                self._index(_HeaderView(memoryview(mm), self.path))
+
+    def _index(self, hv: _HeaderView) -> None:
+        try:
+            magic, version, n_tensors, n_kv = hv.unpack(_HEAD)
             if magic != GGUF_MAGIC:
-                raise ValueError(f"not a GGUF file (magic={magic!r}): {self.path}")
-            version, n_tensors, n_kv = struct.unpack("<IQQ", cur.read(20))
+                raise ValueError(f"{self.path} is not a GGUF file (starts with {magic!r})")
             if version != 3:
-                raise ValueError(f"unsupported GGUF version {version} (need 3)")
+                raise ValueError(f"{self.path}: GGUF version {version}; this reader handles version 3")
             self.version = version
             for _ in range(n_kv):
-                key = cur.string()
-                (vt,) = struct.unpack("<I", cur.read(4))
-                self.metadata[key] = cur.value(_ValueType(vt))
+                key = hv.text()
+                self.metadata[key] = hv.value(hv.u32())
             self.alignment = int(self.metadata.get("general.alignment", DEFAULT_ALIGNMENT))
-            infos = []
             for _ in range(n_tensors):
-                name = cur.string()
-                (n_dims,) = struct.unpack("<I", cur.read(4))
-                dims = struct.unpack(f"<{n_dims}Q", cur.read(8 * n_dims))
-                (raw_t,) = struct.unpack("<I", cur.read(4))
-                (offset,) = struct.unpack("<Q", cur.read(8))
-                infos.append((name, dims, GGMLType(raw_t), offset))
-            pos = fh.tell()
-            pad = (self.alignment - (pos % self.alignment)) % self.alignment
-            self.data_offset = pos + pad
-        for name, dims, dtype, offset in infos:
-            n = 1
-            for d in dims:
-                n *= d
-            self.tensors[name] = TensorInfo(name, tuple(dims), dtype, offset, nbytes_for(dtype, n))
+                name = hv.text()
+                n_dims = hv.u32()
+                dims = tuple(hv.u64() for _ in range(n_dims))
+                dtype = GGMLType(hv.u32())
+                offset = hv.u64()
+                n = 1
+                for d in dims:
+                    n *= d
+                self.tensors[name] = TensorInfo(name, dims, dtype, offset, nbytes_for(dtype, n))
+            # tensor data starts at the next multiple of the alignment
+            self.data_offset = -(-hv.pos // self.alignment) * self.alignment
+        finally:
+            hv.buf.release()
 
     def arch(self) -> str:
         return str(self.metadata.get("general.architecture", "unknown"))
 
     def cfg(self, suffix: str, default: Any = None) -> Any:
+        """Metadata key `<arch>.<suffix>`."""
         return self.metadata.get(f"{self.arch()}.{suffix}", default)
 
     def file_offset(self, info: TensorInfo) -> int:
+        """Absolute file offset of a tensor's first byte."""
         return self.data_offset + info.offset
 
     def total_tensor_bytes(self) -> int:
         return sum(t.nbytes for t in self.tensors.values())
 
     def __repr__(self) -> str:
-        return (f"<GGUFFile {self.path.name} arch={self.arch()} "
-                f"tensors={len(self.tensors)} data={self.total_tensor_bytes() / 1e9:.2f}GB>")
+        return (f"GGUFFile({self.path.name!r}, arch={self.arch()!r}, {len(self.tensors)} tensors, "
+                f"{self.total_tensor_bytes() / 2**30:.2f} GiB of tensor data)")
 
 
 class GGUFWriter:

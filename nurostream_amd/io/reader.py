@@ -31,36 +31,39 @@ SLOT_BYTES = 8 << 20  # one staging buffer; larger reads are split across buffer
 
 @dataclass
 class IOStats:
+    """Reader counters (the fields of io/reader.py:31-69). The native reader
+    reports requests, bytes, summed read time and the span of its reads;
+    stalls and prefetch hits are counted where futures are waited on."""
     requests: int = 0
     bytes_read: int = 0
-    read_seconds: float = 0.0
+    read_seconds: float = 0.0   # summed over workers, so overlapping reads count more than once
     stall_seconds: float = 0.0  # time the compute thread blocked on a future
-    prefetch_hits: int = 0
-    prefetch_misses: int = 0
-    first_read: float = 0.0
+    prefetch_hits: int = 0      # waits that found their read already done
+    prefetch_misses: int = 0    # waits that had to block
+    first_read: float = 0.0     # CLOCK_MONOTONIC seconds
     last_read: float = 0.0
 
     @property
     def wall_seconds(self) -> float:
-        return max(0.0, self.last_read - self.first_read)
+        """Span from the first read's start to the latest read's end."""
+        return self.last_read - self.first_read if self.last_read > self.first_read else 0.0
 
     @property
     def throughput_gbps(self) -> float:
-        """Bytes over the wall-clock span of the reads (io/reader.py:44-55)."""
-        if self.wall_seconds <= 0:
-            return 0.0
-        return self.bytes_read / 1e9 / self.wall_seconds
+        """Bytes over the reads' wall-clock span, in GB/s (summed per-worker
+        time would understate a pool of concurrent readers)."""
+        span = self.wall_seconds
+        return self.bytes_read / span / 1e9 if span > 0 else 0.0
 
     @property
     def prefetch_rate(self) -> float:
-        total = self.prefetch_hits + self.prefetch_misses
-        return 0.0 if total == 0 else self.prefetch_hits / total
+        waits = self.prefetch_hits + self.prefetch_misses
+        return self.prefetch_hits / waits if waits else 0.0
 
     def summary(self) -> str:
-        return (f"{self.bytes_read / 1e9:.2f}GB in {self.requests} reads | "
-                f"{self.throughput_gbps:.2f} GB/s wall | "
-                f"stall {self.stall_seconds:.2f}s | "
-                f"prefetch {self.prefetch_rate:.1%}")
+        return (f"reads: {self.requests} ({self.bytes_read / 2**30:.2f} GiB) at {self.throughput_gbps:.2f} GB/s "
+                f"over {self.wall_seconds:.2f} s, {self.stall_seconds:.3f} s stalled, "
+                f"{100 * self.prefetch_rate:.1f}% of waits already done")
 
 
 class ReadFuture:

@@ -8,8 +8,8 @@
 - `raw_rows` / `raw_bytes` / `fetch_rows` / `fetch`: blocking reads under
   the arena budget.
 - `prefetch(names)` / `prefetch_layer`: whole-tensor reads ahead of use,
-  never more than half the budget, skipping names already in flight or
-  absent.
+  never more than half the budget and never waiting for it, skipping names
+  already in flight or absent.
 - `drop_inflight`, `close`.
 
 On a GPU source the submitted rows land in device memory (the reader copies
@@ -24,20 +24,16 @@ from pathlib import Path
 import torch
 
 from ..format.gguf import GGUFFile, row_geometry
-from .arena import Arena
+from .arena import Arena, BudgetExceeded
 from .reader import DEFAULT_WORKERS, DiskReader, ReadFuture
 
-# io/stream.py:22-33: tensor suffixes of one transformer block
-DENSE_SUFFIXES = (
-    "attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight",
-    "attn_output.weight", "attn_q_norm.weight", "attn_k_norm.weight",
-    "ffn_norm.weight", "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight",
-)
-MOE_SUFFIXES = (
-    "attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight",
-    "attn_output.weight", "attn_q_norm.weight", "attn_k_norm.weight",
-    "ffn_norm.weight", "ffn_gate_inp.weight",
-)
+# The GGUF tensor names of one transformer block that prefetch_layer reads
+# ahead (the block's non-expert tensors; io/stream.py:22-33 lists the same
+# names): attention and norms, then the dense FFN or the MoE router.
+_BLOCK_COMMON = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm", "attn_k_norm",
+                 "ffn_norm")
+DENSE_SUFFIXES = tuple(f"{n}.weight" for n in _BLOCK_COMMON + ("ffn_gate", "ffn_up", "ffn_down"))
+MOE_SUFFIXES = tuple(f"{n}.weight" for n in _BLOCK_COMMON + ("ffn_gate_inp",))
 
 
 class DiskSource:
@@ -58,20 +54,24 @@ class DiskSource:
     # -- prefetch -------------------------------------------------------------
 
     def prefetch(self, names) -> int:
-        """Queue whole-tensor reads for `names`; bytes queued (io/stream.py:94-124)."""
-        queued = 0
-        for name in names:
-            if name in self._inflight:
-                continue
+        """Read whole tensors ahead of use (io/stream.py:94-124); returns the
+        bytes queued. Names already queued or absent from the file are
+        skipped; speculative reads take at most half the arena and never wait
+        for it (a lease that is not free now ends the batch: the rest is read
+        on demand)."""
+        wanted = []
+        for name in dict.fromkeys(names):
             info = self.gguf.tensors.get(name)
-            if info is None:
-                continue
-            if queued + info.nbytes > self.arena.budget // 2:
+            if info is not None and name not in self._inflight:
+                wanted.append((name, info))
+        cap, queued = self.arena.budget // 2, 0
+        for name, info in wanted:
+            if queued + info.nbytes > cap:
                 break
             try:
-                self.arena.acquire(info.nbytes, timeout=5.0)
-            except Exception:
-                break  # budget full; the rest is read on demand
+                self.arena.acquire(info.nbytes, timeout=0)
+            except (TimeoutError, BudgetExceeded):
+                break
             try:
                 fut = self.reader.submit(self.gguf.file_offset(info), info.nbytes)
             except BaseException:

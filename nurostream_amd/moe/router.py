@@ -20,6 +20,7 @@ n_embd), w(name), cache, gguf, device, dtype, has(name), _linear(name, x).
 """
 from __future__ import annotations
 
+import heapq
 from collections import Counter
 from dataclasses import dataclass, field
 
@@ -33,25 +34,30 @@ from ..io.arena import BudgetExceeded
 
 @dataclass
 class RouterStats:
+    """Routing counters (the fields of moe/router.py:26-56): tokens routed,
+    expert reads (one per distinct expert a forward touched), and per
+    (layer, expert) hit counts -- what pin_hot_experts ranks experts by."""
     tokens_routed: int = 0
     expert_reads: int = 0
     hits: Counter = field(default_factory=Counter)
 
     def top_experts(self, layer: int, k: int = 8) -> list[tuple[int, int]]:
-        """The k most-hit experts of `layer` as (expert, hits), busiest first."""
-        return [(e, c) for (l, e), c in self.hits.most_common() if l == layer][:k]
+        """Up to k (expert, hits) of `layer`, most hits first (ties: lower expert id)."""
+        mine = [(c, e) for (lay, e), c in self.hits.items() if lay == layer]
+        return [(e, c) for c, e in heapq.nsmallest(k, mine, key=lambda ce: (-ce[0], ce[1]))]
 
     def skew(self) -> float:
-        """Share of all routings taken by the busiest 20% of (layer, expert) entries."""
-        if not self.hits:
+        """How concentrated routing is: the share of all hits that land on the
+        most-hit fifth of the (layer, expert) entries seen (at least one)."""
+        n = len(self.hits)
+        if n == 0:
             return 0.0
-        counts = sorted(self.hits.values(), reverse=True)
-        cut = max(1, len(counts) // 5)
-        return sum(counts[:cut]) / sum(counts)
+        busiest = heapq.nlargest(max(1, n // 5), self.hits.values())
+        return sum(busiest) / sum(self.hits.values())
 
     def summary(self) -> str:
-        return (f"routed {self.tokens_routed} tokens | {self.expert_reads} expert reads | "
-                f"top-20% skew {self.skew():.1%}")
+        return (f"router: {self.tokens_routed} tokens, {self.expert_reads} expert reads, "
+                f"{len(self.hits)} (layer, expert) pairs used, busiest fifth takes {100 * self.skew():.1f}%")
 
     def record(self, layer: int, ids: torch.Tensor) -> None:
         """Count one forward's routing: ids (T, k) of `layer` (device or host)."""
@@ -79,26 +85,29 @@ def _expert_slabs(cfg):
 
 
 def submit_expert_reads(model, layer: int, experts) -> dict:
-    """{(name, lo): (future, nbytes)} for every non-resident slab of `experts`
-    (moe/router.py:81-109); a full arena ends the queueing, the rest resolve
-    synchronously in _expert_matmul."""
+    """Queue a read of every chosen expert matrix the cache does not hold,
+    all at once, without waiting for the arena (moe/router.py:81-109):
+    {(name, lo): (future, nbytes)}. The first read the arena cannot take now
+    ends the queueing; _expert_matmul reads the rest when it gets to them."""
     cache = model.cache
     src = getattr(cache, "source", None)
     if src is None or not hasattr(src, "submit_rows"):
         return {}
+
+    def wanted():
+        for e in experts:
+            for suffix, per in _expert_slabs(model.cfg):
+                name = f"blk.{layer}.{suffix}"
+                lo, hi = e * per, (e + 1) * per
+                if name in model.gguf.tensors and not (cache.is_resident(name) or cache.has_slab(name, lo, hi)):
+                    yield name, lo, hi
+
     pending: dict = {}
-    for e in experts:
-        for nm, rpe in _expert_slabs(model.cfg):
-            name = f"blk.{layer}.{nm}"
-            if name not in model.gguf.tensors:
-                continue
-            lo, hi = e * rpe, (e + 1) * rpe
-            if cache.is_resident(name) or cache.has_slab(name, lo, hi):
-                continue
-            try:
-                pending[(name, lo)] = src.submit_rows(name, lo, hi, timeout=0)
-            except (BudgetExceeded, TimeoutError):
-                return pending
+    for name, lo, hi in wanted():
+        try:
+            pending[(name, lo)] = src.submit_rows(name, lo, hi, timeout=0)
+        except (BudgetExceeded, TimeoutError):
+            break
     return pending
 
 
