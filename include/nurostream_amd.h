@@ -203,6 +203,22 @@ int nsx_moe_phase(const nsx_moe_layer *L, int phase, const float *h, int64_t T,
                   float *out, int32_t *ids, float *weights, void *workspace,
                   int64_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference. nsx_moe_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): it allocates nothing and takes no
+ * workspace. Its workspace is a library-owned device array of
+ * NSX_STATIC_WORKSPACE_BYTES per GPU (each GPU the library runs on holds its
+ * own copy until the process ends); a call whose workspace
+ * (nsx_moe_workspace_bytes, for at most one grouped pass of tokens) exceeds
+ * it fails with NSX_EINVAL. Each call first clears the part it uses, on the
+ * stream, with a fill kernel. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other host threads) race on
+ * it. Outputs are those of nsx_moe_forward. */
+#define NSX_STATIC_WORKSPACE_BYTES (32ll << 20)
+int nsx_moe_forward_static(const nsx_moe_layer *L, const float *h, int64_t T,
+                           float *out, int32_t *ids, float *weights,
+                           void *stream);
+
 /* compute/ops.py:14-20 rms_norm in fp32 over rows of n (n <= 4096), with the
  * residual add of model/gpt_oss.py:177 folded in: sum = x + r and
  * y = sum * rsqrt(mean(sum^2) + eps) * w. r, w, sum and y may each be NULL

@@ -71,6 +71,7 @@ _SIGS = {
     "nsx_moe_workspace_bytes": (_i64, [C.POINTER(MoeLayerC), _i64]),
     "nsx_moe_forward": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p, _i64, _p]),
     "nsx_moe_phase": (_i, [C.POINTER(MoeLayerC), _i, _p, _i64, _p, _p, _p, _p, _i64, _p]),
+    "nsx_moe_forward_static": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p]),
     "nsx_add_rmsnorm": (_i, [_p, _p, _i64, _i64, C.c_float, _p, _p, _p, _p]),
     "nsx_copy_blocks_async": (_i, [_i64, _p, _p, _p, _p, _p]),
     "nsx_gather_copy": (_i, [_i64, _p, _p, _p, _p]),
@@ -90,6 +91,7 @@ _SIGS = {
     "nsx_reader_close": (_i, [_p]),
 }
 PHASE_ROUTER, PHASE_GATE_UP, PHASE_DOWN, PHASE_COMBINE = 0, 1, 2, 3
+STATIC_WORKSPACE_BYTES = 32 << 20  # NSX_STATIC_WORKSPACE_BYTES
 
 
 class NativeError(RuntimeError):

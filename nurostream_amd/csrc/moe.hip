@@ -15,6 +15,7 @@
 #include "raw_dot.h"
 
 #include <algorithm>
+#include <mutex>
 #include <stdlib.h>
 
 static inline hipStream_t S(void* s) { return (hipStream_t)s; }
@@ -2177,6 +2178,63 @@ extern "C" int nsx_moe_phase(const nsx_moe_layer* L, int phase, const float* h, 
   NSX_REQUIRE(L == nullptr || !use_grouped(L, T) || T <= grp_chunk_tokens(L), NSX_EINVAL,
               "grouped phases take at most %d pairs (T=%lld)", GRP_MAX_PAIRS, (long long)T);
   return moe_run(L, h, T, out, ids, weights, workspace, workspace_bytes, stream, phase, phase);
+}
+
+// ---------------------------------------------------------------------------
+// nsx_moe_forward without a caller workspace and without any allocation: the
+// workspace is `scratch`, a file-scope device array (one copy per GPU, held
+// until the process ends). Host code never passes the array's name to a
+// kernel -- on the host it is only a stand-in for the symbol -- but the
+// address hipGetSymbolAddress reports for the current device, looked up once
+// per device and kept in scratch_addr. Each call clears the part of the array
+// it uses with a fill kernel (not hipMemsetAsync, so the call can be captured
+// into a graph), then runs nsx_moe_forward's kernels on it. Calls on one GPU
+// share the array: calls that overlap (different streams, or host threads)
+// race on it.
+
+constexpr int MAX_DEVICES = 64;
+static __device__ __align__(256) uint8_t scratch[NSX_STATIC_WORKSPACE_BYTES];
+static std::mutex scratch_mu;
+static void* scratch_addr[MAX_DEVICES];
+
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  NSX_HIP(hipGetDevice(&dev));
+  NSX_REQUIRE(dev >= 0 && dev < MAX_DEVICES, NSX_EINVAL, "device %d outside 0..%d", dev, MAX_DEVICES - 1);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    NSX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    NSX_REQUIRE(p != nullptr, NSX_EHIP, "hipGetSymbolAddress returned a null address for the scratch array");
+    scratch_addr[dev] = p;
+  }
+  *out = scratch_addr[dev];
+  return NSX_OK;
+}
+
+__global__ __launch_bounds__(256) void ws_zero_kernel(uint4* __restrict__ p, int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
+extern "C" int nsx_moe_forward_static(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids,
+                                      float* weights, void* stream) {
+  int rc = check_layer(L, T);
+  if (rc) return rc;
+  NSX_REQUIRE(h && out && ids && weights, NSX_EINVAL, "null buffer");
+  // nsx_moe_forward runs grouped passes of at most grp_chunk_tokens tokens, each planned for its own size
+  const int64_t tc = use_grouped(L, T) ? std::min(T, grp_chunk_tokens(L)) : T;
+  const int64_t need = moe_plan(L, tc).total;
+  NSX_REQUIRE(need <= NSX_STATIC_WORKSPACE_BYTES, NSX_EINVAL,
+              "T=%lld needs a %lld-byte workspace; the static workspace holds %lld bytes (use nsx_moe_forward "
+              "with a caller workspace, or fewer tokens per call)",
+              (long long)T, (long long)need, (long long)NSX_STATIC_WORKSPACE_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_for_current_device(&ws))) return rc;
+  const int64_t n16 = nsx_cdiv(need, 16);
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(1024, nsx_cdiv(n16, 256)));
+  if ((rc = nsx_launch(ws_zero_kernel, dim3(grid), dim3(256), 0, S(stream), (uint4*)ws, n16))) return rc;
+  return nsx_moe_forward(L, h, T, out, ids, weights, ws, need, stream);
 }
 
 // ---------------------------------------------------------------------------

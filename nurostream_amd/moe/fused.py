@@ -161,6 +161,18 @@ class MoELayer:
         self._check_buffers(T, out, ids, weights)
         return h, T, out, ids, weights
 
+    def forward_static(self, h: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                       weights: torch.Tensor | None = None):
+        """forward() through nsx_moe_forward_static: no workspace, no device
+        allocation by the library (the workspace is its per-GPU static array,
+        shared by every such call on the GPU). The same outputs as forward()."""
+        h, T, out, ids, weights = self._prepare(h, out, ids, weights)
+        with torch.cuda.device(self.device):
+            N.check(N.load().nsx_moe_forward_static(C.byref(self._c), h.data_ptr(), T, out.data_ptr(),
+                                                    ids.data_ptr(), weights.data_ptr(), N.stream_ptr(self.device)),
+                    "moe_forward_static")
+        return out, ids, weights
+
     def forward(self, h: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
                 weights: torch.Tensor | None = None):
         """h: (T, n_embd) fp32 -> (out (T, n_embd) fp32, ids (T, k) int32, weights (T, k) fp32)."""

@@ -124,6 +124,23 @@ def test_validation_errors_return_codes(lib):
         N.check(rc)
 
 
+def test_static_workspace_limit(lib):
+    """nsx_moe_forward_static takes no workspace: a call whose workspace would
+    exceed the library's static array is refused on the host, before any HIP
+    call (the pointers below are never dereferenced)."""
+    L = _gptoss_layer()
+    cap = N.STATIC_WORKSPACE_BYTES
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 128) <= cap  # config 3 (T=128, grouped) fits
+    T = 1024  # one grouped pass of 4096 pairs: per-pair outputs alone are 47 MB
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), T) > cap
+    rc = lib.nsx_moe_forward_static(C.byref(L), 1, T, 1, 1, 1, None)
+    assert rc == N.EINVAL and b"static workspace" in lib.nsx_last_error()
+    with pytest.raises(ValueError):
+        N.check(rc)
+    rc = lib.nsx_moe_forward_static(C.byref(L), None, 1, 1, 1, 1, None)
+    assert rc == N.EINVAL and b"null" in lib.nsx_last_error()
+
+
 def test_moe_layer_rejects_bad_outputs():
     """MoELayer checks out / ids / weights before the native call writes
     through their pointers (shape, dtype, contiguity, device)."""
