@@ -376,6 +376,10 @@ template <int NT>
 __host__ __device__ constexpr int gv_x_bytes(int K) {
   return ((NT * (K + K / 32) * 4) + 15) & ~15;
 }
+// XREG: x staged once per workgroup, 32-element chunks GV_XPAD floats apart
+constexpr int GV_XPAD = 36;
+constexpr int GV_XQ = 4;  // float4s of x per thread when staging (K <= 4 * GV_XQ * GV_THREADS)
+__host__ __device__ constexpr int gv_xreg_bytes(int K) { return (K / 32) * GV_XPAD * 4; }
 
 // Activations of one unit held in registers (unit order), one token, with
 // the unit's sum and its four 8-element group sums.
@@ -398,71 +402,37 @@ struct RawXSumReg {
 // XREG (one token, K <= 4096, so one chunk per row): each lane's two units
 // are the same for every row, so their activations are read from LDS once
 // into registers instead of once per row.
-template <int FMT, int NT, bool XREG>
-__global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
+template <int FMT, int NT, bool XREG, int WAVES = GV_WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
     const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int n_rows, int K,
     const void* __restrict__ x, int x_dtype, int T, float* __restrict__ y, int64_t ystride,
     const float* __restrict__ bias, const float* resid) {  // resid may be y (read, then written, per element)
   using C = GvChunk<FMT>;
   constexpr int BE = RawBlock<FMT>::BE, BB = RawBlock<FMT>::BB;
   extern __shared__ __align__(16) uint8_t gv_smem[];
-  // LDS: [NT][K] activations and [NT][K/32] block sums (not with XREG), then
-  // one chunk buffer per wave
+  // LDS: without XREG, [NT][K] activations and [NT][K/32] block sums; with
+  // XREG, x in 32-element chunks at a GV_XPAD-float stride; then one chunk
+  // buffer per wave
   float* xs = (float*)gv_smem;
   constexpr bool SUMS = FMT == NSX_Q4_0 || FMT == NSX_Q4_K;
   if constexpr (!XREG) stage_x<NT>(xs, x, x_dtype, K, T, K, SUMS);
   const float* xsum = xs + NT * K;
   const int lane = __lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // with XREG the wave buffers overlay the x staging area (x is in registers before any row bytes land)
   uint8_t* wbuf = gv_smem + (XREG ? 0 : gv_x_bytes<NT>(K)) + wave * C::WAVE_BYTES;
-  float xra[XREG ? 32 : 1], xrb[XREG ? 32 : 1], xsa = 0.f, xsb = 0.f, xga[4], xgb[4];
-  if constexpr (XREG) {
-    // The lane's two units of x straight from global memory (L2-resident
-    // after the first waves), four elements per load; sums in the same
-    // sequential order as stage_x.
-    const int nu0 = K / 32;
-    const uint32_t align = x_dtype == NSX_DT_F32 ? 15u : 7u;
-    const bool vec = ((uintptr_t)x & align) == 0;
-    auto gather = [&](int u, float (&xr)[32], float& sum, float (&gs)[4]) {
-      const bool on = u < nu0;
-      const int uu = on ? u : 0;
-#pragma unroll
-      for (int k4 = 0; k4 < 8; ++k4) {
-        const v4f v = nsx_load_act4(x, x_dtype, raw_unit_elem<FMT>(uu, 4 * k4), vec);
-        xr[4 * k4] = on ? v.x : 0.f;
-        xr[4 * k4 + 1] = on ? v.y : 0.f;
-        xr[4 * k4 + 2] = on ? v.z : 0.f;
-        xr[4 * k4 + 3] = on ? v.w : 0.f;
-      }
-      if constexpr (SUMS || FMT == NSX_Q8_0) {
-        float a = 0.f;
-#pragma unroll
-        for (int k = 0; k < 32; ++k) a += xr[k];
-        sum = a;
-      }
-      if constexpr (FMT == NSX_Q6_K) {
-#pragma unroll
-        for (int L = 0; L < 4; ++L) {
-          float a = 0.f;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) a += xr[8 * L + k];
-          gs[L] = a;
-        }
-      }
-    };
-    gather(lane, xra, xsa, xga);
-    gather(lane + 64, xrb, xsb, xgb);
-  }
+  constexpr int THREADS = 64 * WAVES;
+  constexpr int XQ = (GV_XQ * GV_THREADS + THREADS - 1) / THREADS;  // float4s of x per thread (K <= 4096)
   const __amdgpu_buffer_rsrc_t rs = nsx_rsrc(base, range);
-  const int nwaves = gridDim.x * GV_WAVES;
+  const int nwaves = gridDim.x * WAVES;
   const uint32_t rb = raw_row_bytes<FMT>(K);
   const int nblk = K / BE;                        // blocks per row
   const int nch = (nblk + C::BLOCKS - 1) / C::BLOCKS;  // chunks per row
 
   // Work items of this wave: (row r0 + (k / nch) * nwaves, chunk k % nch).
-  const int r0 = blockIdx.x * GV_WAVES + wave;
-  if (r0 >= n_rows) return;
-  const int nitems = ((n_rows - 1 - r0) / nwaves + 1) * nch;
+  const int r0 = blockIdx.x * WAVES + wave;
+  if (!XREG && r0 >= n_rows) return;  // (with XREG every wave takes part in staging x first)
+  const int nitems = r0 < n_rows ? ((n_rows - 1 - r0) / nwaves + 1) * nch : 0;
   auto item_row = [&](int k) { return r0 + (k / nch) * nwaves; };
   auto chunk_start = [&](int k) {
     return head + (uint32_t)item_row(k) * rb + (uint32_t)((k % nch) * C::BLOCKS * BB);
@@ -489,6 +459,77 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
       S.D[g] = off - s0;
     }
   };
+  float xra[XREG ? 32 : 1], xrb[XREG ? 32 : 1], xsa = 0.f, xsb = 0.f, xga[4], xgb[4];
+  Slot S0, S1;
+  if constexpr (!XREG) {
+    if (nitems > 0) issue(0, S0);
+    if (GV_DEPTH > 1 && nitems > 1) issue(1, S1);
+  } else {  // fp32 x, 16-byte aligned (the host's condition for XREG)
+    // x into LDS with coalesced loads (consecutive threads, consecutive 16
+    // bytes), 32-element chunk c at float offset GV_XPAD * c: with that
+    // padding the lanes' 16-byte reads of their own units below (lane l,
+    // chunk l) hit distinct banks. The x loads go out first and the first
+    // rows' loads right behind them, so the rows stream while x is staged
+    // (the memory counter retires loads in issue order). Then each lane keeps
+    // its two units of x in registers for every row (K <= 4096: one chunk of
+    // units per row), with the unit sums in the same sequential order as
+    // stage_x.
+    // No control flow between these loads and the rows' (a branch makes the
+    // compiler wait for every load before it): the rows' first item is
+    // always issued (a wave past the last row reads clamped, in-range bytes
+    // it never uses) and the second one repeats the first when there is none.
+    const int nq = K >> 2;  // <= XQ * THREADS
+    v4f xv[XQ];
+#pragma unroll
+    for (int g = 0; g < XQ; ++g) xv[g] = ((const v4f*)x)[min((int)threadIdx.x + g * THREADS, nq - 1)];
+    issue(0, S0);
+    if constexpr (GV_DEPTH > 1) issue(nitems > 1 ? 1 : 0, S1);
+#pragma unroll
+    for (int g = 0; g < XQ; ++g) {
+      const int q = (int)threadIdx.x + g * THREADS;
+      if (q < nq) *(v4f*)(xs + GV_XPAD * (q >> 3) + 4 * (q & 7)) = xv[g];
+    }
+    // LDS barrier without a memory-counter wait: lgkmcnt(0) (this wave's LDS
+    // writes are done), then s_barrier; the memory clobber keeps the compiler
+    // from moving the LDS reads above it. The row loads stay in flight.
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
+    const int nu0 = K / 32;
+    auto gather = [&](int u, float (&xr)[32], float& sum, float (&gs)[4]) {
+      const bool on = u < nu0;
+      const int uu = on ? u : 0;
+#pragma unroll
+      for (int k4 = 0; k4 < 8; ++k4) {
+        const int e = raw_unit_elem<FMT>(uu, 4 * k4);
+        const v4f v = *(const v4f*)(xs + GV_XPAD * (e >> 5) + (e & 31));
+        xr[4 * k4] = on ? v.x : 0.f;
+        xr[4 * k4 + 1] = on ? v.y : 0.f;
+        xr[4 * k4 + 2] = on ? v.z : 0.f;
+        xr[4 * k4 + 3] = on ? v.w : 0.f;
+      }
+      if constexpr (SUMS || FMT == NSX_Q8_0) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) a += xr[k];
+        sum = a;
+      }
+      if constexpr (FMT == NSX_Q6_K) {
+#pragma unroll
+        for (int L = 0; L < 4; ++L) {
+          float a = 0.f;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) a += xr[8 * L + k];
+          gs[L] = a;
+        }
+      }
+    };
+    gather(lane, xra, xsa, xga);
+    gather(lane + 64, xrb, xsb, xgb);
+    // every wave has its x in registers before any wave overwrites the area with row bytes
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
+    if (r0 >= n_rows) return;
+  }
   float acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = 0.f;
@@ -533,13 +574,8 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
     }
   };
   if constexpr (GV_DEPTH == 1) {
-    Slot S0;
-    issue(0, S0);
     for (int k = 0; k < nitems; ++k) step(k, S0);
   } else {
-    Slot S0, S1;
-    issue(0, S0);
-    if (nitems > 1) issue(1, S1);
     for (int k = 0; k < nitems; k += 2) {
       step(k, S0);
       if (k + 1 < nitems) step(k + 1, S1);
@@ -547,9 +583,9 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_raw_kernel(
   }
 }
 
-// Workgroups of `kernel` (GV_THREADS threads, `lds` bytes) resident on the
+// Workgroups of `kernel` (`threads` threads, `lds` bytes) resident on the
 // current device at once: CUs x blocks per CU, cached per kernel and LDS size.
-static int resident_workgroups(const void* kernel, size_t lds) {
+static int resident_workgroups(const void* kernel, size_t lds, int threads = GV_THREADS) {
   struct Entry { const void* k; size_t lds; int dev; int n; };
   static std::mutex mu;
   static Entry cache[64];
@@ -561,7 +597,8 @@ static int resident_workgroups(const void* kernel, size_t lds) {
     if (cache[i].k == kernel && cache[i].lds == lds && cache[i].dev == dev) return cache[i].n;
   int cus = 0, per = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, GV_THREADS, lds) != hipSuccess || per <= 0) per = 1;
+  if (lds > 64 * 1024) (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per <= 0) per = 1;
   (void)hipGetLastError();
   const int n = cus * per;
   if (used < 64) cache[used++] = Entry{kernel, lds, dev, n};
@@ -573,27 +610,50 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
                            int64_t T, float* y, const float* bias, const float* resid, hipStream_t st) {
   const int64_t row_bytes = raw_row_bytes<FMT>((int)K);
   const int64_t rows_per_launch = std::max<int64_t>(1, ((int64_t)1 << 31) / row_bytes);
-  constexpr bool XR = NT == 1;  // the register path exists for one token only
-  const bool xreg = XR && K <= GV_CHUNK_UNITS * 32;
-  const size_t lds = (xreg ? 0 : (size_t)gv_x_bytes<NT>((int)K)) + (size_t)GV_WAVES * GvChunk<FMT>::WAVE_BYTES;
+  constexpr bool XR = NT == 1;  // the register path exists for one token only (fp32 x, 16-byte aligned)
+  const bool xreg = XR && K <= GV_CHUNK_UNITS * 32 && xdt == NSX_DT_F32 && ((uintptr_t)x & 15u) == 0;
+  const size_t bufs = (size_t)GV_WAVES * GvChunk<FMT>::WAVE_BYTES;
+  const size_t lds = xreg ? std::max((size_t)gv_xreg_bytes((int)K), bufs) : (size_t)gv_x_bytes<NT>((int)K) + bufs;
   const void* kern = xreg ? (const void*)gemv_raw_kernel<FMT, NT, XR> : (const void*)gemv_raw_kernel<FMT, NT, false>;
   if (lds > 64 * 1024) NSX_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   const int64_t resident = resident_workgroups(kern, lds);
+  // Small one-token matrices (a row per wave fits the machine in one pass of
+  // 16-wave workgroups): every row's loads go out at once and x is staged
+  // once per workgroup. For the formats whose unit arithmetic fits the
+  // 128-VGPR budget of a 1024-thread workgroup (Q4_0, MXFP4; the others would
+  // spill and keep the 4-wave persistent grid).
+  constexpr int BIG = 16;
+  constexpr bool BIG_OK = XR && (FMT == NSX_Q4_0 || FMT == NSX_MXFP4);
+  const size_t lds_big = std::max((size_t)gv_xreg_bytes((int)K), (size_t)BIG * GvChunk<FMT>::WAVE_BYTES);
+  int64_t big_resident = 0;
+  if constexpr (BIG_OK)
+    big_resident = resident_workgroups((const void*)gemv_raw_kernel<FMT, NT, XR, BIG>, lds_big, 64 * BIG);
   for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_launch) {
     const int64_t nr = std::min(rows_per_launch, n_rows - r0);
     const uint8_t* p = (const uint8_t*)raw + r0 * row_bytes;
     const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
     const uint32_t head = (uint32_t)((uintptr_t)p - a);
     const uint32_t range = head + (uint32_t)(nr * row_bytes);
+    const float* b = bias ? bias + r0 : nullptr;
+    const float* rr = resid ? resid + r0 : nullptr;
+    if constexpr (BIG_OK) {
+      if (xreg && nr <= BIG * big_resident) {
+        if (lds_big > 64 * 1024)
+          NSX_HIP(hipFuncSetAttribute((const void*)gemv_raw_kernel<FMT, NT, XR, BIG>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_big));
+        hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, XR, BIG>), dim3((unsigned)nsx_cdiv(nr, BIG)), dim3(64 * BIG),
+                           lds_big, st, (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0,
+                           n_rows, b, rr);
+        NSX_LAUNCHED();
+        continue;
+      }
+    }
     // Persistent: the resident workgroups for large matrices; for small ones
     // (under two rounds of that grid) half of them, so each wave has several
-    // rows and overlaps their loads (QKV-sized Q8_0: 10.4 -> 9.4 us; a large
-    // matrix on half the grid is slower).
+    // rows and overlaps their loads (a large matrix on half the grid is slower).
     const int64_t per_row = nsx_cdiv(nr, GV_WAVES);
     const int64_t cap = per_row <= 2 * resident ? std::max<int64_t>(1, resident / 2) : resident;
     const unsigned grid = (unsigned)std::min<int64_t>(per_row, cap);
-    const float* b = bias ? bias + r0 : nullptr;
-    const float* rr = resid ? resid + r0 : nullptr;
     if (xreg)
       hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, XR>), dim3(grid), dim3(GV_THREADS), lds, st,
                          (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows, b, rr);

@@ -347,6 +347,35 @@ __device__ __forceinline__ v4f nsx_load_act4(const void* __restrict__ p, int dty
              nsx_load_act(p, dtype, i + 3)};
 }
 
+// G independent nsx_load_act4 loads at element offsets idx[g], with the
+// dtype / alignment branch taken once outside them: inside one branch the
+// loads have no control flow between them, so they are all in flight
+// together (a branch per load makes each one wait for the last).
+template <int G>
+__device__ __forceinline__ void nsx_load_act4_n(const void* __restrict__ p, int dtype, const int64_t (&idx)[G],
+                                                bool vec, v4f (&out)[G]) {
+  if (vec && dtype == NSX_DT_F32) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) out[g] = *(const v4f*)((const float*)p + idx[g]);
+  } else if (vec) {
+    v2u w[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) w[g] = *(const v2u*)((const uint16_t*)p + idx[g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (dtype == NSX_DT_F16)
+        out[g] = v4f{nsx_h2f(w[g].x & 0xffffu), nsx_h2f(w[g].x >> 16), nsx_h2f(w[g].y & 0xffffu),
+                     nsx_h2f(w[g].y >> 16)};
+      else
+        out[g] = v4f{nsx_bf2f(w[g].x & 0xffffu), nsx_bf2f(w[g].x >> 16), nsx_bf2f(w[g].y & 0xffffu),
+                     nsx_bf2f(w[g].y >> 16)};
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) out[g] = nsx_load_act4(p, dtype, idx[g], false);
+  }
+}
+
 // Stage NT activation rows (token stride `xstride` elements, dtype `xdt`) into
 // LDS as fp32 [NT][K] followed by per-32 sums [NT][K/32]. Rows >= T are zero.
 // K is a multiple of 32. Each thread issues its loads in groups of four
@@ -362,13 +391,21 @@ __device__ __forceinline__ void stage_x(float* __restrict__ xs, const void* __re
   constexpr int G = 4;
   for (int q0 = threadIdx.x; q0 < nq; q0 += G * blockDim.x) {
     v4f v[G];
+    int64_t idx[G];
+    bool live[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < G; ++g) {  // addresses clamped to a valid element, values masked after the loads
       const int q = q0 + g * blockDim.x;
       const int t = q / kq;
-      v[g] = q < nq && t < T ? nsx_load_act4(x, xdt, (int64_t)t * xstride + 4 * (q - t * kq), vec)
-                             : v4f{0.f, 0.f, 0.f, 0.f};
+      live[g] = q < nq && t < T;
+      const int qc = live[g] ? q : 0;
+      const int tc = qc / kq;
+      idx[g] = (int64_t)tc * xstride + 4 * (qc - tc * kq);
     }
+    nsx_load_act4_n<G>(x, xdt, idx, vec, v);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (!live[g]) v[g] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int q = q0 + g * blockDim.x;

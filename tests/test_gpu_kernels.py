@@ -118,6 +118,31 @@ def test_fused_gemv_matches_oracle(dev, fmt, rows, K, T):
     np.testing.assert_allclose(y, ref, atol=1e-4 * np.abs(ref).max() + 1e-6, rtol=1e-4)
 
 
+@pytest.mark.parametrize("fmt,rows,K", [("Q4_0", 4096, 4096), ("Q4_0", 4097, 4096), ("MXFP4", 5000, 2880),
+                                        ("Q4_0", 4095, 1024), ("Q8_0", 4096, 4096)])
+def test_fused_gemv_one_token_paths_agree(dev, fmt, rows, K):
+    """T = 1 runs on one of three kernel paths by shape and x: one row per wave
+    in 16-wave workgroups (small Q4_0 / MXFP4 matrices, fp32 x 16-byte
+    aligned), the 4-wave persistent grid with x in registers, or x staged per
+    row from LDS (f16 or misaligned x). BASELINE config 1's shape, partial last
+    workgroups and the fallbacks, against the float64 oracle; fp32 and f16
+    views of one x must agree with the oracle alike."""
+    from nurostream_amd.compute.kernels import fused_gemv
+    t = getattr(OQ, fmt)
+    raw = _gemv_case(fmt, rows, K, seed=rows * 7 + K)
+    x = np.random.default_rng(rows).standard_normal((1, K)).astype(np.float16).astype(np.float32)
+    ref = OQ.gemv(raw, t, x, rows, K, f64=True)
+    w = torch.from_numpy(raw).to(dev)
+    y = to_np(fused_gemv(w, t, torch.from_numpy(x).to(dev), rows, K, out_dtype=torch.float32))
+    assert rel_max(y, ref) < GEMV_TIGHT
+    y16 = to_np(fused_gemv(w, t, torch.from_numpy(x).to(dev).half(), rows, K, out_dtype=torch.float32))
+    assert rel_max(y16, ref) < GEMV_TIGHT
+    buf = torch.zeros(K + 1, dtype=torch.float32, device=dev)  # x at a 4-byte but not 16-byte aligned address
+    buf[1:] = torch.from_numpy(x[0]).to(dev)
+    ym = to_np(fused_gemv(w, t, buf[1:].reshape(1, K), rows, K, out_dtype=torch.float32))
+    assert rel_max(ym, ref) < GEMV_TIGHT
+
+
 @pytest.mark.parametrize("offset", [1, 2, 3])
 def test_fused_gemv_q6k_any_alignment(dev, offset):
     """Q6_K rows are 210 B per block, so rows start at any byte: the kernel's
