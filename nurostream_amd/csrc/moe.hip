@@ -669,9 +669,11 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
   const int k = a.top_k, t = p / k, j = p - t * k;
   MxRegs<GU_S> R;
-  mx_load_b<GU_S, false>(R, a.xq_h + (int64_t)t * a.ggu.ns * XQ_STEP, 0, 0, 1, s0, s1);  // no expert needed
   // the top-k by wave 0 alone (sixteen waves selecting at once would share each SIMD four ways);
-  // the token's first item also writes the ids/weights outputs, which the down phase reads
+  // the token's first item also writes the ids/weights outputs, which the down phase reads. Its
+  // logits load is the critical path, so no other load of the CU queues ahead of it: the
+  // activation terms (L2 hits after the first workgroups) are requested with the weights, step by
+  // step.
   if (wave == 0) {
     int si[MAX_TOPK];
     float sw[MAX_TOPK];
@@ -695,7 +697,7 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   const int e = s_e;
   const uint8_t* mat = m == 0 ? tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile)
                               : tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
-  mx_load_a<GU_S>(R, mat, a.ggu, s0, s1);
+  mx_load_ab<GU_S>(R, mat, a.ggu, s0, s1, a.xq_h + (int64_t)t * a.ggu.ns * XQ_STEP, 0, 0, 1);
   const int row = tile * 64 + lane;
   const int rowc = min(row, a.n_ff - 1);
   float gb = 0.f, ub = 0.f;  // wave 0's biases, requested while the weights stream
@@ -781,14 +783,16 @@ __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& 
   d.p = d.t * k + j;
   d.s0 = c * a.sd;
   d.s1 = min(a.gdn.ns, d.s0 + a.sd);
-  // this wave's activation terms (steps s0 .. s1 - 1) and the token's ids and weights, in one round trip
+  // the token's ids and weights, then this wave's activation terms (steps s0 .. s1 - 1), in one round
+  // trip; the ids go first, so the weights' addresses wait on them alone (loads retire in issue order)
   const int npc = (d.s1 - d.s0) * (XQ_STEP / 16);
   const uint8_t* xsrc = a.xq_a + ((int64_t)d.p * a.gdn.ns + d.s0) * XQ_STEP;
+  const int id_raw = a.ids[(int64_t)d.t * k + min(lane, k - 1)];  // lane jj < k: slot jj
+  d.my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
   v4u stage[DC_STAGE];
 #pragma unroll
   for (int i = 0; i < DC_STAGE; ++i) stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
-  d.id_l = clamp_expert(a.ids[(int64_t)d.t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
-  d.my_w = a.wts[(int64_t)d.t * k + min(lane, k - 1)];
+  d.id_l = clamp_expert(id_raw, a.E);
   const int e = __builtin_amdgcn_readlane(d.id_l, j);
   mx_load_a<DC_S, 1>(d.R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, d.tile), a.gdn,
                      d.s0, d.s1, d.rg);

@@ -204,6 +204,41 @@ __device__ __forceinline__ void mx_load_b(MxRegs<S, G>& R, const uint8_t* __rest
   mx_load_b_at<S, BLDS, G>(R, xq + (int64_t)tok * xq_stride, xs0, s0, s1);
 }
 
+// mx_load_a and mx_load_b (global activation terms) of the same steps,
+// interleaved step by step: the loads retire in issue order, so step u's
+// MFMAs wait only for steps 0..u, weights and activations alike.
+template <int S, int G = 4>
+__device__ __forceinline__ void mx_load_ab(MxRegs<S, G>& R, const uint8_t* __restrict__ tile, const MxGeom& G_,
+                                           int s0, int s1, const uint8_t* __restrict__ xq, int xs0,
+                                           int64_t xq_stride, int ntok, int g0 = 0) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  typedef const __attribute__((address_space(1))) uint32_t gu32;
+  const int lane = __lane_id(), grp = lane >> 4;
+  const int tok0 = (lane & 15) / XQ_NT;
+  const int tok = tok0 < ntok ? tok0 : ntok - 1;
+  const uint8_t* xtok = xq + (int64_t)tok * xq_stride;
+  const int term = lane & (XQ_NT - 1);
+  const uint8_t* xt = xtok + (grp * XQ_NT + term) * 32;
+  const uint8_t* xst = xtok + XQ_CODES + (grp * XQ_NT + term) * 4;
+#pragma unroll
+  for (int u = 0; u < S; ++u) {
+    const int s = s0 + u;
+    if (s < s1) {
+      const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
+      const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
+      const bool alane = grp < rs;
+      const int la = alane ? lane : 16 * rs - 1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
+      R.SA[u] = __builtin_nontemporal_load((gu32*)(ch + rs * 1024 + la * 4));
+      const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
+      R.B0[u] = *(gv4u*)(xt + xo);
+      R.B1[u] = *(gv4u*)(xt + xo + 16);
+      R.SB[u] = *(gu32*)(xst + xo);
+    }
+  }
+}
+
 // D[g] (rows 16 (g0 + g) .. + 15 of the tile, 16 columns) += the loaded steps
 // (the same G_, s0, s1, g0 as mx_load_a).
 template <int S, int G = 4>
