@@ -13,9 +13,11 @@
 #include "nsx_common.h"
 #include "mx.h"
 #include "raw_dot.h"
+#include "q4k_a8.h"
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <stdlib.h>
 
 static inline hipStream_t S(void* s) { return (hipStream_t)s; }
@@ -565,8 +567,8 @@ struct MoeDev {
   const float* h;
   float* out;
   float* act;            // (pairs, n_ff) fp32 activations (GGUF-layout path)
-  const uint8_t* xq_h;   // activation terms of h, per token (t64 path)
-  uint8_t* xq_a;         // activation terms of the expert activation, per pair (t64 path)
+  const uint8_t* xq_h;   // activation terms of h, per token (t64, Q4_K matrix-core and grouped Q4_K paths)
+  uint8_t* xq_a;         // activation terms of the expert activation, per pair (same paths)
   int n_embd, n_ff;
   MxGeom ggu, gdn;       // t64 geometry of a gate/up and of a down matrix
   int cg, sg;            // gate/up K-chunks and K-steps per chunk
@@ -630,8 +632,11 @@ __device__ __forceinline__ float combine_one(float acc, float w, float y) { retu
 // partial sums go to separate slots and are added in a fixed order by the
 // next kernel: results do not depend on scheduling.
 
+// (the table is read as constant memory: for a wave-uniform e that is a scalar
+// load, whose wait does not hold up the wave's vector loads in flight)
 __device__ __forceinline__ const uint8_t* expert_base(const void* base, int64_t stride, const uint64_t* ptrs, int e) {
-  return base ? (const uint8_t*)base + (int64_t)e * stride : (const uint8_t*)ptrs[e];
+  typedef const __attribute__((address_space(4))) uint64_t cu64;
+  return base ? (const uint8_t*)base + (int64_t)e * stride : (const uint8_t*)*((cu64*)ptrs + e);
 }
 
 // tile `tile` of expert e's t64 matrix: from the tile table when there is one
@@ -1201,109 +1206,70 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K experts over raw GGUF rows (a row is K/256 super-blocks of 144 B, so
-// rows and super-blocks are 16-byte aligned). A row splits into 16-byte code
-// units, 8 per super-block: unit u = 8 sb + 2 g + h holds code bytes
-// 16 h .. 16 h + 15 of sub-block pair g -- low nibbles are elements 16 h + j of
-// sub-block 2 g, high nibbles those of sub-block 2 g + 1 (compute/quant.py:
-// 24-56 dequant_q4_k). Lane l of a wave owns units l, l + 64, ...; it keeps
-// their 32 activations and the two 16-element activation sums in registers
-// for every row it visits, and per row loads the unit's codes and its
-// super-block header (d, dmin, 12 scale bytes) as two 128-bit loads, all rows
-// of a wave in flight together. Per unit:
-//   (d sc_2g) sum q_lo x - (dmin m_2g) sum x + (d sc_2g+1) sum q_hi x - (dmin m_2g+1) sum x
-// with d sc and dmin m exact in fp32 (11-bit times 6-bit integers).
+// Q4_K experts over raw GGUF rows, on the int8 dot instruction with the
+// activations as two int8 terms per element (q4k_a8.h). A row of K elements
+// is K/256 super-blocks of 144 B (d, dmin, 12 scale bytes, 128 code bytes;
+// compute/quant.py:24-56), so rows and super-blocks are 16-byte aligned.
+// Lane q of a row's LPR = q4k_lpr(K) lanes takes block pair q of the row
+// (nq = K / 64 pairs; a lane with q >= nq loads pair nq - 1 and adds zero):
+// code bytes 32 g .. 32 g + 31 (g = q & 3) of super-block q / 4 and that
+// super-block's 16-byte header, three 128-bit loads. A wave covers 64 / LPR
+// rows per step, and a row's partial sums meet in a8_group_sum. Every kernel
+// below runs this arithmetic per (pair, row), so the per-pair and grouped
+// kernels give identical bits.
 
-constexpr int Q4K_UMAX = 2;     // units per lane: K <= 64 * 2 * 32 = 4096
+constexpr int Q4K_KMAX = 4096;   // K of the Q4_K kernels (nq <= 64)
 constexpr int Q4K_GU_WAVES = 8;
-constexpr int Q4K_GU_RPW = 2;   // gate and up rows per wave
-constexpr int Q4K_DN_ROWS = 16; // output rows per down workgroup
+constexpr int Q4K_GU_STEPS = 3;  // row steps of gate and of up per wave (per-pair kernel)
+constexpr int Q4K_GG_STEPS = 2;  // the same, grouped kernel (rows held while the tokens go by)
+constexpr int Q4K_DN_STEPS = 4;  // row steps per down wave (per-pair kernel, two waves per expert slot)
+constexpr int Q4K_DG_WAVES = 4, Q4K_DG_STEPS = 2;  // grouped down
 
-struct Q4kX {
-  float x0[16], x1[16];
-  float s0, s1;
+struct Q4kRow {
+  v4u c0, c1, hd;
 };
 
-// the unit's activations (x: the token's K floats, 16-byte aligned; zeros when !valid)
-__device__ __forceinline__ void q4k_unit_x(const float* __restrict__ x, int u, bool valid, Q4kX& X) {
-  const int sb = u >> 3, g = (u >> 1) & 3, h = u & 1;
-  const float* p0 = x + sb * 256 + g * 64 + 16 * h;
-  const float* p1 = p0 + 32;
-  float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v4f a = *(const v4f*)(p0 + 4 * i), b = *(const v4f*)(p1 + 4 * i);
-    if (!valid) a = b = v4f{0.f, 0.f, 0.f, 0.f};
-    X.x0[4 * i] = a.x; X.x0[4 * i + 1] = a.y; X.x0[4 * i + 2] = a.z; X.x0[4 * i + 3] = a.w;
-    X.x1[4 * i] = b.x; X.x1[4 * i + 1] = b.y; X.x1[4 * i + 2] = b.z; X.x1[4 * i + 3] = b.w;
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    s0 += X.x0[j];
-    s1 += X.x1[j];
-  }
-  X.s0 = s0;
-  X.s1 = s1;
-}
-
-// get_scale_min_k4 (compute/quant.py:24-40) for sub-block s of the 12 scale bytes in y, z, w
-__device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w, int s, float& sc, float& m) {
-  auto byte = [&](int i) -> uint32_t {
-    const uint32_t d = i < 4 ? y : (i < 8 ? z : w);
-    return (d >> (8 * (i & 3))) & 0xffu;
-  };
-  const uint32_t lo_sc = byte(s & 3) & 63u, lo_m = byte((s & 3) + 4) & 63u;
-  const uint32_t bs4 = byte((s & 3) + 8);  // s >= 4: byte s + 4
-  const uint32_t hi_sc = (bs4 & 0x0fu) | ((byte(s & 3) >> 6) << 4);
-  const uint32_t hi_m = (bs4 >> 4) | ((byte((s & 3) + 4) >> 6) << 4);
-  sc = (float)(s < 4 ? lo_sc : hi_sc);
-  m = (float)(s < 4 ? lo_m : hi_m);
-}
-
-__device__ __forceinline__ float q4k_unit_dot(const v4u& c, const v4u& hd, int u, const Q4kX& X) {
-  const int g = (u >> 1) & 3;
-  float sc0, m0, sc1, m1;
-  q4k_scale_min(hd.y, hd.z, hd.w, 2 * g, sc0, m0);
-  q4k_scale_min(hd.y, hd.z, hd.w, 2 * g + 1, sc1, m1);
-  const float d = nsx_h2f(hd.x & 0xffffu), dmin = nsx_h2f(hd.x >> 16);
-  float p0 = 0.f, p1 = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = c[i] & 0x0f0f0f0fu, hi = (c[i] >> 4) & 0x0f0f0f0fu;
-    p0 = fmaf(nsx_ub<0>(lo), X.x0[4 * i], p0);
-    p0 = fmaf(nsx_ub<1>(lo), X.x0[4 * i + 1], p0);
-    p0 = fmaf(nsx_ub<2>(lo), X.x0[4 * i + 2], p0);
-    p0 = fmaf(nsx_ub<3>(lo), X.x0[4 * i + 3], p0);
-    p1 = fmaf(nsx_ub<0>(hi), X.x1[4 * i], p1);
-    p1 = fmaf(nsx_ub<1>(hi), X.x1[4 * i + 1], p1);
-    p1 = fmaf(nsx_ub<2>(hi), X.x1[4 * i + 2], p1);
-    p1 = fmaf(nsx_ub<3>(hi), X.x1[4 * i + 3], p1);
-  }
-  return fmaf(d * sc0, p0, -(dmin * m0) * X.s0) + fmaf(d * sc1, p1, -(dmin * m1) * X.s1);
-}
-
-// codes and header of unit u of `row` (clamped in-bounds loads)
-__device__ __forceinline__ void q4k_unit_load(const uint8_t* __restrict__ mat, int row, uint32_t rb, int u, v4u& c,
-                                              v4u& hd) {
+// this lane's block pair q of `row` (rb: bytes per row)
+__device__ __forceinline__ void q4k_row_load(const uint8_t* __restrict__ mat, int row, uint32_t rb, int q, Q4kRow& r) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
-  const uint8_t* sbp = mat + (int64_t)row * rb + (u >> 3) * 144;
-  hd = *(gv4u*)sbp;  // (cached: eight lanes share a header, and tokens routed alike share rows)
-  c = *(gv4u*)(sbp + 16 + 16 * (u & 7));
+  const uint8_t* sb = mat + (int64_t)row * rb + (q >> 2) * 144;
+  // (plain loads: a non-temporal hint on the codes, whose cache lines the
+  // header loads also touch, measured 25% slower)
+  r.hd = *(gv4u*)sb;  // the four lanes of a super-block share it
+  r.c0 = *(gv4u*)(sb + 16 + 32 * (q & 3));
+  r.c1 = *(gv4u*)(sb + 32 + 32 * (q & 3));
 }
 
-// gate/up: workgroup = (pair, 16 rows), wave = 2 rows of gate and of up
-template <int U>  // (4 waves per SIMD: two workgroups share a CU, VGPRs <= 128)
+// LDS barrier that leaves the memory counter alone: lgkmcnt(0) (this wave's
+// LDS writes have landed), then s_barrier; the memory clobber keeps the
+// compiler from moving LDS accesses across it. Row loads stay in flight.
+__device__ __forceinline__ void q4k_lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// gate/up: workgroup = (pair, RPG rows); wave = Q4K_GU_STEPS steps of
+// 64 / LPR rows of gate and of up. The workgroup first turns the token's h
+// into activation terms in LDS (wave 0 meanwhile selects the top-k when the
+// kernel does that), then issues all its row loads.
+template <int LPR>  // (4 waves per SIMD: two workgroups share a CU, VGPRs <= 128)
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void moe_gu_q4k_kernel(MoeDev a) {
-  extern __shared__ __align__(16) float q4k_xs[];
-  constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
+  constexpr int RS = 64 / LPR, RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * RS;
+  __shared__ __align__(16) uint8_t xs[a8_bytes(Q4K_KMAX)];
+  __shared__ int s_e;
+  typedef const __attribute__((address_space(1))) v4f gv4f;
   nsx_hoist(a.n_ff, a.n_embd, a.top_k, a.E, (const void*)a.ids, (const void*)a.h, a.gate_base, a.up_base,
             (const void*)a.gate_ptrs, (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias,
             (const void*)a.up_bias, (const void*)a.act, a.act_kind, a.alpha, a.limit);
-  __shared__ int s_e;
   const int groups = (a.n_ff + RPG - 1) / RPG;
   const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
-  const int K = a.n_embd, t = p / a.top_k;
+  const int K = a.n_embd, nq = K / 64, t = p / a.top_k;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  // loads first: this thread's 8 activations of h (K <= 8 x 512), the pair's expert id
+  // (issued together with the top-k's logits load: one round trip)
+  const int i8 = min((int)threadIdx.x, K / 8 - 1);
+  const v4f hlo = *(gv4f*)(a.h + (int64_t)t * K + 8 * i8), hhi = *(gv4f*)(a.h + (int64_t)t * K + 8 * i8 + 4);
+  const int e_in = a.topk_in_gu ? 0 : a.ids[p];
   if (a.topk_in_gu && wave == 0) {
     // the top-k from the router's logits by wave 0 (as moe_gu_kernel); the
     // token's first workgroup also writes the ids / weights the down phase reads
@@ -1326,40 +1292,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void m
     }
     if (lane == 0) s_e = clamp_expert(ej, a.E);
   }
-  for (int i = threadIdx.x; i < K / 4; i += blockDim.x) ((v4f*)q4k_xs)[i] = ((const v4f*)(a.h + (int64_t)t * K))[i];
+  if ((int)threadIdx.x < K / 8) {  // K / 8 is a multiple of 4: DPP quads stay whole
+    const float v[8] = {hlo.x, hlo.y, hlo.z, hlo.w, hhi.x, hhi.y, hhi.z, hhi.w};
+    a8_quad(v, (int)threadIdx.x >> 2, nq, xs);
+  }
+  // The terms are in LDS before any row load goes out: a wave's loads can
+  // stall at issue once the memory system is saturated, and a barrier behind
+  // them would keep every wave of the workgroup from computing until the last
+  // one had issued its last load.
   __syncthreads();
-  const int e = a.topk_in_gu ? s_e : clamp_expert(a.ids[p], a.E);
-  const int nu = K / 32;
+  const int e = a.topk_in_gu ? s_e : clamp_expert(e_in, a.E);
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
   const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
   const uint8_t* um = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
-  v4u cg[Q4K_GU_RPW][U], hg[Q4K_GU_RPW][U], cu[Q4K_GU_RPW][U], hu[Q4K_GU_RPW][U];
+  const int q = min(lane % LPR, nq - 1), sub = lane / LPR;
+  const bool live = lane % LPR < nq;
+  const int rw = r0 + wave * Q4K_GU_STEPS * RS + sub;  // this lane's row at step 0
+  Q4kRow G[Q4K_GU_STEPS], U[Q4K_GU_STEPS];
 #pragma unroll
-  for (int j = 0; j < Q4K_GU_RPW; ++j) {
-    const int row = min(r0 + wave * Q4K_GU_RPW + j, a.n_ff - 1);
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int u = min(lane + 64 * i, nu - 1);
-      q4k_unit_load(gm, row, rb, u, cg[j][i], hg[j][i]);
-      q4k_unit_load(um, row, rb, u, cu[j][i], hu[j][i]);
-    }
+  for (int j = 0; j < Q4K_GU_STEPS; ++j) {
+    const int row = min(rw + j * RS, a.n_ff - 1);
+    q4k_row_load(gm, row, rb, q, G[j]);
+    q4k_row_load(um, row, rb, q, U[j]);
   }
-  Q4kX X[U];
+  A8Pair X;
+  a8_load(xs, q, nq, X);
 #pragma unroll
-  for (int i = 0; i < U; ++i) q4k_unit_x(q4k_xs, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
-#pragma unroll
-  for (int j = 0; j < Q4K_GU_RPW; ++j) {
-    const int row = r0 + wave * Q4K_GU_RPW + j;
-    float gs = 0.f, us = 0.f;
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int u = min(lane + 64 * i, nu - 1);
-      gs += q4k_unit_dot(cg[j][i], hg[j][i], u, X[i]);
-      us += q4k_unit_dot(cu[j][i], hu[j][i], u, X[i]);
-    }
-    gs = nsx_wave_sum(gs);
-    us = nsx_wave_sum(us);
-    if (lane == 0 && row < a.n_ff) {
+  for (int j = 0; j < Q4K_GU_STEPS; ++j) {
+    float gs = q4k_a8_dot(G[j].c0, G[j].c1, G[j].hd, q & 3, X);
+    float us = q4k_a8_dot(U[j].c0, U[j].c1, U[j].hd, q & 3, X);
+    gs = a8_group_sum<LPR>(live ? gs : 0.f);
+    us = a8_group_sum<LPR>(live ? us : 0.f);
+    const int row = rw + j * RS;
+    if (lane % LPR == 0 && row < a.n_ff) {
       if (a.gate_bias) gs += a.gate_bias[(int64_t)e * a.n_ff + row];
       if (a.up_bias) us += a.up_bias[(int64_t)e * a.n_ff + row];
       a.act[(int64_t)p * a.n_ff + row] = moe_act(a.act_kind, gs, us, a.alpha, a.limit);
@@ -1367,185 +1332,184 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void m
   }
 }
 
-// down and combine: workgroup = (token, 16 output rows), wave j = expert slot j
-template <int U>
-__global__ __launch_bounds__(512) void moe_down_q4k_kernel(MoeDev a) {
-  __shared__ float red[MAX_TOPK][Q4K_DN_ROWS];
+// down and combine: workgroup = (token, RPG output rows), two waves per
+// expert slot, each Q4K_DN_STEPS steps of 64 / LPR rows. The workgroup turns
+// the token's k activation vectors into terms in LDS, then issues its row
+// loads; the slots' outputs are added in ascending expert id.
+constexpr int Q4K_DN_SLICES = Q4K_KMAX / 8 / 128;  // 8-element slices per thread (k x n_ff / 8 over 128 k threads)
+
+template <int LPR>
+__global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
+  constexpr int RS = 64 / LPR, RPW = Q4K_DN_STEPS * RS, RPG = 2 * RPW;
+  extern __shared__ __align__(16) uint8_t q4k_xa[];  // k vectors of terms
+  __shared__ float red[MAX_TOPK][RPG];
   __shared__ int s_slot[MAX_TOPK];
+  typedef const __attribute__((address_space(1))) v4f gv4f;
   nsx_hoist(a.n_embd, a.n_ff, a.top_k, a.E, (const void*)a.ids, (const void*)a.wts, (const void*)a.act,
             a.down_base, (const void*)a.down_ptrs, a.down_stride, (const void*)a.down_bias, (const void*)a.out);
-  const int groups = (a.n_embd + Q4K_DN_ROWS - 1) / Q4K_DN_ROWS;
-  const int t = blockIdx.x / groups, r0 = (blockIdx.x - t * groups) * Q4K_DN_ROWS;
+  const int groups = (a.n_embd + RPG - 1) / RPG;
+  const int t = blockIdx.x / groups, r0 = (blockIdx.x - t * groups) * RPG;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int k = a.top_k, K = a.n_ff;
-  if (wave < k) {
-    const int p = t * k + wave;
-    const int id_l = clamp_expert(a.ids[(int64_t)t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
-    const int e = __builtin_amdgcn_readlane(id_l, wave);
-    // this slot's rank in ascending expert id (ties: lower slot)
-    const uint64_t before = __builtin_amdgcn_ballot_w64(lane < k && (id_l < e || (id_l == e && lane < wave)));
-    if (lane == 0) s_slot[__builtin_popcountll(before)] = wave;
-    const int nu = K / 32;
-    const uint32_t rb = (uint32_t)(K / 256) * 144u;
-    const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
-    Q4kX X[U];
+  const int k = a.top_k, K = a.n_ff, nq = K / 64, slot = wave >> 1;
+  // loads first: the token's slot ids, then its k activation vectors (8-element slices)
+  const int id_l = clamp_expert(a.ids[(int64_t)t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
+  const int per = K / 8, items = k * per, nthr = 128 * k;
+  v4f xv[Q4K_DN_SLICES][2];
 #pragma unroll
-    for (int i = 0; i < U; ++i)
-      q4k_unit_x(a.act + (int64_t)p * K, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
-    constexpr int RB = Q4K_DN_ROWS / U;  // rows in flight per batch
-    float mine = 0.f;                    // lane j keeps row j's result
+  for (int i = 0; i < Q4K_DN_SLICES; ++i) {
+    const int it = min((int)threadIdx.x + i * nthr, items - 1);
+    const float* src = a.act + ((int64_t)t * k + it / per) * K + 8 * (it % per);
+    xv[i][0] = *(gv4f*)src;
+    xv[i][1] = *(gv4f*)(src + 4);
+  }
 #pragma unroll
-    for (int j0 = 0; j0 < Q4K_DN_ROWS; j0 += RB) {
-      v4u c[RB][U], hd[RB][U];
-#pragma unroll
-      for (int j = 0; j < RB; ++j) {
-        const int row = min(r0 + j0 + j, a.n_embd - 1);
-#pragma unroll
-        for (int i = 0; i < U; ++i) q4k_unit_load(dm, row, rb, min(lane + 64 * i, nu - 1), c[j][i], hd[j][i]);
-      }
-#pragma unroll
-      for (int j = 0; j < RB; ++j) {
-        float y = 0.f;
-#pragma unroll
-        for (int i = 0; i < U; ++i) y += q4k_unit_dot(c[j][i], hd[j][i], min(lane + 64 * i, nu - 1), X[i]);
-        y = nsx_wave_sum(y);
-        mine = lane == j0 + j ? y : mine;
-      }
+  for (int i = 0; i < Q4K_DN_SLICES; ++i) {
+    const int it = (int)threadIdx.x + i * nthr;  // items and nthr are multiples of 4: quads stay whole
+    if (it < items) {
+      const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                          xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+      a8_quad(v, (it % per) >> 2, nq, q4k_xa + (it / per) * a8_bytes(K));
     }
-    const int row = r0 + lane;
-    if (lane < Q4K_DN_ROWS) {
-      if (a.down_bias && row < a.n_embd) mine += a.down_bias[(int64_t)e * a.n_embd + row];
-      red[wave][lane] = mine;
+  }
+  const int e = __builtin_amdgcn_readlane(id_l, slot);
+  if ((wave & 1) == 0) {  // this slot's rank in ascending expert id (ties: lower slot)
+    const uint64_t before = __builtin_amdgcn_ballot_w64(lane < k && (id_l < e || (id_l == e && lane < slot)));
+    if (lane == 0) s_slot[__builtin_popcountll(before)] = slot;
+  }
+  __syncthreads();  // the terms are in LDS before the row loads go out (see the gate/up kernel)
+  const uint32_t rb = (uint32_t)(K / 256) * 144u;
+  const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
+  const int q = min(lane % LPR, nq - 1), sub = lane / LPR;
+  const bool live = lane % LPR < nq;
+  const int rw = r0 + (wave & 1) * RPW + sub;
+  Q4kRow R[Q4K_DN_STEPS];
+#pragma unroll
+  for (int j = 0; j < Q4K_DN_STEPS; ++j) q4k_row_load(dm, min(rw + j * RS, a.n_embd - 1), rb, q, R[j]);
+  A8Pair X;
+  a8_load(q4k_xa + slot * a8_bytes(K), q, nq, X);
+#pragma unroll
+  for (int j = 0; j < Q4K_DN_STEPS; ++j) {
+    float y = q4k_a8_dot(R[j].c0, R[j].c1, R[j].hd, q & 3, X);
+    y = a8_group_sum<LPR>(live ? y : 0.f);
+    const int row = rw + j * RS;
+    if (lane % LPR == 0) {
+      if (a.down_bias && row < a.n_embd) y += a.down_bias[(int64_t)e * a.n_embd + row];
+      red[slot][row - r0] = y;
     }
   }
   __syncthreads();
-  if (wave != 0 || lane >= Q4K_DN_ROWS) return;
-  const int row = r0 + lane;
+  if (threadIdx.x >= RPG) return;
+  const int row = r0 + (int)threadIdx.x;
   float o = 0.f;
   for (int jj = 0; jj < k; ++jj) {
     const int jx = s_slot[jj];
-    o = combine_one(o, a.wts[(int64_t)t * k + jx], red[jx][lane]);
+    o = combine_one(o, a.wts[(int64_t)t * k + jx], red[jx][threadIdx.x]);
   }
   if (row < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
 }
 
 // Grouped Q4_K (several tokens per expert): the same per-(pair, row)
 // arithmetic as the kernels above, with the rows' codes and headers held in
-// registers while the work item's tokens go by one at a time (activations
-// from L2), so an expert's rows are read from HBM once per item.
+// registers while the work item's tokens go by one at a time, their
+// activation terms (a8_terms_kernel) read from L2, so an expert's rows are
+// read from HBM once per item.
 
-// gate/up: workgroup = (item, 16 rows); wave = 2 rows of gate and of up
-template <int U>
+// activation terms of the vectors x[v * K .. v * K + K), one workgroup per vector
+__global__ __launch_bounds__(256) void a8_terms_kernel(const float* __restrict__ x, int K, uint8_t* __restrict__ dst) {
+  a8_vector(x + (int64_t)blockIdx.x * K, K, dst + (int64_t)blockIdx.x * a8_bytes(K), (int)threadIdx.x, 256);
+}
+
+// gate/up: workgroup = (item, RPG rows); wave = Q4K_GG_STEPS steps of 64 / LPR rows of gate and of up
+template <int LPR>
 __global__ __launch_bounds__(512) void moe_gu_q4k_grouped_kernel(MoeDev a) {
-  constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
+  constexpr int RS = 64 / LPR, RPG = Q4K_GU_WAVES * Q4K_GG_STEPS * RS;
   int grp;
   int4 item;
   if (!grp_work(a, (a.n_ff + RPG - 1) / RPG, grp, item)) return;
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int K = a.n_embd, nu = K / 32;
+  const int K = a.n_embd, nq = K / 64;
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
   const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
   const uint8_t* um = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
-  const int r0 = grp * RPG + wave * Q4K_GU_RPW;
-  v4u cg[Q4K_GU_RPW][U], hg[Q4K_GU_RPW][U], cu[Q4K_GU_RPW][U], hu[Q4K_GU_RPW][U];
+  const int q = min(lane % LPR, nq - 1), sub = lane / LPR;
+  const bool live = lane % LPR < nq;
+  const int rw = grp * RPG + wave * Q4K_GG_STEPS * RS + sub;
+  Q4kRow G[Q4K_GG_STEPS], U[Q4K_GG_STEPS];
+  float gb[Q4K_GG_STEPS], ub[Q4K_GG_STEPS];
 #pragma unroll
-  for (int j = 0; j < Q4K_GU_RPW; ++j) {
-    const int row = min(r0 + j, a.n_ff - 1);
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int u = min(lane + 64 * i, nu - 1);
-      q4k_unit_load(gm, row, rb, u, cg[j][i], hg[j][i]);
-      q4k_unit_load(um, row, rb, u, cu[j][i], hu[j][i]);
-    }
-  }
-  float gb[Q4K_GU_RPW], ub[Q4K_GU_RPW];
-#pragma unroll
-  for (int j = 0; j < Q4K_GU_RPW; ++j) {
-    const int row = min(r0 + j, a.n_ff - 1);
+  for (int j = 0; j < Q4K_GG_STEPS; ++j) {
+    const int row = min(rw + j * RS, a.n_ff - 1);
+    q4k_row_load(gm, row, rb, q, G[j]);
+    q4k_row_load(um, row, rb, q, U[j]);
     gb[j] = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + row] : 0.f;
     ub[j] = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + row] : 0.f;
   }
   const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
+  const int64_t xstride = a8_bytes(K);
 #pragma nounroll
   for (int w = 0; w < n; ++w) {
-    // decode the codes per token (hoisting the decoded weights out of the loop would need
-    // 4 x 36 registers per unit and row): the empty asm marks them as changed
+    // unpack the codes per token (unpacked codes held across tokens would double
+    // their registers): the empty asm marks them as changed
 #pragma unroll
-    for (int j = 0; j < Q4K_GU_RPW; ++j)
-#pragma unroll
-      for (int i = 0; i < U; ++i) asm volatile("" : "+v"(cg[j][i]), "+v"(hg[j][i]), "+v"(cu[j][i]), "+v"(hu[j][i]));
+    for (int j = 0; j < Q4K_GG_STEPS; ++j)
+      asm volatile("" : "+v"(G[j].c0), "+v"(G[j].c1), "+v"(G[j].hd), "+v"(U[j].c0), "+v"(U[j].c1), "+v"(U[j].hd));
     const int pr = __builtin_amdgcn_readlane(my_pair, w);
-    const float* x = a.h + (int64_t)(pr / a.top_k) * K;
-    Q4kX X[U];
+    A8Pair X;
+    a8_load(a.xq_h + (int64_t)(pr / a.top_k) * xstride, q, nq, X);
 #pragma unroll
-    for (int i = 0; i < U; ++i) q4k_unit_x(x, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
-#pragma unroll
-    for (int j = 0; j < Q4K_GU_RPW; ++j) {
-      float gs = 0.f, us = 0.f;
-#pragma unroll
-      for (int i = 0; i < U; ++i) {
-        const int u = min(lane + 64 * i, nu - 1);
-        gs += q4k_unit_dot(cg[j][i], hg[j][i], u, X[i]);
-        us += q4k_unit_dot(cu[j][i], hu[j][i], u, X[i]);
-      }
-      gs = nsx_wave_sum(gs);
-      us = nsx_wave_sum(us);
-      const int row = r0 + j;
-      if (lane == 0 && row < a.n_ff)
+    for (int j = 0; j < Q4K_GG_STEPS; ++j) {
+      float gs = q4k_a8_dot(G[j].c0, G[j].c1, G[j].hd, q & 3, X);
+      float us = q4k_a8_dot(U[j].c0, U[j].c1, U[j].hd, q & 3, X);
+      gs = a8_group_sum<LPR>(live ? gs : 0.f);
+      us = a8_group_sum<LPR>(live ? us : 0.f);
+      const int row = rw + j * RS;
+      if (lane % LPR == 0 && row < a.n_ff)
         a.act[(int64_t)pr * a.n_ff + row] = moe_act(a.act_kind, gs + gb[j], us + ub[j], a.alpha, a.limit);
     }
   }
 }
 
-// down: workgroup = (item, 16 output rows); wave = 4 rows; y[pair, rows] =
-// the expert's down rows . activation(pair) + bias (moe_combine_kernel adds
-// the pairs of a token in ascending expert id)
-constexpr int Q4K_DG_WAVES = 4, Q4K_DG_RPW = 4;
-
-template <int U>
+// down: workgroup = (item, RPG output rows); y[pair, rows] = the expert's
+// down rows . activation(pair) + bias (moe_combine_kernel adds the pairs of a
+// token in ascending expert id)
+template <int LPR>
 __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
-  constexpr int RPG = Q4K_DG_WAVES * Q4K_DG_RPW;
+  constexpr int RS = 64 / LPR, RPG = Q4K_DG_WAVES * Q4K_DG_STEPS * RS;
   int grp;
   int4 item;
   if (!grp_work(a, (a.n_embd + RPG - 1) / RPG, grp, item)) return;
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int K = a.n_ff, nu = K / 32;
+  const int K = a.n_ff, nq = K / 64;
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
   const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
-  const int r0 = grp * RPG + wave * Q4K_DG_RPW;
-  v4u c[Q4K_DG_RPW][U], hd[Q4K_DG_RPW][U];
+  const int q = min(lane % LPR, nq - 1), sub = lane / LPR;
+  const bool live = lane % LPR < nq;
+  const int rw = grp * RPG + wave * Q4K_DG_STEPS * RS + sub;
+  Q4kRow R[Q4K_DG_STEPS];
+  float bias[Q4K_DG_STEPS];
 #pragma unroll
-  for (int j = 0; j < Q4K_DG_RPW; ++j) {
-    const int row = min(r0 + j, a.n_embd - 1);
-#pragma unroll
-    for (int i = 0; i < U; ++i) q4k_unit_load(dm, row, rb, min(lane + 64 * i, nu - 1), c[j][i], hd[j][i]);
+  for (int j = 0; j < Q4K_DG_STEPS; ++j) {
+    const int row = min(rw + j * RS, a.n_embd - 1);
+    q4k_row_load(dm, row, rb, q, R[j]);
+    bias[j] = a.down_bias ? a.down_bias[(int64_t)e * a.n_embd + row] : 0.f;
   }
-  float bias[Q4K_DG_RPW];
-#pragma unroll
-  for (int j = 0; j < Q4K_DG_RPW; ++j)
-    bias[j] = a.down_bias ? a.down_bias[(int64_t)e * a.n_embd + min(r0 + j, a.n_embd - 1)] : 0.f;
   const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
+  const int64_t xstride = a8_bytes(K);
 #pragma nounroll
   for (int w = 0; w < n; ++w) {
 #pragma unroll
-    for (int j = 0; j < Q4K_DG_RPW; ++j)
-#pragma unroll
-      for (int i = 0; i < U; ++i) asm volatile("" : "+v"(c[j][i]), "+v"(hd[j][i]));  // decode per token
+    for (int j = 0; j < Q4K_DG_STEPS; ++j) asm volatile("" : "+v"(R[j].c0), "+v"(R[j].c1), "+v"(R[j].hd));
     const int pr = __builtin_amdgcn_readlane(my_pair, w);
-    Q4kX X[U];
+    A8Pair X;
+    a8_load(a.xq_a + (int64_t)pr * xstride, q, nq, X);
 #pragma unroll
-    for (int i = 0; i < U; ++i)
-      q4k_unit_x(a.act + (int64_t)pr * K, min(lane + 64 * i, nu - 1), lane + 64 * i < nu, X[i]);
-#pragma unroll
-    for (int j = 0; j < Q4K_DG_RPW; ++j) {
-      float y = 0.f;
-#pragma unroll
-      for (int i = 0; i < U; ++i) y += q4k_unit_dot(c[j][i], hd[j][i], min(lane + 64 * i, nu - 1), X[i]);
-      y = nsx_wave_sum(y);
-      const int row = r0 + j;
-      if (lane == 0 && row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y + bias[j];
+    for (int j = 0; j < Q4K_DG_STEPS; ++j) {
+      float y = q4k_a8_dot(R[j].c0, R[j].c1, R[j].hd, q & 3, X);
+      y = a8_group_sum<LPR>(live ? y : 0.f);
+      const int row = rw + j * RS;
+      if (lane % LPR == 0 && row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y + bias[j];
     }
   }
 }
@@ -1846,7 +1810,7 @@ constexpr int GRP_AUTO_MIN_T = 8;  // NSX_DISPATCH_AUTO groups from this many to
 
 // The Q4_K kernels take K <= 4096 and 16-byte aligned expert rows.
 static bool q4k_fast(const nsx_moe_layer* L) {
-  if (L->ggml_type != NSX_Q4_K || L->n_embd > 64 * Q4K_UMAX * 32 || L->n_ff > 64 * Q4K_UMAX * 32) return false;
+  if (L->ggml_type != NSX_Q4_K || L->n_embd > Q4K_KMAX || L->n_ff > Q4K_KMAX) return false;
   if (L->gate_base) {
     const uintptr_t m = (uintptr_t)L->gate_base | (uintptr_t)L->up_base | (uintptr_t)L->down_base |
                         (uintptr_t)L->gate_stride | (uintptr_t)L->up_stride | (uintptr_t)L->down_stride;
@@ -1893,10 +1857,12 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   o = al(o + T * L->n_expert * 4);
   p.off_act = o;
   o = al(o + (t64 ? 0 : P * L->n_ff * 4));
+  const bool a8 = p.grouped && !p.mq && !t64;  // grouped Q4_K on the int8 dot: activation terms per vector
   p.off_xqh = o;
-  o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP : (p.mq ? T * mq_row_bytes(L->n_embd) : 0)));
+  o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP
+                  : (p.mq ? T * mq_row_bytes(L->n_embd) : (a8 ? T * a8_bytes(L->n_embd) : 0))));
   p.off_xqa = o;
-  o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : (p.mq ? P * mq_row_bytes(L->n_ff) : 0)));
+  o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : (p.mq ? P * mq_row_bytes(L->n_ff) : (a8 ? P * a8_bytes(L->n_ff) : 0))));
   p.off_items = o;
   o = al(o + (int64_t)p.max_items * 16);
   p.off_nitems = o;
@@ -1966,28 +1932,38 @@ static int check_layer(const nsx_moe_layer* L, int64_t T) {
 }
 
 
-template <int UG, int UD>
+// f(std::integral_constant<int, LPR>) for the lanes per row of a Q4_K dot of K elements
+template <typename F>
+static int with_q4k_lpr(int K, F&& f) {
+  switch (q4k_lpr(K)) {
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    case 16: return f(std::integral_constant<int, 16>{});
+    case 32: return f(std::integral_constant<int, 32>{});
+    default: return f(std::integral_constant<int, 64>{});
+  }
+}
+
 static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
   const int64_t P = T * d.top_k;
   if (gate_up) {
-    constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_RPW;
-    const size_t lds = (size_t)d.n_embd * 4;
-    if (lds > 64 * 1024)
-      NSX_HIP(hipFuncSetAttribute((const void*)moe_gu_q4k_kernel<UG>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds));
-    int rc = nsx_launch(moe_gu_q4k_kernel<UG>, dim3((unsigned)(P * nsx_cdiv(d.n_ff, RPG))), dim3(64 * Q4K_GU_WAVES),
-                        lds, st, d);
+    const int rc = with_q4k_lpr(d.n_embd, [&](auto lpr) {
+      constexpr int LPR = decltype(lpr)::value, RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * (64 / LPR);
+      return nsx_launch(moe_gu_q4k_kernel<LPR>, dim3((unsigned)(P * nsx_cdiv(d.n_ff, RPG))),
+                        dim3(64 * Q4K_GU_WAVES), 0, st, d);
+    });
     if (rc) return rc;
   }
   if (!down) return NSX_OK;
-  return nsx_launch(moe_down_q4k_kernel<UD>, dim3((unsigned)(T * nsx_cdiv(d.n_embd, Q4K_DN_ROWS))),
-                    dim3(64 * MAX_TOPK), 0, st, d);
-}
-
-static int launch_q4k_any(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
-  const bool g2 = d.n_embd > 64 * 32, d2 = d.n_ff > 64 * 32;  // units per lane of gate/up and of down
-  if (g2) return d2 ? launch_q4k<2, 2>(d, T, st, gate_up, down) : launch_q4k<2, 1>(d, T, st, gate_up, down);
-  return d2 ? launch_q4k<1, 2>(d, T, st, gate_up, down) : launch_q4k<1, 1>(d, T, st, gate_up, down);
+  return with_q4k_lpr(d.n_ff, [&](auto lpr) {
+    constexpr int LPR = decltype(lpr)::value, RPG = 2 * Q4K_DN_STEPS * (64 / LPR);
+    const size_t lds = (size_t)d.top_k * (size_t)a8_bytes(d.n_ff);
+    if (lds > 64 * 1024)
+      NSX_HIP(hipFuncSetAttribute((const void*)moe_down_q4k_kernel<LPR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds));
+    return nsx_launch(moe_down_q4k_kernel<LPR>, dim3((unsigned)(T * nsx_cdiv(d.n_embd, RPG))),
+                      dim3(128 * d.top_k), lds, st, d);
+  });
 }
 
 template <int FMT>
@@ -2108,11 +2084,15 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
                              (uint8_t*)(ws + p.off_xqh))))
           return rc;
         rc = nsx_launch(moe_q4k_mfma_kernel<true>, grid8(nsx_cdiv(L->n_ff, MQ_WG_ROWS)), dim3(256), 0, st, d);
-      } else {
-        const int64_t g = nsx_cdiv(L->n_ff, Q4K_GU_WAVES * Q4K_GU_RPW);
-        rc = L->n_embd > 64 * 32
-                 ? nsx_launch(moe_gu_q4k_grouped_kernel<2>, grid8(g), dim3(64 * Q4K_GU_WAVES), 0, st, d)
-                 : nsx_launch(moe_gu_q4k_grouped_kernel<1>, grid8(g), dim3(64 * Q4K_GU_WAVES), 0, st, d);
+      } else {  // Q4_K on the int8 dot: the tokens' activation terms, then the rows
+        if ((rc = nsx_launch(a8_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
+                             (uint8_t*)(ws + p.off_xqh))))
+          return rc;
+        rc = with_q4k_lpr(L->n_embd, [&](auto lpr) {
+          constexpr int LPR = decltype(lpr)::value;
+          const int64_t g = nsx_cdiv(L->n_ff, Q4K_GU_WAVES * Q4K_GG_STEPS * (64 / LPR));
+          return nsx_launch(moe_gu_q4k_grouped_kernel<LPR>, grid8(g), dim3(64 * Q4K_GU_WAVES), 0, st, d);
+        });
       }
       if (rc) return rc;
     }
@@ -2125,10 +2105,14 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
           return rc;
         rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, 2 * MQ_WG_ROWS)), dim3(256), 0, st, d);
       } else {
-        const int64_t g = nsx_cdiv(L->n_embd, Q4K_DG_WAVES * Q4K_DG_RPW);
-        rc = L->n_ff > 64 * 32
-                 ? nsx_launch(moe_down_q4k_grouped_kernel<2>, grid8(g), dim3(64 * Q4K_DG_WAVES), 0, st, d)
-                 : nsx_launch(moe_down_q4k_grouped_kernel<1>, grid8(g), dim3(64 * Q4K_DG_WAVES), 0, st, d);
+        if ((rc = nsx_launch(a8_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
+                             (int)L->n_ff, d.xq_a)))
+          return rc;
+        rc = with_q4k_lpr(L->n_ff, [&](auto lpr) {
+          constexpr int LPR = decltype(lpr)::value;
+          const int64_t g = nsx_cdiv(L->n_embd, Q4K_DG_WAVES * Q4K_DG_STEPS * (64 / LPR));
+          return nsx_launch(moe_down_q4k_grouped_kernel<LPR>, grid8(g), dim3(64 * Q4K_DG_WAVES), 0, st, d);
+        });
       }
       if (rc) return rc;
     }
@@ -2151,7 +2135,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   switch (L->ggml_type) {  // the GGUF-layout down kernel also combines
     case NSX_MXFP4: return launch_raw_phases<NSX_MXFP4>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q4_K:
-      if (q4k_fast(L)) return launch_q4k_any(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
+      if (q4k_fast(L)) return launch_q4k(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
       return launch_raw_phases<NSX_Q4_K>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q4_0: return launch_raw_phases<NSX_Q4_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));
     case NSX_Q8_0: return launch_raw_phases<NSX_Q8_0>(d, T, st, on(NSX_PHASE_GATE_UP), on(NSX_PHASE_DOWN));

@@ -93,11 +93,14 @@ def test_workspace_bytes_by_dispatch(lib):
     L.n_embd, L.n_ff = 4096, 1536
     L.gate_stride = L.up_stride = L.down_stride = 1536 * 2304
     L.gate_base = L.up_base = L.down_base = 1 << 20
-    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) > 0
     wq = lib.nsx_moe_workspace_bytes(C.byref(L), 8)
-    L.dispatch = N.DISPATCH_MFMA  # plus the activation terms: 8 tokens of h, 32 pairs of activations
+    L.dispatch = N.DISPATCH_PAIRS
+    wp = lib.nsx_moe_workspace_bytes(C.byref(L), 8)
+    a8 = 8 * (4096 // 64 * 160) + 32 * (1536 // 64 * 160)  # int8 terms of 8 tokens of h, 32 activations
+    assert 0 < wp and wq >= wp + a8
+    L.dispatch = N.DISPATCH_MFMA  # the matrix-core terms in their place
     terms = 8 * (4 * 4096 + 4096 // 8 + 16) + 32 * (4 * 1536 + 1536 // 8 + 16)
-    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) >= wq + terms
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) >= wq - a8 + terms
     L.down_base = (1 << 20) + 8  # not 16-byte aligned: no Q4_K fast path, so no grouping
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
     assert b"MFMA" in lib.nsx_last_error()

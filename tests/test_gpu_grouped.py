@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import FFN_BAR, MFMA_TOL, rel_max, to_np
+from helpers import FFN_BAR, MFMA_TOL, Q4K_TOL, rel_max, to_np
 from moe_cases import _expert_set, _layer, _oracle_layer, _small
 from oracle import moe as OM
 
@@ -129,7 +129,7 @@ def test_grouped_q4k_equals_pairs_bitwise(dev, T):
     assert torch.equal(ip, ig) and torch.equal(wp, wg)
     assert torch.equal(op, og)
     ref, _, _, _ = _oracle_layer(cfg, t, h.cpu().numpy())
-    assert rel_max(to_np(og), ref) < 1e-5
+    assert rel_max(to_np(og), ref) < Q4K_TOL
 
 
 def test_config4_qwen3_t32_grouped(dev):
@@ -147,15 +147,16 @@ def test_config4_qwen3_t32_grouped(dev):
     sub = slice(0, 2)
     ref, rid, _, _ = _oracle_layer(cfg, t, h[sub].cpu().numpy())
     np.testing.assert_array_equal(np.sort(to_np(ia)[sub], 1), np.sort(rid, 1))
-    assert rel_max(to_np(oa)[sub], ref) < 1e-5
+    assert rel_max(to_np(oa)[sub], ref) < Q4K_TOL
 
 
 @pytest.mark.parametrize("T,scale", [(1, 1.0), (5, 1.0), (8, 1.0), (40, 1.0), (5, 1e3), (5, 1e-3)])
 def test_mfma_q4k_matches_oracle_and_pairs(dev, T, scale):
     """NSX_DISPATCH_MFMA (grouped Q4_K on the matrix cores: f16 products of the exact sc * q
     codes with a two-term split of power-of-two-scaled activations): the same routing as the
-    per-pair kernels, outputs within 1e-5 of theirs and of the float64 oracle, also for
-    activations scaled far from 1 (T=40 splits busy experts over several work items)."""
+    per-pair kernels (int8 dot), outputs within 1e-5 of the float64 oracle and within the
+    per-pair kernels' bound of theirs, also for activations scaled far from 1 (T=40 splits
+    busy experts over several work items)."""
     from nurostream_amd import synth
     cfg = _small("qwen3-small")
     t = synth.make_layer(cfg, seed=21, device=dev)
@@ -166,14 +167,14 @@ def test_mfma_q4k_matches_oracle_and_pairs(dev, T, scale):
     om, im, wm = lm(h)
     assert torch.equal(ip, im) and torch.equal(wp, wm)
     assert bool(torch.isfinite(om).all())
-    assert rel_max(to_np(om), to_np(op)) < 1e-5
+    assert rel_max(to_np(om), to_np(op)) < Q4K_TOL
     ref, _, _, _ = _oracle_layer(cfg, t, h.cpu().numpy())
     assert rel_max(to_np(om), ref) < 1e-5
 
 
 def test_config4_qwen3_t32_mfma(dev):
-    """BASELINE config 4 at T=32 on the matrix cores: within 1e-5 of the per-pair kernels on all
-    32 tokens; the oracle checks 2."""
+    """BASELINE config 4 at T=32 on the matrix cores: within the per-pair kernels' bound of
+    theirs on all 32 tokens; the oracle checks 2."""
     from nurostream_amd import synth
     cfg = synth.QWEN3_235B
     t = synth.make_layer(cfg, seed=0, device=dev)
@@ -183,7 +184,7 @@ def test_config4_qwen3_t32_mfma(dev):
     om, im, _ = lm(h)
     op, ip, _ = lp(h)
     assert torch.equal(im, ip)
-    assert rel_max(to_np(om), to_np(op)) < 1e-5
+    assert rel_max(to_np(om), to_np(op)) < Q4K_TOL
     sub = slice(0, 2)
     ref, rid, _, _ = _oracle_layer(cfg, t, h[sub].cpu().numpy())
     np.testing.assert_array_equal(np.sort(to_np(im)[sub], 1), np.sort(rid, 1))
