@@ -49,7 +49,7 @@ __device__ __forceinline__ void load8_w(const void* W, int64_t off, float (&w)[8
   }
 }
 
-constexpr int RT_MAXC = 8;   // 512-element chunks per lane and pass (K <= 4096 in one pass)
+constexpr int RT_U = 2;      // 8-element chunks per thread and pass of the router (K <= 4096 in one pass)
 constexpr int RT_XQ_WGS = 16;  // extra workgroups that quantize h for the t64 expert kernels
 
 // ---------------------------------------------------------------------------
@@ -85,10 +85,12 @@ __device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, f
 // maximum of the remaining keys (DPP), and the expert holding it with the
 // lowest index is the lowest set bit of the first slot's ballot of "remaining
 // and equal to the maximum". Results are wave-uniform. With weights false the
-// softmax is skipped (sel_w is left zero).
+// softmax is skipped (sel_w is left zero), and only the first `rounds`
+// experts are selected (the rest of sel_i is left zero).
 template <int NV>
 __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mode, int (&sel_i)[MAX_TOPK],
-                                            float (&sel_w)[MAX_TOPK], bool weights = true) {
+                                            float (&sel_w)[MAX_TOPK], bool weights = true, int rounds = MAX_TOPK) {
+  const int nr = weights ? k : min(k, rounds);
   const int lane = __lane_id();
   bool ok[NV];
 #pragma unroll
@@ -123,7 +125,7 @@ __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mo
   }
 #pragma unroll
   for (int j = 0; j < MAX_TOPK; ++j) {
-    if (j >= k) break;
+    if (j >= nr) break;
     uint32_t lk = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) lk = max(lk, ok[i] ? key[i] : 0u);
@@ -162,24 +164,27 @@ __device__ __forceinline__ void topk_select(float (&v)[NV], int E, int k, int mo
 
 // One token's top-k from its logits row (loads and selection), any E <= MAX_EXPERTS.
 __device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, int k, int mode,
-                                          int (&sel_i)[MAX_TOPK], float (&sel_w)[MAX_TOPK], bool weights = true) {
+                                          int (&sel_i)[MAX_TOPK], float (&sel_w)[MAX_TOPK], bool weights = true,
+                                          int rounds = MAX_TOPK) {
   if (E <= 128) {
     float v[2];
     topk_load<2>(lg, E, v);
-    topk_select<2>(v, E, k, mode, sel_i, sel_w, weights);
+    topk_select<2>(v, E, k, mode, sel_i, sel_w, weights, rounds);
   } else {
     float v[TOPK_NV];
     topk_load<TOPK_NV>(lg, E, v);
-    topk_select<TOPK_NV>(v, E, k, mode, sel_i, sel_w, weights);
+    topk_select<TOPK_NV>(v, E, k, mode, sel_i, sel_w, weights, rounds);
   }
 }
 
 // Router logits (model/gpt_oss.py:97-99,116-121; moe/router.py:59-69).
-// Workgroups [0, ceil(E/4)) of grid row y compute the logits of tokens
-// 8y .. 8y + 7 (one wave per expert); with xq set, RT_XQ_WGS more workgroups
-// per grid row build the tokens' activation terms. Loads are unpredicated
-// (addresses clamped, tails zeroed after the load) so that they are all in
-// flight together.
+// Workgroup e < E of grid row y computes expert e's logits for tokens 8y ..
+// 8y + 7: its 256 threads split K into 8-element chunks (thread i: chunks i,
+// i + 256, ...), so that a small batch spreads the router matrix over E
+// compute units, and the four waves' partial sums meet in LDS in a fixed
+// order. With xq set, RT_XQ_WGS more workgroups per grid row build the
+// tokens' activation terms. Loads are unpredicated (addresses clamped, tails
+// zeroed after the load) so that they are all in flight together.
 template <int WDT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restrict__ h, int T, int K,
                                                             const void* __restrict__ W,
@@ -187,12 +192,11 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
                                                             float* __restrict__ logits, uint8_t* __restrict__ xq) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int ewgs = (E + 3) / 4;
-  if ((int)blockIdx.x >= ewgs) {  // activation terms of h, two blocks per wave task
+  if ((int)blockIdx.x >= E) {  // activation terms of h, two blocks per wave task
     const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
     const int64_t tasks = (int64_t)T * pairs;
     const int64_t nwaves = (int64_t)gridDim.y * RT_XQ_WGS * 4;
-    for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - ewgs)) * 4 + wave; task < tasks;
+    for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - E)) * 4 + wave; task < tasks;
          task += nwaves) {
       const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
       const float r = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
@@ -200,55 +204,60 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
     }
     return;
   }
-  const int e = blockIdx.x * 4 + wave;
+  __shared__ float red[4][RT_TT];
+  const int e = blockIdx.x;
   const int t0 = blockIdx.y * RT_TT;
   const int nt = min(RT_TT, T - t0);
-  if (e < E) {
-    float acc[RT_TT];
+  const int nc = K / 8;  // 8-element chunks
+  float acc[RT_TT];
 #pragma unroll
-    for (int i = 0; i < RT_TT; ++i) acc[i] = 0.f;
-    for (int k0 = 0; k0 < K; k0 += RT_MAXC * 512) {
-      float w[RT_MAXC][8];
+  for (int i = 0; i < RT_TT; ++i) acc[i] = 0.f;
+  for (int c0 = 0; c0 < nc; c0 += RT_U * 256) {
+    float w[RT_U][8];
 #pragma unroll
-      for (int c = 0; c < RT_MAXC; ++c) {
-        const int kk = k0 + c * 512 + lane * 8;
-        load8_w<WDT>(W, (int64_t)e * K + (kk < K ? kk : K - 8), w[c]);
-      }
+    for (int u = 0; u < RT_U; ++u) {
+      const int c = c0 + u * 256 + (int)threadIdx.x;
+      load8_w<WDT>(W, (int64_t)e * K + 8 * (int64_t)min(c, nc - 1), w[u]);
+    }
 #pragma unroll
-      for (int c = 0; c < RT_MAXC; ++c) {
-        const bool in = k0 + c * 512 + lane * 8 < K;
+    for (int u = 0; u < RT_U; ++u) {
+      const bool in = c0 + u * 256 + (int)threadIdx.x < nc;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) w[c][u] = in ? w[c][u] : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < RT_TT; ++i) {
-        if (i >= nt) break;
-        const float* hp = h + (int64_t)(t0 + i) * K;
-        v4f ha[RT_MAXC], hb[RT_MAXC];
-#pragma unroll
-        for (int c = 0; c < RT_MAXC; ++c) {
-          const int kk = k0 + c * 512 + lane * 8;
-          const int kc = kk < K ? kk : K - 8;
-          ha[c] = *(gv4f*)(hp + kc);
-          hb[c] = *(gv4f*)(hp + kc + 4);
-        }
-        float sacc = acc[i];
-#pragma unroll
-        for (int c = 0; c < RT_MAXC; ++c) {  // w is zero past K
-          sacc = fmaf(w[c][0], ha[c].x, sacc); sacc = fmaf(w[c][1], ha[c].y, sacc);
-          sacc = fmaf(w[c][2], ha[c].z, sacc); sacc = fmaf(w[c][3], ha[c].w, sacc);
-          sacc = fmaf(w[c][4], hb[c].x, sacc); sacc = fmaf(w[c][5], hb[c].y, sacc);
-          sacc = fmaf(w[c][6], hb[c].z, sacc); sacc = fmaf(w[c][7], hb[c].w, sacc);
-        }
-        acc[i] = sacc;
-      }
+      for (int j = 0; j < 8; ++j) w[u][j] = in ? w[u][j] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < RT_TT; ++i) {
       if (i >= nt) break;
-      const float sum = nsx_wave_sum(acc[i]);
-      if (lane == 0) logits[(int64_t)(t0 + i) * E + e] = bias ? sum + bias[e] : sum;
+      const float* hp = h + (int64_t)(t0 + i) * K;
+      v4f ha[RT_U], hb[RT_U];
+#pragma unroll
+      for (int u = 0; u < RT_U; ++u) {
+        const int c = min(c0 + u * 256 + (int)threadIdx.x, nc - 1);
+        ha[u] = *(gv4f*)(hp + 8 * c);
+        hb[u] = *(gv4f*)(hp + 8 * c + 4);
+      }
+      float sacc = acc[i];
+#pragma unroll
+      for (int u = 0; u < RT_U; ++u) {  // w is zero past K
+        sacc = fmaf(w[u][0], ha[u].x, sacc); sacc = fmaf(w[u][1], ha[u].y, sacc);
+        sacc = fmaf(w[u][2], ha[u].z, sacc); sacc = fmaf(w[u][3], ha[u].w, sacc);
+        sacc = fmaf(w[u][4], hb[u].x, sacc); sacc = fmaf(w[u][5], hb[u].y, sacc);
+        sacc = fmaf(w[u][6], hb[u].z, sacc); sacc = fmaf(w[u][7], hb[u].w, sacc);
+      }
+      acc[i] = sacc;
     }
+  }
+#pragma unroll
+  for (int i = 0; i < RT_TT; ++i) {
+    if (i >= nt) break;
+    const float sum = nsx_wave_sum(acc[i]);
+    if (lane == 0) red[wave][i] = sum;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < nt) {
+    const int i = threadIdx.x;
+    const float sum = (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+    logits[(int64_t)(t0 + i) * E + e] = bias ? sum + bias[e] : sum;
   }
 }
 
@@ -280,7 +289,7 @@ static int check_router(int64_t T, int64_t K, int wdt, int64_t E, int k, int mod
 
 static int launch_logits(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias, int64_t E,
                          float* logits, uint8_t* xq, hipStream_t st) {
-  const dim3 grid((unsigned)(nsx_cdiv(E, 4) + (xq ? RT_XQ_WGS : 0)), (unsigned)nsx_cdiv(T, RT_TT));
+  const dim3 grid((unsigned)(E + (xq ? RT_XQ_WGS : 0)), (unsigned)nsx_cdiv(T, RT_TT));
   if (wdt == NSX_BF16)
     return nsx_launch(router_logits_kernel<NSX_BF16>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E,
                       logits, xq);
@@ -683,7 +692,7 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
     int si[MAX_TOPK];
     float sw[MAX_TOPK];
     const bool writes = j == 0 && tile == 0;  // the token's first item writes the ids and weights
-    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes);
+    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes, j + 1);
     int my_e = 0, e = 0;
     float my_w = 0.f;
 #pragma unroll
@@ -1219,9 +1228,9 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 // kernels give identical bits.
 
 constexpr int Q4K_KMAX = 4096;   // K of the Q4_K kernels (nq <= 64)
-constexpr int Q4K_GU_WAVES = 8;
+constexpr int Q4K_GU_WAVES = 16;
 constexpr int Q4K_GU_STEPS = 3;  // row steps of gate and of up per wave (per-pair kernel)
-constexpr int Q4K_GG_STEPS = 2;  // the same, grouped kernel (rows held while the tokens go by)
+constexpr int Q4K_GG_WAVES = 8, Q4K_GG_STEPS = 2;  // grouped kernel (rows held while the tokens go by)
 constexpr int Q4K_DN_STEPS = 4;  // row steps per down wave (per-pair kernel, two waves per expert slot)
 constexpr int Q4K_DG_WAVES = 4, Q4K_DG_STEPS = 2;  // grouped down
 
@@ -1248,36 +1257,32 @@ __device__ __forceinline__ void q4k_lds_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-// gate/up: workgroup = (pair, RPG rows); wave = Q4K_GU_STEPS steps of
-// 64 / LPR rows of gate and of up. The workgroup first turns the token's h
-// into activation terms in LDS (wave 0 meanwhile selects the top-k when the
-// kernel does that), then issues all its row loads.
-template <int LPR>  // (4 waves per SIMD: two workgroups share a CU, VGPRs <= 128)
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void moe_gu_q4k_kernel(MoeDev a) {
-  constexpr int RS = 64 / LPR, RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * RS;
-  __shared__ __align__(16) uint8_t xs[a8_bytes(Q4K_KMAX)];
-  __shared__ int s_e;
+// Prologue of a gate/up work item of pair p (rows r0 ..): the token's h as
+// activation terms in xs, and the pair's expert -- from the ids, or
+// (topk_in_gu) from the top-k of the token's logits by wave 0 (through s_e),
+// which in the token's first workgroup also writes the ids / weights the down
+// phase reads. The terms are in
+// LDS before any row load goes out: a wave's loads can stall at issue once the
+// memory system is saturated, and a barrier behind them would keep every wave
+// of the workgroup from computing until the last one had issued its last load.
+__device__ __forceinline__ int q4k_gu_prologue(const MoeDev& a, int p, int r0, uint8_t* xs, int* s_e) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
-  nsx_hoist(a.n_ff, a.n_embd, a.top_k, a.E, (const void*)a.ids, (const void*)a.h, a.gate_base, a.up_base,
-            (const void*)a.gate_ptrs, (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias,
-            (const void*)a.up_bias, (const void*)a.act, a.act_kind, a.alpha, a.limit);
-  const int groups = (a.n_ff + RPG - 1) / RPG;
-  const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
   const int K = a.n_embd, nq = K / 64, t = p / a.top_k;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  // loads first: this thread's 8 activations of h (K <= 8 x 512), the pair's expert id
-  // (issued together with the top-k's logits load: one round trip)
-  const int i8 = min((int)threadIdx.x, K / 8 - 1);
+  // loads first: the 8 activations of h of each thread past wave 0 (K <= 8 x 960; wave 0 selects
+  // the top-k meanwhile), the pair's expert id (issued together with the top-k's logits load: one
+  // round trip)
+  const int i8 = min(max((int)threadIdx.x - 64, 0), K / 8 - 1);
   const v4f hlo = *(gv4f*)(a.h + (int64_t)t * K + 8 * i8), hhi = *(gv4f*)(a.h + (int64_t)t * K + 8 * i8 + 4);
   const int e_in = a.topk_in_gu ? 0 : a.ids[p];
   if (a.topk_in_gu && wave == 0) {
-    // the top-k from the router's logits by wave 0 (as moe_gu_kernel); the
-    // token's first workgroup also writes the ids / weights the down phase reads
+    // the top-k from the router's logits by wave 0 (as moe_gu_kernel): the first j + 1 experts,
+    // all k (and their weights) in the token's first workgroup, which writes the ids / weights
     const int k = a.top_k, j = p - t * k;
     int si[MAX_TOPK];
     float sw[MAX_TOPK];
     const bool writes = j == 0 && r0 == 0;
-    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes);
+    topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes, j + 1);
     int my_e = 0, ej = 0;
     float my_w = 0.f;
 #pragma unroll
@@ -1290,18 +1295,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void m
       a.ids[(int64_t)t * k + lane] = clamp_expert(my_e, a.E);
       a.wts[(int64_t)t * k + lane] = my_w;
     }
-    if (lane == 0) s_e = clamp_expert(ej, a.E);
+    if (lane == 0) *s_e = clamp_expert(ej, a.E);
   }
-  if ((int)threadIdx.x < K / 8) {  // K / 8 is a multiple of 4: DPP quads stay whole
+  if (wave > 0 && (int)threadIdx.x - 64 < K / 8) {  // K / 8 is even: lane pairs stay whole
     const float v[8] = {hlo.x, hlo.y, hlo.z, hlo.w, hhi.x, hhi.y, hhi.z, hhi.w};
-    a8_quad(v, (int)threadIdx.x >> 2, nq, xs);
+    a8_pair16(v, ((int)threadIdx.x - 64) >> 1, nq, xs);
   }
-  // The terms are in LDS before any row load goes out: a wave's loads can
-  // stall at issue once the memory system is saturated, and a barrier behind
-  // them would keep every wave of the workgroup from computing until the last
-  // one had issued its last load.
   __syncthreads();
-  const int e = a.topk_in_gu ? s_e : clamp_expert(e_in, a.E);
+  return a.topk_in_gu ? *s_e : clamp_expert(e_in, a.E);
+}
+
+// The rows of a gate/up work item: pair p, expert e, rows r0 .. r0 + RPG - 1
+// (wave = Q4K_GU_STEPS steps of 64 / LPR rows of gate and of up), activation
+// terms in xs. The item's activations (RPG of them, whole 16-element blocks)
+// meet in s_act, and the pair's activation terms for the down phase go out
+// from there.
+template <int LPR>
+__device__ __forceinline__ void q4k_gu_rows(const MoeDev& a, int p, int r0, int e, const uint8_t* xs,
+                                            float* s_act) {
+  constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * (64 / LPR);
+  constexpr int RS = 64 / LPR;
+  const int K = a.n_embd, nq = K / 64;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
   const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
   const uint8_t* um = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
@@ -1327,16 +1342,44 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void m
     if (lane % LPR == 0 && row < a.n_ff) {
       if (a.gate_bias) gs += a.gate_bias[(int64_t)e * a.n_ff + row];
       if (a.up_bias) us += a.up_bias[(int64_t)e * a.n_ff + row];
-      a.act[(int64_t)p * a.n_ff + row] = moe_act(a.act_kind, gs, us, a.alpha, a.limit);
+      s_act[row - r0] = moe_act(a.act_kind, gs, us, a.alpha, a.limit);
     }
+  }
+  __syncthreads();
+  // r0 and n_ff are multiples of 16: a lane pair's x-block lies inside or past n_ff as a whole
+  const int i8 = threadIdx.x;
+  if (i8 < RPG / 8 && r0 + 8 * i8 < a.n_ff) {
+    const v4f lo = *(const v4f*)(s_act + 8 * i8), hi = *(const v4f*)(s_act + 8 * i8 + 4);
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    a8_pair16(v, (r0 >> 4) + (i8 >> 1), a.n_ff / 64, a.xq_a + (int64_t)p * a8_bytes(a.n_ff));
   }
 }
 
+#define Q4K_GU_HOIST(a)                                                                                          \
+  nsx_hoist(a.n_ff, a.n_embd, a.top_k, a.E, (const void*)a.ids, (const void*)a.h, a.gate_base, a.up_base,       \
+            (const void*)a.gate_ptrs, (const void*)a.up_ptrs, a.gate_stride, a.up_stride, (const void*)a.gate_bias, \
+            (const void*)a.up_bias, (const void*)a.act, a.act_kind, a.alpha, a.limit)
+
+// gate/up: workgroup = (pair, RPG rows); it writes the pair's activation terms
+// for those rows (the down kernel reads terms, not activations)
+template <int LPR>  // (16 waves: one workgroup per compute unit, VGPRs <= 128)
+__global__ __launch_bounds__(1024) void moe_gu_q4k_kernel(MoeDev a) {
+  constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * (64 / LPR);
+  __shared__ __align__(16) uint8_t xs[a8_bytes(Q4K_KMAX)];
+  __shared__ __align__(16) float s_act[RPG];
+  __shared__ int s_e;
+  Q4K_GU_HOIST(a);
+  const int groups = (a.n_ff + RPG - 1) / RPG;
+  const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
+  const int e = q4k_gu_prologue(a, p, r0, xs, &s_e);
+  q4k_gu_rows<LPR>(a, p, r0, e, xs, s_act);
+}
+
 // down and combine: workgroup = (token, RPG output rows), two waves per
-// expert slot, each Q4K_DN_STEPS steps of 64 / LPR rows. The workgroup turns
-// the token's k activation vectors into terms in LDS, then issues its row
+// expert slot, each Q4K_DN_STEPS steps of 64 / LPR rows. The workgroup copies
+// the activation terms of the token's k pairs into LDS, then issues its row
 // loads; the slots' outputs are added in ascending expert id.
-constexpr int Q4K_DN_SLICES = Q4K_KMAX / 8 / 128;  // 8-element slices per thread (k x n_ff / 8 over 128 k threads)
+constexpr int Q4K_DN_SLICES = (int)((a8_bytes(Q4K_KMAX) / 16 + 127) / 128);  // 16-byte term chunks per thread (k pairs, 128 k threads)
 
 template <int LPR>
 __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
@@ -1351,24 +1394,22 @@ __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
   const int t = blockIdx.x / groups, r0 = (blockIdx.x - t * groups) * RPG;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int k = a.top_k, K = a.n_ff, nq = K / 64, slot = wave >> 1;
-  // loads first: the token's slot ids, then its k activation vectors (8-element slices)
+  // loads first: the token's slot ids, then the activation terms of its k pairs (written by
+  // the gate/up kernel, one contiguous run) into LDS
   const int id_l = clamp_expert(a.ids[(int64_t)t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
-  const int per = K / 8, items = k * per, nthr = 128 * k;
-  v4f xv[Q4K_DN_SLICES][2];
+  {
+    const int n16 = k * (int)(a8_bytes(K) / 16);
+    const v4u* src = (const v4u*)(a.xq_a + (int64_t)t * k * a8_bytes(K));
+    v4u buf[Q4K_DN_SLICES];
 #pragma unroll
-  for (int i = 0; i < Q4K_DN_SLICES; ++i) {
-    const int it = min((int)threadIdx.x + i * nthr, items - 1);
-    const float* src = a.act + ((int64_t)t * k + it / per) * K + 8 * (it % per);
-    xv[i][0] = *(gv4f*)src;
-    xv[i][1] = *(gv4f*)(src + 4);
-  }
+    for (int i = 0; i < Q4K_DN_SLICES; ++i) {
+      const int c = (int)threadIdx.x + i * (int)blockDim.x;
+      if (c < n16) buf[i] = src[c];
+    }
 #pragma unroll
-  for (int i = 0; i < Q4K_DN_SLICES; ++i) {
-    const int it = (int)threadIdx.x + i * nthr;  // items and nthr are multiples of 4: quads stay whole
-    if (it < items) {
-      const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
-                          xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
-      a8_quad(v, (it % per) >> 2, nq, q4k_xa + (it / per) * a8_bytes(K));
+    for (int i = 0; i < Q4K_DN_SLICES; ++i) {
+      const int c = (int)threadIdx.x + i * (int)blockDim.x;
+      if (c < n16) ((v4u*)q4k_xa)[c] = buf[i];
     }
   }
   const int e = __builtin_amdgcn_readlane(id_l, slot);
@@ -1421,8 +1462,8 @@ __global__ __launch_bounds__(256) void a8_terms_kernel(const float* __restrict__
 
 // gate/up: workgroup = (item, RPG rows); wave = Q4K_GG_STEPS steps of 64 / LPR rows of gate and of up
 template <int LPR>
-__global__ __launch_bounds__(512) void moe_gu_q4k_grouped_kernel(MoeDev a) {
-  constexpr int RS = 64 / LPR, RPG = Q4K_GU_WAVES * Q4K_GG_STEPS * RS;
+__global__ __launch_bounds__(64 * Q4K_GG_WAVES) void moe_gu_q4k_grouped_kernel(MoeDev a) {
+  constexpr int RS = 64 / LPR, RPG = Q4K_GG_WAVES * Q4K_GG_STEPS * RS;
   int grp;
   int4 item;
   if (!grp_work(a, (a.n_ff + RPG - 1) / RPG, grp, item)) return;
@@ -1857,10 +1898,11 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   o = al(o + T * L->n_expert * 4);
   p.off_act = o;
   o = al(o + (t64 ? 0 : P * L->n_ff * 4));
-  const bool a8 = p.grouped && !p.mq && !t64;  // grouped Q4_K on the int8 dot: activation terms per vector
+  // Q4_K on the int8 dot: activation terms of h per token (grouped) and of the activations per pair
+  const bool a8 = !p.mq && !t64 && q4k_fast(L);
   p.off_xqh = o;
   o = al(o + (t64 ? T * p.ggu.ns * XQ_STEP
-                  : (p.mq ? T * mq_row_bytes(L->n_embd) : (a8 ? T * a8_bytes(L->n_embd) : 0))));
+                  : (p.mq ? T * mq_row_bytes(L->n_embd) : (a8 && p.grouped ? T * a8_bytes(L->n_embd) : 0))));
   p.off_xqa = o;
   o = al(o + (t64 ? P * p.gdn.ns * XQ_STEP : (p.mq ? P * mq_row_bytes(L->n_ff) : (a8 ? P * a8_bytes(L->n_ff) : 0))));
   p.off_items = o;
@@ -2090,8 +2132,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
           return rc;
         rc = with_q4k_lpr(L->n_embd, [&](auto lpr) {
           constexpr int LPR = decltype(lpr)::value;
-          const int64_t g = nsx_cdiv(L->n_ff, Q4K_GU_WAVES * Q4K_GG_STEPS * (64 / LPR));
-          return nsx_launch(moe_gu_q4k_grouped_kernel<LPR>, grid8(g), dim3(64 * Q4K_GU_WAVES), 0, st, d);
+          const int64_t g = nsx_cdiv(L->n_ff, Q4K_GG_WAVES * Q4K_GG_STEPS * (64 / LPR));
+          return nsx_launch(moe_gu_q4k_grouped_kernel<LPR>, grid8(g), dim3(64 * Q4K_GG_WAVES), 0, st, d);
         });
       }
       if (rc) return rc;

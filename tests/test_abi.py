@@ -96,11 +96,11 @@ def test_workspace_bytes_by_dispatch(lib):
     wq = lib.nsx_moe_workspace_bytes(C.byref(L), 8)
     L.dispatch = N.DISPATCH_PAIRS
     wp = lib.nsx_moe_workspace_bytes(C.byref(L), 8)
-    a8 = 8 * (4096 // 64 * 160) + 32 * (1536 // 64 * 160)  # int8 terms of 8 tokens of h, 32 activations
-    assert 0 < wp and wq >= wp + a8
+    a8_h, a8_a = 8 * (4096 // 64 * 176), 32 * (1536 // 64 * 176)  # int8 terms: 8 tokens of h, 32 activations
+    assert wp >= a8_a and wq >= wp + a8_h  # pairs: the activations' terms; grouped: also h's
     L.dispatch = N.DISPATCH_MFMA  # the matrix-core terms in their place
     terms = 8 * (4 * 4096 + 4096 // 8 + 16) + 32 * (4 * 1536 + 1536 // 8 + 16)
-    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) >= wq - a8 + terms
+    assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) >= wq - a8_h - a8_a + terms
     L.down_base = (1 << 20) + 8  # not 16-byte aligned: no Q4_K fast path, so no grouping
     assert lib.nsx_moe_workspace_bytes(C.byref(L), 8) < 0
     assert b"MFMA" in lib.nsx_last_error()

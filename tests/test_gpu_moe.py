@@ -141,6 +141,7 @@ def test_qwen3_layer_decode(dev):
 @pytest.mark.parametrize("name,layout,T,dispatch", [("gptoss-small", "t64", 3, "auto"),
                                                     ("gptoss-small", "t64", 20, "auto"),
                                                     ("gptoss-small", "t64", 5, "grouped"),
+                                                    ("qwen3-small", "gguf", 1, "auto"),
                                                     ("qwen3-small", "gguf", 2, "auto"),
                                                     ("qwen3-small", "gguf", 17, "auto"),
                                                     ("qwen3-small", "gguf", 3, "mfma"),
@@ -169,3 +170,28 @@ def test_router_phase_alone_writes_ids(dev, name, layout, T, dispatch):
         layer.phase(ph, h, out, ids, wts, ws)
     torch.cuda.synchronize()
     assert torch.equal(out, ref_out)
+
+
+def test_qwen3_one_token_forward_equals_phases(dev):
+    """BASELINE config 4 at T=1: the forward (its gate/up kernel selects the
+    top-k) and the same layer phase by phase (a top-k launch, gate/up from the
+    ids) give equal outputs, ids and weights, also on a repeated forward."""
+    from nurostream_amd import _native as N
+    from nurostream_amd import synth
+    cfg = synth.QWEN3_235B
+    t = synth.make_layer(cfg, seed=3, device=dev)
+    layer = _layer(cfg, t, "gguf")
+    for i in range(2):
+        h = synth.activations(1, cfg.n_embd, seed=50 + i, device=dev)
+        ref_out, ref_ids, ref_w = layer.forward(h)
+        again, _, _ = layer.forward(h)
+        ws = layer.new_workspace(1)
+        out = torch.full_like(ref_out, float("nan"))
+        ids = torch.full_like(ref_ids, -1)
+        wts = torch.full_like(ref_w, float("nan"))
+        for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE):
+            layer.phase(ph, h, out, ids, wts, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ref_ids) and torch.equal(wts, ref_w)
+        assert bool(torch.isfinite(ref_out).all())
+        assert torch.equal(out, ref_out) and torch.equal(again, ref_out)
