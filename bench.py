@@ -311,6 +311,9 @@ def _dtype_label(cfg, layout, mq):
                 "sums 8-product groups with ~12 kept bits)")
     if mq:
         return "q4_k codes as exact f16 (sc*q) x 2-term f16 activation split (f16 MFMA, fp32 accumulate)"
+    if cfg.ggml_type.name == "Q4_K":
+        return ("q4_k codes x 2-term int8 activation split per 16 elements (v_dot4 int8, exact integer sums), "
+                "fp32 scales and accumulate")
     return f"{cfg.ggml_type.name.lower()} weights dequantized in registers x fp32 activations, fp32 accumulate"
 
 

@@ -1230,8 +1230,10 @@ __global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
 constexpr int Q4K_KMAX = 4096;   // K of the Q4_K kernels (nq <= 64)
 constexpr int Q4K_GU_WAVES = 16;
 constexpr int Q4K_GU_STEPS = 3;  // row steps of gate and of up per wave (per-pair kernel)
+constexpr int Q4K_GU_AHEAD = 2;  // steps whose loads are in flight before the first compute
 constexpr int Q4K_GG_WAVES = 8, Q4K_GG_STEPS = 2;  // grouped kernel (rows held while the tokens go by)
 constexpr int Q4K_DN_STEPS = 4;  // row steps per down wave (per-pair kernel, two waves per expert slot)
+constexpr int Q4K_DN_AHEAD = 2;  // steps whose loads are in flight before the first compute
 constexpr int Q4K_DG_WAVES = 4, Q4K_DG_STEPS = 2;  // grouped down
 
 struct Q4kRow {
@@ -1324,16 +1326,23 @@ __device__ __forceinline__ void q4k_gu_rows(const MoeDev& a, int p, int r0, int 
   const bool live = lane % LPR < nq;
   const int rw = r0 + wave * Q4K_GU_STEPS * RS + sub;  // this lane's row at step 0
   Q4kRow G[Q4K_GU_STEPS], U[Q4K_GU_STEPS];
-#pragma unroll
-  for (int j = 0; j < Q4K_GU_STEPS; ++j) {
+  auto load = [&](int j) {
     const int row = min(rw + j * RS, a.n_ff - 1);
     q4k_row_load(gm, row, rb, q, G[j]);
     q4k_row_load(um, row, rb, q, U[j]);
-  }
+  };
+#pragma unroll
+  for (int j = 0; j < Q4K_GU_AHEAD; ++j) load(j);
   A8Pair X;
   a8_load(xs, q, nq, X);
 #pragma unroll
   for (int j = 0; j < Q4K_GU_STEPS; ++j) {
+    if (j > 0 && j + Q4K_GU_AHEAD - 1 < Q4K_GU_STEPS) {
+      // the next step's loads go out once this wave has computed a step: a wave whose loads
+      // stall at issue still computes what has arrived (the clobber keeps them here)
+      asm volatile("" ::: "memory");
+      load(j + Q4K_GU_AHEAD - 1);
+    }
     float gs = q4k_a8_dot(G[j].c0, G[j].c1, G[j].hd, q & 3, X);
     float us = q4k_a8_dot(U[j].c0, U[j].c1, U[j].hd, q & 3, X);
     gs = a8_group_sum<LPR>(live ? gs : 0.f);
@@ -1425,11 +1434,16 @@ __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
   const int rw = r0 + (wave & 1) * RPW + sub;
   Q4kRow R[Q4K_DN_STEPS];
 #pragma unroll
-  for (int j = 0; j < Q4K_DN_STEPS; ++j) q4k_row_load(dm, min(rw + j * RS, a.n_embd - 1), rb, q, R[j]);
+  for (int j = 0; j < Q4K_DN_AHEAD; ++j) q4k_row_load(dm, min(rw + j * RS, a.n_embd - 1), rb, q, R[j]);
   A8Pair X;
   a8_load(q4k_xa + slot * a8_bytes(K), q, nq, X);
 #pragma unroll
   for (int j = 0; j < Q4K_DN_STEPS; ++j) {
+    if (j > 0 && j + Q4K_DN_AHEAD - 1 < Q4K_DN_STEPS) {  // as in the gate/up kernel
+      asm volatile("" ::: "memory");
+      const int jn = j + Q4K_DN_AHEAD - 1;
+      q4k_row_load(dm, min(rw + jn * RS, a.n_embd - 1), rb, q, R[jn]);
+    }
     float y = q4k_a8_dot(R[j].c0, R[j].c1, R[j].hd, q & 3, X);
     y = a8_group_sum<LPR>(live ? y : 0.f);
     const int row = rw + j * RS;
