@@ -1007,14 +1007,19 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   }
 }
 
-// Workgroup index -> (tile, item), tile-major, XCD-aware (workgroup b runs on XCD b % 8).
+// Workgroup index -> (tile, item). Workgroup b runs on XCD b % 8; the
+// tiles x n_items live work units are cut into 8 contiguous runs, one per
+// XCD, item-major, so that an XCD's L2 holds the activation terms of the few
+// items it is working on (and an expert's items follow each other) while the
+// grid, sized for the most items a sort can make, idles evenly on every XCD.
 __device__ __forceinline__ bool grp_work(const MoeDev& a, int tiles, int& tile, int4& item) {
-  const int per = (int)(gridDim.x >> 3);
-  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  if (L >= tiles * a.max_items) return false;
-  tile = L / a.max_items;
-  const int it = L - tile * a.max_items;
-  if (it >= *a.n_items) return false;
+  const int live = tiles * *a.n_items, per = (live + 7) / 8;
+  const int j = (int)(blockIdx.x >> 3);
+  if (j >= per) return false;
+  const int L = (int)(blockIdx.x & 7) * per + j;
+  if (L >= live) return false;
+  const int it = L / tiles;
+  tile = L - it * tiles;
   item = a.items[it];
   return true;
 }
