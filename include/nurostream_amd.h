@@ -179,6 +179,21 @@ int nsx_moe_forward(const nsx_moe_layer *L, const float *h, int64_t T,
                     float *out, int32_t *ids, float *weights, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
+/* One block of a stacked GPT-OSS FFN (model/gpt_oss.py:123-177: the block's
+ * input norm, then the routed experts): x_out = x + r, and out, ids, weights
+ * as nsx_moe_forward of h = rms_norm(x + r) * norm_w (eps; norm_w may be
+ * NULL), h being what nsx_add_rmsnorm(x, r, ...) computes, bit for bit. The
+ * norm runs inside the router kernel, which is the only reader of h in the
+ * t64 layout: no separate launch and no h in memory. For t64 layers below
+ * 16 tokens with n_embd <= 4096 (NSX_ENOTIMPL otherwise: callers then run
+ * nsx_add_rmsnorm and nsx_moe_forward). x_out must not overlap x or r; out
+ * may be r (the router is done with r before any expert kernel writes out).
+ * Same workspace as nsx_moe_forward. */
+int nsx_moe_forward_norm(const nsx_moe_layer *L, const float *x, const float *r,
+                         const float *norm_w, float eps, int64_t T, float *x_out,
+                         float *out, int32_t *ids, float *weights, void *workspace,
+                         int64_t workspace_bytes, void *stream);
+
 /* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, the top-k and the
  * ids/weights outputs, for every layout and dispatch; in the t64 layout also
  * the activation terms of h), NSX_PHASE_GATE_UP (grouped dispatch: the sort

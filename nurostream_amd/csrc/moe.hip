@@ -177,6 +177,60 @@ __device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, i
   }
 }
 
+// The router's input as the residual stream of a stacked layer: h = rms_norm(x
+// + r) * w (gpt_oss.py:126,177 -- the block's input norm), computed where it
+// is read instead of by a launch of its own. `on` false: h is the input.
+struct RtNorm {
+  int on;
+  const float* r;  // the previous block's output, added to x
+  const float* w;  // norm weight (null: none)
+  float eps;
+  float* x_out;    // x + r, written by the first logit workgroup of each grid row
+};
+
+constexpr int NORM_MAXV = 16;  // values per thread of 256 (rows of n <= 4096)
+
+// The residual add of a row (length n) in add_rmsnorm_kernel's layout --
+// thread i of 256 holds elements i, i + 256, ... -- written to LDS row s when
+// s is set; returns the thread's partial sum of squares in that kernel's
+// order, so that a norm folded elsewhere gives its bits.
+__device__ __forceinline__ float norm_stride(const float* __restrict__ x, const float* __restrict__ r, int n,
+                                             float* s) {
+  float v[NORM_MAXV];
+#pragma unroll
+  for (int i = 0; i < NORM_MAXV; ++i) {
+    const int c = min((int)threadIdx.x + i * 256, n - 1);
+    v[i] = x[c] + r[c];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NORM_MAXV; ++i) {
+    if ((int)threadIdx.x + i * 256 >= n) v[i] = 0.f;
+    ss = fmaf(v[i], v[i], ss);
+  }
+  if (s) {
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) {
+      const int c = threadIdx.x + i * 256;
+      if (c < n) s[c] = v[i];
+    }
+  }
+  return ss;
+}
+
+// 1 / rms from the threads' partial sums (wave sums, then the four waves in
+// order, through part[wave][slot]); every thread of the 256 calls it
+__device__ __forceinline__ float norm_inv(float ss, int n, float eps, float (*part)[RT_TT], int slot) {
+  ss = nsx_wave_sum(ss);
+  __syncthreads();  // an earlier call's readers of part are done
+  if (__lane_id() == 0) part[threadIdx.x >> 6][slot] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tot += part[i][slot];
+  return 1.f / sqrtf(tot / (float)n + eps);
+}
+
 // Router logits (model/gpt_oss.py:97-99,116-121; moe/router.py:59-69).
 // Workgroup e < E of grid row y computes expert e's logits for tokens 8y ..
 // 8y + 7: its 256 threads split K into 8-element chunks (thread i: chunks i,
@@ -184,40 +238,121 @@ __device__ __forceinline__ void topk_regs(const float* __restrict__ lg, int E, i
 // compute units, and the four waves' partial sums meet in LDS in a fixed
 // order. With xq set, RT_XQ_WGS more workgroups per grid row build the
 // tokens' activation terms. Loads are unpredicated (addresses clamped, tails
-// zeroed after the load) so that they are all in flight together.
+// zeroed after the load) so that they are all in flight together. With the
+// norm on, h is rms_norm(h + nm.r) * nm.w, as add_rmsnorm_kernel computes it.
 template <int WDT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restrict__ h, int T, int K,
                                                             const void* __restrict__ W,
                                                             const float* __restrict__ bias, int E,
-                                                            float* __restrict__ logits, uint8_t* __restrict__ xq) {
+                                                            float* __restrict__ logits, uint8_t* __restrict__ xq,
+                                                            RtNorm nm) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
+  __shared__ float part[4][RT_TT];
+  __shared__ __align__(16) float s_rows[2][256 * NORM_MAXV];  // norm on: rows of x + r (or x + r and the weights)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int t0 = blockIdx.y * RT_TT;
+  const int nt = min(RT_TT, T - t0);
   if ((int)blockIdx.x >= E) {  // activation terms of h, two blocks per wave task
     const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
-    const int64_t tasks = (int64_t)T * pairs;
-    const int64_t nwaves = (int64_t)gridDim.y * RT_XQ_WGS * 4;
-    for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - E)) * 4 + wave; task < tasks;
-         task += nwaves) {
-      const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
-      const float r = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
-      xq_block(b < nb ? r : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
+    if (!nm.on) {
+      const int64_t tasks = (int64_t)T * pairs;
+      const int64_t nwaves = (int64_t)gridDim.y * RT_XQ_WGS * 4;
+      for (int64_t task = ((int64_t)blockIdx.y * RT_XQ_WGS + (blockIdx.x - E)) * 4 + wave; task < tasks;
+           task += nwaves) {
+        const int t = (int)(task / pairs), b = (int)(task % pairs) * 2 + (lane >> 5);
+        const float r = h[(int64_t)t * K + (b < nb ? b : nb - 1) * 32 + (lane & 31)];
+        xq_block(b < nb ? r : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
+      }
+      return;
+    }
+    // norm on: workgroup j of the row takes token j % nt and every (RT_XQ_WGS / nt)-th task of it
+    const int j = blockIdx.x - E, slices = RT_XQ_WGS / nt;
+    if (j >= slices * nt) return;
+    const int t = t0 + j % nt, sl = j / nt;
+    // x + r and the norm weights go through LDS (one round trip; the terms take one element per lane)
+    float* s_v = s_rows[0];
+    float* s_w = s_rows[1];
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) {
+      const int c = threadIdx.x + i * 256;
+      if (c < K) s_w[c] = nm.w ? nm.w[c] : 1.f;  // a unit weight multiplies exactly
+    }
+    const float ssq = norm_stride(h + (int64_t)t * K, nm.r + (int64_t)t * K, K, s_v);
+    const float inv = norm_inv(ssq, K, nm.eps, part, 0);  // (its barriers publish s_v, s_w)
+    for (int task = sl * 4 + wave; task < pairs; task += slices * 4) {
+      const int b = task * 2 + (lane >> 5);
+      const int c = (b < nb ? b : nb - 1) * 32 + (lane & 31);
+      const float hn = (s_v[c] * inv) * s_w[c];  // a unit weight multiplies exactly
+      xq_block(b < nb ? hn : 0.f, b, xq + (int64_t)t * ns * XQ_STEP);
     }
     return;
   }
-  __shared__ float red[4][RT_TT];
   const int e = blockIdx.x;
-  const int t0 = blockIdx.y * RT_TT;
-  const int nt = min(RT_TT, T - t0);
   const int nc = K / 8;  // 8-element chunks
+  // norm on: h = ((x + r) * inv) * w, x + r of the first RT_KEEP tokens kept in
+  // LDS from the norm pass (add_rmsnorm_kernel's layout) for the dot's chunks
+  constexpr int RT_KEEP = 2;
+  float inv[RT_TT];
+  float w0[RT_U][8], nw0[RT_U][8];  // norm on (K <= 4096, one pass): the router row and the norm weights,
+  if (nm.on) {                       // loaded ahead of the norm pass so that one round trip covers both
+#pragma unroll
+    for (int u = 0; u < RT_U; ++u) {
+      const int c = min(u * 256 + (int)threadIdx.x, nc - 1);
+      load8_w<WDT>(W, (int64_t)e * K + 8 * (int64_t)c, w0[u]);
+      const v4f a = nm.w ? *(gv4f*)(nm.w + 8 * c) : v4f{1.f, 1.f, 1.f, 1.f};
+      const v4f b = nm.w ? *(gv4f*)(nm.w + 8 * c + 4) : v4f{1.f, 1.f, 1.f, 1.f};
+      nw0[u][0] = a.x; nw0[u][1] = a.y; nw0[u][2] = a.z; nw0[u][3] = a.w;
+      nw0[u][4] = b.x; nw0[u][5] = b.y; nw0[u][6] = b.z; nw0[u][7] = b.w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RT_TT; ++i) inv[i] = 1.f;
+  if (nm.on) {
+    float ss[RT_TT];
+#pragma unroll
+    for (int i = 0; i < RT_TT; ++i) {
+      ss[i] = 0.f;
+      if (i >= nt) continue;
+      const float* xr = h + (int64_t)(t0 + i) * K;
+      const float* rr = nm.r + (int64_t)(t0 + i) * K;
+      ss[i] = norm_stride(xr, rr, K, i < RT_KEEP ? s_rows[i] : nullptr);
+      // x + r for the next layer: elements 256 j .. 256 j + 255 written by workgroup j % E
+      float* xo = nm.x_out + (int64_t)(t0 + i) * K;
+      for (int j = e; 256 * j < K; j += E) {
+        const int c = 256 * j + (int)threadIdx.x;
+        if (c < K) xo[c] = xr[c] + rr[c];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RT_TT; ++i) {
+      const float sw = nsx_wave_sum(ss[i]);
+      if (lane == 0 && i < nt) part[wave][i] = sw;
+    }
+    __syncthreads();  // (also publishes the kept rows)
+#pragma unroll
+    for (int i = 0; i < RT_TT; ++i) {
+      float tot = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv) tot += part[wv][i];
+      inv[i] = i < nt ? 1.f / sqrtf(tot / (float)K + nm.eps) : 1.f;
+    }
+  }
   float acc[RT_TT];
 #pragma unroll
   for (int i = 0; i < RT_TT; ++i) acc[i] = 0.f;
   for (int c0 = 0; c0 < nc; c0 += RT_U * 256) {
     float w[RT_U][8];
+    if (nm.on) {
 #pragma unroll
-    for (int u = 0; u < RT_U; ++u) {
-      const int c = c0 + u * 256 + (int)threadIdx.x;
-      load8_w<WDT>(W, (int64_t)e * K + 8 * (int64_t)min(c, nc - 1), w[u]);
+      for (int u = 0; u < RT_U; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[u][j] = w0[u][j];
+    } else {
+#pragma unroll
+      for (int u = 0; u < RT_U; ++u) {
+        const int c = c0 + u * 256 + (int)threadIdx.x;
+        load8_w<WDT>(W, (int64_t)e * K + 8 * (int64_t)min(c, nc - 1), w[u]);
+      }
     }
 #pragma unroll
     for (int u = 0; u < RT_U; ++u) {
@@ -229,24 +364,40 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float* __restr
     for (int i = 0; i < RT_TT; ++i) {
       if (i >= nt) break;
       const float* hp = h + (int64_t)(t0 + i) * K;
-      v4f ha[RT_U], hb[RT_U];
+      float hv[RT_U][8];
 #pragma unroll
       for (int u = 0; u < RT_U; ++u) {
         const int c = min(c0 + u * 256 + (int)threadIdx.x, nc - 1);
-        ha[u] = *(gv4f*)(hp + 8 * c);
-        hb[u] = *(gv4f*)(hp + 8 * c + 4);
+        if (!nm.on) {
+          const v4f ha = *(gv4f*)(hp + 8 * c), hb = *(gv4f*)(hp + 8 * c + 4);
+          hv[u][0] = ha.x; hv[u][1] = ha.y; hv[u][2] = ha.z; hv[u][3] = ha.w;
+          hv[u][4] = hb.x; hv[u][5] = hb.y; hv[u][6] = hb.z; hv[u][7] = hb.w;
+        } else {  // h = ((x + r) * inv) * w, as add_rmsnorm_kernel (K <= 4096: one pass, c0 = 0)
+          float v[8];
+          if (i < RT_KEEP) {
+            const v4f a = *(const v4f*)(s_rows[i < RT_KEEP ? i : 0] + 8 * c);
+            const v4f b = *(const v4f*)(s_rows[i < RT_KEEP ? i : 0] + 8 * c + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+          } else {
+            const float* rp = nm.r + (int64_t)(t0 + i) * K;
+            const v4f xa = *(gv4f*)(hp + 8 * c), xb = *(gv4f*)(hp + 8 * c + 4);
+            const v4f ra = *(gv4f*)(rp + 8 * c), rb = *(gv4f*)(rp + 8 * c + 4);
+            v[0] = xa.x + ra.x; v[1] = xa.y + ra.y; v[2] = xa.z + ra.z; v[3] = xa.w + ra.w;
+            v[4] = xb.x + rb.x; v[5] = xb.y + rb.y; v[6] = xb.z + rb.z; v[7] = xb.w + rb.w;
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) hv[u][j] = (v[j] * inv[i]) * nw0[u][j];  // a unit weight multiplies exactly
+        }
       }
       float sacc = acc[i];
 #pragma unroll
-      for (int u = 0; u < RT_U; ++u) {  // w is zero past K
-        sacc = fmaf(w[u][0], ha[u].x, sacc); sacc = fmaf(w[u][1], ha[u].y, sacc);
-        sacc = fmaf(w[u][2], ha[u].z, sacc); sacc = fmaf(w[u][3], ha[u].w, sacc);
-        sacc = fmaf(w[u][4], hb[u].x, sacc); sacc = fmaf(w[u][5], hb[u].y, sacc);
-        sacc = fmaf(w[u][6], hb[u].z, sacc); sacc = fmaf(w[u][7], hb[u].w, sacc);
-      }
+      for (int u = 0; u < RT_U; ++u)  // w is zero past K
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sacc = fmaf(w[u][j], hv[u][j], sacc);
       acc[i] = sacc;
     }
   }
+  __shared__ float red[4][RT_TT];
 #pragma unroll
   for (int i = 0; i < RT_TT; ++i) {
     if (i >= nt) break;
@@ -288,16 +439,16 @@ static int check_router(int64_t T, int64_t K, int wdt, int64_t E, int k, int mod
 }
 
 static int launch_logits(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias, int64_t E,
-                         float* logits, uint8_t* xq, hipStream_t st) {
+                         float* logits, uint8_t* xq, hipStream_t st, RtNorm nm = RtNorm{0, nullptr, nullptr, 0.f, nullptr}) {
   const dim3 grid((unsigned)(E + (xq ? RT_XQ_WGS : 0)), (unsigned)nsx_cdiv(T, RT_TT));
   if (wdt == NSX_BF16)
     return nsx_launch(router_logits_kernel<NSX_BF16>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E,
-                      logits, xq);
+                      logits, xq, nm);
   if (wdt == NSX_F16)
     return nsx_launch(router_logits_kernel<NSX_F16>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E,
-                      logits, xq);
+                      logits, xq, nm);
   return nsx_launch(router_logits_kernel<NSX_F32>, grid, dim3(256), 0, st, h, (int)T, (int)K, w, bias, (int)E, logits,
-                    xq);
+                    xq, nm);
 }
 
 static int launch_topk(const float* logits, int64_t T, int64_t E, int k, int mode, int32_t* ids, float* wts,
@@ -2048,7 +2199,8 @@ static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool ga
 // Phases ph0..ph1 of one layer (NSX_PHASE_*); each later phase reads what
 // the earlier ones left in the workspace.
 static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
-                   void* workspace, int64_t workspace_bytes, void* stream, int ph0, int ph1) {
+                   void* workspace, int64_t workspace_bytes, void* stream, int ph0, int ph1,
+                   RtNorm nm = RtNorm{0, nullptr, nullptr, 0.f, nullptr}) {
   int rc = check_layer(L, T);
   if (rc) return rc;
   NSX_REQUIRE(h && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
@@ -2124,7 +2276,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
       if (rc) return rc;
     } else {
       rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
-                         (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
+                         (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st, nm);
       if (rc) return rc;
       if ((!t64 || p.grouped || router_alone) && !d.topk_in_gu &&  // else the gate/up kernel selects it
           (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
@@ -2221,6 +2373,26 @@ extern "C" int nsx_moe_forward(const nsx_moe_layer* L, const float* h, int64_t T
   return NSX_OK;
 }
 
+extern "C" int nsx_moe_forward_norm(const nsx_moe_layer* L, const float* x, const float* r, const float* norm_w,
+                                    float eps, int64_t T, float* x_out, float* out, int32_t* ids, float* weights,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_layer(L, T);
+  if (rc) return rc;
+  NSX_REQUIRE(L->layout == NSX_LAYOUT_T64 && T < RM_MIN_T && L->n_embd <= 256 * NORM_MAXV, NSX_ENOTIMPL,
+              "the norm runs in the router for t64 layers below %d tokens with n_embd <= %d", RM_MIN_T,
+              256 * NORM_MAXV);
+  NSX_REQUIRE(x && r && x_out && out && ids && weights, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE(eps >= 0.f, NSX_EINVAL, "eps %g", (double)eps);
+  const uintptr_t bytes = (uintptr_t)(T * L->n_embd * 4);
+  auto overlap = [&](const void* p, const void* q) {
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return a < b + bytes && b < a + bytes;
+  };
+  NSX_REQUIRE(!overlap(x_out, x) && !overlap(x_out, r), NSX_EINVAL, "x_out overlaps x or r");
+  return moe_run(L, x, T, out, ids, weights, workspace, workspace_bytes, stream, NSX_PHASE_ROUTER, NSX_PHASE_COMBINE,
+                 RtNorm{1, r, norm_w, eps, x_out});
+}
+
 extern "C" int nsx_moe_phase(const nsx_moe_layer* L, int phase, const float* h, int64_t T, float* out, int32_t* ids,
                              float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
   NSX_REQUIRE(phase >= NSX_PHASE_ROUTER && phase <= NSX_PHASE_COMBINE, NSX_EINVAL, "phase %d", phase);
@@ -2294,7 +2466,6 @@ extern "C" int nsx_moe_forward_static(const nsx_moe_layer* L, const float* h, in
 // residual, unit weight, no sum or no norm output); s and y may alias x or r.
 
 constexpr int NORM_THREADS = 256;
-constexpr int NORM_MAXV = 16;  // values per thread (n <= 4096)
 
 __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(const float* x, const float* r, int n, float eps,
                                                                    const float* __restrict__ w, float* sum,

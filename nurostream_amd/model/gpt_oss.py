@@ -59,6 +59,7 @@ class GptOssFFNStack:
             raise ValueError("one post-attention norm weight (or None) per layer")
         self.router_stats = RouterStats()
         self._bufs: dict[int, tuple] = {}
+        self._alt: dict[int, torch.Tensor] = {}  # the residual stream's second buffer, per T
 
     def _buffers(self, T: int):
         b = self._bufs.get(T)
@@ -74,19 +75,35 @@ class GptOssFFNStack:
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """x: (T, n_embd) fp32 residual stream in; returns it after every
-        layer's FFN block (into `out` when given). Device-only: no host sync."""
+        layer's FFN block (into `out` when given). Device-only: no host sync.
+        Between layers x += out and h = rms_norm(x) of the next layer run inside
+        that layer's router kernel where the layer allows it
+        (MoELayer.forward_norm, the same bits as add_rms_norm), the residual
+        stream then alternating between two buffers."""
         x = x.reshape(-1, self.cfg.n_embd)
         T = x.shape[0]
         h, y, ids, wts = self._buffers(T)
+        alt = self._alt.get(T)
+        if alt is None:
+            alt = self._alt[T] = torch.empty(T, self.cfg.n_embd, device=self.device)
         res = torch.empty_like(x) if out is None else out
         eps = self.cfg.rms_eps
         add_rms_norm(x.float().contiguous(), None, self.norm_weights[0], eps, out=h, sum_out=res)
-        for li, layer in enumerate(self.layers):
-            layer.forward(h, out=y, ids=ids[li], weights=wts[li])
-            if li + 1 < len(self.layers):  # x += out; h = rms_norm(x) of the next layer
-                add_rms_norm(res, y, self.norm_weights[li + 1], eps, out=h, sum_out=res)
+        self.layers[0].forward(h, out=y, ids=ids[0], weights=wts[0])
+        cur, other = res, alt
+        for li in range(1, len(self.layers)):  # x += out; h = rms_norm(x); out = layer(h)
+            layer = self.layers[li]
+            if layer.norm_folds(T):
+                layer.forward_norm(cur, y, self.norm_weights[li], eps, x_out=other, out=y, ids=ids[li],
+                                   weights=wts[li])
+                cur, other = other, cur
             else:
-                res.add_(y)
+                add_rms_norm(cur, y, self.norm_weights[li], eps, out=h, sum_out=cur)
+                layer.forward(h, out=y, ids=ids[li], weights=wts[li])
+        if cur is res:
+            res.add_(y)
+        else:
+            torch.add(cur, y, out=res)
         return res
 
     __call__ = forward

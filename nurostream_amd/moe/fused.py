@@ -186,6 +186,46 @@ class MoELayer:
 
     __call__ = forward
 
+    def norm_folds(self, T: int) -> bool:
+        """Whether forward_norm runs the block's input norm inside the router
+        kernel for T tokens: t64 layout, n_embd <= 4096, and T <= 2 (nsx_moe_forward_norm
+        takes T < 16, but from three tokens on the router reads x and r twice and a separate
+        norm launch measures faster)."""
+        return self.layout == "t64" and T <= 2 and self.n_embd <= 4096
+
+    def forward_norm(self, x: torch.Tensor, r: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
+                     x_out: torch.Tensor, out: torch.Tensor, ids: torch.Tensor | None = None,
+                     weights: torch.Tensor | None = None):
+        """One stacked block (model/gpt_oss.py:123-177): x_out = x + r and
+        forward(rms_norm(x + r) * norm_w) into out, the norm computed inside the
+        router kernel (norm_folds(T)) -- the bits of add_rms_norm + forward.
+        x, r, x_out: (T, n_embd) contiguous fp32; x_out must not overlap x or r;
+        out may be r."""
+        N.require_device(x, r, x_out)
+        T = x.shape[0]
+        for name, t in (("x", x), ("r", r), ("x_out", x_out)):
+            if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (T, self.n_embd) \
+                    or t.device != self.device:
+                raise ValueError(f"{name} must be a contiguous fp32 ({T}, {self.n_embd}) tensor on {self.device}")
+        if ids is None:
+            ids = torch.empty((T, self.top_k), dtype=torch.int32, device=self.device)
+        if weights is None:
+            weights = torch.empty((T, self.top_k), dtype=torch.float32, device=self.device)
+        self._check_buffers(T, out, ids, weights)
+        w = None
+        if norm_w is not None:
+            w = norm_w.to(device=self.device, dtype=torch.float32).contiguous()
+            if w.numel() != self.n_embd:
+                raise ValueError(f"norm weight of {w.numel()} values, n_embd is {self.n_embd}")
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            N.check(N.load().nsx_moe_forward_norm(C.byref(self._c), x.data_ptr(), r.data_ptr(),
+                                                  None if w is None else w.data_ptr(), float(eps), T,
+                                                  x_out.data_ptr(), out.data_ptr(), ids.data_ptr(),
+                                                  weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                  N.stream_ptr(self.device)), "moe_forward_norm")
+        return out, ids, weights
+
     def phase(self, phase: int, h: torch.Tensor, out: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
               workspace: torch.Tensor | None = None) -> None:
         """Run one phase (_native.PHASE_*) of forward(); later phases read what

@@ -162,3 +162,20 @@ def test_moe_layer_rejects_bad_outputs():
     for out, ids, w in bad:
         with pytest.raises(ValueError):
             lay._check_buffers(3, out, ids, w)
+
+
+def test_forward_norm_validation(lib):
+    """nsx_moe_forward_norm folds the block norm into the router for t64 layers
+    below 16 tokens (NotImplemented otherwise, so callers fall back), and
+    refuses an x_out that overlaps x or r -- all checked on the host before any
+    HIP call (the pointers below are never dereferenced)."""
+    L = _gptoss_layer()
+    args = lambda T, x_out: (C.byref(L), 1 << 20, 2 << 20, None, 1e-5, T, x_out, 4 << 20, 5 << 20, 6 << 20,  # noqa
+                             7 << 20, 1 << 30, None)
+    assert lib.nsx_moe_forward_norm(*args(16, 3 << 20)) == N.ENOTIMPL
+    assert b"router" in lib.nsx_last_error()
+    assert lib.nsx_moe_forward_norm(*args(1, (1 << 20) + 4)) == N.EINVAL
+    assert b"overlaps" in lib.nsx_last_error()
+    assert lib.nsx_moe_forward_norm(*args(1, (2 << 20) - 4)) == N.EINVAL
+    L.layout = N.LAYOUT_GGUF
+    assert lib.nsx_moe_forward_norm(*args(1, 3 << 20)) == N.ENOTIMPL

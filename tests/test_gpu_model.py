@@ -23,6 +23,41 @@ def _oracle_layers(cfg, seed, n_layers, dev):
     return out
 
 
+@pytest.mark.parametrize("T", [1, 5, 15, 16, 20])
+def test_stack_norm_in_router_equals_separate_norm(dev, T):
+    """GptOssFFNStack.forward runs the block's input norm inside the router
+    kernel (MoELayer.forward_norm) where norm_folds(T); spelled out with
+    add_rms_norm and forward() per layer the stack gives the same bits, and so
+    does forward_norm for one layer below 16 tokens (x_out = x + r, out, ids,
+    weights)."""
+    from nurostream_amd import synth
+    from nurostream_amd.compute.ops import add_rms_norm
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack
+    cfg = _small("gptoss-small")
+    L = 3
+    stack = GptOssFFNStack.synthetic(cfg, L, seed=23, device=dev)
+    stack.norm_weights = [None] + [1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(li))
+                                   .to(dev) for li in range(1, L)]
+    x = synth.activations(T, cfg.n_embd, seed=11, device=dev)
+    y = stack(x)
+    res = torch.empty_like(x)
+    h = add_rms_norm(x, None, stack.norm_weights[0], 1e-5, sum_out=res)
+    for li, layer in enumerate(stack.layers):
+        if li:
+            h = add_rms_norm(res, o, stack.norm_weights[li], 1e-5, sum_out=res)
+        o, ids, w = layer.forward(h)
+        if li == 1 and T < 16:  # one layer through forward_norm (the kernel takes T < 16)
+            xo = torch.empty_like(x)
+            o2 = torch.empty_like(x)
+            o2, ids2, w2 = layer.forward_norm(prev_res, prev_o, stack.norm_weights[li], 1e-5, x_out=xo, out=o2)
+            assert torch.equal(xo, res)
+            assert torch.equal(o2, o) and torch.equal(ids2, ids) and torch.equal(w2, w)
+        prev_res, prev_o = res.clone(), o.clone()
+    res.add_(o)
+    torch.cuda.synchronize()
+    assert torch.equal(y, res)
+
+
 @pytest.mark.parametrize("T", [1, 2, 9])
 def test_gptoss_ffn_stack_matches_oracle(dev, T):
     from nurostream_amd import synth
