@@ -873,8 +873,7 @@ __device__ __forceinline__ void gu_item(const MoeDev& a, int p, int tile, float 
   v4f D[4] = {};
   mx_compute<GU_S>(R, a.ggu, s0, s1, D);
   mx_sum_terms(D);
-  __syncthreads();  // an earlier item's wave 0 is done with `red`
-  if ((lane & 15) == 0) {
+  if ((lane & 15) == 0) {  // (one item per workgroup: `red` is not in use yet)
     const int r0 = 4 * (lane >> 4);
 #pragma unroll
     for (int g = 0; g < 4; ++g) *(v4f*)(&red[m][c][16 * g + r0]) = D[g];

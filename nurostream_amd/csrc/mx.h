@@ -103,17 +103,32 @@ __device__ __forceinline__ void xq_block_step(float r, int q, uint8_t* step) {
   const uint32_t mb = __builtin_bit_cast(uint32_t, m);
   const int s0 = (int)((mb >> 23) & 0xffu) - 127 - 8 + ((mb & 0x7fffffu) > 0x600000u ? 1 : 0);
   if (!fin) r = 0.f;
+  uint32_t codes = 0;  // byte t: term t's code of this lane's element
+  v4u sc;
 #pragma unroll
   for (int t = 0; t < XQ_NT; ++t) {
     int sx = s0 - 4 * t;
     sx = sx < -127 ? -127 : sx;
-    const uint32_t sc = !fin ? (t == 0 ? 255u : 0u) : (nz ? (uint32_t)(sx + 127) : 0u);
+    sc[t] = !fin ? (t == 0 ? 255u : 0u) : (nz ? (uint32_t)(sx + 127) : 0u);
     const uint32_t raw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_ldexpf(r, -sx), 0.f, 0, false) & 0xffu;
     r -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8((int)raw, 0), sx);  // exact
-    const uint32_t code = (raw & 0x7fu) != 0u ? raw : 0u;
-    step[(gp * XQ_NT + t) * 32 + j] = (uint8_t)code;
-    if (e == 0) *(uint32_t*)(step + XQ_CODES + (q * XQ_NT + t) * 4) = sc;
+    codes |= ((raw & 0x7fu) != 0u ? raw : 0u) << (8 * t);
   }
+  // The four lanes of a quad hold consecutive elements (one dword of each
+  // term's code row): a 4 x 4 byte transpose over the quad (DPP broadcasts,
+  // byte selects) gives lane i of the quad term i's four codes, so each lane
+  // stores one dword instead of a byte per term.
+  static_assert(XQ_NT == 4, "one term per lane of a quad");
+  const uint32_t i = __lane_id() & 3u;
+  const uint32_t q0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)codes, 0x00, 0xf, 0xf, false);
+  const uint32_t q1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)codes, 0x55, 0xf, 0xf, false);
+  const uint32_t q2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)codes, 0xaa, 0xf, 0xf, false);
+  const uint32_t q3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)codes, 0xff, 0xf, 0xf, false);
+  // v_perm_b32 selectors: 0..3 bytes of the second operand, 4..7 of the first, 0x0c zero
+  const uint32_t lo = __builtin_amdgcn_perm(q1, q0, i | (4u + i) << 8 | 0x0c0c0000u);
+  const uint32_t hi = __builtin_amdgcn_perm(q3, q2, 0x0c0cu | i << 16 | (4u + i) << 24);
+  *(uint32_t*)(step + (gp * XQ_NT + i) * 32 + (j & ~3)) = lo | hi;
+  if (e == 0) *(v4u*)(step + XQ_CODES + q * XQ_NT * 4) = sc;  // the block's four term scales
 }
 __device__ __forceinline__ void xq_block(float r, int b, uint8_t* dst) {
   xq_block_step(r, b & 3, dst + (int64_t)(b >> 2) * XQ_STEP);
