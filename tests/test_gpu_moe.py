@@ -108,34 +108,52 @@ def test_moe_small_layers(dev, name, layout, slabs, T):
     assert torch.equal(out, out2)
 
 
+N_DECODE = 8  # single-token calls per full-shape decode test
+
+
+def _decode_calls(layer, h):
+    """Each row of h through the layer as its own T=1 call (decode batch 1)."""
+    outs, ids, ws = zip(*(layer(h[i:i + 1]) for i in range(h.shape[0])))
+    return torch.cat(outs), torch.cat(ids), torch.cat(ws)
+
+
 @pytest.mark.parametrize("layout", ["t64", "gguf"])
 def test_gptoss_layer_decode(dev, layout):
-    """GPT-OSS-120B-shaped MXFP4 layer at decode batch 1."""
+    """GPT-OSS-120B-shaped MXFP4 layer at decode batch 1,
+    eight tokens each in its own call, every one against the oracle."""
     from nurostream_amd import synth
     cfg = synth.GPTOSS_120B
     t = synth.make_layer(cfg, seed=0, device=dev)
     layer = _layer(cfg, t, layout)
-    h = synth.activations(1, cfg.n_embd, seed=1, device="cpu")
-    out, ids, w = layer(h.to(dev))
+    h = synth.activations(N_DECODE, cfg.n_embd, seed=1, device="cpu")
+    out, ids, w = _decode_calls(layer, h.to(dev))
     ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
-    np.testing.assert_array_equal(to_np(ids), rid)
-    np.testing.assert_allclose(to_np(w), rw, rtol=1e-5)
-    err = rel_max(to_np(out), ref)
+    ok = ~_near_tie_tokens(rlog, cfg.top_k, h.numpy(), t["router_w"].float().cpu().numpy(),
+                           t["router_b"].float().cpu().numpy())
+    assert ok.sum() >= N_DECODE - 1
+    np.testing.assert_array_equal(to_np(ids)[ok], rid[ok])
+    np.testing.assert_allclose(to_np(w)[ok], rw[ok], rtol=1e-5)
+    err = float(np.abs(to_np(out)[ok] - ref[ok]).max() / np.abs(ref).max())
     assert err < FFN_TOL
     assert err < _tol(layout), err
 
 
 def test_qwen3_layer_decode(dev):
-    """BASELINE config 4 at T=1: Qwen3-235B-shaped Q4_K layer."""
+    """BASELINE config 4 at T=1: Qwen3-235B-shaped Q4_K layer, eight tokens
+    each in its own call, every one against the oracle."""
     from nurostream_amd import synth
     cfg = synth.QWEN3_235B
     t = synth.make_layer(cfg, seed=0, device=dev)
     layer = _layer(cfg, t, "gguf")
-    h = synth.activations(1, cfg.n_embd, seed=2, device="cpu")
-    out, ids, w = layer(h.to(dev))
+    h = synth.activations(N_DECODE, cfg.n_embd, seed=2, device="cpu")
+    out, ids, w = _decode_calls(layer, h.to(dev))
     ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
-    np.testing.assert_array_equal(to_np(ids), rid)
-    assert rel_max(to_np(out), ref) < Q4K_TOL
+    ok = ~_near_tie_tokens(rlog, cfg.top_k, h.numpy(), t["router_w"].float().cpu().numpy(), None)
+    assert ok.sum() >= N_DECODE - 1
+    np.testing.assert_array_equal(to_np(ids)[ok], rid[ok])
+    np.testing.assert_allclose(to_np(w)[ok], rw[ok], rtol=2e-5, atol=1e-6)
+    err = float(np.abs(to_np(out)[ok] - ref[ok]).max() / np.abs(ref).max())
+    assert err < Q4K_TOL, err
 
 
 @pytest.mark.parametrize("name,layout,T,dispatch", [("gptoss-small", "t64", 3, "auto"),
