@@ -29,6 +29,8 @@ HIPCC_FLAGS = [
     # never let the compiler emit packed fp32 arithmetic (v_pk_fma_f32 & co.)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # kernel arguments preloaded into SGPRs at wave launch (gfx950), not fetched by the first instructions
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

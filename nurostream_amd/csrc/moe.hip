@@ -1157,19 +1157,20 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   }
 }
 
-// Workgroup index -> (tile, item). Workgroup b runs on XCD b % 8; the
-// tiles x n_items live work units are cut into 8 contiguous runs, one per
+// Workgroup index -> (unit, item), where an item has `units` work units
+// (its tiles, or tile x row group). Workgroup b runs on XCD b % 8; the
+// units x n_items live work units are cut into 8 contiguous runs, one per
 // XCD, item-major, so that an XCD's L2 holds the activation terms of the few
 // items it is working on (and an expert's items follow each other) while the
 // grid, sized for the most items a sort can make, idles evenly on every XCD.
-__device__ __forceinline__ bool grp_work(const MoeDev& a, int tiles, int& tile, int4& item) {
-  const int live = tiles * *a.n_items, per = (live + 7) / 8;
+__device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, int4& item) {
+  const int live = units * *a.n_items, per = (live + 7) / 8;
   const int j = (int)(blockIdx.x >> 3);
   if (j >= per) return false;
   const int L = (int)(blockIdx.x & 7) * per + j;
   if (L >= live) return false;
-  const int it = L / tiles;
-  tile = L - it * tiles;
+  const int it = L / units;
+  unit = L - it * units;
   item = a.items[it];
   return true;
 }
@@ -1225,41 +1226,50 @@ __global__ __launch_bounds__(1024) void moe_gu_grouped_kernel(MoeDev a) {
   }
 }
 
-// down for one (item, tile): waves = (K-chunk, 16-row group) as in
-// moe_down_kernel; y[pair, rows] = the expert's down product plus its bias.
-__global__ __launch_bounds__(1024) void moe_down_grouped_kernel(MoeDev a) {
-  __shared__ float red[16][GRP_TPI][16];  // [wave = chunk * 4 + group][token][row of the group]
+// down for one (item, tile): one wave per K-chunk over all four 16-row
+// groups, so each token's activation terms are read once per (item, tile)
+// rather than once per row group (they are 4.5 bytes per element and token,
+// more than the weights' 0.53 per element and row). A wave's chunk, row group
+// by row group, is the (chunk, row group) wave of moe_down_kernel: same steps,
+// same accumulation order, so y is bit-identical to the per-pair path.
+// y[pair, rows] = the expert's down product plus its bias (chunk 0 carries it).
+__global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(MoeDev a) {
+  __shared__ float red[4][GRP_TPI][64];  // [wave = chunk][token][row of the tile]
   int tile;
   int4 item;
   if (!grp_work(a, (int)a.gdn.tiles, tile, item)) return;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
-  const int c = wave >> 2, rg = wave & 3;
   const int s0 = c * a.sdg, s1 = min(a.gdn.ns, s0 + a.sdg);
-  MxRegs<DC_S, 1> R;
-  mx_load_a<DC_S, 1>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, tile), a.gdn, s0,
-                     s1, rg);
-  const int r0 = tile * 64 + 16 * rg + 4 * (lane >> 4);
-  v4f bias = {0.f, 0.f, 0.f, 0.f};  // chunk 0 carries the bias, as in moe_down_kernel
-  if (c == 0 && a.down_bias && r0 < a.n_embd) bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+  MxRegs<DC_S> R;
+  mx_load_a<DC_S>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, tile), a.gdn, s0, s1);
+  const int r0 = tile * 64 + 4 * (lane >> 4);
+  v4f bias[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    bias[g] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (c == 0 && a.down_bias && r0 + 16 * g < a.n_embd)
+      bias[g] = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0 + 16 * g);
+  }
   const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
   const int64_t xs = (int64_t)a.gdn.ns * XQ_STEP;
   for (int tg = 0; tg * 4 < n; ++tg) {
     const int tok = tg * 4 + ((lane & 15) >> 2);
     const int pr = __shfl(my_pair, min(tok, n - 1), 64);
-    mx_load_b_at<DC_S, false, 1>(R, a.xq_a + (int64_t)pr * xs, 0, s0, s1);
-    v4f D[1] = {};
-    mx_compute<DC_S, 1>(R, a.gdn, s0, s1, D, rg);
-    mx_sum_terms<1>(D);
-    if ((lane & 3) == 0 && tok < n) *(v4f*)(&red[wave][tok][4 * (lane >> 4)]) = D[0] + bias;
+    mx_load_b_at<DC_S, false>(R, a.xq_a + (int64_t)pr * xs, 0, s0, s1);
+    v4f D[4] = {};
+    mx_compute<DC_S>(R, a.gdn, s0, s1, D);
+    mx_sum_terms<4>(D);
+    if ((lane & 3) == 0 && tok < n) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(v4f*)(&red[c][tok][16 * g + 4 * (lane >> 4)]) = D[g] + bias[g];
+    }
   }
   __syncthreads();
-  const int nw = 4 * a.cdg;
-  const int g = lane >> 4, r16 = lane & 15;
   const int row = tile * 64 + lane;
-  for (int w = wave; w < n; w += nw) {  // token w of the item
+  for (int w = c; w < n; w += a.cdg) {  // token w of the item: chunks in order
     float y = 0.f;
-    for (int cc = 0; cc < a.cdg; ++cc) y += red[cc * 4 + g][w][r16];
+    for (int cc = 0; cc < a.cdg; ++cc) y += red[cc][w][lane];
     const int pr = __builtin_amdgcn_readlane(my_pair, w);
     if (row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y;
   }
@@ -2310,7 +2320,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     }
     if (on(NSX_PHASE_DOWN)) {
       if (t64) {
-        rc = nsx_launch(moe_down_grouped_kernel, grid8(p.gdn.tiles), dim3(256 * p.cdg), 0, st, d);
+        rc = nsx_launch(moe_down_grouped_kernel, grid8(p.gdn.tiles), dim3(64 * p.cdg), 0, st, d);
       } else if (p.mq) {
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
                              (int)L->n_ff, d.xq_a)))
