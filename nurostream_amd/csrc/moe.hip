@@ -1175,45 +1175,58 @@ __device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, 
   return true;
 }
 
-// gate/up for one (item, tile): the waves are (gate|up, K-chunk) as in
-// moe_gu_kernel; each holds its weights in registers and runs the item's
-// tokens four at a time (16 MFMA columns = 4 tokens x 4 terms).
-__global__ __launch_bounds__(1024) void moe_gu_grouped_kernel(MoeDev a) {
+// gate/up for one (item, tile): one wave per K-chunk, computing that chunk
+// of both the gate and the up tile, so a token's activation terms are read
+// once per (item, tile, chunk) rather than once per matrix. A wave's gate
+// (up) chunk is the (gate (up), chunk) wave of moe_gu_kernel: same steps,
+// same accumulation order, so the activations are bit-identical to the
+// per-pair path. The item's tokens go four at a time (16 MFMA columns = 4
+// tokens x 4 terms).
+__global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev a) {
   __shared__ float red[2][MAX_CHUNKS][GRP_TPI][64];
   int tile;
   int4 item;
   if (!grp_work(a, (int)a.ggu.tiles, tile, item)) return;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
-  const int m = wave / a.cg, c = wave - m * a.cg;
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
-  const uint8_t* mat = m == 0 ? tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile)
-                              : tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
-  MxRegs<GU_S> R;
-  mx_load_a<GU_S>(R, mat, a.ggu, s0, s1);
+  MxRegs<GU_S> Rg, Ru;
+  mx_load_a<GU_S>(Rg, tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile), a.ggu, s0, s1);
+  mx_load_a<GU_S>(Ru, tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile), a.ggu, s0, s1);
   const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
   const int64_t xs = (int64_t)a.ggu.ns * XQ_STEP;
   for (int tg = 0; tg * 4 < n; ++tg) {
     const int tok = tg * 4 + ((lane & 15) >> 2);
     const int pr = __shfl(my_pair, min(tok, n - 1), 64);
-    mx_load_b_at<GU_S, false>(R, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
-    v4f D[4] = {};
-    mx_compute<GU_S>(R, a.ggu, s0, s1, D);
-    mx_sum_terms(D);
+    mx_load_b_at<GU_S, false>(Rg, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
+#pragma unroll
+    for (int u = 0; u < GU_S; ++u) {  // the up tile takes the same activation operands
+      Ru.B0[u] = Rg.B0[u];
+      Ru.B1[u] = Rg.B1[u];
+      Ru.SB[u] = Rg.SB[u];
+    }
+    v4f Dg[4] = {}, Du[4] = {};
+    mx_compute<GU_S>(Rg, a.ggu, s0, s1, Dg);
+    mx_compute<GU_S>(Ru, a.ggu, s0, s1, Du);
+    mx_sum_terms(Dg);
+    mx_sum_terms(Du);
     if ((lane & 3) == 0 && tok < n) {
       const int r0 = 4 * (lane >> 4);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) *(v4f*)(&red[m][c][tok][16 * g + r0]) = D[g];
+      for (int g = 0; g < 4; ++g) {
+        *(v4f*)(&red[0][c][tok][16 * g + r0]) = Dg[g];
+        *(v4f*)(&red[1][c][tok][16 * g + r0]) = Du[g];
+      }
     }
   }
   __syncthreads();
-  const int nw = 2 * a.cg;
-  if (wave >= n) return;
+  const int nw = a.cg;
+  if (c >= n) return;
   const int row = tile * 64 + lane;
   const int rowc = min(row, a.n_ff - 1);
   const float gb = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
   const float ub = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
-  for (int w = wave; w < n; w += nw) {  // token w of the item
+  for (int w = c; w < n; w += nw) {  // token w of the item
     float gs = 0.f, us = 0.f;
     for (int cc = 0; cc < a.cg; ++cc) {
       gs += red[0][cc][w][lane];
@@ -2300,7 +2313,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     if (on(NSX_PHASE_GATE_UP)) {
       if ((rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
       if (t64) {
-        rc = nsx_launch(moe_gu_grouped_kernel, grid8(p.ggu.tiles), dim3(128 * p.cg), 0, st, d);
+        rc = nsx_launch(moe_gu_grouped_kernel, grid8(p.ggu.tiles), dim3(64 * p.cg), 0, st, d);
       } else if (p.mq) {
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))
