@@ -744,6 +744,7 @@ struct MoeDev {
   int max_items;
   int cdg, sdg;          // grouped down: K-chunks and K-steps per chunk
   int topk_in_gu;        // per-pair Q4_K: the gate/up kernel selects the top-k (no top-k launch)
+  int topk_in_sort;      // grouped, T < RM_MIN_T: the sort kernel selects the top-k (no top-k launch)
 };
 
 __device__ __forceinline__ float moe_act(int kind, float g, float u, float alpha, float limit) {
@@ -1086,17 +1087,51 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   const int T = a.T, k = a.top_k, E = a.E, P = T * k;
   const int nch = (P + 63) / 64;
   for (int i = tid; i < GRP_CHUNKS * MAX_EXPERTS; i += 1024) (&s_run[0][0])[i] = 0;
-  for (int p = tid; p < P; p += 1024) {  // each pair's expert and its token's combine slot
+  if (a.topk_in_sort) {  // (T < 16: a wave per token) the top-k from the router's logits, as topk_kernel
+    for (int t = wave; t < T; t += 16) {
+      int si[MAX_TOPK];
+      float sw[MAX_TOPK];
+      topk_regs(a.logits + (int64_t)t * E, E, k, a.mode, si, sw);
+      int my_e = 0;
+      float my_w = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < MAX_TOPK; ++jj) {  // lane jj < k: slot jj
+        my_e = lane == jj ? si[jj] : my_e;
+        my_w = lane == jj ? sw[jj] : my_w;
+      }
+      if (lane < k) {
+        a.ids[(int64_t)t * k + lane] = my_e;
+        a.wts[(int64_t)t * k + lane] = my_w;
+        s_exp[t * k + lane] = (uint8_t)clamp_expert(my_e, E);
+      }
+    }
+    __syncthreads();
+  }
+  // each pair's expert and its token's combine slot
+  auto expert_of = [&](int p) { return a.topk_in_sort ? (int)s_exp[p] : clamp_expert(a.ids[p], E); };
+  int pe[(GRP_MAX_PAIRS + 1023) / 1024];
+#pragma unroll
+  for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i) {
+    const int p = tid + 1024 * i;
+    pe[i] = p < P ? expert_of(p) : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i) {
+    const int p = tid + 1024 * i;
+    if (p >= P) break;
     const int t = p / k, j = p - t * k;
-    const int e = clamp_expert(a.ids[p], E);
+    const int e = pe[i];
     int rank = 0;
     for (int jj = 0; jj < k; ++jj) {
-      const int ej = clamp_expert(a.ids[(int64_t)t * k + jj], E);
+      const int ej = expert_of(t * k + jj);
       rank += (ej < e || (ej == e && jj < j)) ? 1 : 0;
     }
     a.corder[t * k + rank] = p;
-    s_exp[p] = (uint8_t)e;
   }
+  __syncthreads();  // (every expert_of read of s_exp is done before it is written)
+#pragma unroll
+  for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i)
+    if (tid + 1024 * i < P) s_exp[tid + 1024 * i] = (uint8_t)pe[i];
   __syncthreads();
   for (int c = wave; c < nch; c += 16) {  // per-chunk counts (one lane per expert present writes)
     const int p = c * 64 + lane;
@@ -2285,6 +2320,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   // when this call runs both phases -- a router phase run on its own always leaves the ids and weights written.
   d.topk_in_gu = !t64 && !p.grouped && q4k_fast(L) && T < RM_MIN_T && ph0 <= NSX_PHASE_ROUTER &&
                  ph1 >= NSX_PHASE_GATE_UP;
+  // Grouped below RM_MIN_T tokens: the sort kernel selects the top-k itself, under the same condition.
+  d.topk_in_sort = p.grouped && T < RM_MIN_T && ph0 <= NSX_PHASE_ROUTER && ph1 >= NSX_PHASE_GATE_UP;
   // The per-pair t64 gate/up kernel always selects the top-k itself; a router phase that ends the call launches
   // the top-k too, so that phase-by-phase callers read the ids after it.
   const bool router_alone = ph1 == NSX_PHASE_ROUTER;
@@ -2300,7 +2337,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
       rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
                          (float*)(ws + p.off_logits), t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st, nm);
       if (rc) return rc;
-      if ((!t64 || p.grouped || router_alone) && !d.topk_in_gu &&  // else the gate/up kernel selects it
+      if ((!t64 || p.grouped || router_alone) && !d.topk_in_gu && !d.topk_in_sort &&  // else gate/up or sort selects it
           (rc = launch_topk(d.logits, T, L->n_expert, L->top_k, L->router_mode, ids, weights, st)))
         return rc;
     }

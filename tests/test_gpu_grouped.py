@@ -157,25 +157,26 @@ def test_grouped_q4k_equals_pairs_bitwise(dev, T):
     assert rel_max(to_np(og), ref) < Q4K_TOL
 
 
-_C4 = {}
+@pytest.fixture(scope="module")
+def config4_t32(dev):
+    """The config 4 layer at T=32, the per-pair (int8 dot) outputs and the oracle's, built once for the
+    tests below and freed after them (later tests look at fresh device allocations)."""
+    from nurostream_amd import synth
+    cfg = synth.QWEN3_235B
+    t = synth.make_layer(cfg, seed=0, device=dev)
+    h = synth.activations(32, cfg.n_embd, seed=9, device=dev)
+    op, ip, wp = _layer(cfg, t, "gguf", dispatch="pairs")(h)
+    c = dict(cfg=cfg, t=t, h=h, op=op, ip=ip, wp=wp, oracle=_oracle_layer(cfg, t, h.cpu().numpy()))
+    yield c
+    c.clear()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
 
-def _config4_t32(dev):
-    """The config 4 layer at T=32 and the per-pair (int8 dot) outputs, built once for the tests below."""
-    if not _C4:
-        from nurostream_amd import synth
-        cfg = synth.QWEN3_235B
-        t = synth.make_layer(cfg, seed=0, device=dev)
-        h = synth.activations(32, cfg.n_embd, seed=9, device=dev)
-        op, ip, wp = _layer(cfg, t, "gguf", dispatch="pairs")(h)
-        _C4.update(cfg=cfg, t=t, h=h, op=op, ip=ip, wp=wp, oracle=_oracle_layer(cfg, t, h.cpu().numpy()))
-    return _C4
-
-
-def test_config4_qwen3_t32_grouped(dev):
+def test_config4_qwen3_t32_grouped(config4_t32):
     """BASELINE config 4 at T=32: the Qwen3-235B-shaped Q4_K layer, grouped
     == per-pair on all 32 tokens, and all 32 against the oracle."""
-    c = _config4_t32(dev)
+    c = config4_t32
     cfg, t, h = c["cfg"], c["t"], c["h"]
     oa, ia, wa = _layer(cfg, t, "gguf", dispatch="grouped")(h)
     assert torch.equal(ia, c["ip"]) and torch.equal(oa, c["op"])
@@ -204,10 +205,10 @@ def test_mfma_q4k_matches_oracle_and_pairs(dev, T, scale):
     assert rel_max(to_np(om), ref) < 1e-5
 
 
-def test_config4_qwen3_t32_mfma(dev):
+def test_config4_qwen3_t32_mfma(config4_t32):
     """BASELINE config 4 at T=32 on the matrix cores: within the per-pair kernels' bound of
     theirs on all 32 tokens, and all 32 against the oracle."""
-    c = _config4_t32(dev)
+    c = config4_t32
     cfg, t, h = c["cfg"], c["t"], c["h"]
     om, im, wm = _layer(cfg, t, "gguf", dispatch="mfma")(h)
     assert torch.equal(im, c["ip"])
