@@ -1336,24 +1336,34 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
 }
 
 // ---------------------------------------------------------------------------
-// raw GGUF rows (any format): phase 1 workgroup = (pair p, 32 rows), each wave
-// computes whole gate and up rows; phase 2 workgroup = (token t, 32 output
-// rows) with the token's top_k activation vectors staged in LDS.
-
-constexpr int RAW_ROWS_PER_WG = 32;
+// Raw GGUF rows (any format), one row per wave: the row's units are fetched
+// with range-checked dword buffer loads (any byte alignment) and realigned in
+// registers, every load of a wave in flight before its arithmetic.
+// gate/up: workgroup = (pair p, RAW_WAVES rows); a wave loads its row of gate
+// and of up, the workgroup stages the token's h in LDS meanwhile, then each
+// wave adds its units in the order of the former row loop (units lane, lane +
+// 64, ...), reduces over the wave and writes act = activation(gate, up).
+// down: workgroup = (token t, RAW_WAVES output rows) with the token's k
+// activation vectors staged in LDS; a wave loads its row of every routed
+// expert (RAW_EB experts at a time) before any arithmetic, then combines the
+// experts' results in ascending id.
+constexpr int RAW_WAVES = 16;
+constexpr int RAW_UPL = 2;  // units per lane in flight (128 units = K of 4096 at a time)
+// experts whose row loads are in flight together (down; Q4_K's 48-byte units take two, within 128 VGPRs)
+template <int FMT>
+constexpr int raw_eb() { return FMT == NSX_Q4_K ? 2 : 4; }
 
 template <int FMT>
-__global__ __launch_bounds__(256) void moe_gu_raw_kernel(MoeDev a) {
+__global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
   extern __shared__ float xs[];
-  const int groups = (a.n_ff + RAW_ROWS_PER_WG - 1) / RAW_ROWS_PER_WG;
+  const int groups = (a.n_ff + RAW_WAVES - 1) / RAW_WAVES;
   const int p = blockIdx.x / groups;
-  const int r0 = (blockIdx.x % groups) * RAW_ROWS_PER_WG;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int r = (blockIdx.x - p * groups) * RAW_WAVES + wave;
   if (p >= a.T * a.top_k) return;
   const int e = clamp_expert(a.ids[p], a.E);
   const int t = p / a.top_k;
   const int K = a.n_embd;
-  stage_x<1>(xs, a.h + (int64_t)t * K, NSX_DT_F32, K, 1, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
-  const float* xsum = xs + K;
   const uint32_t rb = raw_row_bytes<FMT>(K);
   const uint8_t* gp = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
   const uint8_t* up = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
@@ -1361,70 +1371,126 @@ __global__ __launch_bounds__(256) void moe_gu_raw_kernel(MoeDev a) {
   const uint32_t gh = (uint32_t)((uintptr_t)gp - ga), uh = (uint32_t)((uintptr_t)up - ua);
   const __amdgpu_buffer_rsrc_t rg = nsx_rsrc((const void*)ga, (gh + rb * (uint32_t)a.n_ff + 3u) & ~3u);
   const __amdgpu_buffer_rsrc_t ru = nsx_rsrc((const void*)ua, (uh + rb * (uint32_t)a.n_ff + 3u) & ~3u);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int nu = raw_units<FMT>(K);
-  for (int r = r0 + wave; r < min(a.n_ff, r0 + RAW_ROWS_PER_WG); r += 4) {
-    float g[1] = {0.f}, u[1] = {0.f};
-    for (int k = lane; k < nu; k += 64) {
-      raw_unit_dot<FMT, 1>(rg, gh + (uint32_t)r * rb, k, xs, K, xsum, g);
-      raw_unit_dot<FMT, 1>(ru, uh + (uint32_t)r * rb, k, xs, K, xsum, u);
+  const uint32_t orow = (uint32_t)min(r, a.n_ff - 1) * rb;
+  float g[1] = {0.f}, u[1] = {0.f};
+  for (int u0 = 0; u0 < nu; u0 += 64 * RAW_UPL) {
+    RawUnit<FMT> G[RAW_UPL], U[RAW_UPL];
+#pragma unroll
+    for (int i = 0; i < RAW_UPL; ++i) {  // (units past the row read its last unit again; not added)
+      const int uu = min(u0 + lane + 64 * i, nu - 1);
+      G[i] = raw_unit_fetch<FMT>(RawBufSrc{rg}, gh + orow, uu);
+      U[i] = raw_unit_fetch<FMT>(RawBufSrc{ru}, uh + orow, uu);
     }
-    float gv = nsx_wave_sum(g[0]), uv = nsx_wave_sum(u[0]);
-    if (lane == 0) {
-      if (a.gate_bias) gv += a.gate_bias[(int64_t)e * a.n_ff + r];
-      if (a.up_bias) uv += a.up_bias[(int64_t)e * a.n_ff + r];
-      a.act[(int64_t)p * a.n_ff + r] = moe_act(a.act_kind, gv, uv, a.alpha, a.limit);
+    if (u0 == 0)  // the token's h into LDS while the first units stream (ends with a barrier)
+      stage_x<1>(xs, a.h + (int64_t)t * K, NSX_DT_F32, K, 1, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
+    const float* xsum = xs + K;
+#pragma unroll
+    for (int i = 0; i < RAW_UPL; ++i) {
+      const int uu = u0 + lane + 64 * i;
+      if (uu < nu) {
+        raw_unit_math<FMT, 1>(G[i], uu, RawXLds<FMT>{xs, K, uu}, RawXSumLds{xsum, K >> 5, uu}, g);
+        raw_unit_math<FMT, 1>(U[i], uu, RawXLds<FMT>{xs, K, uu}, RawXSumLds{xsum, K >> 5, uu}, u);
+      }
     }
+  }
+  float gv = nsx_wave_sum(g[0]), uv = nsx_wave_sum(u[0]);
+  if (lane == 0 && r < a.n_ff) {
+    if (a.gate_bias) gv += a.gate_bias[(int64_t)e * a.n_ff + r];
+    if (a.up_bias) uv += a.up_bias[(int64_t)e * a.n_ff + r];
+    a.act[(int64_t)p * a.n_ff + r] = moe_act(a.act_kind, gv, uv, a.alpha, a.limit);
   }
 }
 
 template <int FMT>
-__global__ __launch_bounds__(256) void moe_down_raw_kernel(MoeDev a) {
+__global__ __launch_bounds__(64 * RAW_WAVES) void moe_down_raw_kernel(MoeDev a) {
   extern __shared__ float xs[];  // [top_k][n_ff] then [top_k][n_ff/32]
-  const int groups = (a.n_embd + RAW_ROWS_PER_WG - 1) / RAW_ROWS_PER_WG;
+  const int groups = (a.n_embd + RAW_WAVES - 1) / RAW_WAVES;
   const int t = blockIdx.x / groups;
-  const int r0 = (blockIdx.x % groups) * RAW_ROWS_PER_WG;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int r = (blockIdx.x - t * groups) * RAW_WAVES + wave;
   if (t >= a.T) return;
   const int K = a.n_ff, k = a.top_k;
-  const bool sums = FMT == NSX_Q4_0 || FMT == NSX_Q4_K;
-  for (int i = threadIdx.x; i < k * K; i += blockDim.x) xs[i] = a.act[(int64_t)t * k * K + i];
-  __syncthreads();
-  const int nsb = K / 32;
-  float* xsum = xs + k * K;
-  if (sums) {
-    for (int i = threadIdx.x; i < k * nsb; i += blockDim.x) {
-      const float* s = xs + (i / nsb) * K + (i % nsb) * 32;
-      float v = 0.f;
-      for (int jj = 0; jj < 32; ++jj) v += s[jj];
-      xsum[i] = v;
-    }
-    __syncthreads();
-  }
+  const int id_l = clamp_expert(a.ids[(int64_t)t * k + min(lane, k - 1)], a.E);  // lane jj < k: slot jj
   int si[MAX_TOPK];
-  for (int jj = 0; jj < k; ++jj) si[jj] = clamp_expert(a.ids[(int64_t)t * k + jj], a.E);
+#pragma unroll
+  for (int jj = 0; jj < MAX_TOPK; ++jj) si[jj] = __builtin_amdgcn_readlane(id_l, jj < k ? jj : k - 1);
   int order[MAX_TOPK];
   slot_order(si, k, order);
   const uint32_t rb = raw_row_bytes<FMT>(K);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int nu = raw_units<FMT>(K);
-  for (int r = r0 + wave; r < min(a.n_embd, r0 + RAW_ROWS_PER_WG); r += 4) {
-    float o = 0.f;
-    for (int jj = 0; jj < k; ++jj) {
-      const int j = order[jj];
-      const int eq = si[j];
-      const uint8_t* dp = expert_base(a.down_base, a.down_stride, a.down_ptrs, eq);
-      const uintptr_t da = (uintptr_t)dp & ~(uintptr_t)3;
-      const uint32_t dh = (uint32_t)((uintptr_t)dp - da);
-      const __amdgpu_buffer_rsrc_t rd = nsx_rsrc((const void*)da, (dh + rb * (uint32_t)a.n_embd + 3u) & ~3u);
-      float acc[1] = {0.f};
-      for (int u = lane; u < nu; u += 64)
-        raw_unit_dot<FMT, 1>(rd, dh + (uint32_t)r * rb, u, xs + j * K, K, xsum + j * nsb, acc);
-      float y = nsx_wave_sum(acc[0]);
-      if (a.down_bias) y += a.down_bias[(int64_t)eq * a.n_embd + r];
-      o = combine_one(o, a.wts[(int64_t)t * k + j], y);
+  const int nu = raw_units<FMT>(K), nsb = K / 32;
+  const uint32_t orow = (uint32_t)min(r, a.n_embd - 1) * rb;
+  constexpr int RAW_EB = raw_eb<FMT>();
+  float y[MAX_TOPK];
+  for (int b0 = 0; b0 < k; b0 += RAW_EB) {  // RAW_EB experts (ascending id) at a time
+    float acc[RAW_EB];
+#pragma unroll
+    for (int q = 0; q < RAW_EB; ++q) acc[q] = 0.f;
+    for (int u0 = 0; u0 < nu; u0 += 64 * RAW_UPL) {
+      RawUnit<FMT> R[RAW_EB][RAW_UPL];
+#pragma unroll
+      for (int q = 0; q < RAW_EB; ++q) {
+        const int eq = si[order[min(b0 + q, k - 1)]];
+        const uint8_t* dp = expert_base(a.down_base, a.down_stride, a.down_ptrs, eq);
+        const uintptr_t da = (uintptr_t)dp & ~(uintptr_t)3;
+        const uint32_t dh = (uint32_t)((uintptr_t)dp - da);
+        const __amdgpu_buffer_rsrc_t rd = nsx_rsrc((const void*)da, (dh + rb * (uint32_t)a.n_embd + 3u) & ~3u);
+#pragma unroll
+        for (int i = 0; i < RAW_UPL; ++i)
+          R[q][i] = raw_unit_fetch<FMT>(RawBufSrc{rd}, dh + orow, min(u0 + lane + 64 * i, nu - 1));
+      }
+      if (b0 == 0 && u0 == 0) {  // the k activation vectors (and per-32 sums) into LDS while the rows stream
+        typedef const __attribute__((address_space(1))) v4f gv4f;
+        const int n4 = k * K / 4;
+        const float* src = a.act + (int64_t)t * k * K;
+        for (int i0 = (int)threadIdx.x; i0 < n4; i0 += 4 * 64 * RAW_WAVES) {
+          v4f v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = *(gv4f*)(src + 4 * min(i0 + q * 64 * RAW_WAVES, n4 - 1));
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (i0 + q * 64 * RAW_WAVES < n4) *(v4f*)(xs + 4 * (i0 + q * 64 * RAW_WAVES)) = v[q];
+        }
+        __syncthreads();
+        if (FMT == NSX_Q4_0 || FMT == NSX_Q4_K) {
+          float* xsum = xs + k * K;
+          for (int i = threadIdx.x; i < k * nsb; i += blockDim.x) {
+            const float* s = xs + (i / nsb) * K + (i % nsb) * 32;
+            float v = 0.f;
+            for (int jj = 0; jj < 32; ++jj) v += s[jj];
+            xsum[i] = v;
+          }
+          __syncthreads();
+        }
+      }
+      const float* xsum = xs + k * K;
+#pragma unroll
+      for (int q = 0; q < RAW_EB; ++q) {
+        if (b0 + q >= k) break;
+        const int j = order[b0 + q];
+#pragma unroll
+        for (int i = 0; i < RAW_UPL; ++i) {
+          const int uu = u0 + lane + 64 * i;
+          float one[1] = {acc[q]};
+          if (uu < nu)
+            raw_unit_math<FMT, 1>(R[q][i], uu, RawXLds<FMT>{xs + j * K, K, uu}, RawXSumLds{xsum + j * nsb, K >> 5, uu},
+                                  one);
+          acc[q] = one[0];
+        }
+      }
     }
-    if (lane == 0) a.out[(int64_t)t * a.n_embd + r] = o;
+#pragma unroll
+    for (int q = 0; q < RAW_EB; ++q)
+      if (b0 + q < k) y[b0 + q] = nsx_wave_sum(acc[q]);
   }
+  float o = 0.f;
+  for (int jj = 0; jj < k; ++jj) {  // ascending expert id
+    const int j = order[jj];
+    float v = y[jj];
+    if (a.down_bias) v += a.down_bias[(int64_t)si[j] * a.n_embd + min(r, a.n_embd - 1)];
+    o = combine_one(o, a.wts[(int64_t)t * k + j], v);
+  }
+  if (lane == 0 && r < a.n_embd) a.out[(int64_t)t * a.n_embd + r] = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -2239,9 +2305,12 @@ template <int FMT>
 static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
   const int64_t P = T * d.top_k;
   const size_t lds1 = (size_t)(d.n_embd + d.n_embd / 32) * 4;
-  const unsigned g1 = (unsigned)(P * nsx_cdiv(d.n_ff, RAW_ROWS_PER_WG));
+  const unsigned g1 = (unsigned)(P * nsx_cdiv(d.n_ff, RAW_WAVES));
   if (gate_up) {
-    int rc = nsx_launch(moe_gu_raw_kernel<FMT>, dim3(g1), dim3(256), lds1, st, d);
+    if (lds1 > 64 * 1024)
+      NSX_HIP(hipFuncSetAttribute((const void*)moe_gu_raw_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds1));
+    int rc = nsx_launch(moe_gu_raw_kernel<FMT>, dim3(g1), dim3(64 * RAW_WAVES), lds1, st, d);
     if (rc) return rc;
   }
   if (!down) return NSX_OK;
@@ -2249,8 +2318,8 @@ static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool ga
   if (lds2 > 64 * 1024)
     NSX_HIP(hipFuncSetAttribute((const void*)moe_down_raw_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds2));
-  const unsigned g2 = (unsigned)(T * nsx_cdiv(d.n_embd, RAW_ROWS_PER_WG));
-  return nsx_launch(moe_down_raw_kernel<FMT>, dim3(g2), dim3(256), lds2, st, d);
+  const unsigned g2 = (unsigned)(T * nsx_cdiv(d.n_embd, RAW_WAVES));
+  return nsx_launch(moe_down_raw_kernel<FMT>, dim3(g2), dim3(64 * RAW_WAVES), lds2, st, d);
 }
 
 // Phases ph0..ph1 of one layer (NSX_PHASE_*); each later phase reads what
