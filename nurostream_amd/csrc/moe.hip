@@ -1349,9 +1349,58 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
 // experts' results in ascending id.
 constexpr int RAW_WAVES = 16;
 constexpr int RAW_UPL = 2;  // units per lane in flight (128 units = K of 4096 at a time)
-// experts whose row loads are in flight together (down; Q4_K's 48-byte units take two, within 128 VGPRs)
+
+// x rows in LDS as 32-element chunks RAW_XPAD floats apart (row j's chunk c at
+// j * (K / 32) * RAW_XPAD + RAW_XPAD * c), so that the lanes' 16-byte reads of
+// their own units (lane l, chunk u0 + l) fall on distinct banks; then, for the
+// formats whose codes carry an offset, the per-32 sums (row j's at
+// nrows * (K / 32) * RAW_XPAD + j * (K / 32)), added in element order. The
+// whole workgroup calls it; it ends with a barrier.
+constexpr int RAW_XPAD = 36;
+__host__ __device__ constexpr int64_t raw_xpad_bytes(int64_t nrows, int64_t K) {
+  return nrows * (K / 32) * (RAW_XPAD + 1) * 4;
+}
+__device__ __forceinline__ void stage_rows_pad(float* __restrict__ xs, const float* __restrict__ src, int nrows,
+                                               int K, bool sums) {
+  typedef const __attribute__((address_space(1))) v4f gv4f;
+  const int q4 = K / 4, n4 = nrows * q4, nc = K / 32, nt = (int)blockDim.x;
+  for (int i0 = (int)threadIdx.x; i0 < n4; i0 += 4 * nt) {
+    v4f v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = *(gv4f*)(src + 4 * min(i0 + q * nt, n4 - 1));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = i0 + q * nt;
+      if (i < n4) {
+        const int j = i / q4, c4 = i - j * q4;
+        *(v4f*)(xs + (j * nc + (c4 >> 3)) * RAW_XPAD + 4 * (c4 & 7)) = v[q];
+      }
+    }
+  }
+  __syncthreads();
+  if (!sums) return;
+  float* xsum = xs + nrows * nc * RAW_XPAD;
+  for (int i = (int)threadIdx.x; i < nrows * nc; i += nt) {
+    const float* c = xs + i * RAW_XPAD;
+    float a = 0.f;
+    for (int k = 0; k < 32; ++k) a += c[k];
+    xsum[i] = a;
+  }
+  __syncthreads();
+}
+
+// one token's unit u from the padded rows above (row base xr)
 template <int FMT>
-constexpr int raw_eb() { return FMT == NSX_Q4_K ? 2 : 4; }
+struct RawXLdsPad {
+  static constexpr bool kRegSums = false;
+  const float* xr;
+  int u;
+  __device__ __forceinline__ v4f operator()(int, int k4) const { return *(const v4f*)(xr + RAW_XPAD * u + 4 * k4); }
+};
+// experts whose row loads are in flight together (down; Q4_K's and Q8_0's 40-48-byte units take two, within
+// 128 VGPRs)
+template <int FMT>
+constexpr int raw_eb() { return FMT == NSX_Q4_K || FMT == NSX_Q8_0 ? 2 : 4; }
 
 template <int FMT>
 __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
@@ -1383,14 +1432,14 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
       U[i] = raw_unit_fetch<FMT>(RawBufSrc{ru}, uh + orow, uu);
     }
     if (u0 == 0)  // the token's h into LDS while the first units stream (ends with a barrier)
-      stage_x<1>(xs, a.h + (int64_t)t * K, NSX_DT_F32, K, 1, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
-    const float* xsum = xs + K;
+      stage_rows_pad(xs, a.h + (int64_t)t * K, 1, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
+    const float* xsum = xs + (K / 32) * RAW_XPAD;
 #pragma unroll
     for (int i = 0; i < RAW_UPL; ++i) {
       const int uu = u0 + lane + 64 * i;
       if (uu < nu) {
-        raw_unit_math<FMT, 1>(G[i], uu, RawXLds<FMT>{xs, K, uu}, RawXSumLds{xsum, K >> 5, uu}, g);
-        raw_unit_math<FMT, 1>(U[i], uu, RawXLds<FMT>{xs, K, uu}, RawXSumLds{xsum, K >> 5, uu}, u);
+        raw_unit_math<FMT, 1>(G[i], uu, RawXLdsPad<FMT>{xs, uu}, RawXSumLds{xsum, K >> 5, uu}, g);
+        raw_unit_math<FMT, 1>(U[i], uu, RawXLdsPad<FMT>{xs, uu}, RawXSumLds{xsum, K >> 5, uu}, u);
       }
     }
   }
@@ -1404,7 +1453,7 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
 
 template <int FMT>
 __global__ __launch_bounds__(64 * RAW_WAVES) void moe_down_raw_kernel(MoeDev a) {
-  extern __shared__ float xs[];  // [top_k][n_ff] then [top_k][n_ff/32]
+  extern __shared__ float xs[];  // the token's top_k activation rows, padded (stage_rows_pad)
   const int groups = (a.n_embd + RAW_WAVES - 1) / RAW_WAVES;
   const int t = blockIdx.x / groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
@@ -1439,31 +1488,9 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_down_raw_kernel(MoeDev a) 
         for (int i = 0; i < RAW_UPL; ++i)
           R[q][i] = raw_unit_fetch<FMT>(RawBufSrc{rd}, dh + orow, min(u0 + lane + 64 * i, nu - 1));
       }
-      if (b0 == 0 && u0 == 0) {  // the k activation vectors (and per-32 sums) into LDS while the rows stream
-        typedef const __attribute__((address_space(1))) v4f gv4f;
-        const int n4 = k * K / 4;
-        const float* src = a.act + (int64_t)t * k * K;
-        for (int i0 = (int)threadIdx.x; i0 < n4; i0 += 4 * 64 * RAW_WAVES) {
-          v4f v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = *(gv4f*)(src + 4 * min(i0 + q * 64 * RAW_WAVES, n4 - 1));
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (i0 + q * 64 * RAW_WAVES < n4) *(v4f*)(xs + 4 * (i0 + q * 64 * RAW_WAVES)) = v[q];
-        }
-        __syncthreads();
-        if (FMT == NSX_Q4_0 || FMT == NSX_Q4_K) {
-          float* xsum = xs + k * K;
-          for (int i = threadIdx.x; i < k * nsb; i += blockDim.x) {
-            const float* s = xs + (i / nsb) * K + (i % nsb) * 32;
-            float v = 0.f;
-            for (int jj = 0; jj < 32; ++jj) v += s[jj];
-            xsum[i] = v;
-          }
-          __syncthreads();
-        }
-      }
-      const float* xsum = xs + k * K;
+      if (b0 == 0 && u0 == 0)  // the k activation vectors (and per-32 sums) into LDS while the rows stream
+        stage_rows_pad(xs, a.act + (int64_t)t * k * K, k, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
+      const float* xsum = xs + k * nsb * RAW_XPAD;
 #pragma unroll
       for (int q = 0; q < RAW_EB; ++q) {
         if (b0 + q >= k) break;
@@ -1473,8 +1500,8 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_down_raw_kernel(MoeDev a) 
           const int uu = u0 + lane + 64 * i;
           float one[1] = {acc[q]};
           if (uu < nu)
-            raw_unit_math<FMT, 1>(R[q][i], uu, RawXLds<FMT>{xs + j * K, K, uu}, RawXSumLds{xsum + j * nsb, K >> 5, uu},
-                                  one);
+            raw_unit_math<FMT, 1>(R[q][i], uu, RawXLdsPad<FMT>{xs + j * nsb * RAW_XPAD, uu},
+                                  RawXSumLds{xsum + j * nsb, K >> 5, uu}, one);
           acc[q] = one[0];
         }
       }
@@ -2304,7 +2331,7 @@ static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, 
 template <int FMT>
 static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
   const int64_t P = T * d.top_k;
-  const size_t lds1 = (size_t)(d.n_embd + d.n_embd / 32) * 4;
+  const size_t lds1 = (size_t)raw_xpad_bytes(1, d.n_embd);
   const unsigned g1 = (unsigned)(P * nsx_cdiv(d.n_ff, RAW_WAVES));
   if (gate_up) {
     if (lds1 > 64 * 1024)
@@ -2314,7 +2341,7 @@ static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool ga
     if (rc) return rc;
   }
   if (!down) return NSX_OK;
-  const size_t lds2 = (size_t)d.top_k * (d.n_ff + d.n_ff / 32) * 4;
+  const size_t lds2 = (size_t)raw_xpad_bytes(d.top_k, d.n_ff);
   if (lds2 > 64 * 1024)
     NSX_HIP(hipFuncSetAttribute((const void*)moe_down_raw_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds2));
