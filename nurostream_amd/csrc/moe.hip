@@ -1389,6 +1389,13 @@ __device__ __forceinline__ void stage_rows_pad(float* __restrict__ xs, const flo
   __syncthreads();
 }
 
+// one token's unit, read once into registers (shared by the gate and up rows)
+struct RawXArr {
+  static constexpr bool kRegSums = false;
+  const v4f (&x)[8];
+  __device__ __forceinline__ v4f operator()(int, int k4) const { return x[k4]; }
+};
+
 // one token's unit u from the padded rows above (row base xr)
 template <int FMT>
 struct RawXLdsPad {
@@ -1402,9 +1409,48 @@ struct RawXLdsPad {
 template <int FMT>
 constexpr int raw_eb() { return FMT == NSX_Q4_K || FMT == NSX_Q8_0 ? 2 : 4; }
 
+// Rows staged through LDS (L16 > 0: formats whose unit fetch realigns any
+// byte offset): a wave reads the aligned span holding its row with coalesced
+// 16-byte loads, L16 per lane (each instruction 1 KiB of consecutive bytes,
+// against ~9 cache lines per dword instruction when every lane loads its own
+// 17-byte block), writes them into its own LDS buffer at their offsets from
+// the span start (offsets modulo 4 kept), and fetches its units from there.
+// A slot past the row repeats its last slot; one that would cross the end of
+// the buffer range is moved back to end there (its bytes land at their own
+// offsets), so every load is in range.
 template <int FMT>
+constexpr bool raw_stageable() { return FMT == NSX_MXFP4 || FMT == NSX_Q4_0 || FMT == NSX_Q8_0; }
+constexpr int RAW_L16_MAX = 4;  // rows staged up to 64 x 4 slots (4096 bytes)
+__host__ __device__ constexpr int raw_slots(uint32_t rb) { return (int)((rb + 3u + 15u) >> 4); }
+
+template <int L16>
+__device__ __forceinline__ void raw_row_issue(__amdgpu_buffer_rsrc_t rs, uint32_t s0, uint32_t rend, int n16,
+                                              v4u (&V)[L16 > 0 ? L16 : 1], uint32_t (&D)[L16 > 0 ? L16 : 1]) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int i = 0; i < L16; ++i) {
+    const uint32_t sl = (uint32_t)min(lane + 64 * i, n16 - 1);
+    const uint32_t off = min(s0 + 16u * sl, rend - 16u);
+    V[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    D[i] = off - s0;
+  }
+}
+template <int L16>
+__device__ __forceinline__ void raw_row_put(uint8_t* buf, const v4u (&V)[L16 > 0 ? L16 : 1],
+                                            const uint32_t (&D)[L16 > 0 ? L16 : 1]) {
+#pragma unroll
+  for (int i = 0; i < L16; ++i) {  // (4-byte aligned: dword writes)
+    uint32_t* w = (uint32_t*)(buf + D[i]);
+    w[0] = V[i].x;
+    w[1] = V[i].y;
+    w[2] = V[i].z;
+    w[3] = V[i].w;
+  }
+}
+
+template <int FMT, int L16>
 __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
-  extern __shared__ float xs[];
+  extern __shared__ float xs[];  // padded h (stage_rows_pad), then with L16 > 0 two row buffers per wave
   const int groups = (a.n_ff + RAW_WAVES - 1) / RAW_WAVES;
   const int p = blockIdx.x / groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
@@ -1418,28 +1464,58 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
   const uint8_t* up = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
   const uintptr_t ga = (uintptr_t)gp & ~(uintptr_t)3, ua = (uintptr_t)up & ~(uintptr_t)3;
   const uint32_t gh = (uint32_t)((uintptr_t)gp - ga), uh = (uint32_t)((uintptr_t)up - ua);
-  const __amdgpu_buffer_rsrc_t rg = nsx_rsrc((const void*)ga, (gh + rb * (uint32_t)a.n_ff + 3u) & ~3u);
-  const __amdgpu_buffer_rsrc_t ru = nsx_rsrc((const void*)ua, (uh + rb * (uint32_t)a.n_ff + 3u) & ~3u);
+  const uint32_t gend = (gh + rb * (uint32_t)a.n_ff + 3u) & ~3u, uend = (uh + rb * (uint32_t)a.n_ff + 3u) & ~3u;
+  const __amdgpu_buffer_rsrc_t rg = nsx_rsrc((const void*)ga, gend);
+  const __amdgpu_buffer_rsrc_t ru = nsx_rsrc((const void*)ua, uend);
   const int nu = raw_units<FMT>(K);
   const uint32_t orow = (uint32_t)min(r, a.n_ff - 1) * rb;
+  const bool sums = FMT == NSX_Q4_0 || FMT == NSX_Q4_K;
+  const float* xsum = xs + (K / 32) * RAW_XPAD;
   float g[1] = {0.f}, u[1] = {0.f};
-  for (int u0 = 0; u0 < nu; u0 += 64 * RAW_UPL) {
-    RawUnit<FMT> G[RAW_UPL], U[RAW_UPL];
-#pragma unroll
-    for (int i = 0; i < RAW_UPL; ++i) {  // (units past the row read its last unit again; not added)
-      const int uu = min(u0 + lane + 64 * i, nu - 1);
-      G[i] = raw_unit_fetch<FMT>(RawBufSrc{rg}, gh + orow, uu);
-      U[i] = raw_unit_fetch<FMT>(RawBufSrc{ru}, uh + orow, uu);
-    }
-    if (u0 == 0)  // the token's h into LDS while the first units stream (ends with a barrier)
-      stage_rows_pad(xs, a.h + (int64_t)t * K, 1, K, FMT == NSX_Q4_0 || FMT == NSX_Q4_K);
-    const float* xsum = xs + (K / 32) * RAW_XPAD;
-#pragma unroll
-    for (int i = 0; i < RAW_UPL; ++i) {
-      const int uu = u0 + lane + 64 * i;
+  if constexpr (L16 > 0) {
+    const int n16 = raw_slots(rb);
+    uint8_t* wg = (uint8_t*)xs + raw_xpad_bytes(1, K) + (size_t)wave * 2 * n16 * 16;
+    uint8_t* wu = wg + n16 * 16;
+    const uint32_t gs = gh + orow, us = uh + orow;
+    v4u GV[L16], UV[L16];
+    uint32_t GD[L16], UD[L16];
+    raw_row_issue<L16>(rg, gs & ~3u, gend, n16, GV, GD);
+    raw_row_issue<L16>(ru, us & ~3u, uend, n16, UV, UD);
+    stage_rows_pad(xs, a.h + (int64_t)t * K, 1, K, sums);  // the token's h (ends with a barrier)
+    raw_row_put<L16>(wg, GV, GD);
+    raw_row_put<L16>(wu, UV, UD);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's row bytes are in LDS before its reads
+    __builtin_amdgcn_wave_barrier();
+    for (int u0 = 0; u0 < nu; u0 += 64) {
+      const int uu = u0 + lane;
       if (uu < nu) {
-        raw_unit_math<FMT, 1>(G[i], uu, RawXLdsPad<FMT>{xs, uu}, RawXSumLds{xsum, K >> 5, uu}, g);
-        raw_unit_math<FMT, 1>(U[i], uu, RawXLdsPad<FMT>{xs, uu}, RawXSumLds{xsum, K >> 5, uu}, u);
+        v4f xv[8];  // the unit's activations, once for both rows
+#pragma unroll
+        for (int k4 = 0; k4 < 8; ++k4) xv[k4] = RawXLdsPad<FMT>{xs, uu}(0, k4);
+        raw_unit_math<FMT, 1>(raw_unit_fetch<FMT>(RawLdsSrc{wg}, gs & 3u, uu), uu, RawXArr{xv},
+                              RawXSumLds{xsum, K >> 5, uu}, g);
+        raw_unit_math<FMT, 1>(raw_unit_fetch<FMT>(RawLdsSrc{wu}, us & 3u, uu), uu, RawXArr{xv},
+                              RawXSumLds{xsum, K >> 5, uu}, u);
+      }
+    }
+  } else {
+    for (int u0 = 0; u0 < nu; u0 += 64 * RAW_UPL) {
+      RawUnit<FMT> G[RAW_UPL], U[RAW_UPL];
+#pragma unroll
+      for (int i = 0; i < RAW_UPL; ++i) {  // (units past the row read its last unit again; not added)
+        const int uu = min(u0 + lane + 64 * i, nu - 1);
+        G[i] = raw_unit_fetch<FMT>(RawBufSrc{rg}, gh + orow, uu);
+        U[i] = raw_unit_fetch<FMT>(RawBufSrc{ru}, uh + orow, uu);
+      }
+      if (u0 == 0)  // the token's h into LDS while the first units stream (ends with a barrier)
+        stage_rows_pad(xs, a.h + (int64_t)t * K, 1, K, sums);
+#pragma unroll
+      for (int i = 0; i < RAW_UPL; ++i) {
+        const int uu = u0 + lane + 64 * i;
+        if (uu < nu) {
+          raw_unit_math<FMT, 1>(G[i], uu, RawXLdsPad<FMT>{xs, uu}, RawXSumLds{xsum, K >> 5, uu}, g);
+          raw_unit_math<FMT, 1>(U[i], uu, RawXLdsPad<FMT>{xs, uu}, RawXSumLds{xsum, K >> 5, uu}, u);
+        }
       }
     }
   }
@@ -2331,13 +2407,25 @@ static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, 
 template <int FMT>
 static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
   const int64_t P = T * d.top_k;
-  const size_t lds1 = (size_t)raw_xpad_bytes(1, d.n_embd);
+  const int n16 = raw_slots(raw_row_bytes<FMT>(d.n_embd));
+  const int l16 = raw_stageable<FMT>() ? (n16 + 63) / 64 : 0;
+  const size_t lds1 = (size_t)raw_xpad_bytes(1, d.n_embd) +
+                      (l16 >= 1 && l16 <= RAW_L16_MAX ? (size_t)RAW_WAVES * 2 * n16 * 16 : 0);
   const unsigned g1 = (unsigned)(P * nsx_cdiv(d.n_ff, RAW_WAVES));
   if (gate_up) {
-    if (lds1 > 64 * 1024)
-      NSX_HIP(hipFuncSetAttribute((const void*)moe_gu_raw_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds1));
-    int rc = nsx_launch(moe_gu_raw_kernel<FMT>, dim3(g1), dim3(64 * RAW_WAVES), lds1, st, d);
+    auto go = [&](auto kern) {
+      if (lds1 > 64 * 1024)
+        NSX_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1));
+      return nsx_launch(kern, dim3(g1), dim3(64 * RAW_WAVES), lds1, st, d);
+    };
+    int rc;
+    if constexpr (raw_stageable<FMT>()) {
+      rc = l16 == 1 ? go(moe_gu_raw_kernel<FMT, 1>) : l16 == 2 ? go(moe_gu_raw_kernel<FMT, 2>)
+         : l16 == 3 ? go(moe_gu_raw_kernel<FMT, 3>) : l16 == 4 ? go(moe_gu_raw_kernel<FMT, 4>)
+         : go(moe_gu_raw_kernel<FMT, 0>);
+    } else {
+      rc = go(moe_gu_raw_kernel<FMT, 0>);
+    }
     if (rc) return rc;
   }
   if (!down) return NSX_OK;
