@@ -743,7 +743,7 @@ struct MoeDev {
   float* y;              // (pairs, n_embd) expert outputs, bias included
   int max_items;
   int cdg, sdg;          // grouped down: K-chunks and K-steps per chunk
-  int topk_in_gu;        // per-pair Q4_K: the gate/up kernel selects the top-k (no top-k launch)
+  int topk_in_gu;        // per-pair GGUF-layout paths: the gate/up kernel selects the top-k (no top-k launch)
   int topk_in_sort;      // grouped, T < RM_MIN_T: the sort kernel selects the top-k (no top-k launch)
 };
 
@@ -1450,14 +1450,42 @@ __device__ __forceinline__ void raw_row_put(uint8_t* buf, const v4u (&V)[L16 > 0
 
 template <int FMT, int L16>
 __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
-  extern __shared__ float xs[];  // padded h (stage_rows_pad), then with L16 > 0 two row buffers per wave
+  extern __shared__ __align__(16) float xs[];  // padded h (stage_rows_pad), then with L16 > 0 two row buffers per wave
+  __shared__ int s_e;
   const int groups = (a.n_ff + RAW_WAVES - 1) / RAW_WAVES;
   const int p = blockIdx.x / groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int r = (blockIdx.x - p * groups) * RAW_WAVES + wave;
+  const int rg0 = blockIdx.x - p * groups;
+  const int r = rg0 * RAW_WAVES + wave;
   if (p >= a.T * a.top_k) return;
-  const int e = clamp_expert(a.ids[p], a.E);
   const int t = p / a.top_k;
+  int e;
+  if (a.topk_in_gu) {  // (forward below RM_MIN_T tokens) the pair's expert from the router's logits, as moe_gu_kernel
+    if (wave == 0) {
+      const int k = a.top_k, j = p - t * k;
+      int si[MAX_TOPK];
+      float sw[MAX_TOPK];
+      const bool writes = j == 0 && rg0 == 0;  // the token's first workgroup writes the ids / weights down reads
+      topk_regs(a.logits + (int64_t)t * a.E, a.E, k, a.mode, si, sw, writes, j + 1);
+      int my_e = 0, ej = 0;
+      float my_w = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < MAX_TOPK; ++jj) {
+        ej = jj == j ? si[jj] : ej;
+        my_e = lane == jj ? si[jj] : my_e;
+        my_w = lane == jj ? sw[jj] : my_w;
+      }
+      if (writes && lane < k) {
+        a.ids[(int64_t)t * k + lane] = clamp_expert(my_e, a.E);
+        a.wts[(int64_t)t * k + lane] = my_w;
+      }
+      if (lane == 0) s_e = clamp_expert(ej, a.E);
+    }
+    __syncthreads();
+    e = s_e;
+  } else {
+    e = clamp_expert(a.ids[p], a.E);
+  }
   const int K = a.n_embd;
   const uint32_t rb = raw_row_bytes<FMT>(K);
   const uint8_t* gp = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
@@ -1529,7 +1557,7 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_gu_raw_kernel(MoeDev a) {
 
 template <int FMT>
 __global__ __launch_bounds__(64 * RAW_WAVES) void moe_down_raw_kernel(MoeDev a) {
-  extern __shared__ float xs[];  // the token's top_k activation rows, padded (stage_rows_pad)
+  extern __shared__ __align__(16) float xs[];  // the token's top_k activation rows, padded (stage_rows_pad)
   const int groups = (a.n_embd + RAW_WAVES - 1) / RAW_WAVES;
   const int t = blockIdx.x / groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
@@ -2502,8 +2530,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.sdg = p.sdg;
   // Per-pair Q4_K below RM_MIN_T tokens: the gate/up kernel selects the top-k itself (no top-k launch), but only
   // when this call runs both phases -- a router phase run on its own always leaves the ids and weights written.
-  d.topk_in_gu = !t64 && !p.grouped && q4k_fast(L) && T < RM_MIN_T && ph0 <= NSX_PHASE_ROUTER &&
-                 ph1 >= NSX_PHASE_GATE_UP;
+  // (the raw-row kernels of the other GGUF layouts likewise)
+  d.topk_in_gu = !t64 && !p.grouped && T < RM_MIN_T && ph0 <= NSX_PHASE_ROUTER && ph1 >= NSX_PHASE_GATE_UP;
   // Grouped below RM_MIN_T tokens: the sort kernel selects the top-k itself, under the same condition.
   d.topk_in_sort = p.grouped && T < RM_MIN_T && ph0 <= NSX_PHASE_ROUTER && ph1 >= NSX_PHASE_GATE_UP;
   // The per-pair t64 gate/up kernel always selects the top-k itself; a router phase that ends the call launches
