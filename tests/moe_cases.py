@@ -60,4 +60,7 @@ def _small(name):
     if name == "q4_0-small":
         return synth.MoEConfig("q40-small", synth.GGMLType.Q4_0, 8, 2, 128, 96, "gptoss", "silu_mul", True,
                                torch.float32)
+    if name == "q8_0-small":  # 170- and 102-byte rows: rows and 34-byte units at 2-byte offsets
+        return synth.MoEConfig("q80-small", synth.GGMLType.Q8_0, 8, 3, 160, 96, "qwen3", "silu_mul", False,
+                               torch.float32)
     raise KeyError(name)

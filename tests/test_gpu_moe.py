@@ -91,7 +91,9 @@ def test_router_mfma_tiles(dev, name, layout, T):
 
 @pytest.mark.parametrize("name,layout,slabs", [("gptoss-small", "t64", False), ("gptoss-small", "t64", True),
                                                ("gptoss-small", "gguf", False), ("gptoss-small", "gguf", True),
-                                               ("qwen3-small", "gguf", False), ("q4_0-small", "gguf", False)])
+                                               ("qwen3-small", "gguf", False), ("qwen3-small", "gguf", True),
+                                               ("q4_0-small", "gguf", False), ("q8_0-small", "gguf", False),
+                                               ("q8_0-small", "gguf", True)])
 @pytest.mark.parametrize("T", [1, 2, 9])
 def test_moe_small_layers(dev, name, layout, slabs, T):
     from nurostream_amd import synth
