@@ -1210,67 +1210,113 @@ __device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, 
   return true;
 }
 
-// gate/up for one (item, tile): one wave per K-chunk, computing that chunk
+// gate/up for (item, tile) units: one wave per K-chunk, computing that chunk
 // of both the gate and the up tile, so a token's activation terms are read
 // once per (item, tile, chunk) rather than once per matrix. A wave's gate
 // (up) chunk is the (gate (up), chunk) wave of moe_gu_kernel: same steps,
 // same accumulation order, so the activations are bit-identical to the
 // per-pair path. The item's tokens go four at a time (16 MFMA columns = 4
-// tokens x 4 terms).
+// tokens x 4 terms). Persistent: the launch is the resident workgroups, 8
+// groups of nx (group x on XCD x: workgroup b runs on XCD b % 8), and group x
+// works through XCD x's contiguous item-major run of units -- workgroup j of
+// it takes units j, j + nx, ... -- so no workgroup is dispatched per unit;
+// the next unit's weights are requested before this unit's epilogue, into
+// the registers its MFMAs have finished with.
 __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev a) {
   __shared__ float red[2][MAX_CHUNKS][GRP_TPI][64];
-  int tile;
-  int4 item;
-  if (!grp_work(a, (int)a.ggu.tiles, tile, item)) return;
+  const int tiles = (int)a.ggu.tiles;
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7);
+  const int live = tiles * *a.n_items, per = (live + 7) / 8;
+  const int hi = min(live, (xcd + 1) * per);
+  int L = xcd * per + (int)(blockIdx.x >> 3);
+  if (L >= hi) return;
   const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
-  const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
-  MxRegs<GU_S> Rg, Ru;
-  mx_load_a<GU_S>(Rg, tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile), a.ggu, s0, s1);
-  mx_load_a<GU_S>(Ru, tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile), a.ggu, s0, s1);
-  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
   const int64_t xs = (int64_t)a.ggu.ns * XQ_STEP;
-  for (int tg = 0; tg * 4 < n; ++tg) {
-    const int tok = tg * 4 + ((lane & 15) >> 2);
-    const int pr = __shfl(my_pair, min(tok, n - 1), 64);
-    mx_load_b_at<GU_S, false>(Rg, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
+  MxRegs<GU_S> Rg, Ru;
+  int4 item = a.items[L / tiles];
+  int tile = L - (L / tiles) * tiles;
+  int e = clamp_expert(item.x, a.E);
+  {  // both tiles' addresses before any load: a pointer-table read between the two load groups would wait on the first
+    const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile);
+    const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
+    mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
+    mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
+  }
+  int my_pair = a.sorted[item.y + min(lane & 15, item.z - 1)];  // lane i < 16: the item's token i
+  for (;;) {
+    const int n = item.z;
+    for (int tg = 0; tg * 4 < n; ++tg) {
+      const int tok = tg * 4 + ((lane & 15) >> 2);
+      const int pr = __shfl(my_pair, min(tok, n - 1), 64);
+      mx_load_b_at<GU_S, false>(Rg, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
 #pragma unroll
-    for (int u = 0; u < GU_S; ++u) {  // the up tile takes the same activation operands
-      Ru.B0[u] = Rg.B0[u];
-      Ru.B1[u] = Rg.B1[u];
-      Ru.SB[u] = Rg.SB[u];
-    }
-    v4f Dg[4] = {}, Du[4] = {};
-    mx_compute<GU_S>(Rg, a.ggu, s0, s1, Dg);
-    mx_compute<GU_S>(Ru, a.ggu, s0, s1, Du);
-    mx_sum_terms(Dg);
-    mx_sum_terms(Du);
-    if ((lane & 3) == 0 && tok < n) {
-      const int r0 = 4 * (lane >> 4);
+      for (int u = 0; u < GU_S; ++u) {  // the up tile takes the same activation operands
+        Ru.B0[u] = Rg.B0[u];
+        Ru.B1[u] = Rg.B1[u];
+        Ru.SB[u] = Rg.SB[u];
+      }
+      v4f Dg[4] = {}, Du[4] = {};
+      mx_compute<GU_S>(Rg, a.ggu, s0, s1, Dg);
+      mx_compute<GU_S>(Ru, a.ggu, s0, s1, Du);
+      mx_sum_terms(Dg);
+      mx_sum_terms(Du);
+      if ((lane & 3) == 0 && tok < n) {
+        const int r0 = 4 * (lane >> 4);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        *(v4f*)(&red[0][c][tok][16 * g + r0]) = Dg[g];
-        *(v4f*)(&red[1][c][tok][16 * g + r0]) = Du[g];
+        for (int g = 0; g < 4; ++g) {
+          *(v4f*)(&red[0][c][tok][16 * g + r0]) = Dg[g];
+          *(v4f*)(&red[1][c][tok][16 * g + r0]) = Du[g];
+        }
       }
     }
-  }
-  __syncthreads();
-  const int nw = a.cg;
-  if (c >= n) return;
-  const int row = tile * 64 + lane;
-  const int rowc = min(row, a.n_ff - 1);
-  const float gb = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
-  const float ub = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
-  for (int w = c; w < n; w += nw) {  // token w of the item
-    float gs = 0.f, us = 0.f;
-    for (int cc = 0; cc < a.cg; ++cc) {
-      gs += red[0][cc][w][lane];
-      us += red[1][cc][w][lane];
+    const int Ln = L + nx;
+    // LDS-only barriers below: a memory-counter wait would hold the epilogue until the next unit's weights land
+    auto lds_barrier = []() {
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      asm volatile("s_barrier" ::: "memory");
+    };
+    // the biases are read before any next-unit load: loads complete in order, so one issued behind them waits on them
+    const int row = tile * 64 + lane;
+    const int rowc = min(row, a.n_ff - 1);
+    const float gb = a.gate_bias && c < n ? a.gate_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
+    const float ub = a.up_bias && c < n ? a.up_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
+    auto epilogue = [&]() {
+      if (c >= n) return;
+      for (int w = c; w < n; w += a.cg) {  // token w of the item
+        float gs = 0.f, us = 0.f;
+        for (int cc = 0; cc < a.cg; ++cc) {
+          gs += red[0][cc][w][lane];
+          us += red[1][cc][w][lane];
+        }
+        const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
+        const int pr = __builtin_amdgcn_readlane(my_pair, w);
+        xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+        xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+      }
+    };
+    if (Ln >= hi) {  // (a path of its own: the weight registers are not live into a merge with reloaded ones)
+      lds_barrier();
+      epilogue();
+      break;
     }
-    const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
-    const int pr = __builtin_amdgcn_readlane(my_pair, w);
-    xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
-    xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+    // the next unit's weights and pair list go out before this unit's epilogue
+    const int4 item_n = a.items[Ln / tiles];
+    const int tile_n = Ln - (Ln / tiles) * tiles;
+    const int e_n = clamp_expert(item_n.x, a.E);
+    const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e_n, tile_n);
+    const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e_n, tile_n);
+    mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
+    mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
+    const int pair_n = a.sorted[item_n.y + min(lane & 15, item_n.z - 1)];
+    lds_barrier();
+    epilogue();
+    lds_barrier();  // the epilogue's reads of red come before the next unit's writes
+    L = Ln;
+    item = item_n;
+    tile = tile_n;
+    e = e_n;
+    my_pair = pair_n;
   }
 }
 
@@ -2562,7 +2608,11 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     if (on(NSX_PHASE_GATE_UP)) {
       if ((rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
       if (t64) {
-        rc = nsx_launch(moe_gu_grouped_kernel, grid8(p.ggu.tiles), dim3(64 * p.cg), 0, st, d);
+        // persistent: the resident workgroups (a multiple of 8), no more than the units can use
+        const int64_t r = std::max<int64_t>(8, nsx_resident_workgroups((const void*)moe_gu_grouped_kernel, 0,
+                                                                       64 * p.cg) / 8 * 8);
+        rc = nsx_launch(moe_gu_grouped_kernel, dim3((unsigned)std::min<int64_t>(r, 8 * nsx_cdiv(items * p.ggu.tiles, 8))),
+                        dim3(64 * p.cg), 0, st, d);
       } else if (p.mq) {
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))

@@ -176,6 +176,27 @@ __device__ __forceinline__ void mx_load_a(MxRegs<S, G>& R, const uint8_t* __rest
   }
 }
 
+// mx_load_a without control flow between the loads: steps past s1 (s1 > s0)
+// reload step s1 - 1 (mx_compute skips them), so the loads of every step go out
+// back to back even where the registers already hold earlier values.
+template <int S, int G = 4>
+__device__ __forceinline__ void mx_load_a_flat(MxRegs<S, G>& R, const uint8_t* __restrict__ tile, const MxGeom& G_,
+                                               int s0, int s1, int g0 = 0) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  typedef const __attribute__((address_space(1))) uint32_t gu32;
+  const int lane = __lane_id(), grp = lane >> 4;
+#pragma unroll
+  for (int u = 0; u < S; ++u) {
+    const int s = min(s0 + u, s1 - 1);
+    const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
+    const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
+    const int la = grp < rs ? lane : 16 * rs - 1;
+#pragma unroll
+    for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
+    R.SA[u] = __builtin_nontemporal_load((gu32*)(ch + rs * 1024 + la * 4));
+  }
+}
+
 // Activation operands of the same steps for this lane's column, whose token's
 // terms start at xtok (step xs0 of that token; in LDS when BLDS): column
 // c = lane % 16 is term c % XQ_NT of the lane's token.

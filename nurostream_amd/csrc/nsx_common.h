@@ -16,6 +16,9 @@
 // host-side error reporting
 
 int nsx_fail(int code, const char* fmt, ...);
+// Workgroups of `kernel` (`threads` threads, `lds` dynamic bytes) resident on the current device at once
+// (CUs x blocks per CU), cached per kernel, LDS size and device.
+int nsx_resident_workgroups(const void* kernel, size_t lds, int threads);
 
 #define NSX_HIP(call)                                                           \
   do {                                                                          \

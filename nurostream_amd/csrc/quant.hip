@@ -585,7 +585,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
 
 // Workgroups of `kernel` (`threads` threads, `lds` bytes) resident on the
 // current device at once: CUs x blocks per CU, cached per kernel and LDS size.
-static int resident_workgroups(const void* kernel, size_t lds, int threads = GV_THREADS) {
+int nsx_resident_workgroups(const void* kernel, size_t lds, int threads) {
   struct Entry { const void* k; size_t lds; int dev; int n; };
   static std::mutex mu;
   static Entry cache[64];
@@ -616,7 +616,7 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
   const size_t lds = xreg ? std::max((size_t)gv_xreg_bytes((int)K), bufs) : (size_t)gv_x_bytes<NT>((int)K) + bufs;
   const void* kern = xreg ? (const void*)gemv_raw_kernel<FMT, NT, XR> : (const void*)gemv_raw_kernel<FMT, NT, false>;
   if (lds > 64 * 1024) NSX_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-  const int64_t resident = resident_workgroups(kern, lds);
+  const int64_t resident = nsx_resident_workgroups(kern, lds, GV_THREADS);
   // Small one-token matrices (a row per wave fits the machine in one pass of
   // 16-wave workgroups): every row's loads go out at once and x is staged
   // once per workgroup. For the formats whose unit arithmetic fits the
@@ -627,7 +627,7 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
   const size_t lds_big = std::max((size_t)gv_xreg_bytes((int)K), (size_t)BIG * GvChunk<FMT>::WAVE_BYTES);
   int64_t big_resident = 0;
   if constexpr (BIG_OK)
-    big_resident = resident_workgroups((const void*)gemv_raw_kernel<FMT, NT, XR, BIG>, lds_big, 64 * BIG);
+    big_resident = nsx_resident_workgroups((const void*)gemv_raw_kernel<FMT, NT, XR, BIG>, lds_big, 64 * BIG);
   for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_launch) {
     const int64_t nr = std::min(rows_per_launch, n_rows - r0);
     const uint8_t* p = (const uint8_t*)raw + r0 * row_bytes;
