@@ -1237,19 +1237,27 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   int4 item = a.items[L / tiles];
   int tile = L - (L / tiles) * tiles;
   int e = clamp_expert(item.x, a.E);
+  // the pair list goes out ahead of the weights: loads return in order, and the first token group's
+  // activation loads wait on it (behind the weights, they would wait for every weight byte)
+  int my_pair = a.sorted[item.y + min(lane & 15, item.z - 1)];  // lane i < 16: the item's token i
   {  // both tiles' addresses before any load: a pointer-table read between the two load groups would wait on the first
     const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile);
     const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
     mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
     mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
   }
-  int my_pair = a.sorted[item.y + min(lane & 15, item.z - 1)];  // lane i < 16: the item's token i
   for (;;) {
     const int n = item.z;
+    const int Ln = L + nx;
+    // the next unit's item, requested now so that it is at hand when this unit's MFMAs are done (the last unit
+    // re-reads its own); lane i holds word i & 3 -- a lane-varying load stays in VGPRs, where nothing waits on
+    // it before its fields are read after the token loop
+    const int iw_n = ((const int*)a.items)[4 * (min(Ln, hi - 1) / tiles) + (lane & 3)];
     for (int tg = 0; tg * 4 < n; ++tg) {
       const int tok = tg * 4 + ((lane & 15) >> 2);
       const int pr = __shfl(my_pair, min(tok, n - 1), 64);
-      mx_load_b_at<GU_S, false>(Rg, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
+      mx_load_b_at<GU_S, false, 4, true>(Rg, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
+      asm volatile("" ::: "memory");  // all steps' loads go out before the first step's MFMAs wait on one
 #pragma unroll
       for (int u = 0; u < GU_S; ++u) {  // the up tile takes the same activation operands
         Ru.B0[u] = Rg.B0[u];
@@ -1270,7 +1278,6 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
         }
       }
     }
-    const int Ln = L + nx;
     // LDS-only barriers below: a memory-counter wait would hold the epilogue until the next unit's weights land
     auto lds_barrier = []() {
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
@@ -1301,14 +1308,15 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
       break;
     }
     // the next unit's weights and pair list go out before this unit's epilogue
-    const int4 item_n = a.items[Ln / tiles];
+    const int4 item_n = {__builtin_amdgcn_readlane(iw_n, 0), __builtin_amdgcn_readlane(iw_n, 1),
+                         __builtin_amdgcn_readlane(iw_n, 2), 0};
     const int tile_n = Ln - (Ln / tiles) * tiles;
     const int e_n = clamp_expert(item_n.x, a.E);
+    const int pair_n = a.sorted[item_n.y + min(lane & 15, item_n.z - 1)];  // (ahead of the weights, as above)
     const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e_n, tile_n);
     const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e_n, tile_n);
     mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
     mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
-    const int pair_n = a.sorted[item_n.y + min(lane & 15, item_n.z - 1)];
     lds_barrier();
     epilogue();
     lds_barrier();  // the epilogue's reads of red come before the next unit's writes
@@ -1336,7 +1344,11 @@ __global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(MoeDev a) {
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
   const int s0 = c * a.sdg, s1 = min(a.gdn.ns, s0 + a.sdg);
   MxRegs<DC_S> R;
-  mx_load_a<DC_S>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, tile), a.gdn, s0, s1);
+  // the pair list goes out ahead of the weights: loads return in order, and the first token group's
+  // activation loads wait on it (behind the weights, they would wait for every weight byte)
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
+  mx_load_a_flat<DC_S>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, tile), a.gdn, s0,
+                       s1);
   const int r0 = tile * 64 + 4 * (lane >> 4);
   v4f bias[4];
 #pragma unroll
@@ -1345,12 +1357,12 @@ __global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(MoeDev a) {
     if (c == 0 && a.down_bias && r0 + 16 * g < a.n_embd)
       bias[g] = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0 + 16 * g);
   }
-  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
   const int64_t xs = (int64_t)a.gdn.ns * XQ_STEP;
   for (int tg = 0; tg * 4 < n; ++tg) {
     const int tok = tg * 4 + ((lane & 15) >> 2);
     const int pr = __shfl(my_pair, min(tok, n - 1), 64);
-    mx_load_b_at<DC_S, false>(R, a.xq_a + (int64_t)pr * xs, 0, s0, s1);
+    mx_load_b_at<DC_S, false, 4, true>(R, a.xq_a + (int64_t)pr * xs, 0, s0, s1);
+    asm volatile("" ::: "memory");  // all steps' loads go out before the first step's MFMAs wait on one
     v4f D[4] = {};
     mx_compute<DC_S>(R, a.gdn, s0, s1, D);
     mx_sum_terms<4>(D);

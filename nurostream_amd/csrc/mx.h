@@ -148,6 +148,31 @@ struct MxRegs {
   uint32_t SA[S], SB[S];
 };
 
+// A zero scale word for the lanes past a partial last step. It is writable
+// memory on purpose: a load the compiler cannot fold stays a load, so no VALU
+// select on the loaded scales is left to hoist out of a caller's token loop
+// (such a select waits for every weight load before the loop's first
+// activation load can go out).
+static __device__ uint32_t nsx_mx_zero_scale[1];
+
+// The scale operand of this lane for step chunk ch (rs live lane groups): the
+// word of groups g0.. for G = 4, the byte of group g0 for G = 1 (in the low
+// byte either way); the zero word for lanes past the step.
+template <int G>
+__device__ __forceinline__ uint32_t mx_load_sa(const uint8_t* ch, int rs, int lane, int g0) {
+  static_assert(G == 1 || G == 4, "one or all four row groups");
+  typedef const __attribute__((address_space(1))) uint32_t gu32;
+  typedef const __attribute__((address_space(1))) uint8_t gu8;
+  const bool live = (lane >> 4) < rs;
+  if constexpr (G == 4) {
+    const uint8_t* p = live ? ch + rs * 1024 + lane * 4 : (const uint8_t*)nsx_mx_zero_scale;
+    return __builtin_nontemporal_load((gu32*)p);
+  } else {
+    const uint8_t* p = live ? ch + rs * 1024 + lane * 4 + g0 : (const uint8_t*)nsx_mx_zero_scale;
+    return __builtin_nontemporal_load((gu8*)p);
+  }
+}
+
 // Weight operands of steps [s0, min(s1, s0 + S)) of a 64-row tile, read once
 // per call (nontemporal: streamed weights do not displace cached data). Loads
 // are unpredicated so that their waits retire step by step: lanes past a partial
@@ -159,7 +184,6 @@ template <int S, int G = 4>
 __device__ __forceinline__ void mx_load_a(MxRegs<S, G>& R, const uint8_t* __restrict__ tile, const MxGeom& G_,
                                           int s0, int s1, int g0 = 0) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
-  typedef const __attribute__((address_space(1))) uint32_t gu32;
   const int lane = __lane_id(), grp = lane >> 4;
 #pragma unroll
   for (int u = 0; u < S; ++u) {
@@ -167,11 +191,10 @@ __device__ __forceinline__ void mx_load_a(MxRegs<S, G>& R, const uint8_t* __rest
     if (s < s1) {
       const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
       const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
-      const bool alane = grp < rs;
-      const int la = alane ? lane : 16 * rs - 1;
+      const int la = grp < rs ? lane : 16 * rs - 1;
 #pragma unroll
       for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
-      R.SA[u] = __builtin_nontemporal_load((gu32*)(ch + rs * 1024 + la * 4));  // raw: mx_compute selects
+      R.SA[u] = mx_load_sa<G>(ch, rs, lane, g0);
     }
   }
 }
@@ -183,7 +206,6 @@ template <int S, int G = 4>
 __device__ __forceinline__ void mx_load_a_flat(MxRegs<S, G>& R, const uint8_t* __restrict__ tile, const MxGeom& G_,
                                                int s0, int s1, int g0 = 0) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
-  typedef const __attribute__((address_space(1))) uint32_t gu32;
   const int lane = __lane_id(), grp = lane >> 4;
 #pragma unroll
   for (int u = 0; u < S; ++u) {
@@ -193,14 +215,16 @@ __device__ __forceinline__ void mx_load_a_flat(MxRegs<S, G>& R, const uint8_t* _
     const int la = grp < rs ? lane : 16 * rs - 1;
 #pragma unroll
     for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
-    R.SA[u] = __builtin_nontemporal_load((gu32*)(ch + rs * 1024 + la * 4));
+    R.SA[u] = mx_load_sa<G>(ch, rs, lane, g0);
   }
 }
 
 // Activation operands of the same steps for this lane's column, whose token's
 // terms start at xtok (step xs0 of that token; in LDS when BLDS): column
-// c = lane % 16 is term c % XQ_NT of the lane's token.
-template <int S, bool BLDS, int G = 4>
+// c = lane % 16 is term c % XQ_NT of the lane's token. FLAT (s1 > s0): no
+// branch between the steps' loads -- steps past s1 reload step s1 - 1 -- so a
+// wait for one step's operands need not wait for the later steps'.
+template <int S, bool BLDS, int G = 4, bool FLAT = false>
 __device__ __forceinline__ void mx_load_b_at(MxRegs<S, G>& R, const uint8_t* __restrict__ xtok, int xs0, int s0,
                                              int s1) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
@@ -213,8 +237,8 @@ __device__ __forceinline__ void mx_load_b_at(MxRegs<S, G>& R, const uint8_t* __r
   const uint8_t* xst = xtok + XQ_CODES + (grp * XQ_NT + term) * 4;
 #pragma unroll
   for (int u = 0; u < S; ++u) {
-    const int s = s0 + u;
-    if (s < s1) {
+    const int s = FLAT ? min(s0 + u, s1 - 1) : s0 + u;
+    if (FLAT || s < s1) {
       const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
       if (BLDS) {
         R.B0[u] = *(lv4u*)(xt + xo);
@@ -262,11 +286,10 @@ __device__ __forceinline__ void mx_load_ab(MxRegs<S, G>& R, const uint8_t* __res
     if (s < s1) {
       const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
       const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
-      const bool alane = grp < rs;
-      const int la = alane ? lane : 16 * rs - 1;
+      const int la = grp < rs ? lane : 16 * rs - 1;
 #pragma unroll
       for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
-      R.SA[u] = __builtin_nontemporal_load((gu32*)(ch + rs * 1024 + la * 4));
+      R.SA[u] = mx_load_sa<G>(ch, rs, lane, g0);
       const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
       R.B0[u] = *(gv4u*)(xt + xo);
       R.B1[u] = *(gv4u*)(xt + xo + 16);
@@ -280,13 +303,11 @@ __device__ __forceinline__ void mx_load_ab(MxRegs<S, G>& R, const uint8_t* __res
 template <int S, int G = 4>
 __device__ __forceinline__ void mx_compute(const MxRegs<S, G>& R, const MxGeom& G_, int s0, int s1, v4f (&D)[G],
                                            int g0 = 0) {
-  const int grp = __lane_id() >> 4;
 #pragma unroll
   for (int u = 0; u < S; ++u) {
     const int s = s0 + u;
     if (s >= s1) break;
-    const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
-    const uint32_t sa = grp < rs ? R.SA[u] >> (8 * g0) : 0u;  // byte g: group g0 + g; stand-in lanes scale 0
+    const uint32_t sa = R.SA[u];  // byte g: group g0 + g (stand-in lanes: 0)
     const uint32_t sb = R.SB[u];
     const v8i b = {(int)R.B0[u].x, (int)R.B0[u].y, (int)R.B0[u].z, (int)R.B0[u].w,
                    (int)R.B1[u].x, (int)R.B1[u].y, (int)R.B1[u].z, (int)R.B1[u].w};

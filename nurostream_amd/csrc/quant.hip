@@ -586,7 +586,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
 // Workgroups of `kernel` (`threads` threads, `lds` bytes) resident on the
 // current device at once: CUs x blocks per CU, cached per kernel and LDS size.
 int nsx_resident_workgroups(const void* kernel, size_t lds, int threads) {
-  struct Entry { const void* k; size_t lds; int dev; int n; };
+  struct Entry { const void* k; size_t lds; int threads, dev, n; };
   static std::mutex mu;
   static Entry cache[64];
   static int used = 0;
@@ -594,14 +594,15 @@ int nsx_resident_workgroups(const void* kernel, size_t lds, int threads) {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < used; ++i)
-    if (cache[i].k == kernel && cache[i].lds == lds && cache[i].dev == dev) return cache[i].n;
+    if (cache[i].k == kernel && cache[i].lds == lds && cache[i].threads == threads && cache[i].dev == dev)
+      return cache[i].n;
   int cus = 0, per = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   if (lds > 64 * 1024) (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per <= 0) per = 1;
   (void)hipGetLastError();
   const int n = cus * per;
-  if (used < 64) cache[used++] = Entry{kernel, lds, dev, n};
+  if (used < 64) cache[used++] = Entry{kernel, lds, threads, dev, n};
   return n;
 }
 
