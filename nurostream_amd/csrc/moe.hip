@@ -1933,19 +1933,47 @@ __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
 
 // Grouped Q4_K (several tokens per expert): the same per-(pair, row)
 // arithmetic as the kernels above, with the rows' codes and headers held in
-// registers while the work item's tokens go by one at a time, their
-// activation terms (a8_terms_kernel) read from L2, so an expert's rows are
-// read from HBM once per item.
+// registers while the work item's tokens go by one at a time, so an expert's
+// rows are read from HBM once per item. The tokens' activation terms
+// (a8_terms_kernel) are staged in LDS, Q4K_GROUP_NT tokens at a time, by the
+// whole workgroup with one copy: every wave then reads them from LDS rather
+// than each making its own dependent L2 round trip per token.
+
+constexpr int Q4K_GROUP_NT = 4;  // tokens whose terms are in LDS at a time
 
 // activation terms of the vectors x[v * K .. v * K + K), one workgroup per vector
 __global__ __launch_bounds__(256) void a8_terms_kernel(const float* __restrict__ x, int K, uint8_t* __restrict__ dst) {
   a8_vector(x + (int64_t)blockIdx.x * K, K, dst + (int64_t)blockIdx.x * a8_bytes(K), (int)threadIdx.x, 256);
 }
 
+// The terms of tokens w0 .. w0 + nt - 1 of a work item into xs (xp 16-byte
+// pieces per token), the token of item position w at src(w): all of the
+// workgroup's threads, four pieces each in flight at a time.
+template <typename Src>
+__device__ __forceinline__ void q4k_stage_terms(uint8_t* __restrict__ xs, int w0, int nt, int xp, Src src) {
+  constexpr int B = 4;
+  const int tid = (int)threadIdx.x, nthr = (int)blockDim.x, total = nt * xp;
+  for (int c0 = 0; c0 < total; c0 += B * nthr) {
+    v4u buf[B];
+#pragma unroll
+    for (int i = 0; i < B; ++i) {  // (unpredicated: pieces past the end re-read the last one)
+      const int c = min(c0 + tid + i * nthr, total - 1);
+      const int tk = c / xp;
+      buf[i] = *(const v4u*)(src(w0 + tk) + (int64_t)(c - tk * xp) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int c = c0 + tid + i * nthr;
+      if (c < total) ((v4u*)xs)[c] = buf[i];
+    }
+  }
+}
+
 // gate/up: workgroup = (item, RPG rows); wave = Q4K_GG_STEPS steps of 64 / LPR rows of gate and of up
 template <int LPR>
-__global__ __launch_bounds__(64 * Q4K_GG_WAVES) void moe_gu_q4k_grouped_kernel(MoeDev a) {
+__global__ __launch_bounds__(64 * Q4K_GG_WAVES, 4) void moe_gu_q4k_grouped_kernel(MoeDev a) {  // (4 waves per SIMD: two workgroups per CU)
   constexpr int RS = 64 / LPR, RPG = Q4K_GG_WAVES * Q4K_GG_STEPS * RS;
+  __shared__ __align__(16) uint8_t xs[Q4K_GROUP_NT * a8_bytes(Q4K_KMAX)];
   int grp;
   int4 item;
   if (!grp_work(a, (a.n_ff + RPG - 1) / RPG, grp, item)) return;
@@ -1953,6 +1981,8 @@ __global__ __launch_bounds__(64 * Q4K_GG_WAVES) void moe_gu_q4k_grouped_kernel(M
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int K = a.n_embd, nq = K / 64;
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
+  // the pair list ahead of the rows: loads return in order, and the staging below waits on it
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
   const uint8_t* gm = expert_base(a.gate_base, a.gate_stride, a.gate_ptrs, e);
   const uint8_t* um = expert_base(a.up_base, a.up_stride, a.up_ptrs, e);
   const int q = min(lane % LPR, nq - 1), sub = lane / LPR;
@@ -1968,27 +1998,33 @@ __global__ __launch_bounds__(64 * Q4K_GG_WAVES) void moe_gu_q4k_grouped_kernel(M
     gb[j] = a.gate_bias ? a.gate_bias[(int64_t)e * a.n_ff + row] : 0.f;
     ub[j] = a.up_bias ? a.up_bias[(int64_t)e * a.n_ff + row] : 0.f;
   }
-  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // lane i < 16: the item's token i
-  const int64_t xstride = a8_bytes(K);
+  const int64_t xb = a8_bytes(K);
+  auto src = [&](int w) { return a.xq_h + (int64_t)(__shfl(my_pair, w, 64) / a.top_k) * xb; };
+  for (int w0 = 0; w0 < n; w0 += Q4K_GROUP_NT) {
+    const int nt = min(Q4K_GROUP_NT, n - w0);
+    if (w0 > 0) __syncthreads();  // every wave is done with the previous tokens' terms
+    q4k_stage_terms(xs, w0, nt, (int)(xb / 16), src);
+    __syncthreads();
 #pragma nounroll
-  for (int w = 0; w < n; ++w) {
-    // unpack the codes per token (unpacked codes held across tokens would double
-    // their registers): the empty asm marks them as changed
+    for (int w = 0; w < nt; ++w) {
+      // unpack the codes per token (unpacked codes held across tokens would double
+      // their registers): the empty asm marks them as changed
 #pragma unroll
-    for (int j = 0; j < Q4K_GG_STEPS; ++j)
-      asm volatile("" : "+v"(G[j].c0), "+v"(G[j].c1), "+v"(G[j].hd), "+v"(U[j].c0), "+v"(U[j].c1), "+v"(U[j].hd));
-    const int pr = __builtin_amdgcn_readlane(my_pair, w);
-    A8Pair X;
-    a8_load(a.xq_h + (int64_t)(pr / a.top_k) * xstride, q, nq, X);
+      for (int j = 0; j < Q4K_GG_STEPS; ++j)
+        asm volatile("" : "+v"(G[j].c0), "+v"(G[j].c1), "+v"(G[j].hd), "+v"(U[j].c0), "+v"(U[j].c1), "+v"(U[j].hd));
+      const int pr = __builtin_amdgcn_readlane(my_pair, w0 + w);
+      A8Pair X;
+      a8_load(xs + w * xb, q, nq, X);
 #pragma unroll
-    for (int j = 0; j < Q4K_GG_STEPS; ++j) {
-      float gs = q4k_a8_dot(G[j].c0, G[j].c1, G[j].hd, q & 3, X);
-      float us = q4k_a8_dot(U[j].c0, U[j].c1, U[j].hd, q & 3, X);
-      gs = a8_group_sum<LPR>(live ? gs : 0.f);
-      us = a8_group_sum<LPR>(live ? us : 0.f);
-      const int row = rw + j * RS;
-      if (lane % LPR == 0 && row < a.n_ff)
-        a.act[(int64_t)pr * a.n_ff + row] = moe_act(a.act_kind, gs + gb[j], us + ub[j], a.alpha, a.limit);
+      for (int j = 0; j < Q4K_GG_STEPS; ++j) {
+        float gs = q4k_a8_dot(G[j].c0, G[j].c1, G[j].hd, q & 3, X);
+        float us = q4k_a8_dot(U[j].c0, U[j].c1, U[j].hd, q & 3, X);
+        gs = a8_group_sum<LPR>(live ? gs : 0.f);
+        us = a8_group_sum<LPR>(live ? us : 0.f);
+        const int row = rw + j * RS;
+        if (lane % LPR == 0 && row < a.n_ff)
+          a.act[(int64_t)pr * a.n_ff + row] = moe_act(a.act_kind, gs + gb[j], us + ub[j], a.alpha, a.limit);
+      }
     }
   }
 }
@@ -1999,6 +2035,8 @@ __global__ __launch_bounds__(64 * Q4K_GG_WAVES) void moe_gu_q4k_grouped_kernel(M
 template <int LPR>
 __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
   constexpr int RS = 64 / LPR, RPG = Q4K_DG_WAVES * Q4K_DG_STEPS * RS;
+  extern __shared__ __align__(16) uint8_t q4k_xg[];  // Q4K_GROUP_NT * a8_bytes(n_ff): sized at launch
+  uint8_t* xs = q4k_xg;
   int grp;
   int4 item;
   if (!grp_work(a, (a.n_embd + RPG - 1) / RPG, grp, item)) return;
@@ -2006,6 +2044,7 @@ __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int K = a.n_ff, nq = K / 64;
   const uint32_t rb = (uint32_t)(K / 256) * 144u;
+  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];  // (ahead of the rows, as in the gate/up kernel)
   const uint8_t* dm = expert_base(a.down_base, a.down_stride, a.down_ptrs, e);
   const int q = min(lane % LPR, nq - 1), sub = lane / LPR;
   const bool live = lane % LPR < nq;
@@ -2018,21 +2057,27 @@ __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
     q4k_row_load(dm, row, rb, q, R[j]);
     bias[j] = a.down_bias ? a.down_bias[(int64_t)e * a.n_embd + row] : 0.f;
   }
-  const int my_pair = a.sorted[pos0 + min(lane & 15, n - 1)];
-  const int64_t xstride = a8_bytes(K);
+  const int64_t xb = a8_bytes(K);
+  auto src = [&](int w) { return a.xq_a + (int64_t)__shfl(my_pair, w, 64) * xb; };
+  for (int w0 = 0; w0 < n; w0 += Q4K_GROUP_NT) {
+    const int nt = min(Q4K_GROUP_NT, n - w0);
+    if (w0 > 0) __syncthreads();
+    q4k_stage_terms(xs, w0, nt, (int)(xb / 16), src);
+    __syncthreads();
 #pragma nounroll
-  for (int w = 0; w < n; ++w) {
+    for (int w = 0; w < nt; ++w) {
 #pragma unroll
-    for (int j = 0; j < Q4K_DG_STEPS; ++j) asm volatile("" : "+v"(R[j].c0), "+v"(R[j].c1), "+v"(R[j].hd));
-    const int pr = __builtin_amdgcn_readlane(my_pair, w);
-    A8Pair X;
-    a8_load(a.xq_a + (int64_t)pr * xstride, q, nq, X);
+      for (int j = 0; j < Q4K_DG_STEPS; ++j) asm volatile("" : "+v"(R[j].c0), "+v"(R[j].c1), "+v"(R[j].hd));
+      const int pr = __builtin_amdgcn_readlane(my_pair, w0 + w);
+      A8Pair X;
+      a8_load(xs + w * xb, q, nq, X);
 #pragma unroll
-    for (int j = 0; j < Q4K_DG_STEPS; ++j) {
-      float y = q4k_a8_dot(R[j].c0, R[j].c1, R[j].hd, q & 3, X);
-      y = a8_group_sum<LPR>(live ? y : 0.f);
-      const int row = rw + j * RS;
-      if (lane % LPR == 0 && row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y + bias[j];
+      for (int j = 0; j < Q4K_DG_STEPS; ++j) {
+        float y = q4k_a8_dot(R[j].c0, R[j].c1, R[j].hd, q & 3, X);
+        y = a8_group_sum<LPR>(live ? y : 0.f);
+        const int row = rw + j * RS;
+        if (lane % LPR == 0 && row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y + bias[j];
+      }
     }
   }
 }
@@ -2223,8 +2268,8 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
                                               (uint32_t)(NR * rb));
   const __amdgpu_buffer_rsrc_t rs1 =
       GU ? nsx_rsrc(expert_base(a.up_base, a.up_stride, a.up_ptrs, e), (uint32_t)(NR * rb)) : rs0;
-  // Columns past the item's tokens load the last token's terms (valid
-  // memory); their results are never stored, and MFMA columns are independent.
+  // Columns past the item's tokens compute on zero terms (below); their
+  // results are never stored, and MFMA columns are independent.
   const bool tv = lr < n;
   const int pr = a.sorted[pos0 + min(lr, n - 1)];
   const int64_t brow = GU ? pr / a.top_k : pr;
@@ -2233,31 +2278,46 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   // terms rows: GU one per token (T), else one per pair (T * top_k)
   const __amdgpu_buffer_rsrc_t rt = nsx_rsrc(tbase, (uint32_t)((int64_t)(GU ? a.T : a.T * a.top_k) * tb));
   // the lane's token row; lane group g takes, in each super-block, elements
-  // 64 p + 32 hi + 16 (g & 1) + 0..15 of pairs p = g / 2 and 2 + g / 2
-  const uint32_t tv_off = (uint32_t)(brow * tb) + 2u * (64u * (uint32_t)(g >> 1) + 16u * (uint32_t)(g & 1));
-  const uint32_t ts_off = (uint32_t)(brow * tb);
-  // Weights are double-buffered: a super-block's activation terms (L2) are
-  // loaded first, then the next super-block's weights (HBM), so waiting for
-  // the terms does not wait for the prefetch (loads complete in order).
+  // 64 p + 32 hi + 16 (g & 1) + 0..15 of pairs p = g / 2 and 2 + g / 2.
+  // Lanes of columns past the item's tokens get an offset past the buffer's
+  // end: their term loads return zeros without a memory access (an item
+  // averages a few tokens, and the terms of all 16 columns would otherwise
+  // be several times the weight bytes through the load path).
+  const uint32_t oob = 0x80000000u;
+  const uint32_t tv_off = tv ? (uint32_t)(brow * tb) + 2u * (64u * (uint32_t)(g >> 1) + 16u * (uint32_t)(g & 1)) : oob;
+  const uint32_t ts_off = tv ? (uint32_t)(brow * tb) : oob;
+  // Weights are triple-buffered: a super-block's activation terms (L2) are
+  // loaded first, then the weights of the super-block two ahead (HBM), so
+  // waiting for the terms does not wait for the prefetch (loads complete in
+  // order); two super-blocks in flight per wave keep enough bytes in flight
+  // per CU at the two waves per SIMD these registers allow.
   // lane group g reads code bytes 16 g .. + 15 and 64 + 16 g .. + 15, so each
   // load instruction covers 64 contiguous bytes of a row
   struct W {
     v4u H0, H1, A0, B0, A1, B1;
   };
+  // The lane's offsets stay in registers for the whole loop and a super-block
+  // goes in the scalar offset, so no address register is rewritten while an
+  // earlier prefetch is in flight (rewriting one waits for that load). The
+  // prefetches past the last super-block go through a zero-length resource:
+  // they return zeros without a memory access, and the loop needs no branch.
+  const uint32_t qa_off = arow_off + 16u + 16u * (uint32_t)g, qa1_off = arow1_off + 16u + 16u * (uint32_t)g;
+  const __amdgpu_buffer_rsrc_t rnull = nsx_rsrc(tbase, 0u);
   auto load_w = [&](int sb, W& o) {
-    const uint32_t b = arow_off + (uint32_t)sb * 144u, q = b + 16u + 16u * (uint32_t)g;
-    o.H0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, b, 0, 0));
-    o.A0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q, 0, 0));
-    o.B0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q + 64u, 0, 0));
+    const bool in = sb < nsb;
+    const __amdgpu_buffer_rsrc_t r0 = in ? rs0 : rnull, r1 = in ? rs1 : rnull;
+    const int so = in ? sb * 144 : 0;
+    o.H0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r0, arow_off, so, 0));
+    o.A0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r0, qa_off, so, 0));
+    o.B0 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r0, qa_off + 64u, so, 0));
     if constexpr (GU) {
-      o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, b, 0, 0));
-      o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q, 0, 0));
-      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs1, q + 64u, 0, 0));
+      o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r1, arow_off, so, 0));
+      o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r1, qa_off, so, 0));
+      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r1, qa_off + 64u, so, 0));
     } else {  // the second row tile
-      const uint32_t b1 = arow1_off + (uint32_t)sb * 144u, q1 = b1 + 16u + 16u * (uint32_t)g;
-      o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, b1, 0, 0));
-      o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q1, 0, 0));
-      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs0, q1 + 64u, 0, 0));
+      o.H1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r0, arow1_off, so, 0));
+      o.A1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r0, qa1_off, so, 0));
+      o.B1 = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r0, qa1_off + 64u, so, 0));
     }
   };
   mq_f4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
@@ -2276,18 +2336,27 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
     const mq_h8 SH = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + 16 * sb, 0));
     const mq_h8 SL =
         __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
-    if (sb + 1 < nsb) load_w(sb + 1, nxt);
+    load_w(sb + 2, nxt);
+    // every load of the step goes out before the first MFMA waits on one, and the
+    // step's compute stays between its loads and the next step's (left to itself
+    // the scheduler spreads the term loads among the MFMAs, each wait then an L2
+    // round trip, and issues the prefetch after most of the step's compute)
+    __builtin_amdgcn_sched_barrier(0);
     mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
     mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
+    __builtin_amdgcn_sched_barrier(0);
   };
-  W wa, wb;
-  load_w(0, wa);
-  int sb = 0;
-  for (; sb + 1 < nsb; sb += 2) {
-    step(sb, wa, wb);
-    step(sb + 1, wb, wa);
+  W w0, w1, w2;
+  load_w(0, w0);
+  load_w(1, w1);
+  for (int sb = 0;;) {  // step sb computes super-block sb and requests sb + 2 into the buffer sb - 1 used
+    step(sb, w0, w2);
+    if (++sb >= nsb) break;
+    step(sb, w1, w0);
+    if (++sb >= nsb) break;
+    step(sb, w2, w1);
+    if (++sb >= nsb) break;
   }
-  if (sb < nsb) step(sb, wa, wb);
   const float scale = *(const float*)(tbase + brow * tb + 4 * K + K / 8);  // 2^e of this column's terms
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -2657,7 +2726,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         rc = with_q4k_lpr(L->n_ff, [&](auto lpr) {
           constexpr int LPR = decltype(lpr)::value;
           const int64_t g = nsx_cdiv(L->n_embd, Q4K_DG_WAVES * Q4K_DG_STEPS * (64 / LPR));
-          return nsx_launch(moe_down_q4k_grouped_kernel<LPR>, grid8(g), dim3(64 * Q4K_DG_WAVES), 0, st, d);
+          return nsx_launch(moe_down_q4k_grouped_kernel<LPR>, grid8(g), dim3(64 * Q4K_DG_WAVES),
+                            (size_t)(Q4K_GROUP_NT * a8_bytes(L->n_ff)), st, d);
         });
       }
       if (rc) return rc;
