@@ -1947,12 +1947,14 @@ __global__ __launch_bounds__(256) void a8_terms_kernel(const float* __restrict__
 }
 
 // The terms of tokens w0 .. w0 + nt - 1 of a work item into xs (xp 16-byte
-// pieces per token), the token of item position w at src(w): all of the
-// workgroup's threads, four pieces each in flight at a time.
+// pieces per token, xps pieces apart in LDS), the token of item position w at
+// src(w): all of the workgroup's threads, four pieces each in flight at a time.
 template <typename Src>
-__device__ __forceinline__ void q4k_stage_terms(uint8_t* __restrict__ xs, int w0, int nt, int xp, Src src) {
+__device__ __forceinline__ void q4k_stage_terms(uint8_t* __restrict__ xs, int w0, int nt, int xp, Src src,
+                                                int xps = 0) {  // xps: LDS pieces per token (>= xp; 0: xp)
   constexpr int B = 4;
   const int tid = (int)threadIdx.x, nthr = (int)blockDim.x, total = nt * xp;
+  xps = xps > 0 ? xps : xp;
   for (int c0 = 0; c0 < total; c0 += B * nthr) {
     v4u buf[B];
 #pragma unroll
@@ -1964,7 +1966,8 @@ __device__ __forceinline__ void q4k_stage_terms(uint8_t* __restrict__ xs, int w0
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const int c = c0 + tid + i * nthr;
-      if (c < total) ((v4u*)xs)[c] = buf[i];
+      const int tk = c / xp;
+      if (c < total) ((v4u*)xs)[tk * xps + (c - tk * xp)] = buf[i];
     }
   }
 }
@@ -2104,6 +2107,7 @@ __global__ __launch_bounds__(256) void moe_down_q4k_grouped_kernel(MoeDev a) {
 
 constexpr int MQ_ROWS = 16;  // rows per wave (one MFMA tile)
 constexpr int MQ_WG_ROWS = 64;
+constexpr int MQ_LDS_NT = 4;  // items of up to this many tokens keep their activation terms in LDS
 
 typedef _Float16 mq_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mq_h2 __attribute__((ext_vector_type(2)));
@@ -2244,6 +2248,7 @@ __device__ __forceinline__ void mq_superblock(const v4u& H, const v4u& QA, const
 // Workgroup = (item, 64 rows), wave = 16 rows over all of K.
 template <bool GU>
 __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
+  extern __shared__ __align__(16) uint8_t mq_xs[];  // MQ_LDS_NT * (mq_row_bytes(K) + 16): sized at launch
   const int NR = GU ? a.n_ff : a.n_embd, K = GU ? a.n_embd : a.n_ff;
   int tile;
   int4 item;
@@ -2255,8 +2260,9 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int lr = lane & 15, g = lane >> 4;
   const int r0 = (tile * MQ_WG_ROWS + wave * MQ_ROWS) * TILES;
-  if (r0 >= NR) return;  // no barriers below
   const int e = clamp_expert(item.x, a.E), pos0 = item.y, n = item.z;
+  // (a wave past the last row still takes part in the LDS staging and its barrier)
+  if (r0 >= NR && n > MQ_LDS_NT) return;
   const int nsb = K / 256;
   const int64_t rb = (int64_t)nsb * 144;
   // weights through buffer loads (an expert matrix: NR rows of rb bytes), so
@@ -2321,42 +2327,78 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
     }
   };
   mq_f4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
-  auto step = [&](int sb, const W& cur, W& nxt) {
-    mq_h8 BH[8], BL[8];
-    const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
+  // Items of up to MQ_LDS_NT tokens (the common case at a few tokens per
+  // expert): the workgroup copies the tokens' whole term rows into LDS once,
+  // and the super-block loop reads its terms from there -- LDS reads are
+  // tracked apart from the weight loads, so nothing waits on a prefetch.
+  // Larger items read each super-block's terms from L2 (through the buffer
+  // loads above).
+  const int tsb = (int)tb + 16;  // LDS bytes per token row (16 bytes of padding: rows start 8 banks apart)
+  const uint8_t* xrow = mq_xs + min(lr, n - 1) * tsb;
+  const int lane_off = 2 * (64 * (g >> 1) + 16 * (g & 1));
+  auto run = [&](auto blds) {
+    constexpr bool BLDS = decltype(blds)::value;
+    auto step = [&](int sb, const W& cur, W& nxt) {
+      mq_h8 BH[8], BL[8];
+      const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: pair (t >> 1) * 2 + g / 2, elements + 32 hi + 8 (t & 1)
-      const int t = s8 & 3;
-      const uint32_t o = tv_off + 2u * (128u * (uint32_t)(t >> 1) + 32u * (uint32_t)(s8 >> 2) + 8u * (uint32_t)(t & 1));
-      BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, o, sh_off, 0));
-      BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, o, sl_off, 0));
+      for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: pair (t >> 1) * 2 + g / 2, elements + 32 hi + 8 (t & 1)
+        const int t = s8 & 3;
+        const uint32_t o = 2u * (128u * (uint32_t)(t >> 1) + 32u * (uint32_t)(s8 >> 2) + 8u * (uint32_t)(t & 1));
+        if constexpr (BLDS) {
+          BH[s8] = *(const mq_h8*)(xrow + lane_off + o + sh_off);
+          BL[s8] = *(const mq_h8*)(xrow + lane_off + o + sl_off);
+        } else {
+          BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + o, sh_off, 0));
+          BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + o, sl_off, 0));
+        }
+      }
+      // sub-block sums after the terms; the min term's A operand is zero outside
+      // k < 8 (g == 0), so every group may load the same sums
+      mq_h8 SH, SL;
+      if constexpr (BLDS) {
+        SH = *(const mq_h8*)(xrow + 4 * K + 16 * sb);
+        SL = *(const mq_h8*)(xrow + 4 * K + K / 16 + 16 * sb);
+      } else {
+        SH = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + 16 * sb, 0));
+        SL = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
+      }
+      load_w(sb + 2, nxt);
+      // every load of the step goes out before the first MFMA waits on one, and the
+      // step's compute stays between its loads and the next step's (left to itself
+      // the scheduler spreads the term loads among the MFMAs, each wait then an L2
+      // round trip, and issues the prefetch after most of the step's compute)
+      __builtin_amdgcn_sched_barrier(0);
+      if (sb < nsb) {  // (the loop below runs whole rounds of three steps)
+        mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
+        mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    W w0, w1, w2;
+    if (r0 < NR) {
+      load_w(0, w0);
+      load_w(1, w1);
     }
-    // sub-block sums after the terms; the min term's A operand is zero outside
-    // k < 8 (g == 0), so every group may load the same sums
-    const mq_h8 SH = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + 16 * sb, 0));
-    const mq_h8 SL =
-        __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
-    load_w(sb + 2, nxt);
-    // every load of the step goes out before the first MFMA waits on one, and the
-    // step's compute stays between its loads and the next step's (left to itself
-    // the scheduler spreads the term loads among the MFMAs, each wait then an L2
-    // round trip, and issues the prefetch after most of the step's compute)
-    __builtin_amdgcn_sched_barrier(0);
-    mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
-    mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (BLDS) {
+      q4k_stage_terms(mq_xs, 0, n, (int)(tb / 16), [&](int w) { return tbase + (int64_t)__shfl(brow, w, 64) * tb; },
+                      tsb / 16);
+      __syncthreads();
+      if (r0 >= NR) return;
+    }
+    // step sb computes super-block sb and requests sb + 2 into the buffer sb - 1 used; one exit, and every
+    // step's loads unconditional, so the wait counts stay exact around the loop
+    for (int sb = 0; sb < nsb; sb += 3) {
+      step(sb, w0, w2);
+      step(sb + 1, w1, w0);
+      step(sb + 2, w2, w1);
+    }
   };
-  W w0, w1, w2;
-  load_w(0, w0);
-  load_w(1, w1);
-  for (int sb = 0;;) {  // step sb computes super-block sb and requests sb + 2 into the buffer sb - 1 used
-    step(sb, w0, w2);
-    if (++sb >= nsb) break;
-    step(sb, w1, w0);
-    if (++sb >= nsb) break;
-    step(sb, w2, w1);
-    if (++sb >= nsb) break;
-  }
+  if (n <= MQ_LDS_NT)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
+  if (r0 >= NR) return;
   const float scale = *(const float*)(tbase + brow * tb + 4 * K + K / 8);  // 2^e of this column's terms
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -2698,7 +2740,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))
           return rc;
-        rc = nsx_launch(moe_q4k_mfma_kernel<true>, grid8(nsx_cdiv(L->n_ff, MQ_WG_ROWS)), dim3(256), 0, st, d);
+        rc = nsx_launch(moe_q4k_mfma_kernel<true>, grid8(nsx_cdiv(L->n_ff, MQ_WG_ROWS)), dim3(256),
+                        (size_t)(MQ_LDS_NT * (mq_row_bytes(L->n_embd) + 16)), st, d);
       } else {  // Q4_K on the int8 dot: the tokens' activation terms, then the rows
         if ((rc = nsx_launch(a8_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))
@@ -2718,7 +2761,8 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
                              (int)L->n_ff, d.xq_a)))
           return rc;
-        rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, 2 * MQ_WG_ROWS)), dim3(256), 0, st, d);
+        rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, 2 * MQ_WG_ROWS)), dim3(256),
+                        (size_t)(MQ_LDS_NT * (mq_row_bytes(L->n_ff) + 16)), st, d);
       } else {
         if ((rc = nsx_launch(a8_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
                              (int)L->n_ff, d.xq_a)))
