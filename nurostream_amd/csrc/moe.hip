@@ -2182,52 +2182,54 @@ __device__ __forceinline__ void mq_a_pair(uint2 q, mq_h2 ml, mq_h2 cl, mq_h2 mh,
   ahi = __builtin_bit_cast(mq_h8, v4u{hi[0], hi[1], hi[2], hi[3]});
 }
 
-// One super-block of one matrix: header H (d | dmin, scales[12]) and the
-// lane's code bytes Q[j] (sub-block pair j) -> y (rows 4 g + i, the lane's
-// token) += d * (sc q . x) - dmin * (m . xsum).
-__device__ __forceinline__ void mq_superblock(const v4u& H, const v4u& QA, const v4u& QB, const mq_h8 (&BH)[8],
-                                              const mq_h8 (&BL)[8], const mq_h8& SH, const mq_h8& SL, int g,
-                                              mq_f4& y) {
-  // get_scale_min_k4 for all 8 sub-blocks at once: byte s of SC / MN (scales
-  // bytes 0-3 = H.y, 4-7 = H.z, 8-11 = H.w)
-  const uint32_t SC03 = H.y & 0x3F3F3F3Fu, MN03 = H.z & 0x3F3F3F3Fu;
+// The A-operand scale factors of one super-block for lane group g (header H:
+// d | dmin, scales[12]): get_scale_min_k4 for all 8 sub-blocks at once, then
+// per half u (sub-block pairs g / 2 and 2 + g / 2) the multipliers of the low
+// (ml, cl) and high (mh, ch) nibbles, and the scales' min words (MN03, MN47).
+struct MqScales {
+  mq_h2 ml[2], mh[2], cl[2], ch[2];
+  uint32_t MN03, MN47;
+};
+__device__ __forceinline__ mq_h2 mq_biased(uint32_t w, uint32_t sel) {  // a byte b under 0x64 is the f16 1024 + b
+  return __builtin_bit_cast(mq_h2, __builtin_amdgcn_perm(0x64646464u, w, sel));
+}
+__device__ __forceinline__ MqScales mq_scales(const v4u& H, int g) {
+  // scales bytes 0-3 = H.y, 4-7 = H.z, 8-11 = H.w
+  const uint32_t SC03 = H.y & 0x3F3F3F3Fu;
   const uint32_t SC47 = (H.w & 0x0F0F0F0Fu) | ((H.y >> 2) & 0x30303030u);
-  const uint32_t MN47 = ((H.w >> 4) & 0x0F0F0F0Fu) | ((H.z >> 2) & 0x30303030u);
-  // a byte b under 0x64 is the f16 1024 + b
-  auto biased = [](uint32_t w, uint32_t sel) { return __builtin_bit_cast(mq_h2, __builtin_amdgcn_perm(0x64646464u, w, sel)); };
+  MqScales S;
+  S.MN03 = H.z & 0x3F3F3F3Fu;
+  S.MN47 = ((H.w >> 4) & 0x0F0F0F0Fu) | ((H.z >> 2) & 0x30303030u);
   const mq_h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f}, km1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
   const mq_h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, km64 = {(_Float16)-64.f, (_Float16)-64.f};
   // lane group g holds half (g & 1) of sub-block pairs g / 2 (QA) and
   // 2 + g / 2 (QB): their scales (pair p = sub-blocks 2p, 2p + 1)
   const uint32_t blo = 2u * (uint32_t)(g >> 1), bhi = blo + 1u;  // bytes of pair g / 2 in SC03, of pair 2 + g / 2 in SC47
   const uint32_t sel_lo = 0x04000400u | (blo << 16) | blo, sel_hi = 0x04000400u | (bhi << 16) | bhi;
-  mq_h2 ml[2], mh[2], cl[2], ch[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const uint32_t SCW = u == 0 ? SC03 : SC47;
-    ml[u] = biased(SCW, sel_lo) - k1024;
-    mh[u] = __builtin_elementwise_fma(biased(SCW, sel_hi), k16, km64);
-    cl[u] = ml[u] * km1024;
-    ch[u] = mh[u] * km1024;
+    S.ml[u] = mq_biased(SCW, sel_lo) - k1024;
+    S.mh[u] = __builtin_elementwise_fma(mq_biased(SCW, sel_hi), k16, km64);
+    S.cl[u] = S.ml[u] * km1024;
+    S.ch[u] = S.mh[u] * km1024;
   }
-  mq_f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {  // t < 2: QA's bytes 8t .., t >= 2: QB's bytes 8 (t - 2) ..
-    const uint2 q8 = t == 0 ? uint2{QA.x, QA.y} : t == 1 ? uint2{QA.z, QA.w} : t == 2 ? uint2{QB.x, QB.y}
-                                                                                     : uint2{QB.z, QB.w};
-    const int u = t >> 1;
-    mq_h8 alo, ahi;
-    mq_a_pair(q8, ml[u], cl[u], mh[u], ch[u], alo, ahi);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[t], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[t], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[4 + t], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BL[4 + t], acc, 0, 0, 0);
-  }
-  // A2 row = the 8 sub-block mins at k 0..7 (group 0), zero elsewhere
-  const uint32_t m01 = __builtin_bit_cast(uint32_t, biased(MN03, 0x04010400u) - k1024);
-  const uint32_t m23 = __builtin_bit_cast(uint32_t, biased(MN03, 0x04030402u) - k1024);
-  const uint32_t m45 = __builtin_bit_cast(uint32_t, biased(MN47, 0x04010400u) - k1024);
-  const uint32_t m67 = __builtin_bit_cast(uint32_t, biased(MN47, 0x04030402u) - k1024);
+  return S;
+}
+
+// code bytes 8t .. 8t + 7 of the lane's 32 (t < 2: QA's, else QB's)
+__device__ __forceinline__ uint2 mq_codes(const v4u& QA, const v4u& QB, int t) {
+  return t == 0 ? uint2{QA.x, QA.y} : t == 1 ? uint2{QA.z, QA.w} : t == 2 ? uint2{QB.x, QB.y} : uint2{QB.z, QB.w};
+}
+
+// the sub-block mins' MFMA (A2 row = the 8 mins at k 0..7, group 0; zero elsewhere) and y += d acc - dmin am
+__device__ __forceinline__ void mq_finish(const v4u& H, const MqScales& S, const mq_f4& acc, const mq_h8& SH,
+                                          const mq_h8& SL, int g, mq_f4& y) {
+  const mq_h2 k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+  const uint32_t m01 = __builtin_bit_cast(uint32_t, mq_biased(S.MN03, 0x04010400u) - k1024);
+  const uint32_t m23 = __builtin_bit_cast(uint32_t, mq_biased(S.MN03, 0x04030402u) - k1024);
+  const uint32_t m45 = __builtin_bit_cast(uint32_t, mq_biased(S.MN47, 0x04010400u) - k1024);
+  const uint32_t m67 = __builtin_bit_cast(uint32_t, mq_biased(S.MN47, 0x04030402u) - k1024);
   const mq_h8 A2 = __builtin_bit_cast(mq_h8, g == 0 ? v4u{m01, m23, m45, m67} : v4u{0u, 0u, 0u, 0u});
   mq_f4 am = {0.f, 0.f, 0.f, 0.f};
   am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, SH, am, 0, 0, 0);
@@ -2242,12 +2244,67 @@ __device__ __forceinline__ void mq_superblock(const v4u& H, const v4u& QA, const
   }
 }
 
+// One super-block of one matrix: header H (d | dmin, scales[12]) and the
+// lane's code bytes Q[j] (sub-block pair j) -> y (rows 4 g + i, the lane's
+// token) += d * (sc q . x) - dmin * (m . xsum).
+__device__ __forceinline__ void mq_superblock(const v4u& H, const v4u& QA, const v4u& QB, const mq_h8 (&BH)[8],
+                                              const mq_h8 (&BL)[8], const mq_h8& SH, const mq_h8& SL, int g,
+                                              mq_f4& y) {
+  const MqScales S = mq_scales(H, g);
+  mq_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {  // t < 2: QA's bytes 8t .., t >= 2: QB's bytes 8 (t - 2) ..
+    const int u = t >> 1;
+    mq_h8 alo, ahi;
+    mq_a_pair(mq_codes(QA, QB, t), S.ml[u], S.cl[u], S.mh[u], S.ch[u], alo, ahi);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BH[t], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, BL[t], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BH[4 + t], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, BL[4 + t], acc, 0, 0, 0);
+  }
+  mq_finish(H, S, acc, SH, SL, g, y);
+}
+
+// The same for two matrices (gate and up, or two row tiles) over activation
+// terms in LDS: each quarter t's four term operands are read just before its
+// MFMAs (xb: the lane's terms of this super-block, hi at xb, lo at xb + lo_off;
+// xs: the super-block's sub-block sums, lo at xs + slo_off), so 16 term
+// registers are live rather than 72. Each matrix's MFMAs run in the order of
+// mq_superblock: the results are the same bits.
+__device__ __forceinline__ void mq_superblock2_lds(const v4u& H0, const v4u& QA0, const v4u& QB0, const v4u& H1,
+                                                   const v4u& QA1, const v4u& QB1, const uint8_t* xb, int lo_off,
+                                                   const uint8_t* xs, int slo_off, int g, mq_f4& y0, mq_f4& y1) {
+  const MqScales S0 = mq_scales(H0, g), S1 = mq_scales(H1, g);
+  mq_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int u = t >> 1;
+    const int o = 2 * (128 * (t >> 1) + 8 * (t & 1));  // element offset of s8 = t (hi: + 32 elements)
+    const mq_h8 bh = *(const mq_h8*)(xb + o), bl = *(const mq_h8*)(xb + lo_off + o);
+    const mq_h8 bh4 = *(const mq_h8*)(xb + o + 64), bl4 = *(const mq_h8*)(xb + lo_off + o + 64);
+    mq_h8 alo, ahi;
+    mq_a_pair(mq_codes(QA0, QB0, t), S0.ml[u], S0.cl[u], S0.mh[u], S0.ch[u], alo, ahi);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bh, acc0, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bl, acc0, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bh4, acc0, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bl4, acc0, 0, 0, 0);
+    mq_a_pair(mq_codes(QA1, QB1, t), S1.ml[u], S1.cl[u], S1.mh[u], S1.ch[u], alo, ahi);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bh, acc1, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bl, acc1, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bh4, acc1, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bl4, acc1, 0, 0, 0);
+  }
+  const mq_h8 SH = *(const mq_h8*)xs, SL = *(const mq_h8*)(xs + slo_off);
+  mq_finish(H0, S0, acc0, SH, SL, g, y0);
+  mq_finish(H1, S1, acc1, SH, SL, g, y1);
+}
+
 // GU: gate and up rows (n_ff) over h's terms, then the activation into act;
 // else: down rows (n_embd) over the pairs' activation terms, plus the bias,
 // into y (moe_combine_kernel adds a token's pairs in ascending expert id).
 // Workgroup = (item, 64 rows), wave = 16 rows over all of K.
 template <bool GU>
-__global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
+__global__ __launch_bounds__(256, 3) void moe_q4k_mfma_kernel(MoeDev a) {  // (three waves per SIMD)
   extern __shared__ __align__(16) uint8_t mq_xs[];  // MQ_LDS_NT * (mq_row_bytes(K) + 16): sized at launch
   const int NR = GU ? a.n_ff : a.n_embd, K = GU ? a.n_embd : a.n_ff;
   int tile;
@@ -2292,11 +2349,11 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   const uint32_t oob = 0x80000000u;
   const uint32_t tv_off = tv ? (uint32_t)(brow * tb) + 2u * (64u * (uint32_t)(g >> 1) + 16u * (uint32_t)(g & 1)) : oob;
   const uint32_t ts_off = tv ? (uint32_t)(brow * tb) : oob;
-  // Weights are triple-buffered: a super-block's activation terms (L2) are
-  // loaded first, then the weights of the super-block two ahead (HBM), so
-  // waiting for the terms does not wait for the prefetch (loads complete in
-  // order); two super-blocks in flight per wave keep enough bytes in flight
-  // per CU at the two waves per SIMD these registers allow.
+  // Weights are requested AHEAD super-blocks ahead of the one computed,
+  // after that super-block's activation terms, so waiting for the terms does
+  // not wait for the prefetch (loads complete in order); several super-blocks
+  // in flight per wave keep enough bytes in flight per CU at the two waves per
+  // SIMD these registers allow.
   // lane group g reads code bytes 16 g .. + 15 and 64 + 16 g .. + 15, so each
   // load instruction covers 64 contiguous bytes of a row
   struct W {
@@ -2338,60 +2395,62 @@ __global__ __launch_bounds__(256) void moe_q4k_mfma_kernel(MoeDev a) {
   const int lane_off = 2 * (64 * (g >> 1) + 16 * (g & 1));
   auto run = [&](auto blds) {
     constexpr bool BLDS = decltype(blds)::value;
+    // weights requested AHEAD super-blocks ahead: two from LDS terms; one for the larger items, whose 72
+    // registers of terms per super-block leave no room for more at three waves per SIMD
+    constexpr int AHEAD = BLDS ? 2 : 1;
     auto step = [&](int sb, const W& cur, W& nxt) {
-      mq_h8 BH[8], BL[8];
-      const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
+      if constexpr (BLDS) {
+        // the terms from LDS inside the compute (their waits are LDS waits, apart from the weights')
+        load_w(sb + AHEAD, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        if (sb < nsb)  // (the loop below runs whole rounds of steps)
+          mq_superblock2_lds(cur.H0, cur.A0, cur.B0, cur.H1, cur.A1, cur.B1, xrow + lane_off + sb * 512, 2 * K,
+                             xrow + 4 * K + 16 * sb, K / 16, g, y0, y1);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        mq_h8 BH[8], BL[8];
+        const int sh_off = sb * 512, sl_off = 2 * K + sb * 512;  // hi[K] then lo[K], f16
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: pair (t >> 1) * 2 + g / 2, elements + 32 hi + 8 (t & 1)
-        const int t = s8 & 3;
-        const uint32_t o = 2u * (128u * (uint32_t)(t >> 1) + 32u * (uint32_t)(s8 >> 2) + 8u * (uint32_t)(t & 1));
-        if constexpr (BLDS) {
-          BH[s8] = *(const mq_h8*)(xrow + lane_off + o + sh_off);
-          BL[s8] = *(const mq_h8*)(xrow + lane_off + o + sl_off);
-        } else {
+        for (int s8 = 0; s8 < 8; ++s8) {  // s8 = 4 hi + t: pair (t >> 1) * 2 + g / 2, elements + 32 hi + 8 (t & 1)
+          const int t = s8 & 3;
+          const uint32_t o = 2u * (128u * (uint32_t)(t >> 1) + 32u * (uint32_t)(s8 >> 2) + 8u * (uint32_t)(t & 1));
           BH[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + o, sh_off, 0));
           BL[s8] = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, tv_off + o, sl_off, 0));
         }
+        // sub-block sums after the terms; the min term's A operand is zero outside
+        // k < 8 (g == 0), so every group may load the same sums
+        const mq_h8 SH = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + 16 * sb, 0));
+        const mq_h8 SL =
+            __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
+        load_w(sb + AHEAD, nxt);
+        // every load of the step goes out before the first MFMA waits on one, and the
+        // step's compute stays between its loads and the next step's (left to itself
+        // the scheduler spreads the term loads among the MFMAs, each wait then an L2
+        // round trip, and issues the prefetch after most of the step's compute)
+        __builtin_amdgcn_sched_barrier(0);
+        if (sb < nsb) {  // (the loop below runs whole rounds of steps)
+          mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
+          mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // sub-block sums after the terms; the min term's A operand is zero outside
-      // k < 8 (g == 0), so every group may load the same sums
-      mq_h8 SH, SL;
-      if constexpr (BLDS) {
-        SH = *(const mq_h8*)(xrow + 4 * K + 16 * sb);
-        SL = *(const mq_h8*)(xrow + 4 * K + K / 16 + 16 * sb);
-      } else {
-        SH = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + 16 * sb, 0));
-        SL = __builtin_bit_cast(mq_h8, __builtin_amdgcn_raw_buffer_load_b128(rt, ts_off, 4 * K + K / 16 + 16 * sb, 0));
-      }
-      load_w(sb + 2, nxt);
-      // every load of the step goes out before the first MFMA waits on one, and the
-      // step's compute stays between its loads and the next step's (left to itself
-      // the scheduler spreads the term loads among the MFMAs, each wait then an L2
-      // round trip, and issues the prefetch after most of the step's compute)
-      __builtin_amdgcn_sched_barrier(0);
-      if (sb < nsb) {  // (the loop below runs whole rounds of three steps)
-        mq_superblock(cur.H0, cur.A0, cur.B0, BH, BL, SH, SL, g, y0);
-        mq_superblock(cur.H1, cur.A1, cur.B1, BH, BL, SH, SL, g, y1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
     };
-    W w0, w1, w2;
+    W w[AHEAD + 1];
     if (r0 < NR) {
-      load_w(0, w0);
-      load_w(1, w1);
+#pragma unroll
+      for (int j = 0; j < AHEAD; ++j) load_w(j, w[j]);
     }
     if constexpr (BLDS) {
       q4k_stage_terms(mq_xs, 0, n, (int)(tb / 16), [&](int w) { return tbase + (int64_t)__shfl(brow, w, 64) * tb; },
                       tsb / 16);
       __syncthreads();
-      if (r0 >= NR) return;
     }
-    // step sb computes super-block sb and requests sb + 2 into the buffer sb - 1 used; one exit, and every
-    // step's loads unconditional, so the wait counts stay exact around the loop
-    for (int sb = 0; sb < nsb; sb += 3) {
-      step(sb, w0, w2);
-      step(sb + 1, w1, w0);
-      step(sb + 2, w2, w1);
+    if (r0 >= NR) return;
+    // step sb computes super-block sb and requests sb + AHEAD into the buffer sb - 1 used; one exit, and
+    // every step's loads unconditional, so the wait counts stay exact around the loop
+    for (int sb = 0; sb < nsb; sb += AHEAD + 1) {
+#pragma unroll
+      for (int j = 0; j <= AHEAD; ++j) step(sb + j, w[j], w[(j + AHEAD) % (AHEAD + 1)]);
     }
   };
   if (n <= MQ_LDS_NT)
