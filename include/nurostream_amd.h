@@ -99,6 +99,16 @@ int nsx_fused_gemv(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
 int nsx_fused_gemv_ex(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
                       const void *x, int x_dtype, int64_t T, float *y, const float *bias,
                       const float *resid, void *stream);
+/* nsx_fused_gemv_ex for one token whose input is the block norm of the
+ * residual stream: y = resid + (W . h + bias) with h = rms_norm(x + r) * w,
+ * the rms_norm of compute/ops.py:14-20 ahead of the QKV linear
+ * (model/gpt_oss.py:101-114) or the LM head (model/gpt_oss.py:207-228), in
+ * the bits nsx_add_rmsnorm gives h -- one launch instead of two. x, r, w: K
+ * floats (r, w optional), x 16-byte aligned, K <= 4096; s (optional) receives
+ * x + r and must not be x or r. */
+int nsx_fused_gemv_norm(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
+                        const float *x, const float *r, const float *w, float eps, float *s,
+                        float *y, const float *bias, const float *resid, void *stream);
 
 /* 64-row interleaved tiles for VRAM-resident expert slabs. No reference
  * counterpart: residency/cache.py:369-389 admit_slab keeps the raw bytes;

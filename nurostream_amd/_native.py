@@ -63,6 +63,7 @@ _SIGS = {
     "nsx_dequantize": (_i, [_i, _p, _i64, _i64, _p, _i, _p]),
     "nsx_fused_gemv": (_i, [_i, _p, _i64, _i64, _p, _i, _i64, _p, _p]),
     "nsx_fused_gemv_ex": (_i, [_i, _p, _i64, _i64, _p, _i, _i64, _p, _p, _p, _p]),
+    "nsx_fused_gemv_norm": (_i, [_i, _p, _i64, _i64, _p, _p, _p, C.c_float, _p, _p, _p, _p, _p]),
     "nsx_t64_bytes": (_i64, [_i, _i64, _i64]),
     "nsx_t64_pack": (_i, [_i, _p, _i64, _i64, _p, _p]),
     "nsx_t64_unpack": (_i, [_i, _p, _i64, _i64, _p, _p]),

@@ -115,6 +115,44 @@ def can_fuse(dtype, x: torch.Tensor) -> bool:
     return True
 
 
+def fused_gemv_norm(raw, dtype, x: torch.Tensor, r: torch.Tensor | None, weight: torch.Tensor | None, eps: float,
+                    n_rows: int, K: int, sum_out: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                    resid: torch.Tensor | None = None) -> torch.Tensor:
+    """One token's y = W . rms_norm(x + r) * weight (+ bias, + resid) -> (1, n_rows) fp32, the norm in the
+    GEMV's prologue with the bits add_rms_norm gives it (one launch instead of two); with sum_out, x + r is
+    written there too (sum_out must not be x or r). Raw GGUF rows; x, r, weight: K fp32 values."""
+    dtype = GGMLType(dtype)
+    if dtype not in N.BLOCK_TYPES:
+        raise KeyError(dtype)
+    if raw.dtype != torch.uint8:
+        raise TypeError(f"expected uint8 byte buffer, got {raw.dtype}")
+    N.require_device(raw)
+    be, bb = TYPE_LAYOUT[dtype]
+    flat = raw.reshape(-1)
+    if flat.numel() < n_rows * (K // be) * bb:
+        raise ValueError(f"raw has {flat.numel()} bytes, {n_rows} x {K} {dtype.name} needs {n_rows * (K // be) * bb}")
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    vec = {"x": (x, K), "r": (r, K), "weight": (weight, K), "sum_out": (sum_out, K), "bias": (bias, n_rows),
+           "resid": (resid, n_rows)}
+    for name, (t, n) in vec.items():
+        if t is not None and (not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != n):
+            raise ValueError(f"{name} must be a contiguous fp32 device tensor of {n} elements")
+    if x.data_ptr() % 16:
+        raise ValueError("x must be 16-byte aligned")
+    if sum_out is not None and (sum_out.data_ptr() == x.data_ptr() or (r is not None and sum_out.data_ptr() == r.data_ptr())):
+        raise ValueError("sum_out must not be x or r")
+    y = torch.empty((1, n_rows), dtype=torch.float32, device=x.device)
+    if n_rows == 0:
+        return y
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    with torch.cuda.device(x.device):
+        N.check(N.load().nsx_fused_gemv_norm(int(dtype), flat.data_ptr(), n_rows, K, x.data_ptr(), ptr(r),
+                                             ptr(weight), float(eps), ptr(sum_out), y.data_ptr(), ptr(bias),
+                                             ptr(resid), N.stream_ptr(x.device)), "fused_gemv_norm")
+    return y
+
+
 def fused_gemv(raw, dtype, x: torch.Tensor, n_rows: int, K: int,
                out_dtype: torch.dtype = torch.float16, block_n: int = 16,
                num_warps: int = 2, bias: torch.Tensor | None = None,

@@ -402,11 +402,28 @@ struct RawXSumReg {
 // XREG (one token, K <= 4096, so one chunk per row): each lane's two units
 // are the same for every row, so their activations are read from LDS once
 // into registers instead of once per row.
-template <int FMT, int NT, bool XREG, int WAVES = GV_WAVES>
+// The one-token GEMV's input as the residual stream of a block (NORM):
+// h = rms_norm(x + r) * w (compute/ops.py:14-20), computed in the prologue the
+// way add_rmsnorm_kernel computes it -- 256 threads, thread i holding elements
+// i, i + 256, ..., the same sum order -- so h has the bits of that launch,
+// which this replaces. The first workgroup writes x + r to s (when r and s are
+// set).
+struct GvNorm {
+  const float* r;  // added to x (null: none)
+  const float* w;  // norm weight (null: none)
+  float eps;
+  float* s;        // x + r out (null: not written); must not overlap x or r
+};
+constexpr int GV_NORM_MAXV = 16;  // values per thread (K <= 4096)
+
+template <int FMT, int NT, bool XREG, int WAVES = GV_WAVES, bool NORM = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
     const uint8_t* __restrict__ base, uint32_t head, uint32_t range, int n_rows, int K,
     const void* __restrict__ x, int x_dtype, int T, float* __restrict__ y, int64_t ystride,
-    const float* __restrict__ bias, const float* resid) {  // resid may be y (read, then written, per element)
+    const float* __restrict__ bias, const float* resid,  // resid may be y (read, then written, per element)
+    GvNorm nm = GvNorm{}) {
+  static_assert(!NORM || (XREG && WAVES * 64 == 256), "the norm prologue is the one-token 256-thread path's");
+  __shared__ float gv_part[NORM ? WAVES : 1];
   using C = GvChunk<FMT>;
   constexpr int BE = RawBlock<FMT>::BE, BB = RawBlock<FMT>::BB;
   extern __shared__ __align__(16) uint8_t gv_smem[];
@@ -478,22 +495,66 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
     // compiler wait for every load before it): the rows' first item is
     // always issued (a wave past the last row reads clamped, in-range bytes
     // it never uses) and the second one repeats the first when there is none.
-    const int nq = K >> 2;  // <= XQ * THREADS
-    v4f xv[XQ];
-#pragma unroll
-    for (int g = 0; g < XQ; ++g) xv[g] = ((const v4f*)x)[min((int)threadIdx.x + g * THREADS, nq - 1)];
-    issue(0, S0);
-    if constexpr (GV_DEPTH > 1) issue(nitems > 1 ? 1 : 0, S1);
-#pragma unroll
-    for (int g = 0; g < XQ; ++g) {
-      const int q = (int)threadIdx.x + g * THREADS;
-      if (q < nq) *(v4f*)(xs + GV_XPAD * (q >> 3) + 4 * (q & 7)) = xv[g];
-    }
     // LDS barrier without a memory-counter wait: lgkmcnt(0) (this wave's LDS
     // writes are done), then s_barrier; the memory clobber keeps the compiler
     // from moving the LDS reads above it. The row loads stay in flight.
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    asm volatile("s_barrier" ::: "memory");
+    auto lds_barrier = []() {
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      asm volatile("s_barrier" ::: "memory");
+    };
+    if constexpr (NORM) {
+      // x (+ r) and the norm weights in add_rmsnorm_kernel's layout, every load unpredicated (clamped, tails
+      // zeroed at use); the rows go out behind them
+      const float* xf = (const float*)x;
+      float v[GV_NORM_MAXV], wv[GV_NORM_MAXV];
+#pragma unroll
+      for (int i = 0; i < GV_NORM_MAXV; ++i) {
+        const int c = min((int)threadIdx.x + i * 256, K - 1);
+        v[i] = xf[c];
+        wv[i] = nm.w ? nm.w[c] : 1.f;
+      }
+      if (nm.r) {
+#pragma unroll
+        for (int i = 0; i < GV_NORM_MAXV; ++i) v[i] += nm.r[min((int)threadIdx.x + i * 256, K - 1)];
+      }
+      issue(0, S0);
+      if constexpr (GV_DEPTH > 1) issue(nitems > 1 ? 1 : 0, S1);
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < GV_NORM_MAXV; ++i) {
+        if ((int)threadIdx.x + i * 256 >= K) v[i] = 0.f;
+        ss = fmaf(v[i], v[i], ss);
+      }
+      ss = nsx_wave_sum(ss);
+      if (lane == 0) gv_part[wave] = ss;
+      lds_barrier();
+      float tot = 0.f;
+#pragma unroll
+      for (int i = 0; i < WAVES; ++i) tot += gv_part[i];
+      const float inv = 1.f / sqrtf(tot / (float)K + nm.eps);
+      const bool wr = nm.s && blockIdx.x == 0;
+#pragma unroll
+      for (int i = 0; i < GV_NORM_MAXV; ++i) {
+        const int c = (int)threadIdx.x + i * 256;
+        if (c < K) {
+          xs[GV_XPAD * (c >> 5) + (c & 31)] = nm.w ? (v[i] * inv) * wv[i] : v[i] * inv;
+          if (wr) nm.s[c] = v[i];
+        }
+      }
+    } else {
+      const int nq = K >> 2;  // <= XQ * THREADS
+      v4f xv[XQ];
+#pragma unroll
+      for (int g = 0; g < XQ; ++g) xv[g] = ((const v4f*)x)[min((int)threadIdx.x + g * THREADS, nq - 1)];
+      issue(0, S0);
+      if constexpr (GV_DEPTH > 1) issue(nitems > 1 ? 1 : 0, S1);
+#pragma unroll
+      for (int g = 0; g < XQ; ++g) {
+        const int q = (int)threadIdx.x + g * THREADS;
+        if (q < nq) *(v4f*)(xs + GV_XPAD * (q >> 3) + 4 * (q & 7)) = xv[g];
+      }
+    }
+    lds_barrier();
     const int nu0 = K / 32;
     auto gather = [&](int u, float (&xr)[32], float& sum, float (&gs)[4]) {
       const bool on = u < nu0;
@@ -608,11 +669,14 @@ int nsx_resident_workgroups(const void* kernel, size_t lds, int threads) {
 
 template <int FMT, int NT>
 static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const void* x, int xdt,
-                           int64_t T, float* y, const float* bias, const float* resid, hipStream_t st) {
+                           int64_t T, float* y, const float* bias, const float* resid, hipStream_t st,
+                           const GvNorm* nm = nullptr) {
   const int64_t row_bytes = raw_row_bytes<FMT>((int)K);
   const int64_t rows_per_launch = std::max<int64_t>(1, ((int64_t)1 << 31) / row_bytes);
   constexpr bool XR = NT == 1;  // the register path exists for one token only (fp32 x, 16-byte aligned)
   const bool xreg = XR && K <= GV_CHUNK_UNITS * 32 && xdt == NSX_DT_F32 && ((uintptr_t)x & 15u) == 0;
+  NSX_REQUIRE(!nm || (xreg && K <= 256 * GV_NORM_MAXV), NSX_EINVAL,
+              "the norm prologue takes one fp32 token, 16-byte aligned, K <= %d", 256 * GV_NORM_MAXV);
   const size_t bufs = (size_t)GV_WAVES * GvChunk<FMT>::WAVE_BYTES;
   const size_t lds = xreg ? std::max((size_t)gv_xreg_bytes((int)K), bufs) : (size_t)gv_x_bytes<NT>((int)K) + bufs;
   const void* kern = xreg ? (const void*)gemv_raw_kernel<FMT, NT, XR> : (const void*)gemv_raw_kernel<FMT, NT, false>;
@@ -638,7 +702,7 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
     const float* b = bias ? bias + r0 : nullptr;
     const float* rr = resid ? resid + r0 : nullptr;
     if constexpr (BIG_OK) {
-      if (xreg && nr <= BIG * big_resident) {
+      if (xreg && !nm && nr <= BIG * big_resident) {
         if (lds_big > 64 * 1024)
           NSX_HIP(hipFuncSetAttribute((const void*)gemv_raw_kernel<FMT, NT, XR, BIG>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_big));
@@ -655,6 +719,17 @@ static int launch_gemv_raw(const void* raw, int64_t n_rows, int64_t K, const voi
     const int64_t per_row = nsx_cdiv(nr, GV_WAVES);
     const int64_t cap = per_row <= 2 * resident ? std::max<int64_t>(1, resident / 2) : resident;
     const unsigned grid = (unsigned)std::min<int64_t>(per_row, cap);
+    if constexpr (XR) {
+      if (nm) {  // (a later launch of a split matrix sees the normed input again, without writing s twice)
+        GvNorm n1 = *nm;
+        if (r0 > 0) n1.s = nullptr;
+        hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, XR, GV_WAVES, true>), dim3(grid), dim3(GV_THREADS), lds, st,
+                           (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows, b, rr,
+                           n1);
+        NSX_LAUNCHED();
+        continue;
+      }
+    }
     if (xreg)
       hipLaunchKernelGGL((gemv_raw_kernel<FMT, NT, XR>), dim3(grid), dim3(GV_THREADS), lds, st,
                          (const uint8_t*)a, head, range, (int)nr, (int)K, x, xdt, (int)T, y + r0, n_rows, b, rr);
@@ -724,6 +799,32 @@ extern "C" int nsx_fused_gemv_ex(int t, const void* raw, int64_t n_rows, int64_t
     if (rc) return rc;
   }
   return NSX_OK;
+}
+
+extern "C" int nsx_fused_gemv_norm(int t, const void* raw, int64_t n_rows, int64_t K, const float* x,
+                                   const float* r, const float* w, float eps, float* s, float* y,
+                                   const float* bias, const float* resid, void* stream) {
+  const int BE = nsx_block_elems(t), BB = nsx_block_bytes(t);
+  NSX_REQUIRE(BB > 0, NSX_ENOTIMPL, "no fused kernel for ggml type %d", t);
+  NSX_REQUIRE(n_rows >= 0 && K > 0 && K % BE == 0, NSX_EINVAL,
+              "K=%lld is not a positive multiple of the %d-element block", (long long)K, BE);
+  NSX_REQUIRE(n_rows < (1ll << 31) && K <= 256 * GV_NORM_MAXV, NSX_EINVAL, "shape too large");
+  if (n_rows == 0) return NSX_OK;
+  NSX_REQUIRE(raw && x && y, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE(((uintptr_t)x & 15) == 0, NSX_EINVAL, "x must be 16-byte aligned");
+  NSX_REQUIRE(!s || (s != x && s != r), NSX_EINVAL, "s must not be x or r (other workgroups read them)");
+  if (t == NSX_Q4_K)
+    NSX_REQUIRE(((uintptr_t)raw & 3) == 0, NSX_EINVAL, "Q4_K rows must be 4-byte aligned");
+  const GvNorm nm{r, w, eps, s};
+  hipStream_t st = S(stream);
+  switch (t) {
+    case NSX_MXFP4: return launch_gemv_raw<NSX_MXFP4, 1>(raw, n_rows, K, x, NSX_DT_F32, 1, y, bias, resid, st, &nm);
+    case NSX_Q4_0: return launch_gemv_raw<NSX_Q4_0, 1>(raw, n_rows, K, x, NSX_DT_F32, 1, y, bias, resid, st, &nm);
+    case NSX_Q8_0: return launch_gemv_raw<NSX_Q8_0, 1>(raw, n_rows, K, x, NSX_DT_F32, 1, y, bias, resid, st, &nm);
+    case NSX_Q4_K: return launch_gemv_raw<NSX_Q4_K, 1>(raw, n_rows, K, x, NSX_DT_F32, 1, y, bias, resid, st, &nm);
+    case NSX_Q6_K: return launch_gemv_raw<NSX_Q6_K, 1>(raw, n_rows, K, x, NSX_DT_F32, 1, y, bias, resid, st, &nm);
+  }
+  return NSX_ENOTIMPL;
 }
 
 // ---------------------------------------------------------------------------

@@ -635,13 +635,22 @@ class GptOssModel:
         from ..format.gguf import row_geometry
         from .decode import attn_decode_qkv
         c, p = self.attn_config(), f"blk.{layer}."
-        h = add_rms_norm(x, pending, self.w(p + "attn_norm.weight"), self.cfg.rms_eps,
-                         sum_out=x if pending is not None else None)
+        wn = self.w(p + "attn_norm.weight")
         cat = self._qkv_raw(layer)
-        if cat is not None and can_fuse(cat[1], h):
-            qkv = fused_gemv(cat[0], cat[1], h, cat[2], h.shape[-1], out_dtype=torch.float32).reshape(-1)
+        if cat is not None and self._norm_fusable(cat[1], x, pending, wn):
+            # the attention norm in the QKV GEMV's prologue; x + pending goes to a new residual buffer
+            # (the GEMV's other workgroups still read x)
+            xs = torch.empty_like(x) if pending is not None else None
+            qkv = self._gemv_norm(cat[0], cat[1], cat[2], x, pending, wn, xs).reshape(-1)
+            if xs is not None:
+                x = xs
         else:
-            qkv = torch.cat([self._linear(p + n + ".weight", h).reshape(-1) for n in ("attn_q", "attn_k", "attn_v")])
+            h = add_rms_norm(x, pending, wn, self.cfg.rms_eps, sum_out=x if pending is not None else None)
+            if cat is not None and can_fuse(cat[1], h):
+                qkv = fused_gemv(cat[0], cat[1], h, cat[2], h.shape[-1], out_dtype=torch.float32).reshape(-1)
+            else:
+                qkv = torch.cat([self._linear(p + n + ".weight", h).reshape(-1)
+                                 for n in ("attn_q", "attn_k", "attn_v")])
         b = lambda n: self.w(p + n + ".bias") if self.has(p + n + ".bias") else None  # noqa: E731
         sinks = self.w(p + "attn_sinks.weight") if self.has(p + "attn_sinks.weight") else None
         att = attn_decode_qkv(qkv, b("attn_q"), b("attn_k"), b("attn_v"), c, self._inv_freq, self._amp, kv, layer,
@@ -670,10 +679,33 @@ class GptOssModel:
             self.router_stats.record(layer, ids)
         return x, out
 
+    def _norm_fusable(self, dtype, x: torch.Tensor, pending: torch.Tensor | None, wn) -> bool:
+        """Whether a one-token GEMV can take the block norm of x (+ pending) in its prologue
+        (nsx_fused_gemv_norm: fp32 vectors of K <= 4096 values, x 16-byte aligned)."""
+        from ..compute.kernels import can_fuse
+        vecs = [x] + [t for t in (pending, wn) if t is not None]
+        K = x.shape[-1]
+        return (can_fuse(dtype, x) and x.numel() == K and K <= 4096 and x.data_ptr() % 16 == 0
+                and all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.numel() == K
+                        for t in vecs))
+
+    def _gemv_norm(self, raw, dtype, n_rows: int, x, pending, wn, sum_out=None) -> torch.Tensor:
+        from ..compute.kernels import fused_gemv_norm
+        K = x.shape[-1]
+        return fused_gemv_norm(raw, dtype, x.reshape(-1), None if pending is None else pending.reshape(-1), wn,
+                               self.cfg.rms_eps, n_rows, K, sum_out=None if sum_out is None else sum_out.reshape(-1))
+
     def _head(self, x: torch.Tensor, pending: torch.Tensor | None = None) -> torch.Tensor:
         """Logits of the last hidden state (+ pending): output_norm, then output.weight (or the tied embedding)."""
-        h = add_rms_norm(x.contiguous(), pending, self.w("output_norm.weight"), self.cfg.rms_eps)
-        return self._linear("output.weight" if self.has("output.weight") else "token_embd.weight", h)
+        from ..format.gguf import row_geometry
+        name = "output.weight" if self.has("output.weight") else "token_embd.weight"
+        wn = self.w("output_norm.weight")
+        hit = self._resident_raw(name) if name in self.gguf.tensors else None
+        x = x.contiguous()
+        if hit is not None and self._norm_fusable(hit[1], x, pending, wn):  # the output norm in the GEMV's prologue
+            return self._gemv_norm(hit[0], hit[1], row_geometry(self.gguf.tensors[name])[0], x, pending, wn)
+        h = add_rms_norm(x, pending, wn, self.cfg.rms_eps)
+        return self._linear(name, h)
 
     def _decode_one(self, ids: torch.Tensor, kv) -> torch.Tensor:
         """One token (device int32 id) through every layer at kv.pos; kv.pos += 1 on the device."""

@@ -277,3 +277,37 @@ def test_add_rmsnorm_matches_oracle(dev, T, n, resid, weight):
     y2 = add_rms_norm(xd, None if r is None else r.to(dev), None if w is None else w.to(dev), 1e-5, sum_out=xd)
     assert torch.equal(y2, y)
     np.testing.assert_array_equal(to_np(xd), v.astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt,rows,K", [("Q8_0", 5120, 2880), ("Q8_0", 300, 4096), ("MXFP4", 700, 2880),
+                                        ("Q4_0", 96, 4096), ("Q4_K", 64, 1536), ("Q6_K", 33, 2816),
+                                        ("Q8_0", 40000, 256), ("Q4_0", 7, 64)])
+@pytest.mark.parametrize("resid,weight", [(True, True), (False, True), (True, False)])
+def test_fused_gemv_norm_equals_norm_then_gemv(dev, fmt, rows, K, resid, weight):
+    """nsx_fused_gemv_norm (the block norm in the one-token GEMV's prologue) against
+    nsx_add_rmsnorm followed by nsx_fused_gemv_ex: the same bits, norm and residual sum
+    included (the prologue keeps add_rmsnorm_kernel's layout and sum order), and the
+    product against the float64 oracle of the normed input. The 40000-row case gives
+    every workgroup of the persistent grid several rows; only the first writes x + r."""
+    from nurostream_amd.compute.kernels import fused_gemv, fused_gemv_norm
+    from nurostream_amd.compute.ops import add_rms_norm
+    t = getattr(OQ, fmt)
+    raw = _gemv_case(fmt, rows, K, seed=rows + 3 * K)
+    g = torch.Generator().manual_seed(rows + K)
+    x = torch.randn(K, generator=g).to(dev)
+    r = torch.randn(K, generator=g).to(dev) if resid else None
+    w = (torch.rand(K, generator=g) + 0.5).to(dev) if weight else None
+    b = torch.randn(rows, generator=g).to(dev)
+    res = torch.randn(rows, generator=g).to(dev)
+    raw_t = torch.from_numpy(raw).to(dev)
+    s = torch.full((K,), float("nan"), device=dev) if resid else None
+    y = fused_gemv_norm(raw_t, t, x, r, w, 1e-5, rows, K, sum_out=s, bias=b, resid=res)
+    h = add_rms_norm(x.reshape(1, K), None if r is None else r.reshape(1, K), w, 1e-5)
+    ref = fused_gemv(raw_t, t, h, rows, K, out_dtype=torch.float32, bias=b, resid=res.reshape(1, rows))
+    assert torch.equal(y, ref)
+    if resid:
+        assert torch.equal(s, x + r)
+    want = to_np(res) + (OQ.gemv(raw, t, to_np(h), rows, K, f64=True)[0] + to_np(b))
+    assert rel_max(to_np(y)[0], want) < GEMV_TIGHT
+    with pytest.raises(ValueError):  # the residual sum may not overwrite what other workgroups still read
+        fused_gemv_norm(raw_t, t, x, r if resid else x.clone(), w, 1e-5, rows, K, sum_out=x)
