@@ -403,7 +403,8 @@ def layer_workload(args, torch, N, synth, dev):
     mq = q4k and (args.dispatch == "mfma" or (args.dispatch == "auto" and T >= 8))
     grouped = mq or (args.dispatch == "grouped" and (layout == "t64" or q4k)) or (
         layout == "t64" and args.dispatch == "auto" and T >= 8)
-    phases = (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_COMBINE)
+    # (per pair, the down kernel combines: the combine phase launches nothing and is not captured)
+    phases = (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN) + ((N.PHASE_COMBINE,) if grouped else ())
     phase_us = {}
     if R > 0:
         P0 = W + K
