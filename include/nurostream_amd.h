@@ -204,6 +204,19 @@ int nsx_moe_forward_norm(const nsx_moe_layer *L, const float *x, const float *r,
                          float *out, int32_t *ids, float *weights, void *workspace,
                          int64_t workspace_bytes, void *stream);
 
+/* One block of a stacked GPT-OSS FFN whose output feeds the next block
+ * (model/gpt_oss.py:123-177, x_{l+1} = x_l + moe(h_l), then the next block's
+ * input norm, compute/ops.py:14-20): nsx_moe_forward of h, then x_out =
+ * x + out and h_out = rms_norm(x_out) * norm_w (eps; norm_w may be NULL) --
+ * the bits of nsx_moe_forward followed by nsx_add_rmsnorm(x, out, ...). On the
+ * grouped path the combine and the add + norm are one launch; the MoE output
+ * itself is not written. x_out may be x; h_out must not overlap x or x_out
+ * (it may be h). n_embd <= 4096. Same workspace as nsx_moe_forward. */
+int nsx_moe_forward_addnorm(const nsx_moe_layer *L, const float *h, int64_t T,
+                            const float *x, const float *norm_w, float eps, float *x_out,
+                            float *h_out, int32_t *ids, float *weights, void *workspace,
+                            int64_t workspace_bytes, void *stream);
+
 /* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, the top-k and the
  * ids/weights outputs, for every layout and dispatch; in the t64 layout also
  * the activation terms of h), NSX_PHASE_GATE_UP (grouped dispatch: the sort

@@ -72,6 +72,8 @@ _SIGS = {
     "nsx_moe_workspace_bytes": (_i64, [C.POINTER(MoeLayerC), _i64]),
     "nsx_moe_forward": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p, _i64, _p]),
     "nsx_moe_forward_norm": (_i, [C.POINTER(MoeLayerC), _p, _p, _p, C.c_float, _i64, _p, _p, _p, _p, _p, _i64, _p]),
+    "nsx_moe_forward_addnorm": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, C.c_float, _p, _p, _p, _p, _p, _i64,
+                                     _p]),
     "nsx_moe_phase": (_i, [C.POINTER(MoeLayerC), _i, _p, _i64, _p, _p, _p, _p, _i64, _p]),
     "nsx_moe_forward_static": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p]),
     "nsx_add_rmsnorm": (_i, [_p, _p, _i64, _i64, C.c_float, _p, _p, _p, _p]),

@@ -1393,6 +1393,85 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
   a.out[(int64_t)t * a.n_embd + row] = o;
 }
 
+// The combine fused with the next block's residual add and norm (a stacked
+// layer's output goes nowhere else): for token t, o = the combine above, then
+// x_out = x + o and h_out = rms_norm(x + o) * w in add_rmsnorm_kernel's layout
+// and order -- the bits of moe_combine_kernel followed by that kernel, one
+// launch instead of two. One workgroup per token; x_out may be x (each thread
+// reads its elements before writing them).
+struct AddNorm {
+  const float* x;
+  const float* w;  // norm weight (null: none)
+  float eps;
+  float* x_out;
+  float* h_out;
+};
+template <int KMAX>  // top_k <= KMAX
+__global__ __launch_bounds__(1024) void moe_combine_norm_kernel(MoeDev a, AddNorm an) {
+  __shared__ float part[4];
+  __shared__ __align__(16) float s_row[256 * NORM_MAXV];  // x + o of the token
+  const int t = blockIdx.x, n = a.n_embd, k = a.top_k, tid = threadIdx.x;
+  int pj[KMAX];
+  float wj[KMAX];
+#pragma unroll
+  for (int jj = 0; jj < KMAX; ++jj) {
+    pj[jj] = a.corder[t * k + min(jj, k - 1)];
+    wj[jj] = a.wts[pj[jj]];
+  }
+  // x + o over the whole row by all 1024 threads, every load unpredicated and in flight together
+  constexpr int EPT = 256 * NORM_MAXV / 1024;
+  const float* xr = an.x + (int64_t)t * n;
+  float wv[NORM_MAXV];  // the norm weights of the norm threads' elements, requested with the rest
+  if (tid < 256) {
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) wv[i] = an.w ? an.w[min(tid + i * 256, n - 1)] : 1.f;
+  }
+  float yv[EPT][KMAX], xv[EPT];
+#pragma unroll
+  for (int q = 0; q < EPT; ++q) {
+    const int c = min(tid + q * 1024, n - 1);
+    xv[q] = xr[c];
+#pragma unroll
+    for (int jj = 0; jj < KMAX; ++jj) yv[q][jj] = a.y[(int64_t)pj[jj] * n + c];
+  }
+#pragma unroll
+  for (int q = 0; q < EPT; ++q) {
+    float o = 0.f;  // moe_combine_kernel's sum, in its order
+#pragma unroll
+    for (int jj = 0; jj < KMAX; ++jj) o = jj < k ? combine_one(o, wj[jj], yv[q][jj]) : o;
+    const int c = tid + q * 1024;
+    if (c < n) s_row[c] = xv[q] + o;
+  }
+  __syncthreads();  // every read of x is done before any write below
+  // the norm in add_rmsnorm_kernel's layout and order: 256 threads, thread i holding i, i + 256, ...
+  float v[NORM_MAXV];
+  float ss = 0.f;
+  if (tid < 256) {
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) {
+      const int c = tid + i * 256;
+      v[i] = c < n ? s_row[c] : 0.f;
+      ss = fmaf(v[i], v[i], ss);
+    }
+    ss = nsx_wave_sum(ss);
+    if (__lane_id() == 0) part[tid >> 6] = ss;
+  }
+  __syncthreads();
+  if (tid >= 256) return;
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tot += part[i];
+  const float inv = 1.f / sqrtf(tot / (float)n + an.eps);
+#pragma unroll
+  for (int i = 0; i < NORM_MAXV; ++i) {
+    const int c = tid + i * 256;
+    if (c < n) {
+      an.x_out[(int64_t)t * n + c] = v[i];
+      an.h_out[(int64_t)t * n + c] = an.w ? (v[i] * inv) * wv[i] : v[i] * inv;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Raw GGUF rows (any format), one row per wave: the row's units are fetched
 // with range-checked dword buffer loads (any byte alignment) and realigned in
@@ -2697,7 +2776,7 @@ static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool ga
 // the earlier ones left in the workspace.
 static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
                    void* workspace, int64_t workspace_bytes, void* stream, int ph0, int ph1,
-                   RtNorm nm = RtNorm{0, nullptr, nullptr, 0.f, nullptr}) {
+                   RtNorm nm = RtNorm{0, nullptr, nullptr, 0.f, nullptr}, const AddNorm* an = nullptr) {
   int rc = check_layer(L, T);
   if (rc) return rc;
   NSX_REQUIRE(h && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
@@ -2835,10 +2914,15 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
       }
       if (rc) return rc;
     }
-    if (on(NSX_PHASE_COMBINE) &&
-        (rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
-                         d)))
-      return rc;
+    if (on(NSX_PHASE_COMBINE)) {
+      if (an)
+        rc = L->top_k <= 4 ? nsx_launch(moe_combine_norm_kernel<4>, dim3((unsigned)T), dim3(1024), 0, st, d, *an)
+                           : nsx_launch(moe_combine_norm_kernel<MAX_TOPK>, dim3((unsigned)T), dim3(1024), 0, st, d, *an);
+      else
+        rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
+                        d);
+      if (rc) return rc;
+    }
     return NSX_OK;
   }
   if (t64) {
@@ -2897,6 +2981,37 @@ extern "C" int nsx_moe_forward_norm(const nsx_moe_layer* L, const float* x, cons
   NSX_REQUIRE(!overlap(x_out, x) && !overlap(x_out, r), NSX_EINVAL, "x_out overlaps x or r");
   return moe_run(L, x, T, out, ids, weights, workspace, workspace_bytes, stream, NSX_PHASE_ROUTER, NSX_PHASE_COMBINE,
                  RtNorm{1, r, norm_w, eps, x_out});
+}
+
+extern "C" int nsx_moe_forward_addnorm(const nsx_moe_layer* L, const float* h, int64_t T, const float* x,
+                                       const float* norm_w, float eps, float* x_out, float* h_out, int32_t* ids,
+                                       float* weights, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_layer(L, T);
+  if (rc) return rc;
+  NSX_REQUIRE(h && x && x_out && h_out && ids && weights, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE(eps >= 0.f, NSX_EINVAL, "eps %g", (double)eps);
+  NSX_REQUIRE(L->n_embd <= 256 * NORM_MAXV, NSX_EINVAL, "n_embd %d above %d", L->n_embd, 256 * NORM_MAXV);
+  const uintptr_t bytes = (uintptr_t)(T * L->n_embd * 4);
+  auto overlap = [&](const void* p, const void* q) {
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return a < b + bytes && b < a + bytes;
+  };
+  NSX_REQUIRE((x_out == x || !overlap(x_out, x)) && !overlap(h_out, x) && !overlap(h_out, x_out), NSX_EINVAL,
+              "x_out must be x or apart from it, h_out apart from both");
+  if (!use_grouped(L, T)) {  // the per-pair kernels combine in their down kernel: into h_out, then the norm
+    if ((rc = nsx_moe_forward(L, h, T, h_out, ids, weights, workspace, workspace_bytes, stream))) return rc;
+    return nsx_add_rmsnorm(x, h_out, T, L->n_embd, eps, norm_w, x_out, h_out, stream);
+  }
+  const int64_t tc = grp_chunk_tokens(L), k = L->top_k, ne = L->n_embd;
+  for (int64_t t0 = 0; t0 < T; t0 += tc) {  // grouped passes in token order, as nsx_moe_forward
+    const int64_t nt = std::min(tc, T - t0);
+    const AddNorm an{x + t0 * ne, norm_w, eps, x_out + t0 * ne, h_out + t0 * ne};
+    // (no combine output: h_out stands in for `out`, which the grouped phases before the combine never touch)
+    rc = moe_run(L, h + t0 * ne, nt, h_out + t0 * ne, ids + t0 * k, weights + t0 * k, workspace, workspace_bytes,
+                 stream, NSX_PHASE_ROUTER, NSX_PHASE_COMBINE, RtNorm{0, nullptr, nullptr, 0.f, nullptr}, &an);
+    if (rc) return rc;
+  }
+  return NSX_OK;
 }
 
 extern "C" int nsx_moe_phase(const nsx_moe_layer* L, int phase, const float* h, int64_t T, float* out, int32_t* ids,

@@ -7,8 +7,10 @@ x = x + out (gpt_oss.py:126,177). Attention is not on the MoE path and is
 not modelled: layer l + 1 reads layer l's output directly.
 
 `forward` runs the whole chain on the device with no host synchronisation:
-per layer one fused residual-add + norm kernel (nsx_add_rmsnorm) and one
-MoE layer call (nsx_moe_forward, device-side routing). `_route` and
+per layer one MoE layer call (device-side routing), the residual add and
+the next layer's norm folded into the next router kernel (up to two tokens,
+nsx_moe_forward_norm) or into the layer's own last launch (nsx_moe_forward_addnorm),
+the same bits as a separate nsx_add_rmsnorm. `_route` and
 `_ffn_block` keep the reference's per-layer signatures; `_route` returns the
 chosen experts as a host list (a device-to-host copy, as the reference's
 torch.unique(...).tolist() at gpt_oss.py:121).
@@ -78,8 +80,9 @@ class GptOssFFNStack:
         layer's FFN block (into `out` when given). Device-only: no host sync.
         Between layers x += out and h = rms_norm(x) of the next layer run inside
         that layer's router kernel where the layer allows it
-        (MoELayer.forward_norm, the same bits as add_rms_norm), the residual
-        stream then alternating between two buffers."""
+        (MoELayer.forward_norm, the residual stream then alternating between two
+        buffers), else inside this layer's last launch (MoELayer.forward_addnorm,
+        in place); both the same bits as add_rms_norm."""
         x = x.reshape(-1, self.cfg.n_embd)
         T = x.shape[0]
         h, y, ids, wts = self._buffers(T)
@@ -89,17 +92,22 @@ class GptOssFFNStack:
         res = torch.empty_like(x) if out is None else out
         eps = self.cfg.rms_eps
         add_rms_norm(x.float().contiguous(), None, self.norm_weights[0], eps, out=h, sum_out=res)
-        self.layers[0].forward(h, out=y, ids=ids[0], weights=wts[0])
         cur, other = res, alt
-        for li in range(1, len(self.layers)):  # x += out; h = rms_norm(x); out = layer(h)
-            layer = self.layers[li]
-            if layer.norm_folds(T):
+        n = len(self.layers)
+        pending = False  # y holds the last layer's output, not yet added to cur
+        for li, layer in enumerate(self.layers):  # x += out; h = rms_norm(x); out = layer(h)
+            if pending:  # this layer's add + norm inside its router kernel
                 layer.forward_norm(cur, y, self.norm_weights[li], eps, x_out=other, out=y, ids=ids[li],
                                    weights=wts[li])
                 cur, other = other, cur
+            elif li + 1 < n and not self.layers[li + 1].norm_folds(T):
+                # the next layer's add + norm in this layer's last launch (h is its input, then the next one's)
+                layer.forward_addnorm(h, cur, self.norm_weights[li + 1], eps, x_out=cur, h_out=h, ids=ids[li],
+                                      weights=wts[li])
+                continue
             else:
-                add_rms_norm(cur, y, self.norm_weights[li], eps, out=h, sum_out=cur)
                 layer.forward(h, out=y, ids=ids[li], weights=wts[li])
+            pending = True
         if cur is res:
             res.add_(y)
         else:

@@ -226,6 +226,40 @@ class MoELayer:
                                                   N.stream_ptr(self.device)), "moe_forward_norm")
         return out, ids, weights
 
+    def forward_addnorm(self, h: torch.Tensor, x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
+                        x_out: torch.Tensor, h_out: torch.Tensor, ids: torch.Tensor | None = None,
+                        weights: torch.Tensor | None = None):
+        """One stacked block whose output feeds the next (model/gpt_oss.py:123-177):
+        x_out = x + forward(h) and h_out = rms_norm(x_out) * norm_w, the next
+        block's input -- the bits of forward + add_rms_norm; on the grouped path the
+        combine, the add and the norm are one launch (the MoE output is not kept).
+        h, x, x_out, h_out: (T, n_embd) contiguous fp32; x_out may be x, h_out may be
+        h but must not overlap x or x_out. Returns (ids, weights)."""
+        N.require_device(h, x, x_out, h_out)
+        T = x.shape[0]
+        for name, t in (("h", h), ("x", x), ("x_out", x_out), ("h_out", h_out)):
+            if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (T, self.n_embd) \
+                    or t.device != self.device:
+                raise ValueError(f"{name} must be a contiguous fp32 ({T}, {self.n_embd}) tensor on {self.device}")
+        if ids is None:
+            ids = torch.empty((T, self.top_k), dtype=torch.int32, device=self.device)
+        if weights is None:
+            weights = torch.empty((T, self.top_k), dtype=torch.float32, device=self.device)
+        self._check_buffers(T, h_out, ids, weights)
+        w = None
+        if norm_w is not None:
+            w = norm_w.to(device=self.device, dtype=torch.float32).contiguous()
+            if w.numel() != self.n_embd:
+                raise ValueError(f"norm weight of {w.numel()} values, n_embd is {self.n_embd}")
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            N.check(N.load().nsx_moe_forward_addnorm(C.byref(self._c), h.data_ptr(), T, x.data_ptr(),
+                                                     None if w is None else w.data_ptr(), float(eps),
+                                                     x_out.data_ptr(), h_out.data_ptr(), ids.data_ptr(),
+                                                     weights.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                     N.stream_ptr(self.device)), "moe_forward_addnorm")
+        return ids, weights
+
     def phase(self, phase: int, h: torch.Tensor, out: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
               workspace: torch.Tensor | None = None) -> None:
         """Run one phase (_native.PHASE_*) of forward(); later phases read what

@@ -179,3 +179,18 @@ def test_forward_norm_validation(lib):
     assert lib.nsx_moe_forward_norm(*args(1, (2 << 20) - 4)) == N.EINVAL
     L.layout = N.LAYOUT_GGUF
     assert lib.nsx_moe_forward_norm(*args(1, 3 << 20)) == N.ENOTIMPL
+
+
+def test_forward_addnorm_validation(lib):
+    """nsx_moe_forward_addnorm refuses an h_out that overlaps x or x_out and an x_out
+    that overlaps x without being it -- checked on the host before any HIP call (the
+    pointers below are never dereferenced)."""
+    L = _gptoss_layer()
+    T, row = 4, 4 * 2880 * 4
+    args = lambda x, x_out, h_out: (C.byref(L), 1 << 20, T, x, None, 1e-5, x_out, h_out, 5 << 20, 6 << 20,  # noqa
+                                    7 << 20, 1 << 30, None)
+    x = 2 << 20
+    assert lib.nsx_moe_forward_addnorm(*args(x, x, x + row // 2)) == N.EINVAL  # h_out over x
+    assert b"h_out" in lib.nsx_last_error()
+    assert lib.nsx_moe_forward_addnorm(*args(x, x + 4, 3 << 20)) == N.EINVAL  # x_out overlapping x, not x
+    assert lib.nsx_moe_forward_addnorm(*args(x, 3 << 20, (3 << 20) + 8)) == N.EINVAL  # h_out over x_out

@@ -58,6 +58,36 @@ def test_stack_norm_in_router_equals_separate_norm(dev, T):
     assert torch.equal(y, res)
 
 
+@pytest.mark.parametrize("T,weight", [(5, True), (9, True), (40, False), (300, True)])
+def test_forward_addnorm_equals_forward_then_norm(dev, T, weight):
+    """MoELayer.forward_addnorm (nsx_moe_forward_addnorm: the next block's residual add and
+    norm in the layer's last launch -- the combine kernel on the grouped path, from 8 tokens)
+    against forward() followed by add_rms_norm: the same bits for x + out and the normed
+    h, in place (x_out = x, h_out = h) and apart, and the same routing."""
+    from nurostream_amd import synth
+    from nurostream_amd.compute.ops import add_rms_norm
+    from nurostream_amd.moe.fused import MoELayer  # noqa: F401
+    cfg = _small("gptoss-small")
+    t = synth.make_layer(cfg, seed=31, device=dev)
+    from moe_cases import _layer
+    layer = _layer(cfg, t, "t64")
+    h = synth.activations(T, cfg.n_embd, seed=41, device=dev)
+    x = synth.activations(T, cfg.n_embd, seed=42, device=dev)
+    w = (1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(5))).to(dev) if weight else None
+    out, ids, wts = layer.forward(h)
+    xr = torch.empty_like(x)
+    hr = add_rms_norm(x, out, w, 1e-5, sum_out=xr)
+    xo, ho = torch.empty_like(x), torch.empty_like(x)
+    ids2, wts2 = layer.forward_addnorm(h, x, w, 1e-5, x_out=xo, h_out=ho)
+    assert torch.equal(ids2, ids) and torch.equal(wts2, wts)
+    assert torch.equal(xo, xr) and torch.equal(ho, hr)
+    xi, hi = x.clone(), h.clone()  # in place: x_out = x, h_out = h
+    layer.forward_addnorm(hi, xi, w, 1e-5, x_out=xi, h_out=hi)
+    assert torch.equal(xi, xr) and torch.equal(hi, hr)
+    with pytest.raises(Exception):  # h_out over x
+        layer.forward_addnorm(h, xi, w, 1e-5, x_out=xo, h_out=xi)
+
+
 @pytest.mark.parametrize("T", [1, 2, 9])
 def test_gptoss_ffn_stack_matches_oracle(dev, T):
     from nurostream_amd import synth
