@@ -1210,6 +1210,115 @@ __device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, 
   return true;
 }
 
+// Pairs up to which the grouped gate/up kernel selects the top-k and sorts
+// the pairs itself (one 64-lane chunk), with no sort launch before it.
+constexpr int GRP_SMALL_P = 64;
+
+// LDS-only workgroup barrier: waits on the wave's LDS operations, not on its
+// loads and stores to memory still in flight
+__device__ __forceinline__ void grp_lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// moe_sort_kernel's results for P = T * top_k <= GRP_SMALL_P pairs, computed
+// by a workgroup of the gate/up kernel into its LDS: each token's top-k from
+// the router's logits (a wave per token, as the sort kernel), then wave 0
+// sorts the pairs -- a single chunk, so the chunk prefix of the sort kernel
+// is zero and the items, sorted list and combine order are the same values.
+// Every workgroup computes them; the writer also stores ids, weights, items,
+// n_items, sorted and corder for the down and combine phases and the caller.
+// Every thread of the workgroup calls it.
+__device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, int* s_nitems, uint8_t* s_exp,
+                               int* s_cnt, int* s_off, bool writer) {
+  const int tid = threadIdx.x, nt = blockDim.x, nw = nt >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = __lane_id();
+  const int T = a.T, k = a.top_k, E = a.E, P = T * k;
+  for (int e = tid; e < E; e += nt) s_cnt[e] = 0;
+  for (int t = wave; t < T; t += nw) {
+    int si[MAX_TOPK];
+    float sw[MAX_TOPK];
+    topk_regs(a.logits + (int64_t)t * E, E, k, a.mode, si, sw);
+    int my_e = 0;
+    float my_w = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {  // lane jj < k: slot jj
+      my_e = lane == jj ? si[jj] : my_e;
+      my_w = lane == jj ? sw[jj] : my_w;
+    }
+    if (lane < k) {
+      s_exp[t * k + lane] = (uint8_t)clamp_expert(my_e, E);
+      if (writer) {
+        a.ids[(int64_t)t * k + lane] = my_e;
+        a.wts[(int64_t)t * k + lane] = my_w;
+      }
+    }
+  }
+  grp_lds_barrier();
+  if (writer) {
+    for (int p = tid; p < P; p += nt) {  // the token's combine order: its slots by (expert, slot)
+      const int t = p / k, j = p - t * k, e = s_exp[p];
+      int rank = 0;
+      for (int jj = 0; jj < k; ++jj) {
+        const int ej = s_exp[t * k + jj];
+        rank += (ej < e || (ej == e && jj < j)) ? 1 : 0;
+      }
+      a.corder[t * k + rank] = p;
+    }
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int e_l = lane < P ? s_exp[lane] : 0;  // pair `lane`'s expert
+  const uint64_t m = grp_match(lane < P, e_l);
+  if (wave == 0 && lane < P && (m & below) == 0ull) s_cnt[e_l] = (int)__popcll(m);
+  grp_lds_barrier();
+  if (wave == 0) {  // exclusive scans over experts (4 per lane) of the pair and item counts
+    int cn[MAX_EXPERTS / 64], ni[MAX_EXPERTS / 64];
+    int sc = 0, sn = 0;
+#pragma unroll
+    for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
+      const int e = lane * (MAX_EXPERTS / 64) + i;
+      cn[i] = e < E ? s_cnt[e] : 0;
+      ni[i] = (cn[i] + GRP_TPI - 1) / GRP_TPI;
+      sc += cn[i];
+      sn += ni[i];
+    }
+    int isc = sc, isn = sn;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64);
+      if (lane >= d) {
+        isc += oc;
+        isn += on;
+      }
+    }
+    int bc = isc - sc, bn = isn - sn;
+#pragma unroll
+    for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
+      const int e = lane * (MAX_EXPERTS / 64) + i;
+      if (e < E) {
+        s_off[e] = bc;
+        for (int q = 0; q < ni[i]; ++q) {
+          const int4 it = make_int4(e, bc + q * GRP_TPI, min(GRP_TPI, cn[i] - q * GRP_TPI), 0);
+          s_items[bn + q] = it;
+          if (writer) a.items[bn + q] = it;
+        }
+      }
+      bc += cn[i];
+      bn += ni[i];
+    }
+    if (lane == 63) {
+      *s_nitems = isn;
+      if (writer) *a.n_items = isn;
+    }
+  }
+  grp_lds_barrier();
+  if (wave == 0 && lane < P) {  // stable scatter
+    const int pos = s_off[e_l] + (int)__popcll(m & below);
+    s_sorted[pos] = lane;
+    if (writer) a.sorted[pos] = lane;
+  }
+  grp_lds_barrier();
+}
+
 // gate/up for (item, tile) units: one wave per K-chunk, computing that chunk
 // of both the gate and the up tile, so a token's activation terms are read
 // once per (item, tile, chunk) rather than once per matrix. A wave's gate
@@ -1221,12 +1330,23 @@ __device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, 
 // works through XCD x's contiguous item-major run of units -- workgroup j of
 // it takes units j, j + nx, ... -- so no workgroup is dispatched per unit;
 // the next unit's weights are requested before this unit's epilogue, into
-// the registers its MFMAs have finished with.
+// the registers its MFMAs have finished with. SIN: every workgroup first
+// selects the top-k and sorts the pairs itself (grp_small_sort; workgroup 0
+// stores the results), so small batches launch no sort kernel.
+template <bool SIN>
 __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev a) {
   __shared__ float red[2][MAX_CHUNKS][GRP_TPI][64];
+  __shared__ int4 s_items[SIN ? GRP_SMALL_P : 1];
+  __shared__ int s_sorted[SIN ? GRP_SMALL_P : 1], s_cnt[SIN ? MAX_EXPERTS : 1], s_off[SIN ? MAX_EXPERTS : 1];
+  __shared__ int s_nitems;
+  __shared__ uint8_t s_exp[SIN ? GRP_SMALL_P : 1];
+  if constexpr (SIN) grp_small_sort(a, s_items, s_sorted, &s_nitems, s_exp, s_cnt, s_off, blockIdx.x == 0);
+  auto item_at = [&](int i) { return SIN ? s_items[i] : a.items[i]; };
+  auto item_word = [&](int i, int w) { return SIN ? ((const int*)s_items)[4 * i + w] : ((const int*)a.items)[4 * i + w]; };
+  auto sorted_at = [&](int i) { return SIN ? s_sorted[i] : a.sorted[i]; };
   const int tiles = (int)a.ggu.tiles;
   const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7);
-  const int live = tiles * *a.n_items, per = (live + 7) / 8;
+  const int live = tiles * (SIN ? s_nitems : *a.n_items), per = (live + 7) / 8;
   const int hi = min(live, (xcd + 1) * per);
   int L = xcd * per + (int)(blockIdx.x >> 3);
   if (L >= hi) return;
@@ -1234,12 +1354,12 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
   const int64_t xs = (int64_t)a.ggu.ns * XQ_STEP;
   MxRegs<GU_S> Rg, Ru;
-  int4 item = a.items[L / tiles];
+  int4 item = item_at(L / tiles);
   int tile = L - (L / tiles) * tiles;
   int e = clamp_expert(item.x, a.E);
   // the pair list goes out ahead of the weights: loads return in order, and the first token group's
   // activation loads wait on it (behind the weights, they would wait for every weight byte)
-  int my_pair = a.sorted[item.y + min(lane & 15, item.z - 1)];  // lane i < 16: the item's token i
+  int my_pair = sorted_at(item.y + min(lane & 15, item.z - 1));  // lane i < 16: the item's token i
   {  // both tiles' addresses before any load: a pointer-table read between the two load groups would wait on the first
     const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile);
     const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
@@ -1252,7 +1372,7 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
     // the next unit's item, requested now so that it is at hand when this unit's MFMAs are done (the last unit
     // re-reads its own); lane i holds word i & 3 -- a lane-varying load stays in VGPRs, where nothing waits on
     // it before its fields are read after the token loop
-    const int iw_n = ((const int*)a.items)[4 * (min(Ln, hi - 1) / tiles) + (lane & 3)];
+    const int iw_n = item_word(min(Ln, hi - 1) / tiles, lane & 3);
     for (int tg = 0; tg * 4 < n; ++tg) {
       const int tok = tg * 4 + ((lane & 15) >> 2);
       const int pr = __shfl(my_pair, min(tok, n - 1), 64);
@@ -1312,7 +1432,7 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
                          __builtin_amdgcn_readlane(iw_n, 2), 0};
     const int tile_n = Ln - (Ln / tiles) * tiles;
     const int e_n = clamp_expert(item_n.x, a.E);
-    const int pair_n = a.sorted[item_n.y + min(lane & 15, item_n.z - 1)];  // (ahead of the weights, as above)
+    const int pair_n = sorted_at(item_n.y + min(lane & 15, item_n.z - 1));  // (ahead of the weights, as above)
     const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e_n, tile_n);
     const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e_n, tile_n);
     mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
@@ -2867,13 +2987,16 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     const int64_t items = (int64_t)p.max_items;
     auto grid8 = [&](int64_t groups) { return dim3((unsigned)(8 * nsx_cdiv(items * groups, 8))); };
     if (on(NSX_PHASE_GATE_UP)) {
-      if ((rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
+      // a small batch whose top-k the sort would select: the t64 gate/up workgroups sort the pairs themselves
+      const bool sin = t64 && d.topk_in_sort && P <= GRP_SMALL_P;
+      if (!sin && (rc = nsx_launch(moe_sort_kernel, dim3(1), dim3(1024), 0, st, d))) return rc;
       if (t64) {
         // persistent: the resident workgroups (a multiple of 8), no more than the units can use
-        const int64_t r = std::max<int64_t>(8, nsx_resident_workgroups((const void*)moe_gu_grouped_kernel, 0,
-                                                                       64 * p.cg) / 8 * 8);
-        rc = nsx_launch(moe_gu_grouped_kernel, dim3((unsigned)std::min<int64_t>(r, 8 * nsx_cdiv(items * p.ggu.tiles, 8))),
-                        dim3(64 * p.cg), 0, st, d);
+        const void* kern = sin ? (const void*)moe_gu_grouped_kernel<true> : (const void*)moe_gu_grouped_kernel<false>;
+        const int64_t r = std::max<int64_t>(8, nsx_resident_workgroups(kern, 0, 64 * p.cg) / 8 * 8);
+        const dim3 grid((unsigned)std::min<int64_t>(r, 8 * nsx_cdiv(items * p.ggu.tiles, 8)));
+        rc = sin ? nsx_launch(moe_gu_grouped_kernel<true>, grid, dim3(64 * p.cg), 0, st, d)
+                 : nsx_launch(moe_gu_grouped_kernel<false>, grid, dim3(64 * p.cg), 0, st, d);
       } else if (p.mq) {
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))

@@ -32,9 +32,11 @@ def test_grouped_equals_pairs_bitwise(dev, T):
     assert torch.equal(op, og)
 
 
-def test_grouped_one_hot_expert(dev):
+@pytest.mark.parametrize("T", [8, 15, 40])
+def test_grouped_one_hot_expert(dev, T):
     """Every token routed to the same experts (a bias that dominates the logits):
-    one expert holds all pairs, several items per expert."""
+    one expert holds all pairs, several items per expert from 17 tokens (below
+    16 tokens the gate/up kernel sorts the pairs itself)."""
     from nurostream_amd import synth
     cfg = _small("gptoss-small")
     t = synth.make_layer(cfg, seed=12, device=dev)
@@ -42,7 +44,7 @@ def test_grouped_one_hot_expert(dev):
     b[[3, 7, 8, 12]] = 50.0
     t["router_b"] = b
     lp, lg = _pair_and_grouped(cfg, t)
-    h = synth.activations(40, cfg.n_embd, seed=7, device=dev)
+    h = synth.activations(T, cfg.n_embd, seed=7, device=dev)
     op, ip, _ = lp(h)
     og, ig, _ = lg(h)
     assert torch.equal(ip, ig) and torch.equal(op, og)
