@@ -397,12 +397,12 @@ def layer_workload(args, torch, N, synth, dev):
     tok_s = K * T / (ms_total / 1e3)
 
     # per-phase durations: R further steps, one workspace each. Which kernels a phase runs follows the
-    # library's dispatch rule (moe.hip use_grouped / use_mq): t64 layers group from 8 tokens (or on request);
+    # library's dispatch rule (moe.hip use_grouped / use_mq): t64 layers group from 3 tokens (or on request);
     # stacked aligned Q4_K layers take the matrix-core kernels from 8 tokens (or on request).
     q4k = layout == "gguf" and cfg.ggml_type == synth.GGMLType.Q4_K
     mq = q4k and (args.dispatch == "mfma" or (args.dispatch == "auto" and T >= 8))
     grouped = mq or (args.dispatch == "grouped" and (layout == "t64" or q4k)) or (
-        layout == "t64" and args.dispatch == "auto" and T >= 8)
+        layout == "t64" and args.dispatch == "auto" and T >= 3)
     # (per pair, the down kernel combines: the combine phase launches nothing and is not captured)
     phases = (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN) + ((N.PHASE_COMBINE,) if grouped else ())
     phase_us = {}
@@ -573,7 +573,7 @@ def stack_workload(args, torch, N, synth, dev):
         gu_us = e0.elapsed_time(e1) * 1e3 / n_layers
         per_layer = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
         gu_bytes = sum(_expert_bytes(cfg, d)[0] for d in per_layer) / n_layers
-        grouped = args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 8)
+        grouped = args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 3)
         kname = "moe_gu_grouped_kernel" if grouped else "moe_gu_kernel"
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         step_alg = sum(sum(_expert_bytes(cfg, d)) for d in per_layer)

@@ -2698,7 +2698,11 @@ struct MoePlan {
   bool mq;  // grouped Q4_K on the matrix cores: xqh / xqa hold activation terms (mq_row_bytes per row)
 };
 
-constexpr int GRP_AUTO_MIN_T = 8;  // NSX_DISPATCH_AUTO groups from this many tokens
+// NSX_DISPATCH_AUTO groups t64 layers from GRP_AUTO_MIN_T tokens (the 36-layer GPT-OSS stack at T = 2 / 3 / 5 / 7:
+// 455 / 620 / 832 / 1034 us per pair, 520 / 591 / 778 / 939 us grouped), and takes the Q4_K matrix-core
+// kernels from MQ_AUTO_MIN_T tokens
+constexpr int GRP_AUTO_MIN_T = 3;
+constexpr int MQ_AUTO_MIN_T = 8;
 
 // The Q4_K kernels take K <= 4096 and 16-byte aligned expert rows.
 static bool q4k_fast(const nsx_moe_layer* L) {
@@ -2712,9 +2716,9 @@ static bool q4k_fast(const nsx_moe_layer* L) {
 }
 
 // Grouped Q4_K on the matrix cores (moe_q4k_mfma_kernel): on request, and by
-// AUTO from GRP_AUTO_MIN_T tokens (config 4, T=32: 0.58 ms against 0.92 ms per pair).
+// AUTO from MQ_AUTO_MIN_T tokens (config 4, T=32: 0.58 ms against 0.92 ms per pair).
 static bool use_mq(const nsx_moe_layer* L, int64_t T) {
-  const bool want = L->dispatch == NSX_DISPATCH_MFMA || (L->dispatch == NSX_DISPATCH_AUTO && T >= GRP_AUTO_MIN_T);
+  const bool want = L->dispatch == NSX_DISPATCH_MFMA || (L->dispatch == NSX_DISPATCH_AUTO && T >= MQ_AUTO_MIN_T);
   return want && L->layout == NSX_LAYOUT_GGUF && q4k_fast(L);
 }
 

@@ -42,7 +42,7 @@ class MoELayer:
         tensors (one slab each). dispatch: "pairs" runs each (token, expert)
         pair on its own, "grouped" sorts the pairs by expert and reads each
         active expert once per work item of up to 16 tokens (t64 layout),
-        "auto" groups from 8 tokens on (t64). These give identical outputs.
+        "auto" groups from 3 tokens on (t64). These give identical outputs.
         "mfma" groups stacked Q4_K experts and runs them on the matrix cores
         (within 1e-5 of the others, not identical); "auto" takes it for such
         layers from 8 tokens on."""

@@ -58,10 +58,11 @@ def test_stack_norm_in_router_equals_separate_norm(dev, T):
     assert torch.equal(y, res)
 
 
-@pytest.mark.parametrize("T,weight", [(5, True), (9, True), (40, False), (300, True)])
+@pytest.mark.parametrize("T,weight", [(2, True), (3, True), (5, True), (9, True), (40, False), (300, True)])
 def test_forward_addnorm_equals_forward_then_norm(dev, T, weight):
     """MoELayer.forward_addnorm (nsx_moe_forward_addnorm: the next block's residual add and
-    norm in the layer's last launch -- the combine kernel on the grouped path, from 8 tokens)
+    norm in the layer's last launch -- the combine kernel on the grouped path, from 3 tokens;
+    a separate add + norm launch per pair)
     against forward() followed by add_rms_norm: the same bits for x + out and the normed
     h, in place (x_out = x, h_out = h) and apart, and the same routing."""
     from nurostream_amd import synth
