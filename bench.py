@@ -398,9 +398,9 @@ def layer_workload(args, torch, N, synth, dev):
 
     # per-phase durations: R further steps, one workspace each. Which kernels a phase runs follows the
     # library's dispatch rule (moe.hip use_grouped / use_mq): t64 layers group from 3 tokens (or on request);
-    # stacked aligned Q4_K layers take the matrix-core kernels from 8 tokens (or on request).
+    # stacked aligned Q4_K layers take the matrix-core kernels from 104 (token, expert) pairs (or on request).
     q4k = layout == "gguf" and cfg.ggml_type == synth.GGMLType.Q4_K
-    mq = q4k and (args.dispatch == "mfma" or (args.dispatch == "auto" and T >= 8))
+    mq = q4k and (args.dispatch == "mfma" or (args.dispatch == "auto" and T * cfg.top_k >= 104))
     grouped = mq or (args.dispatch == "grouped" and (layout == "t64" or q4k)) or (
         layout == "t64" and args.dispatch == "auto" and T >= 3)
     # (per pair, the down kernel combines: the combine phase launches nothing and is not captured)

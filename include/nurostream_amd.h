@@ -58,7 +58,8 @@ enum { NSX_ACT_CLAMPED_SWIGLU = 0, NSX_ACT_SILU_MUL = 1 };
  * matrix cores (f16 products of the exact sc * q codes and a two-term split
  * of the activations; outputs within 1e-5 of the per-pair kernels' rather
  * than identical to them). AUTO groups t64 layers from T >= 3 and takes MFMA
- * for stacked aligned Q4_K layers from T >= 8; below that it runs pairs. */
+ * for stacked aligned Q4_K layers from T * top_k >= 104; below that it runs
+ * pairs. */
 enum { NSX_DISPATCH_AUTO = 0, NSX_DISPATCH_PAIRS = 1, NSX_DISPATCH_GROUPED = 2, NSX_DISPATCH_MFMA = 3 };
 
 const char *nsx_last_error(void);

@@ -2700,9 +2700,11 @@ struct MoePlan {
 
 // NSX_DISPATCH_AUTO groups t64 layers from GRP_AUTO_MIN_T tokens (the 36-layer GPT-OSS stack at T = 2 / 3 / 5 / 7:
 // 455 / 620 / 832 / 1034 us per pair, 520 / 591 / 778 / 939 us grouped), and takes the Q4_K matrix-core
-// kernels from MQ_AUTO_MIN_T tokens
+// kernels from MQ_AUTO_MIN_PAIRS (token, expert) pairs: a Qwen3-235B-shaped layer (top-8 of 128) at T = 8 /
+// 12 / 14 / 16 / 24 took 169 / 237 / 276 / 303 / 431 us per pair against 191 / 247 / 262 / 284 / 339 us on the
+// matrix cores, whose lead grows with the tokens per expert
 constexpr int GRP_AUTO_MIN_T = 3;
-constexpr int MQ_AUTO_MIN_T = 8;
+constexpr int MQ_AUTO_MIN_PAIRS = 104;
 
 // The Q4_K kernels take K <= 4096 and 16-byte aligned expert rows.
 static bool q4k_fast(const nsx_moe_layer* L) {
@@ -2716,9 +2718,9 @@ static bool q4k_fast(const nsx_moe_layer* L) {
 }
 
 // Grouped Q4_K on the matrix cores (moe_q4k_mfma_kernel): on request, and by
-// AUTO from MQ_AUTO_MIN_T tokens (config 4, T=32: 0.58 ms against 0.92 ms per pair).
+// AUTO from MQ_AUTO_MIN_PAIRS pairs (config 4, T=32: 0.37 ms against 0.56 ms per pair).
 static bool use_mq(const nsx_moe_layer* L, int64_t T) {
-  const bool want = L->dispatch == NSX_DISPATCH_MFMA || (L->dispatch == NSX_DISPATCH_AUTO && T >= MQ_AUTO_MIN_T);
+  const bool want = L->dispatch == NSX_DISPATCH_MFMA || (L->dispatch == NSX_DISPATCH_AUTO && T * L->top_k >= MQ_AUTO_MIN_PAIRS);
   return want && L->layout == NSX_LAYOUT_GGUF && q4k_fast(L);
 }
 

@@ -45,7 +45,7 @@ class MoELayer:
         "auto" groups from 3 tokens on (t64). These give identical outputs.
         "mfma" groups stacked Q4_K experts and runs them on the matrix cores
         (within 1e-5 of the others, not identical); "auto" takes it for such
-        layers from 8 tokens on."""
+        layers from 104 (token, expert) pairs on (T * top_k)."""
         if dispatch not in _DISPATCH:
             raise ValueError(f"dispatch {dispatch!r} not in {sorted(_DISPATCH)}")
         self.device = router_w.device
