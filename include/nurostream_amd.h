@@ -228,8 +228,13 @@ int nsx_moe_forward_addnorm(const nsx_moe_layer *L, const float *h, int64_t T,
  * and NSX_PHASE_COMBINE (grouped dispatch: the ascending-expert combine;
  * otherwise nothing). A phase reads what the earlier phases of the same call
  * sequence left in the workspace; running the four in order is
- * nsx_moe_forward (which skips the top-k launch where a gate/up kernel selects
- * the top-k itself: per-pair t64, and per-pair Q4_K below 16 tokens). Callers
+ * nsx_moe_forward (which skips the top-k launch where a later kernel selects
+ * the top-k itself: the per-pair t64 gate/up kernel, per-pair Q4_K below 16
+ * tokens, and below 16 tokens on the grouped path the sort kernel -- or, for
+ * t64 layers with at most 64 (token, expert) pairs, the grouped gate/up
+ * kernel, which then sorts the pairs itself and launches no sort kernel).
+ * Only a call that runs the router and gate/up phases together does this: a
+ * call that ends with the router phase always writes ids/weights. Callers
  * use it to interleave other work (block reads, another layer's router)
  * between phases or to time one phase; the
  * reference runs these steps as separate torch calls
