@@ -3134,6 +3134,18 @@ extern "C" int nsx_moe_forward_addnorm(const nsx_moe_layer* L, const float* h, i
   const int64_t tc = grp_chunk_tokens(L), k = L->top_k, ne = L->n_embd;
   for (int64_t t0 = 0; t0 < T; t0 += tc) {  // grouped passes in token order, as nsx_moe_forward
     const int64_t nt = std::min(tc, T - t0);
+    // moe_run plans each pass for its own token count: a short last pass (AUTO: t64 below GRP_AUTO_MIN_T tokens,
+    // Q4_K below MQ_AUTO_MIN_PAIRS pairs) runs the per-pair kernels, whose down kernel combines and which take no
+    // fused add + norm -- that pass gets the separate norm, as the ungrouped branch above
+    if (!use_grouped(L, nt)) {
+      if ((rc = moe_run(L, h + t0 * ne, nt, h_out + t0 * ne, ids + t0 * k, weights + t0 * k, workspace,
+                        workspace_bytes, stream, NSX_PHASE_ROUTER, NSX_PHASE_COMBINE)))
+        return rc;
+      if ((rc = nsx_add_rmsnorm(x + t0 * ne, h_out + t0 * ne, nt, ne, eps, norm_w, x_out + t0 * ne, h_out + t0 * ne,
+                                stream)))
+        return rc;
+      continue;
+    }
     const AddNorm an{x + t0 * ne, norm_w, eps, x_out + t0 * ne, h_out + t0 * ne};
     // (no combine output: h_out stands in for `out`, which the grouped phases before the combine never touch)
     rc = moe_run(L, h + t0 * ne, nt, h_out + t0 * ne, ids + t0 * k, weights + t0 * k, workspace, workspace_bytes,

@@ -89,6 +89,37 @@ def test_forward_addnorm_equals_forward_then_norm(dev, T, weight):
         layer.forward_addnorm(h, xi, w, 1e-5, x_out=xo, h_out=xi)
 
 
+@pytest.mark.parametrize("name,layout,T", [("gptoss-small", "t64", 1025), ("gptoss-small", "t64", 1026),
+                                           ("gptoss-small", "t64", 1027), ("qwen3-small", "gguf", 513),
+                                           ("qwen3-small", "gguf", 525)])
+def test_forward_addnorm_short_last_pass(dev, name, layout, T):
+    """A grouped call longer than one pass (4096 pairs: 1024 tokens at top-4, 512
+    at top-8) whose last pass is too short to group under AUTO (t64: fewer than 3
+    tokens; Q4_K on the matrix cores: fewer than 104 pairs) runs that pass on the
+    per-pair kernels; its x + out and normed rows must still be written, with the
+    same bits as forward() followed by add_rms_norm on every token."""
+    from nurostream_amd import synth
+    from nurostream_amd.compute.ops import add_rms_norm
+    from moe_cases import _layer
+    cfg = _small(name)
+    t = synth.make_layer(cfg, seed=33, device=dev)
+    layer = _layer(cfg, t, layout)
+    h = synth.activations(T, cfg.n_embd, seed=43, device=dev)
+    x = synth.activations(T, cfg.n_embd, seed=44, device=dev)
+    w = (1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(6))).to(dev)
+    out, ids, wts = layer.forward(h)
+    xr = torch.empty_like(x)
+    hr = add_rms_norm(x, out, w, 1e-5, sum_out=xr)
+    xo = torch.full_like(x, float("nan"))
+    ho = torch.full_like(x, float("nan"))
+    ids2, wts2 = layer.forward_addnorm(h, x, w, 1e-5, x_out=xo, h_out=ho)
+    torch.cuda.synchronize()
+    assert torch.equal(ids2, ids) and torch.equal(wts2, wts)
+    tail = slice(T - 8, T)  # the short pass's rows first, so a failure names them
+    assert torch.equal(xo[tail], xr[tail]) and torch.equal(ho[tail], hr[tail])
+    assert torch.equal(xo, xr) and torch.equal(ho, hr)
+
+
 @pytest.mark.parametrize("T", [1, 2, 9])
 def test_gptoss_ffn_stack_matches_oracle(dev, T):
     from nurostream_amd import synth
