@@ -11,7 +11,10 @@ activations already resident in HBM.
 Weights of `--layers` independently seeded layers (1.7 GB of experts each)
 rotate step by step and every step has its own tokens, so the expert bytes of
 a step come from HBM rather than the 256 MB Infinity Cache. The K timed steps
-run as one HIP graph (launch overhead as in a serving loop). Per-kernel
+are captured as one HIP graph (launch overhead as in a serving loop); after
+one untimed replay, `--replays` replays run back to back with a HIP event
+between each two, and `ms_per_step` is the median replay over K (the fastest
+and slowest are in `timing`). Per-kernel
 durations: `--profile-steps` further steps, each with its own workspace, go
 through the layer phase by phase (nsx_moe_phase); each phase is one HIP graph
 of that phase launched back to back over all those steps, timed with HIP
@@ -55,8 +58,17 @@ Other workloads (`--workload`, one JSON line each, for the design notes):
 
 Prints one JSON line (the driver's contract) with a `roofline` object for the
 dominant kernel (the gate/up dequant-GEMV) and a `cpu_baseline` object: the
-numpy restatement of the reference path (oracle/) on host cores, over a
-bounded sample of the same workload (default workload only).
+reference's torch CPU path restated under oracle/, on the host cores, over a
+bounded sample of the same workload.
+
+The default run also measures the other BASELINE configs, each at its own
+default steps and with a short CPU baseline, and adds them to the same line
+under "configs" (compact: ms_per_step, value, spread, roofline kernel /
+bytes / avg_us / frac, cpu_baseline): "1" (q4_0-gemv), "3" (gptoss-t128),
+"4_t1" / "4_t32" (qwen3-t1 / -t32), "5_t1" / "5_t8" (one resident 36-layer
+stack at T=1 and T=8) and "5b_t1" (the 25%-host stack at T=1: the kernels
+reading host tiles over PCIe, and under "prefetch" the same stack staging its
+host blocks through BlockPrefetcher at depth 4). `--configs none` skips them.
 """
 from __future__ import annotations
 
@@ -67,6 +79,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+PCIE_PEAK_GBS = 64.0  # PCIe Gen5 x16, one direction
 WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "stack-t1", "stack-t8", "stack-t1-host25",
              "stack-t8-host25", "q4_0-gemv", "lmhead-q6k", "lmhead-q8", "disk-stream", "gptoss-token")
 
@@ -105,25 +118,50 @@ def _parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-probe", action="store_true", help="skip the HBM read-bandwidth probe")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--host-mode", choices=("read", "stage"), default="read",
-                   help="config 5b: kernels read pinned host tiles over PCIe (read) or DMA-stage them per layer")
+    p.add_argument("--host-mode", choices=("read", "stage", "prefetch"), default="read",
+                   help="config 5b: kernels read pinned host tiles over PCIe (read), or they are DMA-staged per "
+                        "layer all at once (stage) or through BlockPrefetcher at depth 4 (prefetch)")
     p.add_argument("--context", type=int, default=1024,
                    help="gptoss-token: positions already in the KV cache when the timed tokens start")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after the run, copy a buffer of this size 3 times (calibrates rocprofv3 byte counters)")
+    p.add_argument("--replays", type=int, default=20,
+                   help="timed replays of the captured steps (after one untimed replay); the median is reported")
+    p.add_argument("--configs", choices=("all", "none"), default="all",
+                   help="default workload only: also measure BASELINE configs 1, 3, 4, 5 and 5b (compact results "
+                        "under 'configs'), each at its own default steps")
+    p.add_argument("--sub-cpu-seconds", type=float, default=3.0,
+                   help="budget of each sub-config's CPU baseline sample")
     return p.parse_args()
+
+
+def csrc_digest():
+    """sha256 (first 16 hex digits) over the library's HIP sources, in name
+    order: the code a committed counter measurement was taken on."""
+    import hashlib
+    d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "nurostream_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".h")):
+            with open(os.path.join(d, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
 
 
 def _traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size),
-    or None when no such measurement is committed."""
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size,
+    written by bench_pmc.py), or None when there is no such measurement or it
+    was taken on other kernel sources than the ones built now."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.json")
     try:
         with open(path) as f:
-            rec = json.load(f).get("kernels", {}).get(kernel)
+            doc = json.load(f)
     except (OSError, ValueError):
         return None
+    if doc.get("csrc_digest") != csrc_digest():
+        return None
+    rec = doc.get("kernels", {}).get(kernel)
     return None if rec is None else rec.get("traffic_bytes")
 
 
@@ -208,10 +246,9 @@ def _cpu_baseline_layer(torch, cfg, t_cpu, h, budget_s, block_rows=512, n_layers
             + ("" if n_sample == len(chosen) else " (time scaled to all of them)"))
     return {"value": round(T / step_s, 4), "unit": "tok/s", "cores": n, "kind": "port",
             "cpu_model": model, "ms_per_step": round(step_s * 1e3, 2),
-            "sample": f"one step of {T} token(s) through {'one layer' if n_layers == 1 else f'layer 0, scaled to {n_layers} layers'}: "
-                      f"router, then {what} via oracle.torch_path (the reference's torch CPU path: per "
-                      f"{block_rows}-row block dequantize then x @ w.T in fp32) with torch.set_num_threads({n}); "
-                      f"median of {len(runs)} runs after 3 warm-ups (expert runs {', '.join(f'{r:.3f}' for r in runs)} s)"}
+            "sample": f"{T} token(s) through {'one layer' if n_layers == 1 else f'layer 0 (x{n_layers} layers)'}: "
+                      f"router, {what}; oracle.torch_path ({block_rows}-row blocks: dequantize, x @ w.T, fp32), "
+                      f"{n} threads, median of {len(runs)} after 3 warm-ups"}
 
 
 def _cpu_baseline_gemv(torch, raw_cpu, t, x, rows, K, budget_s, block_rows=512, unit="tok/s", nbytes=None):
@@ -236,10 +273,9 @@ def _cpu_baseline_gemv(torch, raw_cpu, t, x, rows, K, budget_s, block_rows=512, 
     return {"value": round(value, 4 if unit == "tok/s" else 2), "unit": unit, "cores": n, "kind": "port",
             "cpu_model": model, "ms_per_pass": round(pass_s * 1e3, 3),
             "sample": f"{'the whole' if n_rows == rows else f'the first {n_rows} rows of the'} {rows} x {K} matrix"
-                      + ("" if n_rows == rows else " (time scaled to every row)")
-                      + f", T=1, via oracle.torch_path.stream_linear (the reference's CPU stream_linear: per "
-                      f"{block_rows}-row block dequantize then x @ w.T in fp32) with torch.set_num_threads({n}); "
-                      f"median of {len(runs)} runs after 3 warm-ups ({', '.join(f'{r:.4f}' for r in runs)} s)"}
+                      + ("" if n_rows == rows else " (scaled to every row)")
+                      + f", T=1; oracle.torch_path.stream_linear ({block_rows}-row blocks: dequantize, x @ w.T, fp32), "
+                      f"{n} threads, median of {len(runs)} after 3 warm-ups"}
 
 
 def _build_layer(torch, synth, cfg, li, args, dev, zipf, keep_cpu):
@@ -265,9 +301,25 @@ def _build_layer(torch, synth, cfg, li, args, dev, zipf, keep_cpu):
     return layer, t_cpu, c, layout
 
 
-def _graph_time(torch, run_steps, W, K):
-    """Eager warm-up steps 0..W-1, then steps W..W+K-1 captured as one graph
-    and replayed once under HIP events: (ms total, wall seconds, stream)."""
+class _Timed:
+    """Replays of a captured run of K steps: `ms` is the median replay in ms,
+    `lo` / `hi` the fastest and slowest, `n` the number timed."""
+
+    def __init__(self, times, wall_s, stream, K):
+        ts = sorted(times)
+        self.ms, self.lo, self.hi, self.n = ts[len(ts) // 2], ts[0], ts[-1], len(ts)
+        self.wall_s, self.stream, self.K = wall_s, stream, K
+
+    def spread(self):
+        """[fastest, median, slowest] ms per step over the timed replays."""
+        return [round(v / self.K, 5) for v in (self.lo, self.ms, self.hi)]
+
+
+def _graph_time(torch, run_steps, W, K, replays=20):
+    """Eager warm-up steps 0..W-1, then steps W..W+K-1 captured as one graph.
+    One untimed replay (the graph's upload), then `replays` replays queued back
+    to back on the capture stream with a HIP event between each two, so every
+    replay has its own interval and the host runs ahead of the GPU: a _Timed."""
     run_steps(range(W))
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
@@ -276,13 +328,19 @@ def _graph_time(torch, run_steps, W, K):
         with torch.cuda.graph(graph, stream=stream):
             run_steps(range(W, W + K))
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_wall = time.perf_counter()
-    ev0.record()
-    graph.replay()
-    ev1.record()
+    n = max(1, replays)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    with torch.cuda.stream(stream):
+        graph.replay()  # upload + first run, untimed
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter()
+        evs[0].record(stream)
+        for i in range(n):
+            graph.replay()
+            evs[i + 1].record(stream)
     torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1), time.perf_counter() - t_wall, stream
+    wall = time.perf_counter() - t_wall
+    return _Timed([evs[i].elapsed_time(evs[i + 1]) for i in range(n)], wall, stream, K)
 
 
 def _expert_bytes(cfg, n_experts):
@@ -307,8 +365,7 @@ _WORKLOAD = {"gptoss-decode": "gpt-oss-120b MoE layer, decode batch 1 (BASELINE 
 def _dtype_label(cfg, layout, mq):
     """The arithmetic the expert kernels run."""
     if layout == "t64":
-        return ("mxfp4 weights x 4-term e4m3 activation split (block-scaled MFMA, fp32 accumulate; the hardware "
-                "sums 8-product groups with ~12 kept bits)")
+        return "mxfp4 weights x 4-term e4m3 activation split, block-scaled MFMA, fp32 accumulate"
     if mq:
         return "q4_k codes as exact f16 (sc*q) x 2-term f16 activation split (f16 MFMA, fp32 accumulate)"
     if cfg.ggml_type.name == "Q4_K":
@@ -318,12 +375,12 @@ def _dtype_label(cfg, layout, mq):
 
 
 def _read_probe(torch, N, dev):
-    """Same-box HBM read bandwidth (nsx_read_probe) beside the 8 TB/s peak:
-    35,343,360 bytes (one config-2 gate/up launch) with the gate/up kernel's
-    grid (180 workgroups of 1024 threads) and with larger grids, and 1 GiB.
-    Each figure is a graph of back-to-back launches over distinct regions of a
-    2 GiB buffer (more than the 256 MB Infinity Cache between reuses), timed
-    with HIP events around its replay on the launching stream."""
+    """Same-box HBM read bandwidth (nsx_read_probe) beside the 8 TB/s peak, at
+    the sizes of config 2's two expert launches: 35,343,360 bytes (gate/up)
+    and 17,671,680 bytes (down), each over several grids, and 1 GiB. Each
+    figure is a graph of back-to-back launches over distinct regions of a 2 GiB
+    buffer (more than the 256 MB Infinity Cache between reuses), timed with HIP
+    events around its replay on the launching stream; the best grid counts."""
     lib = N.load()
     buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
     buf.fill_(1)
@@ -346,17 +403,15 @@ def _read_probe(torch, N, dev):
             e1.record(stream)
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / len(regions)
-        return {"bytes": nbytes, "workgroups": wgs, "threads": threads, "us": round(us, 3),
-                "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        return round(nbytes / (us * 1e-6) / 1e9, 1)
 
-    gu = 35343360
-    rows = [timed(gu, w, t) for w, t in ((180, 1024), (256, 1024), (512, 1024), (1024, 256), (2048, 256),
-                                         (4096, 256), (2048, 512))]
+    grids = ((180, 1024), (256, 1024), (512, 1024), (1024, 256), (2048, 256), (4096, 256))
+    gu = [timed(35343360, w, t) for w, t in grids]
+    dn = [timed(17671680, w, t) for w, t in grids]
     big = [timed(1 << 30, w, t) for w, t in ((4096, 1024), (16384, 256))]
     del buf
     torch.cuda.empty_cache()
-    return {"35MB": rows, "1GiB": big, "best_35MB_GBps": max(r["GBps"] for r in rows),
-            "expert_grid_35MB_GBps": rows[0]["GBps"], "best_1GiB_GBps": max(r["GBps"] for r in big)}
+    return {"35MB_GBps": max(gu), "35MB_expert_grid_GBps": gu[0], "17.7MB_GBps": max(dn), "1GiB_GBps": max(big)}
 
 
 def layer_workload(args, torch, N, synth, dev):
@@ -392,7 +447,8 @@ def layer_workload(args, torch, N, synth, dev):
         for i in rng:
             layers[i % n_layers].forward(X[i], out=outs[i], ids=ids[i], weights=wts[i])
 
-    ms_total, wall_s, stream = _graph_time(torch, run_steps, W, K)
+    tm = _graph_time(torch, run_steps, W, K, args.replays)
+    ms_total, wall_s, stream = tm.ms, tm.wall_s, tm.stream
     ms_per_step = ms_total / K
     tok_s = K * T / (ms_total / 1e3)
 
@@ -459,8 +515,7 @@ def layer_workload(args, torch, N, synth, dev):
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname),
                     "kernel": kname, "bytes_per_launch": int(kbytes), "avg_us": round(kus, 3),
-                    "timing": f"HIP events around a graph of {R} back-to-back gate/up phases (one per token group, "
-                              "each with its own workspace) on the launching stream"}
+                    "timing": f"graph of {R} gate/up phases, each its own tokens and workspace"}
         if len(gu_phase) > 1:
             roofline["note"] = "avg_us is the whole gate/up phase: " + " + ".join(gu_phase)
     step_bytes = sum(_expert_bytes(cfg, mean_distinct))
@@ -470,9 +525,6 @@ def layer_workload(args, torch, N, synth, dev):
                      "down": round(phase_us[N.PHASE_DOWN], 3)}
         if grouped:
             kernel_us["combine"] = round(phase_us[N.PHASE_COMBINE], 3)
-        if layout == "t64" and not grouped:
-            kernel_us["note"] = ("the router phase run on its own also launches the top-k (its ids are outputs); "
-                                 "in the forward the gate/up kernel selects the top-k itself")
     result = {
         "metric": _METRIC[name],
         "value": round(tok_s, 2),
@@ -492,7 +544,7 @@ def layer_workload(args, torch, N, synth, dev):
         "distinct_experts_per_step": round(mean_distinct, 2),
         "expert_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "kernel_us": kernel_us,
-        "wall_s": round(wall_s, 4),
+        "timing": {"replays": tm.n, "ms_per_step_min_med_max": tm.spread(), "wall_s": round(wall_s, 4)},
         "roofline": roofline,
     }
     if zipf:
@@ -502,32 +554,53 @@ def layer_workload(args, torch, N, synth, dev):
     result["cpu_baseline"] = None if args.no_cpu else _cpu_baseline_layer(
         torch, cfg, t_cpu, X[0].cpu(), args.cpu_seconds)
     if default and not args.no_probe:
-        result["hbm_read_probe"] = _read_probe(torch, N, dev)
-        best = result["hbm_read_probe"]["best_35MB_GBps"]
+        probe = result["hbm_read_probe"] = _read_probe(torch, N, dev)
         if roofline is not None:
-            roofline["frac_of_probe"] = round(roofline["achieved"] / best, 4)
-            roofline["probe_GBps"] = best
+            roofline["frac_of_probe"] = round(roofline["achieved"] / probe["35MB_GBps"], 4)
+        if kernel_us is not None:  # the down kernel against the same-size read
+            dn_gbs = dn_bytes / (kernel_us["down"] * 1e-6) / 1e9
+            kernel_us["down_frac"] = round(dn_gbs / HBM_PEAK_GBS, 4)
+            kernel_us["down_frac_of_probe"] = round(dn_gbs / probe["17.7MB_GBps"], 4)
     return result
 
 
-def stack_workload(args, torch, N, synth, dev):
-    """36 resident layers chained x <- x + moe_l(rms_norm(x))."""
+def build_stack(args, torch, synth, dev, name):
+    """The config-5 stack (resident) or config-5b stack (25% of the 512-row
+    blocks in pinned host RAM, host mode args.host_mode) for workload `name`."""
     from nurostream_amd.model.gpt_oss import GptOssFFNStack, GptOssHostStreamedStack
-    name = args.workload
-    cfg_name, T, K0, W0, L0, _ = _DEFAULTS[name]
-    cfg = getattr(synth, cfg_name)
-    K = args.steps if args.steps is not None else K0
-    W = args.warmup if args.warmup is not None else W0
-    n_layers = args.layers if args.layers is not None else L0
-    streamed = name.endswith("host25")
-    if streamed:
+    cfg = getattr(synth, _DEFAULTS[name][0])
+    n_layers = args.layers if args.layers is not None else _DEFAULTS[name][4]
+    if name.endswith("host25"):
         stack = GptOssHostStreamedStack.synthetic(cfg, n_layers, seed=args.seed, device=dev, host_fraction=0.25,
-                                                  block_rows=512, dispatch=args.dispatch, mode=args.host_mode)
+                                                  block_rows=512, dispatch=args.dispatch, mode=args.host_mode,
+                                                  depth=4)
     else:
         stack = GptOssFFNStack.synthetic(cfg, n_layers, seed=args.seed, device=dev, layout=args.layout,
                                          dispatch=args.dispatch)
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+    return stack
+
+
+def stack_workload(args, torch, N, synth, dev, stack=None, cpu_cache=None):
+    """BASELINE config 5: 36 resident layers chained x <- x + moe_l(rms_norm(x));
+    5b (`*-host25`): 25% of the blocks in pinned host RAM, reached as
+    args.host_mode says ("read": the kernels read them over PCIe, one graph per
+    step; "stage" / "prefetch": copied into staging slots per layer, all at once
+    or through BlockPrefetcher at depth 4, eager with one host sync per layer).
+    `stack` reuses a stack built by build_stack; `cpu_cache` (a dict) keeps the
+    CPU baseline's per-layer time between calls on the same layer shape."""
+    name = args.workload
+    cfg_name, T, K0, W0, L0, _ = _DEFAULTS[name]
+    cfg = getattr(synth, cfg_name)
+    K = args.steps if args.steps is not None else K0
+    W = args.warmup if args.warmup is not None else W0
+    streamed = name.endswith("host25")
+    if stack is None:
+        stack = build_stack(args, torch, synth, dev, name)
+    elif streamed:
+        stack.set_mode(args.host_mode)
+    n_layers = len(stack.layers)
     n_steps = W + K
     X = synth.activations(n_steps * T, cfg.n_embd, seed=args.seed + 1, device=dev).view(n_steps, T, cfg.n_embd)
     Y = torch.empty_like(X)
@@ -536,22 +609,28 @@ def stack_workload(args, torch, N, synth, dev):
         for i in rng:
             stack(X[i], out=Y[i])
 
-    staged = streamed and args.host_mode == "stage"
-    if staged:  # host synchronisations inside a step: timed eagerly
+    staged = streamed and args.host_mode != "read"
+    tm = None
+    if staged:  # host synchronisations inside a step: timed eagerly, an event pair per step
         run_steps(range(W))
         torch.cuda.synchronize()
         b0 = stack.bytes_from_host
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
         t_wall = time.perf_counter()
-        ev0.record()
-        run_steps(range(W, W + K))
-        ev1.record()
+        evs[0].record()
+        for j, i in enumerate(range(W, W + K)):
+            stack(X[i], out=Y[i])
+            evs[j + 1].record()
         torch.cuda.synchronize()
         wall_s = time.perf_counter() - t_wall
-        ms_total = ev0.elapsed_time(ev1)
+        per = sorted(evs[j].elapsed_time(evs[j + 1]) for j in range(K))
+        ms_total = per[len(per) // 2] * K  # the median step
+        spread = [round(per[0], 5), round(per[len(per) // 2], 5), round(per[-1], 5)]
         host_bytes_step = (stack.bytes_from_host - b0) / K
     else:
-        ms_total, wall_s, stream = _graph_time(torch, run_steps, W, K)
+        tm = _graph_time(torch, run_steps, W, K, args.replays)
+        ms_total, wall_s, stream = tm.ms, tm.wall_s, tm.stream
+        spread = tm.spread()
     ids, _ = stack.last_routing(T)
     ids_cpu = ids.cpu()
     roofline = None
@@ -563,14 +642,18 @@ def stack_workload(args, torch, N, synth, dev):
         with torch.cuda.stream(stream), torch.cuda.graph(g, stream=stream):
             for li, layer in enumerate(stack.layers):
                 layer.phase(N.PHASE_GATE_UP, h_b, y_b, ids_b[li], wts_b[li], layer.workspace(T))
+        gts = []
         with torch.cuda.stream(stream):
             g.replay()  # upload, untimed
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            g.replay()
-            e1.record(stream)
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
+                gts.append((e0, e1))
         torch.cuda.synchronize()
-        gu_us = e0.elapsed_time(e1) * 1e3 / n_layers
+        gt = sorted(a.elapsed_time(b) for a, b in gts)
+        gu_us = gt[len(gt) // 2] * 1e3 / n_layers
         per_layer = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
         gu_bytes = sum(_expert_bytes(cfg, d)[0] for d in per_layer) / n_layers
         grouped = args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 3)
@@ -580,22 +663,23 @@ def stack_workload(args, torch, N, synth, dev):
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname) if T == 1 else None,
                     "kernel": kname, "bytes_per_launch": int(gu_bytes), "avg_us": round(gu_us, 3),
-                    "timing": f"HIP events around a graph of the {n_layers} layers' gate/up phases on the "
-                              "launching stream",
+                    "timing": f"median of 5 replays of a graph of the {n_layers} layers' gate/up phases",
                     "step_frac": round(step_alg / (ms_total / K * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         if grouped:
             roofline["note"] = "avg_us is the whole gate/up phase: moe_sort_kernel + moe_gu_grouped_kernel"
-        if streamed:
-            roofline["note"] = ("25% of the expert tiles sit in pinned host RAM and are read over PCIe by the "
-                                "kernels: the gate/up launches are PCIe-bound, not HBM-bound")
     cpu = None
     if not args.no_cpu:
-        t0 = synth.make_layer(cfg, seed=args.seed, device=dev, layer=0)
-        t_cpu = {k: (None if v is None else v.float().cpu().numpy() if v.dtype != torch.uint8 else v.cpu().numpy())
-                 for k, v in t0.items()}
-        del t0
-        torch.cuda.empty_cache()
-        cpu = _cpu_baseline_layer(torch, cfg, t_cpu, X[0].cpu(), args.cpu_seconds, n_layers=n_layers)
+        key = (cfg_name, T)
+        cpu = None if cpu_cache is None else cpu_cache.get(key)
+        if cpu is None:
+            t0 = synth.make_layer(cfg, seed=args.seed, device=dev, layer=0)
+            t_cpu = {k: (None if v is None else v.float().cpu().numpy() if v.dtype != torch.uint8
+                         else v.cpu().numpy()) for k, v in t0.items()}
+            del t0
+            torch.cuda.empty_cache()
+            cpu = _cpu_baseline_layer(torch, cfg, t_cpu, X[0].cpu(), args.cpu_seconds, n_layers=n_layers)
+            if cpu_cache is not None:
+                cpu_cache[key] = cpu
     if streamed and not staged:  # the kernels read the host tiles themselves: bytes of the last step's routing
         host_bytes_step = stack.host_bytes_of_routing(ids_cpu)
     distinct = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
@@ -605,12 +689,25 @@ def stack_workload(args, torch, N, synth, dev):
     extra = {}
     if streamed:
         host_gb = sum(st.host_bytes for st in stack.stores) / 1e9
+        pcie = host_bytes_step / (ms_per_step * 1e-3) / 1e9
         extra = {"host_resident_GB": round(host_gb, 2), "host_bytes_per_step": int(host_bytes_step),
-                 "pcie_GBps": round(host_bytes_step / (ms_total / K * 1e-3) / 1e9, 1), "host_mode": args.host_mode,
-                 "note": ("value includes the host-to-device copies (PCIe-inclusive); eager, one host sync per layer"
-                          if staged else "value includes the kernels' reads of pinned host RAM over PCIe "
-                          "(PCIe-inclusive); one graph per step, no host sync; host bytes from the last step's "
-                          "routing")}
+                 "pcie_GBps": round(pcie, 1), "pcie_frac": round(pcie / PCIE_PEAK_GBS, 4),
+                 "host_mode": args.host_mode,
+                 "note": {"stage": "PCIe-inclusive: every host block of the chosen experts DMA-copied per layer at "
+                                   "once over 4 copy streams; eager, one host sync per layer",
+                          "prefetch": "PCIe-inclusive: host blocks through BlockPrefetcher (depth 4, 512-row blocks, "
+                                      "arena of 5 blocks), DMA copies on side streams into staging slots; eager, one "
+                                      "host sync per layer",
+                          "read": "PCIe-inclusive: the kernels read pinned host tiles over PCIe; one graph per step, "
+                                  "no host sync; host bytes from the last step's routing"}[args.host_mode]}
+        if args.host_mode == "prefetch":
+            extra["prefetch"] = stack.prefetch_stats()
+        # a step reading 25% of its expert bytes from pinned host RAM is PCIe-bound: its roofline is the link's
+        roofline = {"bound": "pcie", "achieved": round(pcie, 1), "peak": PCIE_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(pcie / PCIE_PEAK_GBS, 4), "traffic": None,
+                    "kernel": f"whole step ({args.host_mode}: host blocks over PCIe)",
+                    "bytes_per_launch": int(host_bytes_step), "avg_us": round(ms_per_step * 1e3, 1),
+                    "timing": "the step's host bytes over its median time; peak = PCIe Gen5 x16, one direction"}
     return {
         "metric": f"MoE-FFN stack tok/s ({n_layers} GPT-OSS-120B-shaped MXFP4 layers, T={T}"
                   + (", 25% of blocks from pinned host RAM)" if streamed else ")"),
@@ -635,7 +732,8 @@ def stack_workload(args, torch, N, synth, dev):
         "distinct_experts_per_layer": round(mean_distinct, 2),
         "expert_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "roofline_tok_s": round(T / (step_bytes / (HBM_PEAK_GBS * 1e9)), 1),
-        "wall_s": round(wall_s, 4),
+        "timing": {"replays" if tm else "steps": tm.n if tm else K, "ms_per_step_min_med_max": spread,
+                   "wall_s": round(wall_s, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
@@ -664,7 +762,8 @@ def gemv_workload(args, torch, N, synth, dev):
             N.check(lib.nsx_fused_gemv(int(t), raws[i % n_copies].data_ptr(), rows, K, xs[i].data_ptr(), N.DT_F32,
                                        1, ys[i].data_ptr(), s), "fused_gemv")
 
-    ms, wall_s, _ = _graph_time(torch, run_steps, W, K_steps)
+    tm = _graph_time(torch, run_steps, W, K_steps, args.replays)
+    ms, wall_s = tm.ms, tm.wall_s
     us = ms * 1e3 / K_steps
     # parity spot check of the timed outputs against the oracle (a row block)
     from oracle import quant as OQ
@@ -703,7 +802,7 @@ def gemv_workload(args, torch, N, synth, dev):
                      "kernel": kname, "bytes_per_launch": alg_bytes, "avg_us": round(us, 3),
                      "timing": f"HIP events around a graph of {K_steps} launches on the launching stream"},
         "parity_max_rel_err": err,
-        "wall_s": round(wall_s, 4),
+        "timing": {"replays": tm.n, "ms_per_step_min_med_max": tm.spread(), "wall_s": round(wall_s, 4)},
         "cpu_baseline": cpu,
     }
     return out
@@ -967,6 +1066,80 @@ def token_workload(args, torch, N, synth, dev):
     }
 
 
+_SUBCONFIGS = (("1", "q4_0-gemv"), ("3", "gptoss-t128"), ("4_t1", "qwen3-t1"), ("4_t32", "qwen3-t32"),
+               ("5_t1", "stack-t1"), ("5_t8", "stack-t8"), ("5b_t1", "stack-t1-host25"))
+
+
+def _compact(r):
+    """The figures of one workload's line that the sub-config summary keeps."""
+    lo, _, hi = r["timing"]["ms_per_step_min_med_max"]
+    out = {"ms_per_step": r["ms_per_step"], "value": r["value"], "unit": r["unit"], "spread": [lo, hi]}
+    rf = r.get("roofline")
+    if rf:
+        out["roofline"] = {"kernel": rf["kernel"], "bytes_per_launch": rf.get("bytes_per_launch"),
+                           "avg_us": rf.get("avg_us"), "frac": rf["frac"]}
+        if rf.get("traffic") and rf.get("bytes_per_launch"):
+            out["roofline"]["traffic_x"] = round(rf["traffic"] / rf["bytes_per_launch"], 3)
+    cb = r.get("cpu_baseline")
+    if cb:
+        out["cpu_baseline"] = {"value": cb["value"], "cores": cb["cores"],
+                               "ms_per_step": cb.get("ms_per_step", cb.get("ms_per_pass"))}
+    for k in ("distinct_experts_per_step", "distinct_experts_per_layer", "pcie_GBps", "pcie_frac"):
+        if k in r:
+            out[k] = r[k]
+    return out
+
+
+def run_configs(args, torch, N, synth, dev):
+    """BASELINE configs 1, 3, 4 (T=1, 32), 5 (T=1, 8) and 5b (T=1: the kernels
+    reading the host blocks over PCIe, and the blocks staged through
+    BlockPrefetcher at depth 4), each at its workload's default steps, with a
+    short CPU baseline: {key: compact result}."""
+    import copy
+    import gc
+
+    def sub(workload, **kw):
+        a = copy.copy(args)
+        a.workload, a.steps, a.warmup, a.layers, a.profile_steps = workload, None, None, None, None
+        a.cpu_seconds, a.no_probe, a.copy_probe_mib = args.sub_cpu_seconds, True, 0
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+    def free():
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+    t0 = time.perf_counter()
+    out = {}
+    for key, wl in _SUBCONFIGS[:4]:
+        r = (gemv_workload if wl == "q4_0-gemv" else layer_workload)(sub(wl), torch, N, synth, dev)
+        out[key] = _compact(r)
+        del r
+        free()
+    cache = {}
+    stack = build_stack(sub("stack-t1"), torch, synth, dev, "stack-t1")
+    for key, wl in _SUBCONFIGS[4:6]:
+        out[key] = _compact(stack_workload(sub(wl), torch, N, synth, dev, stack=stack, cpu_cache=cache))
+    del stack
+    free()
+    hs = build_stack(sub("stack-t1-host25", host_mode="read"), torch, synth, dev, "stack-t1-host25")
+    r = _compact(stack_workload(sub("stack-t1-host25", host_mode="read"), torch, N, synth, dev, stack=hs,
+                                cpu_cache=cache))
+    pf = stack_workload(sub("stack-t1-host25", host_mode="prefetch"), torch, N, synth, dev, stack=hs,
+                        cpu_cache=cache)
+    lo, _, hi = pf["timing"]["ms_per_step_min_med_max"]
+    r["prefetch"] = {"ms_per_step": pf["ms_per_step"], "value": pf["value"], "pcie_GBps": pf["pcie_GBps"],
+                     "pcie_frac": pf["pcie_frac"], "spread": [lo, hi], "hits": pf["prefetch"]["hits"],
+                     "blocks": pf["prefetch"]["blocks"]}
+    out["5b_t1"] = r
+    del hs, pf
+    free()
+    out["wall_s"] = round(time.perf_counter() - t0, 1)
+    return out
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -994,6 +1167,8 @@ def main():
         result = token_workload(args, torch, N, synth, dev)
     else:
         result = layer_workload(args, torch, N, synth, dev)
+        if args.workload == "gptoss-decode" and args.configs == "all":
+            result["configs"] = run_configs(args, torch, N, synth, dev)
     if args.copy_probe_mib > 0:  # a plain copy of known size for the counter calibration
         n = args.copy_probe_mib << 18
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -1002,7 +1177,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    print(json.dumps(result), flush=True)
+    print(json.dumps(result, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

@@ -260,9 +260,111 @@ class _HostBlockStore:
         return sum(n for (ee, _), (loc, _, _, n) in self.where[kind].items() if ee == e and loc == "host")
 
 
+class _CopyFuture:
+    """One block's DMA copy in flight: `done` polls its event, `result` orders
+    the caller's stream after it on the GPU (no host wait) and returns the
+    block's device address."""
+
+    __slots__ = ("event", "address")
+
+    def __init__(self, event, address: int) -> None:
+        self.event, self.address = event, address
+
+    def done(self) -> bool:
+        return self.event.query()
+
+    def result(self) -> int:
+        torch.cuda.current_stream().wait_event(self.event)
+        return self.address
+
+    def cancel(self) -> bool:  # the copy is queued on the GPU already; its slot is the caller's
+        return False
+
+
+class _TileBlockSource:
+    """One layer's host-resident expert blocks behind the block-source protocol
+    BlockPrefetcher consumes (compute/blockffn.py:278-393 of the reference:
+    `gguf.tensors` with row geometry, `has_slab`, `submit_rows(name, lo, hi)
+    -> (future, nbytes)` under an arena lease, `reader.wait`, `arena`).
+
+    Tensor names are the projections ("gate", "up", "down"); rows are the
+    stacked experts' rows (expert e owns rows [e*out, (e+1)*out), as
+    io/source.py:38-62), and a row's bytes are its share of the t64 tiles, so
+    a block of 512 rows is 8 whole tiles. Windows whose blocks all sit in HBM
+    count as held slabs. A submitted block is copied from pinned host RAM by
+    DMA on the next of the stack's copy streams, straight to the address the
+    caller put in `dest[(name, lo)]` (its place in a staging slot), so no
+    block is copied twice; its future is that copy's event."""
+
+    def __init__(self, store: _HostBlockStore, rows: dict, K: dict, block_rows: int, arena, streams) -> None:
+        from ..format.gguf import GGMLType, TensorInfo
+        from ..io.source import BlockReader, _Index
+        self.store, self.rows, self.block_rows = store, rows, block_rows
+        self.arena, self.streams = arena, streams
+        self.reader = BlockReader()
+        n_expert = len(store.whole[store.kinds[0]])
+        infos = {}
+        for kind in store.kinds:
+            padded = store.tiles[kind] * 64
+            rb = store.per[kind] // padded
+            n_rows = n_expert * rows[kind]
+            infos[kind] = TensorInfo(kind, (K[kind], n_rows), GGMLType.MXFP4, 0, n_expert * store.per[kind],
+                                     geom=(n_rows, K[kind], rb))
+        self.gguf = _Index(infos)
+        self.dest: dict = {}
+        self._next = 0
+        self.bytes_copied = 0
+
+    def _block(self, name: str, lo: int, hi: int):
+        rows = self.rows[name]
+        e, r0 = divmod(lo, rows)
+        i = r0 // self.block_rows
+        if r0 % self.block_rows or hi != e * rows + min(rows, (i + 1) * self.block_rows):
+            raise ValueError(f"{name}: rows [{lo}, {hi}) are not one {self.block_rows}-row block of one expert")
+        return e, i
+
+    def is_resident(self, name: str) -> bool:
+        return False
+
+    def has_slab(self, name: str, lo: int, hi: int) -> bool:
+        rows, br = self.rows[name], self.block_rows
+        where = self.store.where[name]
+        for r in range(lo, hi, br):
+            e, r0 = divmod(r, rows)
+            if where[(e, r0 // br)][0] != "dev":
+                return False
+        return True
+
+    def submit_rows(self, name: str, start: int, end: int, *, timeout: float | None = None):
+        """DMA-copy one host block to dest[(name, start)]: (future, nbytes); the caller releases."""
+        from .. import _native as N
+        e, i = self._block(name, start, end)
+        loc, off, _b0, n = self.store.where[name][(e, i)]
+        if loc != "host":
+            raise ValueError(f"{name} rows [{start}, {end}) are in HBM: nothing to read")
+        dst = self.dest[(name, start)]
+        self.arena.acquire(n, timeout=timeout)
+        try:
+            cs = self.streams[self._next % len(self.streams)]
+            self._next += 1
+            seg = (C.c_uint64 * 1)(self.store.host[name].data_ptr() + off)
+            dd = (C.c_uint64 * 1)(dst)
+            nb = (C.c_int64 * 1)(n)
+            N.check(N.load().nsx_copy_blocks_async(1, seg, dd, nb, cs.cuda_stream, None), "copy_blocks_async")
+            ev = torch.cuda.Event()
+            ev.record(cs)
+            self.reader.stats.requests += 1
+            self.reader.stats.bytes_read += n
+            self.bytes_copied += n
+            return _CopyFuture(ev, dst), n
+        except BaseException:
+            self.arena.release(n)
+            raise
+
+
 class GptOssHostStreamedStack(GptOssFFNStack):
     """BASELINE config 5b: the FFN stack with a seeded share (25%) of the
-    experts' row blocks in pinned host RAM. Two ways to reach them:
+    experts' row blocks in pinned host RAM. Three ways to reach them:
 
     mode "read": every layer gets tile tables (MoELayer.set_tile_tables) that
     point each 64-row tile at HBM or at its pinned host block; the expert
@@ -274,29 +376,65 @@ class GptOssHostStreamedStack(GptOssFFNStack):
     (model/gpt_oss.py:121 does the same to pick its windows); every chosen
     expert matrix with host blocks is assembled in a staging slot -- its host
     blocks as DMA copies from pinned RAM (nsx_copy_blocks_async, all of the
-    layer's blocks queued at once), its HBM blocks as one gather kernel
-    (nsx_gather_copy) -- and the layer's expert address table points at the
-    slots for this step.
+    layer's blocks queued at once over COPY_STREAMS copy streams), its HBM
+    blocks as one gather kernel (nsx_gather_copy) -- and the layer's expert
+    address table points at the slots for this step.
+
+    mode "prefetch": as "stage", but the host blocks go through the
+    reference's prefetcher seam (compute/blockffn.py:278-393, one per layer as
+    model/gpt_oss.py:133-160 builds it): a plan of the chosen experts' host
+    blocks in the order the layer consumes them (ascending expert; gate, up,
+    down), read `depth` blocks ahead by BlockPrefetcher over the layer's
+    _TileBlockSource, each block a DMA copy on a copy stream into its slot
+    under an arena lease of depth + 1 blocks, taken in plan order.
 
     Either way the experts run in the same fused kernels as the resident
     stack, with the same arithmetic: outputs are identical to it."""
 
-    def __init__(self, layers, stores, eps: float = 1e-5, mode: str = "stage") -> None:
+    COPY_STREAMS = 4
+    MODES = ("stage", "read", "prefetch")
+
+    def __init__(self, layers, stores, eps: float = 1e-5, mode: str = "stage", block_rows: int = 512,
+                 depth: int = 4) -> None:
         super().__init__(layers, eps=eps)
-        if mode not in ("stage", "read"):
-            raise ValueError(f"mode {mode!r}: 'stage' or 'read'")
         self.stores = stores
-        self.mode = mode
+        self.block_rows, self.depth = block_rows, depth
         self.bytes_from_host = 0
+        self._tile_tabs = None
+        self._slots = None
+        self._sources = None
+        self.arena = None
+        self.mode = None
+        self.set_mode(mode)
+
+    def set_mode(self, mode: str) -> None:
+        """Switch how the host blocks are reached; each mode's tables, slots
+        and sources are built on first use and kept."""
+        if mode not in self.MODES:
+            raise ValueError(f"mode {mode!r}: one of {self.MODES}")
         if mode == "read":
-            for layer, st in zip(layers, stores):
-                layer.set_tile_tables(*(st.tile_table(k, self.device) for k in ("gate", "up", "down")))
+            if self._tile_tabs is None:
+                self._tile_tabs = [tuple(st.tile_table(k, self.device) for k in ("gate", "up", "down"))
+                                   for st in self.stores]
+            for layer, tabs in zip(self.layers, self._tile_tabs):
+                layer.set_tile_tables(*tabs)
+        else:
+            for layer in self.layers:  # the expert address tables again, rewritten per step
+                layer.set_tile_tables(None, None, None)
+            self._make_slots()
+            if mode == "prefetch":
+                self._make_sources()
+        self.mode = mode
+
+    def _make_slots(self) -> None:
+        if self._slots is not None:
             return
+        stores = self.stores
         n_slots = min(self.cfg.n_expert, 64)
         self._slots = {k: torch.empty(n_slots * stores[0].per[k], dtype=torch.uint8, device=self.device)
                        for k in stores[0].kinds}
         self._tables = [{k: torch.empty(self.cfg.n_expert, dtype=torch.int64, pin_memory=True)
-                         for k in stores[0].kinds} for _ in layers]
+                         for k in stores[0].kinds} for _ in self.layers]
         # per step every entry starts at valid full-size memory: the expert itself or slot 0
         self._default = [{k: torch.tensor([st.address(k, e) or self._slots[k].data_ptr()
                                            for e in range(self.cfg.n_expert)], dtype=torch.int64)
@@ -305,16 +443,31 @@ class GptOssHostStreamedStack(GptOssFFNStack):
         # several DMA engines share the PCIe link
         self._copy_streams = [torch.cuda.Stream(self.device) for _ in range(self.COPY_STREAMS)]
 
-    COPY_STREAMS = 4
+    def _make_sources(self) -> None:
+        if self._sources is not None:
+            return
+        from ..io.arena import Arena
+        stores, depth = self.stores, self.depth
+        rows = {k: (self.cfg.n_ffn_expert if k in ("gate", "up") else self.cfg.n_embd) for k in stores[0].kinds}
+        K = {k: (self.cfg.n_embd if k in ("gate", "up") else self.cfg.n_ffn_expert) for k in stores[0].kinds}
+        widest = max(st.block_bytes[k] for st in stores for k in st.kinds)
+        # depth blocks in flight plus the one being taken (BlockPrefetcher's depth + 1 rule)
+        self.arena = Arena((depth + 1) * widest)
+        self._sources = [_TileBlockSource(st, rows, K, self.block_rows, self.arena,
+                                          self._copy_streams[:max(1, min(depth, self.COPY_STREAMS))])
+                         for st in stores]
 
-    def _stage(self, li: int, chosen) -> None:
+    def _assign_slots(self, li: int, chosen):
+        """Point the layer's expert tables at staging slots for the chosen
+        experts that have host blocks: (host blocks [(kind, expert, block
+        index, host address, slot address, bytes)], HBM segments (n, 3) int64
+        of (source, slot address, bytes) to gather)."""
         import numpy as np
-        from .. import _native as N
-        st, layer, lib = self.stores[li], self.layers[li], N.load()
-        hseg, gseg = [], []
+        st = self.stores[li]
+        hblocks, gseg = [], []
         for kind in st.kinds:
             table = self._tables[li][kind]
-            slot_base, per = self._slots[kind].data_ptr(), st.per[kind]
+            slot_base, per, bb = self._slots[kind].data_ptr(), st.per[kind], st.block_bytes[kind]
             n_slots = self._slots[kind].numel() // per
             table.copy_(self._default[li][kind])
             used = 0
@@ -326,14 +479,27 @@ class GptOssHostStreamedStack(GptOssFFNStack):
                     raise RuntimeError(f"more than {n_slots} staged experts in one layer")
                 dst = slot_base + used * per
                 used += 1
-                for lst, arr in zip((hseg, gseg), seg):
-                    if len(arr):
-                        a = arr.copy()
-                        a[:, 1] += dst
-                        lst.append(a)
+                hs, gs = seg
+                hblocks += [(kind, e, int(b0) // bb, int(src), dst + int(b0), int(n)) for src, b0, n in hs]
+                if len(gs):
+                    a = gs.copy()
+                    a[:, 1] += dst
+                    gseg.append(a)
                 table[e] = dst
-        H = np.concatenate(hseg) if hseg else np.zeros((0, 3), np.int64)
         G = np.concatenate(gseg) if gseg else np.zeros((0, 3), np.int64)
+        return hblocks, G
+
+    def _publish_tables(self, li: int) -> None:
+        layer = self.layers[li]
+        for kind, dev_table in (("gate", layer.gate_ptrs), ("up", layer.up_ptrs), ("down", layer.down_ptrs)):
+            dev_table.copy_(self._tables[li][kind], non_blocking=True)
+
+    def _stage(self, li: int, chosen) -> None:
+        import numpy as np
+        from .. import _native as N
+        lib = N.load()
+        hblocks, G = self._assign_slots(li, chosen)
+        H = np.array([(src, dst, n) for _, _, _, src, dst, n in hblocks], dtype=np.int64).reshape(-1, 3)
         s = N.stream_ptr(self.device)
         col = lambda a, j: np.ascontiguousarray(a[:, j]).ctypes.data_as(C.c_void_p)  # noqa: E731
         with torch.cuda.device(self.device):
@@ -347,9 +513,59 @@ class GptOssHostStreamedStack(GptOssFFNStack):
             N.check(lib.nsx_gather_copy(len(G), col(G, 0), col(G, 1), col(G, 2), s), "gather_copy")
             for cs in self._copy_streams[:len(H)]:
                 cur.wait_stream(cs)
-            for kind, dev_table in (("gate", layer.gate_ptrs), ("up", layer.up_ptrs), ("down", layer.down_ptrs)):
-                dev_table.copy_(self._tables[li][kind], non_blocking=True)
+            self._publish_tables(li)
         self.bytes_from_host += int(H[:, 2].sum()) if len(H) else 0
+
+    def _prefetch(self, li: int, chosen) -> None:
+        """The host blocks of the chosen experts through BlockPrefetcher, in
+        the order the layer consumes them; the HBM blocks of the same experts
+        gathered into their slots by one kernel."""
+        import numpy as np
+        from .. import _native as N
+        from ..compute.blockffn import BlockPrefetcher
+        src = self._sources[li]
+        hblocks, G = self._assign_slots(li, chosen)
+        order = {"gate": 0, "up": 1, "down": 2}
+        hblocks.sort(key=lambda b: (b[1], order[b[0]], b[2]))  # ascending expert; gate, up, down
+        br = self.block_rows
+        plan, dest = [], {}
+        for kind, e, i, _src, dst, _n in hblocks:
+            rows = src.rows[kind]
+            lo = e * rows + i * br
+            plan.append((kind, lo, e * rows + min(rows, (i + 1) * br)))
+            dest[(kind, lo)] = dst
+        src.dest = dest
+        s = N.stream_ptr(self.device)
+        col = lambda a, j: np.ascontiguousarray(a[:, j]).ctypes.data_as(C.c_void_p)  # noqa: E731
+        with torch.cuda.device(self.device):
+            cur = torch.cuda.current_stream(self.device)
+            for cs in src.streams:
+                cs.wait_stream(cur)  # the slots are free once the work queued so far is done
+            N.check(N.load().nsx_gather_copy(len(G), col(G, 0), col(G, 1), col(G, 2), s), "gather_copy")
+            b0 = src.bytes_copied
+            with BlockPrefetcher(src, plan, block_rows=br, depth=self.depth) as pf:
+                if plan and not pf.enabled:
+                    raise RuntimeError("the prefetcher's arena cannot hold depth + 1 blocks")
+                for name, lo, hi in plan:
+                    got = pf.take(name, lo)
+                    if got is None:  # not read ahead: read it now, in order
+                        fut, n = src.submit_rows(name, lo, hi)
+                        src.reader.wait(fut)
+                    else:
+                        _, n = got
+                    src.arena.release(n)  # the block is in its slot (ordered on `cur`): the lease ends
+            self._publish_tables(li)
+        self.bytes_from_host += src.bytes_copied - b0
+
+    def prefetch_stats(self) -> dict:
+        """Prefetch mode: blocks read, prefetch hits (copy already done when
+        taken) and the arena's peak lease, over every call so far."""
+        if not self._sources:
+            return {}
+        req = sum(s.reader.stats.requests for s in self._sources)
+        hits = sum(s.reader.stats.prefetch_hits for s in self._sources)
+        return {"blocks": req, "hits": hits, "arena_budget": self.arena.budget,
+                "arena_peak": self.arena.stats.peak_bytes}
 
     def host_bytes_of_routing(self, ids) -> int:
         """Bytes read from pinned host RAM for a step routed as `ids` (per layer
@@ -361,8 +577,8 @@ class GptOssHostStreamedStack(GptOssFFNStack):
         return total
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-        """As GptOssFFNStack.forward; in "stage" mode one host synchronisation
-        per layer (routing)."""
+        """As GptOssFFNStack.forward; in "stage" and "prefetch" modes one host
+        synchronisation per layer (routing)."""
         if self.mode == "read":
             return GptOssFFNStack.forward(self, x, out)
         from ..moe.fused import router_topk
@@ -372,10 +588,11 @@ class GptOssHostStreamedStack(GptOssFFNStack):
         res = torch.empty_like(x) if out is None else out
         eps = self.cfg.rms_eps
         add_rms_norm(x.float().contiguous(), None, self.norm_weights[0], eps, out=h, sum_out=res)
+        stage = self._prefetch if self.mode == "prefetch" else self._stage
         for li, layer in enumerate(self.layers):
             rid, _, _ = router_topk(h, layer.router_w, layer.router_b, layer.top_k, "gptoss")
             chosen = torch.unique(rid).tolist()  # device -> host, as the reference
-            self._stage(li, chosen)
+            stage(li, chosen)
             layer.forward(h, out=y, ids=ids[li], weights=wts[li])
             if li + 1 < len(self.layers):
                 add_rms_norm(res, y, self.norm_weights[li + 1], eps, out=h, sum_out=res)
@@ -387,9 +604,10 @@ class GptOssHostStreamedStack(GptOssFFNStack):
 
     @classmethod
     def synthetic(cls, cfg, n_layers: int, seed: int, device, host_fraction: float = 0.25, block_rows: int = 512,
-                  dispatch: str = "auto", mode: str = "stage"):
+                  dispatch: str = "auto", mode: str = "stage", depth: int = 4):
         """BASELINE config 5b: the layers of GptOssFFNStack.synthetic with a
-        seeded host_fraction of their block_rows-row blocks in pinned RAM."""
+        seeded host_fraction of their block_rows-row blocks in pinned RAM
+        (prefetch mode: read `depth` blocks ahead)."""
         import numpy as np
         from .. import synth
         from ..compute.kernels import t64_pack_stacked
@@ -418,7 +636,7 @@ class GptOssHostStreamedStack(GptOssFFNStack):
                                    router_mode=cfg.router_mode, act=cfg.act, dispatch=dispatch))
             stores.append(st)
             del t
-        return cls(layers, stores, mode=mode)
+        return cls(layers, stores, mode=mode, block_rows=block_rows, depth=depth)
 
 
 @dataclass

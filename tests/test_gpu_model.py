@@ -198,12 +198,13 @@ def test_qwen3_moe_ffn_over_cache(dev, T):
     assert cache.stats.slab_hits > 0
 
 
-@pytest.mark.parametrize("mode", ["stage", "read"])
+@pytest.mark.parametrize("mode", ["stage", "prefetch", "read"])
 @pytest.mark.parametrize("T,frac", [(1, 0.5), (5, 0.25), (9, 1.0)])
 def test_host_streamed_stack_equals_resident(dev, T, frac, mode):
     """BASELINE config 5b on a small stack: with a share of the row blocks in
-    pinned host RAM -- staged per step, or read over PCIe by the kernels
-    through tile tables -- the outputs equal the resident stack's."""
+    pinned host RAM -- staged per step (all at once, or through
+    BlockPrefetcher at depth 4), or read over PCIe by the kernels through
+    tile tables -- the outputs equal the resident stack's."""
     from nurostream_amd import synth
     from nurostream_amd.model.gpt_oss import GptOssFFNStack, GptOssHostStreamedStack
     cfg = _small("gptoss-small")
@@ -218,7 +219,14 @@ def test_host_streamed_stack_equals_resident(dev, T, frac, mode):
         y_hs = hs(x)
         torch.cuda.synchronize()
         assert torch.equal(y_res, y_hs)
-    if mode == "stage":
+    if mode == "prefetch":  # every lease returned, never more than depth + 1 blocks held
+        ps = hs.prefetch_stats()
+        assert ps["blocks"] > 0 and hs.arena.used == 0
+        assert 0 < ps["arena_peak"] <= ps["arena_budget"] == 5 * max(
+            st.block_bytes[k] for st in hs.stores for k in st.kinds)
+        ids, _ = hs.last_routing(T)
+        assert hs.bytes_from_host == 2 * hs.host_bytes_of_routing(ids.cpu())
+    if mode in ("stage", "prefetch"):
         assert hs.bytes_from_host > 0
         return
     ids, _ = hs.last_routing(T)

@@ -1,9 +1,17 @@
 """BASELINE config 5 at its real shape: 36 GPT-OSS-120B-shaped MXFP4 layers
 (128 experts, hidden 2880, top-4) with every expert slab resident in HBM as
 t64 tiles (61 GB), chained x <- x + moe_l(rms_norm(x)) as the reference's
-decoder wraps its FFN blocks (model/gpt_oss.py:123-177); and config 5b, the
-same stack with a seeded 25% of the 512-row expert blocks in pinned host RAM,
-read by the kernels over PCIe (model/gpt_oss.py:GptOssHostStreamedStack)."""
+decoder wraps its FFN blocks (model/gpt_oss.py:123-177, compute/ops.py:14-20);
+and config 5b, the same stack with a seeded 25% of the 512-row expert blocks
+in pinned host RAM, read by the kernels over PCIe, staged per layer, or
+staged through BlockPrefetcher (model/gpt_oss.py:GptOssHostStreamedStack).
+
+The stack folds each block's residual add and norm into other launches (the
+router kernel up to two tokens, the combine kernel from three). Spelled out
+with the separate add_rms_norm and one forward() per layer, the chain must
+give the stack's bits at hidden 2880, where each of the norm's 256 threads
+holds 12 values, the last one partial; and each layer, fed the GPU's own
+input, must match the oracle's MoE block."""
 from __future__ import annotations
 
 import gc
@@ -86,6 +94,132 @@ def test_full_stack_layer0_matches_oracle(dev, stack):
     ref = OM.ffn_stack(x.cpu().numpy(), layer0, cfg.top_k)
     err = rel_max(to_np(got), ref)
     assert err < FFN_BAR and err < MFMA_TOL, err
+
+
+KEEP = (0, 1, 17, 35)  # layers whose inputs and outputs the chain keeps for the oracle
+
+
+def _norm_weights(n_embd, dev):
+    """Non-unit post-attention norm weights, so the fused norms' weight multiply is exercised."""
+    return [(1 + 0.1 * torch.randn(n_embd, generator=torch.Generator().manual_seed(1000 + li))).to(dev)
+            for li in range(N_LAYERS)]
+
+
+@pytest.fixture(scope="module", params=[1, 8], ids=["T1", "T8"])
+def chain(request, dev, stack):
+    """The stack's output over T tokens, and the same chain spelled out with
+    add_rms_norm + MoELayer.forward per layer; the inputs (x_l before the norm,
+    h_l after it), outputs and routing of the KEEP layers, on the host."""
+    from nurostream_amd import synth
+    from nurostream_amd.compute.ops import add_rms_norm
+    T = request.param
+    cfg = synth.GPTOSS_120B
+    print(f"[stack_full] chain T={T}: fused stack vs spelled out", flush=True)
+    saved = stack.norm_weights
+    stack.norm_weights = nw = _norm_weights(cfg.n_embd, dev)
+    try:  # the weights go back before the fixture returns: later tests of the module share `stack`
+        x = synth.activations(T, cfg.n_embd, seed=70 + T, device=dev)
+        y = stack(x).clone()
+        ids_s, wts_s = (t.clone() for t in stack.last_routing(T))
+        res = torch.empty_like(x)
+        h = add_rms_norm(x, None, nw[0], 1e-5, sum_out=res)
+        kept, ids_c, wts_c = {}, [], []
+        for li, layer in enumerate(stack.layers):
+            if li:
+                h = add_rms_norm(res, o, nw[li], 1e-5, sum_out=res)
+            o, ids, w = layer.forward(h)
+            ids_c.append(ids.clone())
+            wts_c.append(w.clone())
+            if li in KEEP:
+                x_l = x if li == 0 else res
+                kept[li] = tuple(t.cpu().numpy() for t in (x_l, h, o, ids, w)) + (nw[li].cpu().numpy(),)
+        res.add_(o)
+        torch.cuda.synchronize()
+    finally:
+        stack.norm_weights = saved
+    return {"T": T, "y": y, "spelled": res, "ids": (ids_s, torch.stack(ids_c)),
+            "wts": (wts_s, torch.stack(wts_c)), "kept": kept}
+
+
+def test_full_stack_fused_norms_equal_spelled_out_chain(chain):
+    """T=1 runs each block's norm inside the router kernel (nsx_moe_forward_norm),
+    T=8 inside the combine kernel (moe_combine_norm_kernel); both give the
+    separate add_rms_norm's bits at hidden 2880 through all 36 layers."""
+    ids_s, ids_c = chain["ids"]
+    wts_s, wts_c = chain["wts"]
+    assert torch.equal(ids_s, ids_c)
+    assert torch.equal(wts_s, wts_c)
+    assert torch.equal(chain["y"], chain["spelled"])
+
+
+@pytest.mark.parametrize("layer", KEEP)
+def test_full_stack_layer_matches_oracle_teacher_forced(dev, chain, layer):
+    """Layer `layer` of the chain, given the GPU's own input: the norm against
+    oracle.rms_norm, the routing and the MoE block against oracle.moe_gptoss
+    (ids exact outside fp32 near-ties; output within the MFMA bound on every
+    token whose routing is not a near-tie)."""
+    from nurostream_amd import synth
+    cfg = synth.GPTOSS_120B
+    x_l, h, o, ids, w, nw = chain["kept"][layer]
+    assert rel_max(h, OM.rms_norm(x_l, nw, 1e-5)) < 2e-6
+    t = synth.make_layer(cfg, seed=SEED, device=dev, layer=layer)
+    Wr, br = t["router_w"].float().cpu().numpy(), t["router_b"].cpu().numpy()
+    per = {k: cfg.expert_bytes(k) for k in ("gate", "up", "down")}
+    dev_raw = {k: t[k] for k in ("gate", "up", "down")}
+    raw = {k: (lambda e, k=k: dev_raw[k][e * per[k]:(e + 1) * per[k]].cpu().numpy()) for k in per}
+    bias = {k: t[k + "_b"].cpu().numpy() for k in ("gate", "up", "down")}
+    ex = OM.ExpertSet(int(cfg.ggml_type), cfg.n_embd, cfg.n_ff, raw, bias)
+    ref, rid, rw, logits = OM.moe_gptoss(h, Wr, br, cfg.top_k, ex)
+    del t, dev_raw
+    torch.cuda.empty_cache()
+    bound = 4 * np.finfo(np.float32).eps * (np.abs(h) @ np.abs(Wr).T).max(axis=1) * np.sqrt(h.shape[1])
+    ok = OM.topk_margin(logits, cfg.top_k) > bound
+    assert ok.sum() >= len(ok) - 1, "more than one near-tie token"
+    np.testing.assert_array_equal(ids[ok], rid[ok])
+    np.testing.assert_allclose(w[ok], rw[ok], rtol=2e-5, atol=1e-6)
+    err = rel_max(o[ok], ref[ok])
+    print(f"[stack_full] T={chain['T']} layer {layer}: max rel err {err:.3g}", flush=True)
+    assert err < FFN_BAR and err < MFMA_TOL, err
+
+
+@pytest.fixture(scope="module")
+def staged_stack(dev):
+    """Config 5b with the host blocks staged per layer (modes "stage" and "prefetch" share it)."""
+    from nurostream_amd import synth
+    from nurostream_amd.model.gpt_oss import GptOssHostStreamedStack
+    print("[stack_full] building the 25%-host stack (stage mode)", flush=True)
+    hs = GptOssHostStreamedStack.synthetic(synth.GPTOSS_120B, N_LAYERS, seed=SEED, device=dev, host_fraction=0.25,
+                                           block_rows=512, mode="prefetch", depth=4)
+    torch.cuda.synchronize()
+    yield hs
+    del hs
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("mode", ["stage", "prefetch"])
+@pytest.mark.parametrize("T", [1, 8])
+def test_full_stack_host25_staged_equals_resident(dev, stack, staged_stack, mode, T):
+    """Config 5b staged per layer -- every host block of the chosen experts
+    DMA-copied into a staging slot at once (stage), or read through
+    BlockPrefetcher at depth 4 in 512-row blocks (prefetch) -- gives the
+    resident stack's outputs bit for bit at the real shape."""
+    from nurostream_amd import synth
+    hs = staged_stack
+    hs.set_mode(mode)
+    print(f"[stack_full] host25 {mode} T={T}", flush=True)
+    x = synth.activations(T, synth.GPTOSS_120B.n_embd, seed=95 + T, device=dev)
+    ref = stack(x)
+    b0 = hs.bytes_from_host
+    got = hs(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(hs.last_routing(T)[0], stack.last_routing(T)[0])
+    moved = hs.bytes_from_host - b0
+    assert moved == hs.host_bytes_of_routing(hs.last_routing(T)[0].cpu()) > 0
+    if mode == "prefetch":
+        assert hs.arena.used == 0
+        assert hs.prefetch_stats()["arena_peak"] <= hs.arena.budget
 
 
 def test_full_stack_host25_read_equals_resident(dev, stack):
