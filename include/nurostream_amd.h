@@ -106,7 +106,9 @@ int nsx_fused_gemv_ex(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
  * (model/gpt_oss.py:101-114) or the LM head (model/gpt_oss.py:207-228), in
  * the bits nsx_add_rmsnorm gives h -- one launch instead of two. x, r, w: K
  * floats (r, w optional), x 16-byte aligned, K <= 4096; s (optional) receives
- * x + r and must not be x or r. */
+ * x + r. Other workgroups still read x, r and resid while s and y are
+ * written, so s must not overlap x, r, resid or y, and y must not overlap x
+ * or r and is either resid itself or apart from it (NSX_EINVAL otherwise). */
 int nsx_fused_gemv_norm(int ggml_type, const void *raw, int64_t n_rows, int64_t K,
                         const float *x, const float *r, const float *w, float eps, float *s,
                         float *y, const float *bias, const float *resid, void *stream);

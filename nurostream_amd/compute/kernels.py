@@ -120,7 +120,7 @@ def fused_gemv_norm(raw, dtype, x: torch.Tensor, r: torch.Tensor | None, weight:
                     resid: torch.Tensor | None = None) -> torch.Tensor:
     """One token's y = W . rms_norm(x + r) * weight (+ bias, + resid) -> (1, n_rows) fp32, the norm in the
     GEMV's prologue with the bits add_rms_norm gives it (one launch instead of two); with sum_out, x + r is
-    written there too (sum_out must not be x or r). Raw GGUF rows; x, r, weight: K fp32 values."""
+    written there too (sum_out must not overlap x, r, resid or y). Raw GGUF rows; x, r, weight: K fp32 values."""
     dtype = GGMLType(dtype)
     if dtype not in N.BLOCK_TYPES:
         raise KeyError(dtype)

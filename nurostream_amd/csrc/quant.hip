@@ -812,7 +812,19 @@ extern "C" int nsx_fused_gemv_norm(int t, const void* raw, int64_t n_rows, int64
   if (n_rows == 0) return NSX_OK;
   NSX_REQUIRE(raw && x && y, NSX_EINVAL, "null buffer");
   NSX_REQUIRE(((uintptr_t)x & 15) == 0, NSX_EINVAL, "x must be 16-byte aligned");
-  NSX_REQUIRE(!s || (s != x && s != r), NSX_EINVAL, "s must not be x or r (other workgroups read them)");
+  // Workgroup 0 writes s and every workgroup writes its rows of y while the others still read x, r and
+  // resid in the norm prologue and epilogue: no output may overlap an input another workgroup reads (y may be
+  // resid exactly: each element of y is read from resid by the thread that writes it)
+  auto overlap = [](const void* p, int64_t pn, const void* q, int64_t qn) {
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return p && q && a < b + (uintptr_t)(qn * 4) && b < a + (uintptr_t)(pn * 4);
+  };
+  NSX_REQUIRE(!overlap(s, K, x, K) && !overlap(s, K, r, K) && !overlap(s, K, resid, n_rows) &&
+                  !overlap(s, K, y, n_rows),
+              NSX_EINVAL, "s must not overlap x, r, resid or y");
+  NSX_REQUIRE(!overlap(y, n_rows, x, K) && !overlap(y, n_rows, r, K), NSX_EINVAL, "y must not overlap x or r");
+  NSX_REQUIRE(resid == y || !overlap(y, n_rows, resid, n_rows), NSX_EINVAL,
+              "y must be resid or apart from it");
   if (t == NSX_Q4_K)
     NSX_REQUIRE(((uintptr_t)raw & 3) == 0, NSX_EINVAL, "Q4_K rows must be 4-byte aligned");
   const GvNorm nm{r, w, eps, s};

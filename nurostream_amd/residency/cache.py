@@ -80,12 +80,19 @@ class _Resident:
 
 
 class _Tier:
-    """A byte-budgeted LRU of residents; `protected` names are never evicted."""
+    """A byte-budgeted LRU of residents; `protected` names are never evicted.
 
-    def __init__(self, budget: int) -> None:
+    Residents laid out in one shared buffer (TieredCache.fuse_vram) form a
+    group that leaves together: evicting or replacing any member evicts
+    every member, so the bytes the tier counts are the bytes still alive,
+    and `on_group_gone(group)` lets the owner drop the shared buffer."""
+
+    def __init__(self, budget: int, on_group_gone=None) -> None:
         self.budget = int(budget)
         self.held = 0
         self.items: OrderedDict[str, _Resident] = OrderedDict()
+        self.groups: dict[str, tuple] = {}  # member name -> its group (a tuple of names)
+        self.on_group_gone = on_group_gone
 
     def lookup(self, name: str) -> _Resident | None:
         r = self.items.get(name)
@@ -93,19 +100,40 @@ class _Tier:
             self.items.move_to_end(name)  # most recently used last
         return r
 
+    def group(self, names: tuple) -> None:
+        for n in names:
+            self.groups[n] = names
+
+    def _drop(self, name: str) -> int:
+        """Remove `name` and, when it is grouped, the rest of its group: how many residents left."""
+        group = self.groups.get(name)
+        gone = 0
+        for m in (group or (name,)):
+            self.groups.pop(m, None)
+            r = self.items.pop(m, None)
+            if r is not None:
+                self.held -= r.nbytes
+                gone += 1
+        if group is not None and self.on_group_gone is not None:
+            self.on_group_gone(group)
+        return gone
+
     def make_room(self, need: int, protected: set) -> int:
-        """Evict least recently used residents until `need` more bytes fit;
-        returns how many were evicted (it may still not fit if the rest is
-        protected)."""
+        """Evict least recently used residents (a group whole) until `need`
+        more bytes fit; returns how many were evicted (it may still not fit if
+        the rest is protected)."""
         evicted = 0
         for name in [n for n in self.items if n not in protected]:
             if self.held + need <= self.budget:
                 break
-            self.held -= self.items.pop(name).nbytes
-            evicted += 1
+            if name not in self.items or any(m in protected for m in self.groups.get(name, ())):
+                continue
+            evicted += self._drop(name)
         return evicted
 
     def put(self, name: str, r: _Resident) -> None:
+        if name in self.items:  # a replaced member takes its group (and shared buffer) with it
+            self._drop(name)
         self.items[name] = r
         self.held += r.nbytes
 
@@ -163,11 +191,11 @@ class TieredCache:
             raise ValueError(f"slab_layout must be 't64' or 'gguf', not {slab_layout!r}")
         self.slab_layout = slab_layout
         self.slab_budget = 0  # bytes of expert slabs admit_slab may hold (set by the loader)
-        self._hbm = _Tier(vram_budget)
+        self._fused: dict[tuple, torch.Tensor] = {}
+        self._hbm = _Tier(vram_budget, on_group_gone=self._unfuse)
         self._ram = _Tier(ram_budget)
         self._slabs = _SlabIndex()
         self._protected: set[str] = set()
-        self._fused: dict[tuple, torch.Tensor] = {}
         self.stats = CacheStats()
 
     # budgets and holdings (the reference's attribute names)
@@ -309,7 +337,11 @@ class TieredCache:
             r.data = buf[off:off + n]
             off += n
         self._fused[names] = buf
+        self._hbm.group(names)  # the members share `buf`: they leave the tier together
         return buf, rs[0].ggml_type
+
+    def _unfuse(self, names: tuple) -> None:
+        self._fused.pop(names, None)
 
     def _tiered(self, name: str):
         """(resident, "vram" | "ram") with the hit counted, or (None, None)."""
@@ -412,7 +444,7 @@ class TieredCache:
 
     def clear(self) -> None:
         """Drop every resident and slab and reset the counters (budgets stay)."""
-        self._hbm = _Tier(self._hbm.budget)
+        self._hbm = _Tier(self._hbm.budget, on_group_gone=self._unfuse)
         self._ram = _Tier(self._ram.budget)
         self._slabs = _SlabIndex()
         self._fused = {}

@@ -194,3 +194,21 @@ def test_forward_addnorm_validation(lib):
     assert b"h_out" in lib.nsx_last_error()
     assert lib.nsx_moe_forward_addnorm(*args(x, x + 4, 3 << 20)) == N.EINVAL  # x_out overlapping x, not x
     assert lib.nsx_moe_forward_addnorm(*args(x, 3 << 20, (3 << 20) + 8)) == N.EINVAL  # h_out over x_out
+
+
+def test_gemv_norm_overlap_validation(lib):
+    """nsx_fused_gemv_norm: workgroup 0 writes s and every workgroup its rows of y
+    while the others still read x, r and resid, so s may overlap none of x, r,
+    resid, y; y none of x, r; and y is resid exactly or apart from it -- byte
+    ranges, checked on the host before any HIP call (the pointers below are
+    never dereferenced)."""
+    t, n_rows, K = int(GGMLType.Q8_0), 64, 256
+    x, r, resid, y, s = 1 << 20, 2 << 20, 3 << 20, 4 << 20, 5 << 20
+
+    def call(s=s, y=y, resid=resid, r=r):
+        return lib.nsx_fused_gemv_norm(t, 6 << 20, n_rows, K, x, r, None, 1e-5, s, y, None, resid, None)
+
+    for bad in (dict(s=x + 4), dict(s=x - 4 * K + 4), dict(s=r + 512), dict(s=resid + 8), dict(s=y + 16),
+                dict(y=x + 1000), dict(y=r - 4 * n_rows + 4), dict(y=resid + 4), dict(resid=y - 4)):
+        assert call(**bad) == N.EINVAL, bad
+    assert b"overlap" in lib.nsx_last_error() or b"resid" in lib.nsx_last_error()

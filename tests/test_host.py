@@ -171,6 +171,34 @@ def test_slab_serves_subranges_without_source_reads():
     assert not f32.admit_slab("w", 0, 4)  # float tensors are never slabbed
 
 
+def test_fused_residents_leave_the_tier_together():
+    """fuse_vram lays q, k and v out in one buffer; evicting any of them (to
+    make room, or by replacing it) takes the whole group and the shared
+    buffer, so the tier's byte count matches the storage still alive."""
+    rows, K = 4, 32
+    blk = torch.cat((torch.tensor([1.0], dtype=torch.float16).view(torch.uint8), torch.arange(1, 33, dtype=torch.uint8)))
+    names = ("blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.0.attn_v.weight")
+    tensors = {n: (tensor_info(n, (rows, K), GGMLType.Q8_0), blk.repeat(rows)) for n in names + ("blk.0.o.weight",)}
+    src = HostSource(tensors, Arena(1 << 20))
+    one = rows * 34
+    cache = TieredCache(src, device="cpu", vram_budget=3 * one)
+    for n in names:
+        assert cache.admit_vram(n)
+    buf, t = cache.fuse_vram(names)
+    assert t == GGMLType.Q8_0 and buf.numel() == 3 * one and cache.stats.vram_bytes == 3 * one
+    assert cache.admit_vram("blk.0.o.weight")  # needs room: the LRU resident is q, grouped with k and v
+    assert not any(cache.is_resident(n) for n in names)
+    assert cache._fused == {} and cache.stats.vram_bytes == one
+    # replacing a member also dissolves its group
+    cache2 = TieredCache(src, device="cpu", vram_budget=4 * one)
+    for n in names:
+        assert cache2.admit_vram(n)
+    cache2.fuse_vram(names)
+    cache2._hbm.put(names[1], cache2._hbm.items[names[1]])
+    assert cache2._fused == {} and cache2.is_resident(names[1]) and not cache2.is_resident(names[0])
+    assert cache2._hbm.held == one
+
+
 def test_quantized_compute_never_falls_back_to_cpu():
     """Block formats compute on the GPU only: CPU tensors raise instead of taking a CPU path."""
     from nurostream_amd.compute.kernels import can_fuse, fused_gemv
