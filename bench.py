@@ -125,6 +125,9 @@ def _parse():
                    help="gptoss-token: positions already in the KV cache when the timed tokens start")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after the run, copy a buffer of this size 3 times (calibrates rocprofv3 byte counters)")
+    p.add_argument("--decode-chain", choices=("on", "off"), default="on",
+                   help="stack workloads at T=1: the decode chain (no router launch after the first layer) or the "
+                        "folded-norm path (a router launch per layer)")
     p.add_argument("--replays", type=int, default=20,
                    help="timed replays of the captured steps (after one untimed replay); the median is reported")
     p.add_argument("--configs", choices=("all", "none"), default="all",
@@ -148,11 +151,13 @@ def csrc_digest():
     return h.hexdigest()[:16]
 
 
-def _traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size,
-    written by bench_pmc.py), or None when there is no such measurement or it
-    was taken on other kernel sources than the ones built now."""
+def _traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` in `workload` from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel
+    of known size, written by bench_pmc.py), or None when there is no such
+    measurement or it was taken on other kernel sources than the ones built
+    now. A name without template arguments matches the workload's one
+    instantiation of that kernel."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.json")
     try:
         with open(path) as f:
@@ -161,7 +166,11 @@ def _traffic(kernel):
         return None
     if doc.get("csrc_digest") != csrc_digest():
         return None
-    rec = doc.get("kernels", {}).get(kernel)
+    kernels = doc.get("workloads", {}).get(workload, {}).get("kernels", {})
+    rec = kernels.get(kernel)
+    if rec is None:
+        same = [v for k, v in kernels.items() if k.split("<")[0] == kernel.split("<")[0]]
+        rec = same[0] if len(same) == 1 else None
     return None if rec is None else rec.get("traffic_bytes")
 
 
@@ -513,7 +522,7 @@ def layer_workload(args, torch, N, synth, dev):
         kname, kbytes, kus = gu_kernel, gu_bytes, phase_us[N.PHASE_GATE_UP]
         achieved = kbytes / (kus * 1e-6) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname),
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname, name),
                     "kernel": kname, "bytes_per_launch": int(kbytes), "avg_us": round(kus, 3),
                     "timing": f"graph of {R} gate/up phases, each its own tokens and workspace"}
         if len(gu_phase) > 1:
@@ -600,6 +609,7 @@ def stack_workload(args, torch, N, synth, dev, stack=None, cpu_cache=None):
         stack = build_stack(args, torch, synth, dev, name)
     elif streamed:
         stack.set_mode(args.host_mode)
+    stack.decode_chain = args.decode_chain == "on"
     n_layers = len(stack.layers)
     n_steps = W + K
     X = synth.activations(n_steps * T, cfg.n_embd, seed=args.seed + 1, device=dev).view(n_steps, T, cfg.n_embd)
@@ -639,9 +649,19 @@ def stack_workload(args, torch, N, synth, dev, stack=None, cpu_cache=None):
         # (logits and activation terms of that step), as one graph timed with HIP events on its stream
         h_b, y_b, ids_b, wts_b = stack._buffers(T)
         g = torch.cuda.CUDAGraph()
+        # one token runs as a decode chain: layers 1.. launch moe_gu_chain_kernel, which reads the router shares
+        # the last step left (the chain's own gate/up launch, alone)
+        chain = T == 1 and stack.decode_chain and stack._chain_ok()
+        timed_layers = list(range(1, n_layers)) if chain else list(range(n_layers))
+        x_b = Y[W + K - 1].clone()
         with torch.cuda.stream(stream), torch.cuda.graph(g, stream=stream):
-            for li, layer in enumerate(stack.layers):
-                layer.phase(N.PHASE_GATE_UP, h_b, y_b, ids_b[li], wts_b[li], layer.workspace(T))
+            for li in timed_layers:
+                layer = stack.layers[li]
+                if chain:
+                    layer.chain_t1(x_b, stack.norm_weights[li], stack.cfg.rms_eps, stack._share, None, None, None,
+                                   y_b, ids_b[li], wts_b[li], phases=N.CHAIN_GATE_UP)
+                else:
+                    layer.phase(N.PHASE_GATE_UP, h_b, y_b, ids_b[li], wts_b[li], layer.workspace(T))
         gts = []
         with torch.cuda.stream(stream):
             g.replay()  # upload, untimed
@@ -653,17 +673,17 @@ def stack_workload(args, torch, N, synth, dev, stack=None, cpu_cache=None):
                 gts.append((e0, e1))
         torch.cuda.synchronize()
         gt = sorted(a.elapsed_time(b) for a, b in gts)
-        gu_us = gt[len(gt) // 2] * 1e3 / n_layers
+        gu_us = gt[len(gt) // 2] * 1e3 / len(timed_layers)
         per_layer = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
         gu_bytes = sum(_expert_bytes(cfg, d)[0] for d in per_layer) / n_layers
         grouped = args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 3)
-        kname = "moe_gu_grouped_kernel" if grouped else "moe_gu_kernel"
+        kname = "moe_gu_chain_kernel" if chain else "moe_gu_grouped_kernel" if grouped else "moe_gu_kernel"
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         step_alg = sum(sum(_expert_bytes(cfg, d)) for d in per_layer)
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname) if T == 1 else None,
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname, name),
                     "kernel": kname, "bytes_per_launch": int(gu_bytes), "avg_us": round(gu_us, 3),
-                    "timing": f"median of 5 replays of a graph of the {n_layers} layers' gate/up phases",
+                    "timing": f"median of 5 replays of a graph of {len(timed_layers)} layers' gate/up launches",
                     "step_frac": round(step_alg / (ms_total / K * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         if grouped:
             roofline["note"] = "avg_us is the whole gate/up phase: moe_sort_kernel + moe_gu_grouped_kernel"
@@ -725,7 +745,8 @@ def stack_workload(args, torch, N, synth, dev, stack=None, cpu_cache=None):
         "config": {"workload": f"gpt-oss-120b FFN stack, {n_layers} layers, T={T} (BASELINE config "
                                + ("5b)" if streamed else "5)"),
                    "tokens_per_step": T, "layers": n_layers, "layout": args.layout, "dispatch": args.dispatch,
-                   "graph": not staged, "chain": "x <- x + moe_l(rms_norm(x)), unit norm weight, eps 1e-5"},
+                   "graph": not staged, "chain": "x <- x + moe_l(rms_norm(x)), unit norm weight, eps 1e-5",
+                   "decode_chain": bool(T == 1 and not staged and stack.decode_chain and stack._chain_ok())},
         "resident_GB": round(n_layers * cfg.n_expert * sum(cfg.expert_bytes(k) for k in ("gate", "up", "down"))
                              / 1e9 - extra.get("host_resident_GB", 0.0), 2),
         **extra,
@@ -798,7 +819,7 @@ def gemv_workload(args, torch, N, synth, dev):
                                 f"{model} LM head {rows} x {K} {fmt_name}, T=1 ({n_copies} alternating copies)"),
                    "rows": rows, "K": K, "T": 1, "graph": True},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(kname, name),
                      "kernel": kname, "bytes_per_launch": alg_bytes, "avg_us": round(us, 3),
                      "timing": f"HIP events around a graph of {K_steps} launches on the launching stream"},
         "parity_max_rel_err": err,

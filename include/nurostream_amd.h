@@ -220,6 +220,39 @@ int nsx_moe_forward_addnorm(const nsx_moe_layer *L, const float *h, int64_t T,
                             float *h_out, int32_t *ids, float *weights, void *workspace,
                             int64_t workspace_bytes, void *stream);
 
+/* The decode chain of stacked GPT-OSS FFN blocks at T = 1
+ * (model/gpt_oss.py:123-177 layer after layer; the router of
+ * model/gpt_oss.py:116-121 regrouped): x += moe(rms_norm(x) * norm_w), in
+ * place (x: n_embd floats, the token's residual stream). out, ids, weights
+ * as nsx_moe_forward of h = rms_norm(x) * norm_w.
+ * share_in NULL: this block routes from x itself (a norm, a router and the
+ * per-pair gate/up launch). Otherwise share_in holds this block's router
+ * shares, written by the previous block's call: per work item of that call's
+ * down kernel the partial dot of x * norm_w with each router row and the
+ * partial sum of x^2; the gate/up kernel adds them in a fixed order, so
+ * logits = (dot) / rms + bias and the top-k need no router launch, and each
+ * of its workgroups quantizes h = (x / rms) * norm_w itself. With `next`
+ * (the next block, and its norm weight next_norm_w, may be NULL) the down
+ * kernel writes the next block's shares to share_out (which may be
+ * share_in). h equals nsx_add_rmsnorm's but for the rms's summation order, so
+ * outputs match the separate norm to rounding, not bit for bit. t64 layers on
+ * the per-pair kernels (not NSX_DISPATCH_GROUPED), n_embd a multiple of 16 up
+ * to 3072, experts a multiple of 4 up to 128 (NSX_ENOTIMPL otherwise). x, out and the
+ * share buffers must not overlap. Same workspace as nsx_moe_forward(T = 1).
+ * phases: NSX_CHAIN_GATE_UP (the gate/up launch, with the norm and router
+ * before it when share_in is NULL), NSX_CHAIN_DOWN (the down launch: out, the
+ * residual add, the next block's shares), or both -- one launch alone reads
+ * what the other left, for timing one of them. No reference counterpart as
+ * one call: the reference runs the same steps as separate torch calls. */
+#define NSX_CHAIN_GATE_UP 1
+#define NSX_CHAIN_DOWN 2
+int64_t nsx_moe_chain_share_bytes(const nsx_moe_layer *L);
+int nsx_moe_chain_t1(const nsx_moe_layer *L, float *x, const float *norm_w, float eps,
+                     const float *share_in, const nsx_moe_layer *next,
+                     const float *next_norm_w, float *share_out, float *out,
+                     int32_t *ids, float *weights, void *workspace,
+                     int64_t workspace_bytes, int phases, void *stream);
+
 /* One phase of nsx_moe_forward: NSX_PHASE_ROUTER (logits, the top-k and the
  * ids/weights outputs, for every layout and dispatch; in the t64 layout also
  * the activation terms of h), NSX_PHASE_GATE_UP (grouped dispatch: the sort

@@ -74,6 +74,9 @@ _SIGS = {
     "nsx_moe_forward_norm": (_i, [C.POINTER(MoeLayerC), _p, _p, _p, C.c_float, _i64, _p, _p, _p, _p, _p, _i64, _p]),
     "nsx_moe_forward_addnorm": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, C.c_float, _p, _p, _p, _p, _p, _i64,
                                      _p]),
+    "nsx_moe_chain_share_bytes": (_i64, [C.POINTER(MoeLayerC)]),
+    "nsx_moe_chain_t1": (_i, [C.POINTER(MoeLayerC), _p, _p, C.c_float, _p, C.POINTER(MoeLayerC), _p, _p, _p, _p, _p,
+                              _p, _i64, _i, _p]),
     "nsx_moe_phase": (_i, [C.POINTER(MoeLayerC), _i, _p, _i64, _p, _p, _p, _p, _i64, _p]),
     "nsx_moe_forward_static": (_i, [C.POINTER(MoeLayerC), _p, _i64, _p, _p, _p, _p]),
     "nsx_add_rmsnorm": (_i, [_p, _p, _i64, _i64, C.c_float, _p, _p, _p, _p]),
@@ -95,6 +98,7 @@ _SIGS = {
     "nsx_reader_close": (_i, [_p]),
 }
 PHASE_ROUTER, PHASE_GATE_UP, PHASE_DOWN, PHASE_COMBINE = 0, 1, 2, 3
+CHAIN_GATE_UP, CHAIN_DOWN = 1, 2  # nsx_moe_chain_t1 phases
 STATIC_WORKSPACE_BYTES = 32 << 20  # NSX_STATIC_WORKSPACE_BYTES
 
 

@@ -745,6 +745,17 @@ struct MoeDev {
   int cdg, sdg;          // grouped down: K-chunks and K-steps per chunk
   int topk_in_gu;        // per-pair GGUF-layout paths: the gate/up kernel selects the top-k (no top-k launch)
   int topk_in_sort;      // grouped, T < RM_MIN_T: the sort kernel selects the top-k (no top-k launch)
+  // decode chain of stacked layers (T = 1; moe_gu_chain_kernel, moe_down_chain_kernel)
+  float* cx;             // the token's residual stream, updated in place by the down kernel
+  const float* cnorm_w;  // this layer's norm weight (null: unit)
+  float ceps;
+  const float* crouter_b;  // this layer's router bias (null: none)
+  const float* cp_in;    // this layer's router shares: [cp_groups][E] partial logits, then [cp_groups] sums of squares
+  int cp_groups;         // shares per layer: the down kernel's work items of one token
+  const void* cn_w;      // the next layer's router matrix (null: last layer, no shares written)
+  int cn_wdt, cn_E;
+  const float* cn_norm_w;  // the next layer's norm weight (null: unit)
+  float* cp_out;         // the next layer's router shares
 };
 
 __device__ __forceinline__ float moe_act(int kind, float g, float u, float alpha, float limit) {
@@ -931,14 +942,24 @@ constexpr int DC_STAGE = (DC_PIECES + 63) / 64;  // of them per lane
 struct DownItem {
   MxRegs<DC_S, 1> R;
   v4f bias;
-  int t, hh, tile, rg, p, s0, s1, id_l;
+  int item, t, hh, tile, rg, p, s0, s1, id_l;
   float my_w;
+};
+
+// Decode chain (T = 1): what the down kernel's lanes need past the combine --
+// the residual stream at the lane's row (lane & 15 of the item's 16 rows),
+// and for the waves computing the next layer's router shares the next norm
+// weight at that row and expert e's router weights over the item's rows.
+struct DownChain {
+  float x, w;
+  float W[16];
 };
 
 __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& d, uint8_t* xs) {
   typedef const __attribute__((address_space(1))) v4u gv4u;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int groups = 4 * (int)a.gdn.tiles;
+  d.item = item;
   d.t = item / groups;
   d.hh = item - d.t * groups;
   d.tile = d.hh >> 2;
@@ -972,7 +993,9 @@ __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& 
   }
 }
 
-__device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&red)[16][16], const uint8_t* xs) {
+template <bool CHAIN = false>
+__device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&red)[16][16], const uint8_t* xs,
+                                         const DownChain* ch = nullptr) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int k = a.top_k;
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes land before its reads
@@ -982,10 +1005,12 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
   mx_compute<DC_S, 1>(d.R, a.gdn, d.s0, d.s1, D, d.rg);
   mx_sum_terms<1>(D);
   if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + d.bias;
-  // wave 0, while the others finish: the slots in ascending expert id (ties:
-  // lower slot) -- lane jj < k's rank, then rank r's slot jx[r] by ballot
+  // chain: waves 1 .. nlg compute the next layer's router shares from this item's rows (each combines them too)
+  const int nlg = CHAIN && a.cn_w ? (a.cn_E + 63) >> 6 : 0;
+  // wave 0 (and the share waves), while the others finish: the slots in ascending expert id
+  // (ties: lower slot) -- lane jj < k's rank, then rank r's slot jx[r] by ballot
   int jx[MAX_TOPK];
-  if (wave == 0) {
+  if (wave <= nlg) {
     int my_rank = 0;
 #pragma unroll
     for (int jj = 0; jj < MAX_TOPK; ++jj) {
@@ -999,7 +1024,7 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
     }
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave > nlg) return;
   const int row = d.tile * 64 + 16 * d.rg + (lane & 15);
   float o = 0.f;
   if (k <= 4 && a.cd == 4) {  // the usual shape (top-4, four K-chunks): every read issued at once
@@ -1027,7 +1052,28 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
       o = combine_one(o, w, y);
     }
   }
-  if (lane < 16 && row < a.n_embd) a.out[(int64_t)d.t * a.n_embd + row] = o;
+  if (wave == 0 && lane < 16 && row < a.n_embd) a.out[(int64_t)d.t * a.n_embd + row] = o;
+  if constexpr (CHAIN) {
+    // x + out, the residual add of gpt_oss.py:177 (the bits of x + r in add_rmsnorm_kernel), in place; and the
+    // next block's router shares over these rows: sum of x^2, and sum of (x * w) * W[e] per expert, rows in order
+    const bool live = row < a.n_embd;
+    const float xn = ch->x + o;
+    if (wave == 0) {
+      if (lane < 16 && live) a.cx[(int64_t)d.t * a.n_embd + row] = xn;
+      if (a.cn_w) {
+        const float q = nsx_wave_sum(lane < 16 && live ? xn * xn : 0.f);
+        if (lane == 0) a.cp_out[(int64_t)a.cp_groups * a.cn_E + d.item] = q;
+      }
+    } else {
+      const float xw = live ? xn * ch->w : 0.f;
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        acc = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, xw), i)), ch->W[i], acc);
+      const int e = 64 * (wave - 1) + lane;
+      if (e < a.cn_E) a.cp_out[(int64_t)d.item * a.cn_E + e] = acc;
+    }
+  }
 }
 
 // phase 2 on its own: XCD-aware order -- workgroup b runs on XCD b % 8, so
@@ -1044,6 +1090,219 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MoeDev a) {
   DownItem d;
   down_begin(a, item, d, xs[wave]);
   down_end(a, d, red, xs[wave]);
+}
+
+// ---------------------------------------------------------------------------
+// Stacked layers at decode (T = 1) without a router launch after the first
+// layer: model/gpt_oss.py:123-177 layer after layer, x = x + moe(rms_norm(x)
+// * w), with the router (gpt_oss.py:116-121) regrouped across the kernel
+// boundary. The down kernel of layer l, besides its rows of out, adds them to
+// the residual stream in place and writes, per work item (16 rows of the
+// token), its share of layer l + 1's router: the partial dot of x * w_{l+1}
+// over those rows with each expert's router row, and their partial sum of
+// squares. Layer l + 1's gate/up kernel adds the shares in a fixed order --
+// every workgroup the same way, so all of them select the same top-k -- and
+// forms logits = (sum of the dot shares) / rms + bias, which is h . W^T + b
+// for h = rms_norm(x) * w with the 1 / rms factored out of the dot; each
+// workgroup quantizes h = (x / rms) * w (add_rmsnorm_kernel's formula) into
+// LDS for its own MFMAs. Only the rms's summation order differs from the
+// separate norm, so results match it to rounding, not bit for bit.
+
+constexpr int CH_MAX_NS = 24;    // K-steps of h one gate/up workgroup holds in LDS (n_embd <= 3072)
+constexpr int CH_XQ_PASSES = 4;  // h blocks per lane half: 15 waves x 2 halves x 4 passes >= 4 * CH_MAX_NS
+constexpr int CH_SHARE_UNROLL = 8;  // share loads in flight per thread at once
+constexpr int CH_SUB = 32;          // subsets of the items summed apart (at most), then in subset order
+
+// 16 consecutive router weights as floats (dtype known at run time, wave-uniform)
+__device__ __forceinline__ void load16_w(const void* W, int wdt, int64_t off, float (&w)[16]) {
+  float a[8], b[8];
+  if (wdt == NSX_F32) {
+    load8_w<NSX_F32>(W, off, a);
+    load8_w<NSX_F32>(W, off + 8, b);
+  } else if (wdt == NSX_BF16) {
+    load8_w<NSX_BF16>(W, off, a);
+    load8_w<NSX_BF16>(W, off + 8, b);
+  } else {
+    load8_w<NSX_F16>(W, off, a);
+    load8_w<NSX_F16>(W, off + 8, b);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w[i] = a[i];
+    w[8 + i] = b[i];
+  }
+}
+
+// down + combine (as moe_down_kernel), then the residual add and the next layer's router shares
+__global__ __launch_bounds__(1024) void moe_down_chain_kernel(MoeDev a) {
+  __shared__ float red[16][16];
+  __shared__ __align__(16) uint8_t xs[16][DC_S * XQ_STEP];
+  hoist_down_args(a);
+  nsx_hoist((const void*)a.cx, (const void*)a.cn_w, (const void*)a.cn_norm_w, (const void*)a.cp_out, a.cn_wdt,
+            a.cn_E, a.cp_groups);
+  const int per = (int)(gridDim.x >> 3);
+  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (item >= a.T * 4 * (int)a.gdn.tiles) return;  // padding workgroups of the 8-way split
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  DownItem d;
+  down_begin(a, item, d, xs[wave]);
+  // issued behind the weights (loads retire in order: the MFMAs do not wait for these)
+  DownChain ch;
+  const int r0 = d.tile * 64 + 16 * d.rg;
+  const int row = min(r0 + (lane & 15), a.n_embd - 1);
+  ch.x = a.cx[(int64_t)d.t * a.n_embd + row];
+  ch.w = a.cn_norm_w ? a.cn_norm_w[row] : 1.f;
+  const int nlg = a.cn_w ? (a.cn_E + 63) >> 6 : 0;
+  if (wave >= 1 && wave <= nlg) {  // router row e over the item's rows (n_embd % 16 == 0: all 16 inside the row,
+                                    // or none: a group of the last tile past n_embd)
+    const int e = min(64 * (wave - 1) + lane, a.cn_E - 1);
+    if (r0 < a.n_embd) {
+      load16_w(a.cn_w, a.cn_wdt, (int64_t)e * a.n_embd + r0, ch.W);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ch.W[i] = 0.f;
+    }
+  }
+  down_end<true>(a, d, red, xs[wave], &ch);
+}
+
+// gate/up of one (pair, tile) of a chained layer: the router shares summed in
+// a fixed order, the top-k by wave 0 while waves 1.. quantize h into LDS, then
+// gu_item's gate/up with the activation terms read from LDS.
+__global__ __launch_bounds__(1024) void moe_gu_chain_kernel(MoeDev a) {
+  __shared__ float red[2][MAX_CHUNKS][64];
+  __shared__ __align__(16) float s_part[4096];  // [subset][E] sums of the dot shares (nsub * E <= 4096, E <= 128)
+  __shared__ int s_e;
+  __shared__ __align__(16) uint8_t s_xq[CH_MAX_NS * XQ_STEP];
+  typedef const __attribute__((address_space(1))) v4f gv4f;
+  hoist_gu_args(a);
+  nsx_hoist((const void*)a.cx, (const void*)a.cnorm_w, a.ceps, (const void*)a.cp_in, a.cp_groups);
+  const int tiles = (int)a.ggu.tiles;
+  const int p = blockIdx.x / tiles, tile = blockIdx.x - p * tiles;  // T = 1: pair p is slot p
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = __lane_id();
+  const int E = a.E, G = a.cp_groups, K = a.n_embd, nb = K / 32, nblk = 4 * a.ggu.ns;
+  // 1. every load of the prologue in one round, with no control flow between them (a branch makes the compiler
+  //    wait for every load before it): the items' sums of squares (every wave), x and w at this lane's h
+  //    elements, the router bias, then the dot shares -- thread (sub, col) sums 4 experts over items sub,
+  //    sub + nsub, ... in order (G <= CH_SHARE_UNROLL * nsub: one load each; indices clamped, extras masked)
+  const float* ss_sh = a.cp_in + (int64_t)G * E;
+  float ssv[4];  // G <= 256
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ssv[i] = ss_sh[min(lane + 64 * i, G - 1)];
+  float hx[CH_XQ_PASSES], hw[CH_XQ_PASSES];  // waves 1..: block 2 (wave - 1 + 15 i) + (lane >> 5)
+#pragma unroll
+  for (int i = 0; i < CH_XQ_PASSES; ++i) {
+    const int b = 2 * (max(wave - 1, 0) + 15 * i) + (lane >> 5);
+    const int c = min(b * 32 + (lane & 31), K - 1);
+    hx[i] = a.cx[c];
+    hw[i] = a.cnorm_w ? a.cnorm_w[c] : 1.f;
+  }
+  float rbias[2];  // wave 0: the router bias of experts lane + 64 i (E <= 128)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) rbias[i] = a.crouter_b ? a.crouter_b[min(lane + 64 * i, E - 1)] : 0.f;
+  const int ncol = E >> 2, nsub = min(CH_SUB, 1024 / ncol), col = tid % ncol, sub = tid / ncol;
+  const int subc = min(sub, nsub - 1);
+  const float* dot_sh = a.cp_in;
+  v4f v[CH_SHARE_UNROLL];
+#pragma unroll
+  for (int i = 0; i < CH_SHARE_UNROLL; ++i)
+    v[i] = *(gv4f*)(dot_sh + (int64_t)min(subc + i * nsub, G - 1) * E + 4 * col);
+  // 2. the subsets' dot shares meet in LDS; every wave takes 1 / rms from the sums of squares (items in order: the
+  //    same bits in every wave)
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < CH_SHARE_UNROLL; ++i)
+    if (subc + i * nsub < G) acc += v[i];
+  if (sub < nsub) *(v4f*)(s_part + sub * E + 4 * col) = acc;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss += lane + 64 * i < G ? ssv[i] : 0.f;
+  ss = nsx_wave_sum(ss);
+  const float inv = 1.f / sqrtf(ss / (float)K + a.ceps);
+  __syncthreads();
+  // 3. wave 0: each lane the logits of experts lane + 64 i (the subsets' sums in order, / rms, + bias), then the
+  //    top-k from registers (the token's first item writes the ids and weights); meanwhile waves 1..15 put h's
+  //    activation terms into LDS (two blocks a pass: h = (x / rms) * w, add_rmsnorm_kernel's formula) -- before
+  //    any weight load goes out, since a wave's loads stall at issue once HBM is saturated
+  const int k = a.top_k, j = p;
+  if (wave != 0) {
+#pragma unroll
+    for (int i = 0; i < CH_XQ_PASSES; ++i) {
+      const int b0 = 2 * (wave - 1 + 15 * i);  // wave-uniform: both halves' blocks b0, b0 + 1 are < nblk or not
+      if (b0 < nblk) {
+        const int b = b0 + (lane >> 5);
+        xq_block(b < nb ? (hx[i] * inv) * hw[i] : 0.f, b, s_xq);  // (a unit weight multiplies exactly)
+      }
+    }
+  } else {
+    float lv[2];  // E <= 128
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ee = min(lane + 64 * i, E - 1);
+      float sv[CH_SUB];  // every read at once (unpredicated: subsets past nsub read subset 0, then drop out)
+#pragma unroll
+      for (int sb = 0; sb < CH_SUB; ++sb) sv[sb] = s_part[(sb < nsub ? sb : 0) * E + ee];
+      float l = 0.f;
+#pragma unroll
+      for (int sb = 0; sb < CH_SUB; ++sb) l += sb < nsub ? sv[sb] : 0.f;
+      lv[i] = l * inv + rbias[i];
+    }
+    int si[MAX_TOPK];
+    float sw[MAX_TOPK];
+    const bool writes = j == 0 && tile == 0;
+    topk_select<2>(lv, E, k, a.mode, si, sw, writes, j + 1);
+    int my_e = 0, e = 0;
+    float my_w = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < MAX_TOPK; ++jj) {
+      e = jj == j ? si[jj] : e;
+      my_e = lane == jj ? si[jj] : my_e;
+      my_w = lane == jj ? sw[jj] : my_w;
+    }
+    if (writes && lane < k) {
+      a.ids[lane] = clamp_expert(my_e, E);
+      a.wts[lane] = my_w;
+    }
+    if (lane == 0) s_e = clamp_expert(e, E);
+  }
+  __syncthreads();
+  // 4. gu_item's gate/up: the weights' loads with no control flow between the steps, the activation terms from LDS
+  const int e = s_e;
+  const bool on = wave < 2 * a.cg;  // (waves past the gate/up chunks load a chunk too, and drop it)
+  const int m = on ? wave / a.cg : 0, c = on ? wave - m * a.cg : 0;
+  const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
+  const int row = tile * 64 + lane;
+  const int rowc = min(row, a.n_ff - 1);
+  MxRegs<GU_S> R;
+  const uint8_t* mat = m == 0 ? tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile)
+                              : tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
+  mx_load_a_flat<GU_S>(R, mat, a.ggu, s0, s1);
+  float gb = 0.f, ub = 0.f;
+  if (wave == 0) {  // the biases, requested behind the weights
+    if (a.gate_bias) gb = a.gate_bias[(int64_t)e * a.n_ff + rowc];
+    if (a.up_bias) ub = a.up_bias[(int64_t)e * a.n_ff + rowc];
+  }
+  v4f D[4] = {};
+  if (on) {
+    mx_load_b<GU_S, true>(R, s_xq, 0, 0, 1, s0, s1);
+    mx_compute<GU_S>(R, a.ggu, s0, s1, D);
+    mx_sum_terms(D);
+    if ((lane & 15) == 0) {
+      const int r0 = 4 * (lane >> 4);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(v4f*)(&red[m][c][16 * g + r0]) = D[g];
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float gs = 0.f, us = 0.f;
+  for (int cc = 0; cc < a.cg; ++cc) {
+    gs += red[0][cc][lane];
+    us += red[1][cc][lane];
+  }
+  const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
+  xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
+  xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)p * a.gdn.ns * XQ_STEP);
 }
 
 // ---------------------------------------------------------------------------
@@ -2898,22 +3157,10 @@ static int launch_raw_phases(const MoeDev& d, int64_t T, hipStream_t st, bool ga
   return nsx_launch(moe_down_raw_kernel<FMT>, dim3(g2), dim3(64 * RAW_WAVES), lds2, st, d);
 }
 
-// Phases ph0..ph1 of one layer (NSX_PHASE_*); each later phase reads what
-// the earlier ones left in the workspace.
-static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
-                   void* workspace, int64_t workspace_bytes, void* stream, int ph0, int ph1,
-                   RtNorm nm = RtNorm{0, nullptr, nullptr, 0.f, nullptr}, const AddNorm* an = nullptr) {
-  int rc = check_layer(L, T);
-  if (rc) return rc;
-  NSX_REQUIRE(h && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
-  const MoePlan p = moe_plan(L, T);
-  NSX_REQUIRE(workspace_bytes >= p.total, NSX_EINVAL, "workspace of %lld bytes, need %lld",
-              (long long)workspace_bytes, (long long)p.total);
-  NSX_REQUIRE(T * L->top_k < (1ll << 24), NSX_EINVAL, "too many (token, expert) pairs");
-  hipStream_t st = S(stream);
-  char* ws = (char*)workspace;
-  const bool t64 = L->layout == NSX_LAYOUT_T64;
-
+// The device view of a layer call: T tokens h -> out, ids, weights over the
+// workspace laid out by moe_plan.
+static MoeDev make_dev(const nsx_moe_layer* L, const MoePlan& p, char* ws, const float* h, int64_t T, float* out,
+                       int32_t* ids, float* weights) {
   MoeDev d{};
   d.logits = (const float*)(ws + p.off_logits);
   d.ids = ids;
@@ -2961,6 +3208,25 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
   d.max_items = p.max_items;
   d.cdg = p.cdg;
   d.sdg = p.sdg;
+  return d;
+}
+
+// Phases ph0..ph1 of one layer (NSX_PHASE_*); each later phase reads what
+// the earlier ones left in the workspace.
+static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out, int32_t* ids, float* weights,
+                   void* workspace, int64_t workspace_bytes, void* stream, int ph0, int ph1,
+                   RtNorm nm = RtNorm{0, nullptr, nullptr, 0.f, nullptr}, const AddNorm* an = nullptr) {
+  int rc = check_layer(L, T);
+  if (rc) return rc;
+  NSX_REQUIRE(h && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
+  const MoePlan p = moe_plan(L, T);
+  NSX_REQUIRE(workspace_bytes >= p.total, NSX_EINVAL, "workspace of %lld bytes, need %lld",
+              (long long)workspace_bytes, (long long)p.total);
+  NSX_REQUIRE(T * L->top_k < (1ll << 24), NSX_EINVAL, "too many (token, expert) pairs");
+  hipStream_t st = S(stream);
+  char* ws = (char*)workspace;
+  const bool t64 = L->layout == NSX_LAYOUT_T64;
+  MoeDev d = make_dev(L, p, ws, h, T, out, ids, weights);
   // Per-pair Q4_K below RM_MIN_T tokens: the gate/up kernel selects the top-k itself (no top-k launch), but only
   // when this call runs both phases -- a router phase run on its own always leaves the ids and weights written.
   // (the raw-row kernels of the other GGUF layouts likewise)
@@ -3152,6 +3418,102 @@ extern "C" int nsx_moe_forward_addnorm(const nsx_moe_layer* L, const float* h, i
                  stream, NSX_PHASE_ROUTER, NSX_PHASE_COMBINE, RtNorm{0, nullptr, nullptr, 0.f, nullptr}, &an);
     if (rc) return rc;
   }
+  return NSX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// One layer of a stacked FFN chain at decode (T = 1): x += moe(rms_norm(x) *
+// norm_w) in place, the router of every layer after the first regrouped
+// across the kernel boundary (moe_gu_chain_kernel, moe_down_chain_kernel).
+
+// the down kernel's work items of one token: one router share each
+static int64_t chain_groups(const nsx_moe_layer* L) { return 4 * mx_geom(L->n_embd, L->n_ff).tiles; }
+
+static int check_chain_layer(const nsx_moe_layer* L) {
+  int rc = check_layer(L, 1);
+  if (rc) return rc;
+  NSX_REQUIRE(L->layout == NSX_LAYOUT_T64 && !use_grouped(L, 1), NSX_ENOTIMPL,
+              "the decode chain runs t64 layers on the per-pair kernels");
+  const MoePlan p = moe_plan(L, 1);
+  NSX_REQUIRE(L->n_embd % 16 == 0 && p.ggu.ns <= CH_MAX_NS && L->n_expert % 4 == 0 && L->n_expert <= 128 &&
+                  chain_groups(L) <= 256 && p.cg <= MAX_CHUNKS,
+              NSX_ENOTIMPL,
+              "the decode chain takes n_embd a multiple of 16 up to %d and a multiple of 4 experts up to 128",
+              CH_MAX_NS * 128);
+  return NSX_OK;
+}
+
+extern "C" int64_t nsx_moe_chain_share_bytes(const nsx_moe_layer* L) {
+  if (check_chain_layer(L) != NSX_OK) return -1;
+  return chain_groups(L) * (L->n_expert + 1) * 4;
+}
+
+extern "C" int nsx_moe_chain_t1(const nsx_moe_layer* L, float* x, const float* norm_w, float eps,
+                                const float* share_in, const nsx_moe_layer* next, const float* next_norm_w,
+                                float* share_out, float* out, int32_t* ids, float* weights, void* workspace,
+                                int64_t workspace_bytes, int phases, void* stream) {
+  int rc = check_chain_layer(L);
+  if (rc) return rc;
+  NSX_REQUIRE(x && out && ids && weights && workspace, NSX_EINVAL, "null buffer");
+  NSX_REQUIRE(eps >= 0.f, NSX_EINVAL, "eps %g", (double)eps);
+  NSX_REQUIRE(phases >= 1 && phases <= 3, NSX_EINVAL, "phases %d: NSX_CHAIN_GATE_UP | NSX_CHAIN_DOWN", phases);
+  const MoePlan p = moe_plan(L, 1);
+  NSX_REQUIRE(workspace_bytes >= p.total, NSX_EINVAL, "workspace of %lld bytes, need %lld",
+              (long long)workspace_bytes, (long long)p.total);
+  const int64_t G = chain_groups(L);
+  if (next) {
+    if ((rc = check_chain_layer(next))) return rc;
+    NSX_REQUIRE(next->n_embd == L->n_embd, NSX_EINVAL, "the next layer has n_embd %d, this one %d", next->n_embd,
+                L->n_embd);
+    NSX_REQUIRE(share_out, NSX_EINVAL, "a next layer needs share_out");
+    NSX_REQUIRE(L->top_k * p.cd >= 1 + nsx_cdiv(next->n_expert, 64), NSX_ENOTIMPL,
+                "the down workgroup has %d waves, the next router's shares need %d", L->top_k * p.cd,
+                1 + (int)nsx_cdiv(next->n_expert, 64));
+  }
+  // x and out are n_embd floats; a share buffer G * (E + 1) floats (share_in may be share_out: the gate/up
+  // kernel has read it before the down kernel writes)
+  auto overlap = [](const void* a, int64_t an, const void* b, int64_t bn) {
+    const uintptr_t u = (uintptr_t)a, v = (uintptr_t)b;
+    return a && b && u < v + (uintptr_t)(bn * 4) && v < u + (uintptr_t)(an * 4);
+  };
+  const int64_t n = L->n_embd;
+  NSX_REQUIRE(!overlap(x, n, out, n) && !overlap(x, n, share_in, G * (L->n_expert + 1)) &&
+                  !overlap(x, n, share_out, next ? G * (next->n_expert + 1) : 0) &&
+                  !overlap(out, n, share_out, next ? G * (next->n_expert + 1) : 0) &&
+                  !overlap(out, n, share_in, G * (L->n_expert + 1)),
+              NSX_EINVAL, "x, out and the share buffers must not overlap");
+  hipStream_t st = S(stream);
+  char* ws = (char*)workspace;
+  MoeDev d = make_dev(L, p, ws, out, 1, out, ids, weights);
+  d.cx = x;
+  d.cnorm_w = norm_w;
+  d.ceps = eps;
+  d.crouter_b = L->router_bias;
+  d.cp_in = share_in;
+  d.cp_groups = (int)G;
+  d.cn_w = next ? next->router_w : nullptr;
+  d.cn_wdt = next ? next->router_dtype : 0;
+  d.cn_E = next ? next->n_expert : 0;
+  d.cn_norm_w = next_norm_w;
+  d.cp_out = share_out;
+  if (phases & NSX_CHAIN_GATE_UP) {
+    if (share_in == nullptr) {  // the first layer routes from x: h = rms_norm(x) * w into out (scratch until the
+                                // down kernel writes the layer's output there), the router, the per-pair gate/up
+      if ((rc = nsx_add_rmsnorm(x, nullptr, 1, n, eps, norm_w, nullptr, out, stream))) return rc;
+      if ((rc = launch_logits(out, 1, n, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
+                              (float*)(ws + p.off_logits), (uint8_t*)(ws + p.off_xqh), st,
+                              RtNorm{0, nullptr, nullptr, 0.f, nullptr})))
+        return rc;
+      if ((rc = nsx_launch(moe_gu_kernel, dim3((unsigned)(L->top_k * p.ggu.tiles)), dim3(128 * p.cg), 0, st, d)))
+        return rc;
+    } else if ((rc = nsx_launch(moe_gu_chain_kernel, dim3((unsigned)(L->top_k * p.ggu.tiles)), dim3(1024), 0, st,
+                                d))) {
+      return rc;
+    }
+  }
+  if (phases & NSX_CHAIN_DOWN)
+    return nsx_launch(moe_down_chain_kernel, dim3((unsigned)(8 * nsx_cdiv(4 * p.gdn.tiles, 8))),
+                      dim3(64 * L->top_k * p.cd), 0, st, d);
   return NSX_OK;
 }
 

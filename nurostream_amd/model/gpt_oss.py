@@ -62,6 +62,10 @@ class GptOssFFNStack:
         self.router_stats = RouterStats()
         self._bufs: dict[int, tuple] = {}
         self._alt: dict[int, torch.Tensor] = {}  # the residual stream's second buffer, per T
+        # one token runs as a decode chain (no router launch after the first layer) where every layer can
+        self.decode_chain = True
+        self._chain: bool | None = None
+        self._share: torch.Tensor | None = None
 
     def _buffers(self, T: int):
         b = self._bufs.get(T)
@@ -86,6 +90,8 @@ class GptOssFFNStack:
         x = x.reshape(-1, self.cfg.n_embd)
         T = x.shape[0]
         h, y, ids, wts = self._buffers(T)
+        if T == 1 and self.decode_chain and self._chain_ok():
+            return self._forward_chain(x, out, y, ids, wts)
         alt = self._alt.get(T)
         if alt is None:
             alt = self._alt[T] = torch.empty(T, self.cfg.n_embd, device=self.device)
@@ -115,6 +121,30 @@ class GptOssFFNStack:
         return res
 
     __call__ = forward
+
+    def _chain_ok(self) -> bool:
+        if self._chain is None:
+            sizes = [layer.chain_share_bytes() for layer in self.layers]
+            self._chain = min(sizes) >= 0
+            if self._chain:
+                self._share = torch.empty(max(sizes), dtype=torch.uint8, device=self.device)
+        return self._chain
+
+    def _forward_chain(self, x, out, y, ids, wts) -> torch.Tensor:
+        """One token through every layer as a decode chain (MoELayer.chain_t1):
+        the residual stream updated in place in `out`, and after the first layer
+        no router launch -- each down kernel leaves the next layer's router
+        shares in one buffer, which that layer's gate/up kernel reads (matches
+        the separate norm to rounding: the rms is summed in another order)."""
+        res = torch.empty_like(x) if out is None else out
+        res.copy_(x)
+        eps, n = self.cfg.rms_eps, len(self.layers)
+        for li, layer in enumerate(self.layers):
+            nxt = self.layers[li + 1] if li + 1 < n else None
+            layer.chain_t1(res, self.norm_weights[li], eps, self._share if li else None, nxt,
+                           None if nxt is None else self.norm_weights[li + 1], None if nxt is None else self._share,
+                           y, ids[li], wts[li])
+        return res
 
     def last_routing(self, T: int) -> tuple[torch.Tensor, torch.Tensor]:
         """(ids (L, T, k), weights (L, T, k)) of the last forward over T tokens."""

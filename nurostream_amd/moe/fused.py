@@ -260,6 +260,63 @@ class MoELayer:
                                                      N.stream_ptr(self.device)), "moe_forward_addnorm")
         return ids, weights
 
+    def chain_share_bytes(self) -> int:
+        """Bytes of a router-share buffer for chain_t1, or -1 when this layer
+        cannot run in the decode chain (t64 on the per-pair kernels, n_embd a
+        multiple of 16 up to 3072, a multiple of 4 experts up to 128)."""
+        return int(N.load().nsx_moe_chain_share_bytes(C.byref(self._c)))
+
+    def chain_t1(self, x: torch.Tensor, norm_w: torch.Tensor | None, eps: float, share_in: torch.Tensor | None,
+                 next_layer: "MoELayer | None", next_norm_w: torch.Tensor | None, share_out: torch.Tensor | None,
+                 out: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, phases: int = 3) -> None:
+        """One stacked block of a decode chain (T = 1; model/gpt_oss.py:123-177):
+        x += forward(rms_norm(x) * norm_w) in place, out/ids/weights as forward.
+        share_in None: the block routes from x (norm, router, gate/up launches);
+        else it holds this block's router shares, written by the previous
+        block's call, and no router launch runs. With next_layer the down kernel
+        also writes that block's shares to share_out (may be share_in). x, out:
+        (1, n_embd) contiguous fp32; share buffers: uint8 or fp32 device tensors
+        of chain_share_bytes() (nsx_moe_chain_t1). phases: N.CHAIN_GATE_UP,
+        N.CHAIN_DOWN or both (one launch alone reads what the other left, for
+        timing)."""
+        N.require_device(x, out)
+        for name, t in (("x", x), ("out", out)):
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != self.n_embd or t.device != self.device:
+                raise ValueError(f"{name} must be a contiguous fp32 tensor of {self.n_embd} values on {self.device}")
+        self._check_buffers(1, out.view(1, -1), ids, weights)
+
+        def vec(w):
+            if w is None:
+                return None
+            w = w.to(device=self.device, dtype=torch.float32).contiguous()
+            if w.numel() != self.n_embd:
+                raise ValueError(f"norm weight of {w.numel()} values, n_embd is {self.n_embd}")
+            return w
+
+        def share(buf, layer):
+            if buf is None:
+                return None
+            need = layer.chain_share_bytes()
+            if need < 0:
+                raise NotImplementedError("this layer does not run in the decode chain")
+            if buf.device != self.device or not buf.is_contiguous() or buf.numel() * buf.element_size() < need:
+                raise ValueError(f"share buffer must be a contiguous device tensor of >= {need} bytes")
+            return buf
+
+        w, nw = vec(norm_w), vec(next_norm_w)
+        si = share(share_in, self)
+        so = share(share_out, next_layer) if next_layer is not None else None
+        if next_layer is not None and so is None:
+            raise ValueError("a next layer needs share_out")
+        ws = self.workspace(1)
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        with torch.cuda.device(self.device):
+            N.check(N.load().nsx_moe_chain_t1(C.byref(self._c), x.data_ptr(), ptr(w), float(eps), ptr(si),
+                                              None if next_layer is None else C.byref(next_layer._c), ptr(nw),
+                                              ptr(so), out.data_ptr(), ids.data_ptr(), weights.data_ptr(),
+                                              ws.data_ptr(), ws.numel(), int(phases), N.stream_ptr(self.device)),
+                    "moe_chain_t1")
+
     def phase(self, phase: int, h: torch.Tensor, out: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
               workspace: torch.Tensor | None = None) -> None:
         """Run one phase (_native.PHASE_*) of forward(); later phases read what

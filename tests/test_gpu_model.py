@@ -36,6 +36,7 @@ def test_stack_norm_in_router_equals_separate_norm(dev, T):
     cfg = _small("gptoss-small")
     L = 3
     stack = GptOssFFNStack.synthetic(cfg, L, seed=23, device=dev)
+    stack.decode_chain = False  # the folded-norm path (one token's decode chain matches it to rounding)
     stack.norm_weights = [None] + [1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(li))
                                    .to(dev) for li in range(1, L)]
     x = synth.activations(T, cfg.n_embd, seed=11, device=dev)
@@ -118,6 +119,102 @@ def test_forward_addnorm_short_last_pass(dev, name, layout, T):
     tail = slice(T - 8, T)  # the short pass's rows first, so a failure names them
     assert torch.equal(xo[tail], xr[tail]) and torch.equal(ho[tail], hr[tail])
     assert torch.equal(xo, xr) and torch.equal(ho, hr)
+
+
+def test_decode_chain_matches_separate_norm_and_oracle(dev):
+    """One token through a stack as a decode chain (nsx_moe_chain_t1: after the
+    first layer no router launch; each down kernel leaves the next layer's
+    router shares, each gate/up kernel sums them and quantizes h itself):
+    the same routing as the separate-norm path and its outputs to rounding
+    (non-unit norm weights), the oracle's chain within the MFMA bound (unit
+    weights), and graph replays bit-stable with eager work between them."""
+    from nurostream_amd import synth
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack
+    cfg = _small("gptoss-small")
+    L = 4
+    stack = GptOssFFNStack.synthetic(cfg, L, seed=27, device=dev)
+    assert all(layer.chain_share_bytes() > 0 for layer in stack.layers)
+    x = synth.activations(1, cfg.n_embd, seed=13, device=dev)
+    y = stack(x)
+    ids_c = stack.last_routing(1)[0].clone()
+    ref = OM.ffn_stack(x.cpu().numpy(), _oracle_layers(cfg, 27, L, dev), cfg.top_k)
+    err = rel_max(to_np(y), ref)
+    assert err < L * MFMA_TOL, err
+    stack.norm_weights = [(1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(70 + li)))
+                          .to(dev) for li in range(L)]
+    y_c = stack(x)
+    ids_c = stack.last_routing(1)[0].clone()
+    stack.decode_chain = False
+    y_s = stack(x)
+    ids_s = stack.last_routing(1)[0].clone()
+    stack.decode_chain = True
+    torch.cuda.synchronize()
+    assert torch.equal(ids_c, ids_s)
+    assert rel_max(to_np(y_c), to_np(y_s)) < 1e-5
+    out = torch.empty_like(x)
+    stack(x, out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        stack(x, out=out)
+    for i in range(3):
+        out.zero_()
+        stack(synth.activations(1, cfg.n_embd, seed=90 + i, device=dev))  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y_c), i
+
+
+def test_decode_chain_first_layer_is_norm_then_forward(dev):
+    """chain_t1 without shares (the first layer) routes from x itself: out,
+    ids and weights are forward(add_rms_norm(x) * w) bit for bit, x becomes
+    x + out in place, and with a next layer the shares it leaves give that
+    layer the routing forward() gives from add_rms_norm of the new x."""
+    from nurostream_amd import synth
+    from nurostream_amd.compute.ops import add_rms_norm
+    from nurostream_amd.model.gpt_oss import GptOssFFNStack
+    cfg = _small("gptoss-small")
+    stack = GptOssFFNStack.synthetic(cfg, 2, seed=29, device=dev)
+    l0, l1 = stack.layers
+    w0 = (1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(3))).to(dev)
+    w1 = (1 + 0.1 * torch.randn(cfg.n_embd, generator=torch.Generator().manual_seed(4))).to(dev)
+    x = synth.activations(1, cfg.n_embd, seed=17, device=dev)
+    o_ref, ids_ref, w_ref = l0.forward(add_rms_norm(x, None, w0, 1e-5))
+    xr = x.clone()
+    share = torch.zeros(l1.chain_share_bytes(), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(x)
+    ids = torch.empty(1, cfg.top_k, dtype=torch.int32, device=dev)
+    wts = torch.empty(1, cfg.top_k, device=dev)
+    l0.chain_t1(xr, w0, 1e-5, None, l1, w1, share, out, ids, wts)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o_ref) and torch.equal(ids, ids_ref) and torch.equal(wts, w_ref)
+    assert torch.equal(xr, x + o_ref)
+    o1, ids1_ref, _ = l1.forward(add_rms_norm(xr, None, w1, 1e-5))
+    x2 = xr.clone()
+    l1.chain_t1(x2, w1, 1e-5, share, None, None, None, out, ids, wts)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids1_ref)
+    assert rel_max(to_np(out), to_np(o1)) < 1e-5
+    assert torch.equal(x2, xr + out)
+
+
+def test_decode_chain_refuses_what_it_cannot_run(dev):
+    """Layers outside the chain's shapes report no share size and raise
+    instead of running: GGUF-layout Q4_K experts, and grouped dispatch."""
+    from nurostream_amd import synth
+    from moe_cases import _layer
+    q = _small("qwen3-small")
+    lq = _layer(q, synth.make_layer(q, seed=5, device=dev), "gguf")
+    assert lq.chain_share_bytes() < 0
+    g = _small("gptoss-small")
+    lg = _layer(g, synth.make_layer(g, seed=5, device=dev), "t64", dispatch="grouped")
+    assert lg.chain_share_bytes() < 0
+    x = torch.zeros(1, g.n_embd, device=dev)
+    with pytest.raises(NotImplementedError):
+        lg.chain_t1(x, None, 1e-5, None, None, None, None, torch.empty_like(x),
+                    torch.empty(1, g.top_k, dtype=torch.int32, device=dev), torch.empty(1, g.top_k, device=dev))
 
 
 @pytest.mark.parametrize("T", [1, 2, 9])
@@ -212,6 +309,9 @@ def test_host_streamed_stack_equals_resident(dev, T, frac, mode):
     res = GptOssFFNStack.synthetic(cfg, L, seed=31, device=dev)
     hs = GptOssHostStreamedStack.synthetic(cfg, L, seed=31, device=dev, host_fraction=frac, block_rows=64,
                                            mode=mode)
+    # staged modes run add_rms_norm + forward per layer: the resident stack's folded-norm path has their bits
+    # (one token's decode chain matches them to rounding); read mode runs the resident stack's own path
+    res.decode_chain = mode == "read"
     assert sum(st.host_bytes for st in hs.stores) > 0
     x = synth.activations(T, cfg.n_embd, seed=40 + T, device=dev)
     for _ in range(2):  # a second step reuses the slots and tables

@@ -107,9 +107,12 @@ def _norm_weights(n_embd, dev):
 
 @pytest.fixture(scope="module", params=[1, 8], ids=["T1", "T8"])
 def chain(request, dev, stack):
-    """The stack's output over T tokens, and the same chain spelled out with
-    add_rms_norm + MoELayer.forward per layer; the inputs (x_l before the norm,
-    h_l after it), outputs and routing of the KEEP layers, on the host."""
+    """The stack's output over T tokens and the same chain spelled out with
+    add_rms_norm + MoELayer.forward per layer, keeping the inputs (x_l before
+    the norm, h_l after it), outputs and routing of the KEEP layers on the
+    host. At T=1 the stack runs the decode chain (MoELayer.chain_t1), so also:
+    the folded-norm path's output (decode_chain off) and the decode chain
+    spelled out call by call, with its own KEEP layers' inputs and outputs."""
     from nurostream_amd import synth
     from nurostream_amd.compute.ops import add_rms_norm
     T = request.param
@@ -117,10 +120,18 @@ def chain(request, dev, stack):
     print(f"[stack_full] chain T={T}: fused stack vs spelled out", flush=True)
     saved = stack.norm_weights
     stack.norm_weights = nw = _norm_weights(cfg.n_embd, dev)
+    rec = {"T": T}
     try:  # the weights go back before the fixture returns: later tests of the module share `stack`
         x = synth.activations(T, cfg.n_embd, seed=70 + T, device=dev)
-        y = stack(x).clone()
-        ids_s, wts_s = (t.clone() for t in stack.last_routing(T))
+        rec["y"] = stack(x).clone()
+        rec["ids_y"], rec["wts_y"] = (t.clone() for t in stack.last_routing(T))
+        if T == 1:
+            stack.decode_chain = False
+            try:
+                rec["fold"] = stack(x).clone()
+                rec["ids_fold"] = stack.last_routing(T)[0].clone()
+            finally:
+                stack.decode_chain = True
         res = torch.empty_like(x)
         h = add_rms_norm(x, None, nw[0], 1e-5, sum_out=res)
         kept, ids_c, wts_c = {}, [], []
@@ -134,34 +145,55 @@ def chain(request, dev, stack):
                 x_l = x if li == 0 else res
                 kept[li] = tuple(t.cpu().numpy() for t in (x_l, h, o, ids, w)) + (nw[li].cpu().numpy(),)
         res.add_(o)
+        rec.update(spelled=res, ids_spelled=torch.stack(ids_c), wts_spelled=torch.stack(wts_c), kept=kept)
+        if T == 1:  # the decode chain call by call (the calls stack.forward makes at T=1)
+            xs = x.clone()
+            o = torch.empty_like(x)
+            ids = torch.empty(1, cfg.top_k, dtype=torch.int32, device=dev)
+            w = torch.empty(1, cfg.top_k, device=dev)
+            share, n, kc = stack._share, len(stack.layers), {}
+            for li, layer in enumerate(stack.layers):
+                nxt = stack.layers[li + 1] if li + 1 < n else None
+                x_l = xs.cpu().numpy() if li in KEEP else None
+                layer.chain_t1(xs, nw[li], 1e-5, share if li else None, nxt, None if nxt is None else nw[li + 1],
+                               None if nxt is None else share, o, ids, w)
+                if li in KEEP:
+                    kc[li] = (x_l, None) + tuple(t.cpu().numpy() for t in (o, ids, w)) + (nw[li].cpu().numpy(),)
+            rec.update(chain_spelled=xs, kept_chain=kc)
         torch.cuda.synchronize()
     finally:
         stack.norm_weights = saved
-    return {"T": T, "y": y, "spelled": res, "ids": (ids_s, torch.stack(ids_c)),
-            "wts": (wts_s, torch.stack(wts_c)), "kept": kept}
+    return rec
 
 
 def test_full_stack_fused_norms_equal_spelled_out_chain(chain):
-    """T=1 runs each block's norm inside the router kernel (nsx_moe_forward_norm),
-    T=8 inside the combine kernel (moe_combine_norm_kernel); both give the
-    separate add_rms_norm's bits at hidden 2880 through all 36 layers."""
-    ids_s, ids_c = chain["ids"]
-    wts_s, wts_c = chain["wts"]
-    assert torch.equal(ids_s, ids_c)
-    assert torch.equal(wts_s, wts_c)
-    assert torch.equal(chain["y"], chain["spelled"])
+    """T=8 runs each block's norm inside the combine kernel
+    (moe_combine_norm_kernel), T=1 with the decode chain off inside the router
+    kernel (nsx_moe_forward_norm): both give the separate add_rms_norm's bits
+    at hidden 2880 through all 36 layers. The decode chain (T=1) is its own
+    calls spelled out bit for bit, and the separate-norm chain to rounding
+    (the rms is summed in another order), with the same routing."""
+    if chain["T"] == 8:
+        assert torch.equal(chain["ids_y"], chain["ids_spelled"])
+        assert torch.equal(chain["wts_y"], chain["wts_spelled"])
+        assert torch.equal(chain["y"], chain["spelled"])
+        return
+    assert torch.equal(chain["fold"], chain["spelled"])
+    assert torch.equal(chain["ids_fold"], chain["ids_spelled"])
+    assert torch.equal(chain["y"], chain["chain_spelled"])
+    assert torch.equal(chain["ids_y"], chain["ids_spelled"])
+    err = rel_max(to_np(chain["y"]), to_np(chain["spelled"]))
+    print(f"[stack_full] T=1 decode chain vs the separate-norm chain: max rel err {err:.3g}", flush=True)
+    assert err < MFMA_TOL, err
 
 
-@pytest.mark.parametrize("layer", KEEP)
-def test_full_stack_layer_matches_oracle_teacher_forced(dev, chain, layer):
-    """Layer `layer` of the chain, given the GPU's own input: the norm against
-    oracle.rms_norm, the routing and the MoE block against oracle.moe_gptoss
-    (ids exact outside fp32 near-ties; output within the MFMA bound on every
-    token whose routing is not a near-tie)."""
+def _teacher_forced(dev, layer, x_l, h, o, ids, w, nw, T, what):
     from nurostream_amd import synth
     cfg = synth.GPTOSS_120B
-    x_l, h, o, ids, w, nw = chain["kept"][layer]
-    assert rel_max(h, OM.rms_norm(x_l, nw, 1e-5)) < 2e-6
+    href = OM.rms_norm(x_l, nw, 1e-5)
+    if h is not None:
+        assert rel_max(h, href) < 2e-6
+    h = href if h is None else h
     t = synth.make_layer(cfg, seed=SEED, device=dev, layer=layer)
     Wr, br = t["router_w"].float().cpu().numpy(), t["router_b"].cpu().numpy()
     per = {k: cfg.expert_bytes(k) for k in ("gate", "up", "down")}
@@ -178,8 +210,20 @@ def test_full_stack_layer_matches_oracle_teacher_forced(dev, chain, layer):
     np.testing.assert_array_equal(ids[ok], rid[ok])
     np.testing.assert_allclose(w[ok], rw[ok], rtol=2e-5, atol=1e-6)
     err = rel_max(o[ok], ref[ok])
-    print(f"[stack_full] T={chain['T']} layer {layer}: max rel err {err:.3g}", flush=True)
+    print(f"[stack_full] T={T} layer {layer} ({what}): max rel err {err:.3g}", flush=True)
     assert err < FFN_BAR and err < MFMA_TOL, err
+
+
+@pytest.mark.parametrize("layer", KEEP)
+def test_full_stack_layer_matches_oracle_teacher_forced(dev, chain, layer):
+    """Layer `layer` of the chain, given the GPU's own input: the norm against
+    oracle.rms_norm, the routing and the MoE block against oracle.moe_gptoss
+    (ids exact outside fp32 near-ties; output within the MFMA bound on every
+    token whose routing is not a near-tie). At T=1 also the decode chain's
+    layer (x_l -> oracle.rms_norm -> oracle.moe_gptoss against its output)."""
+    _teacher_forced(dev, layer, *chain["kept"][layer], chain["T"], "add_rms_norm + forward")
+    if chain["T"] == 1:
+        _teacher_forced(dev, layer, *chain["kept_chain"][layer], 1, "decode chain")
 
 
 @pytest.fixture(scope="module")
@@ -209,7 +253,11 @@ def test_full_stack_host25_staged_equals_resident(dev, stack, staged_stack, mode
     hs.set_mode(mode)
     print(f"[stack_full] host25 {mode} T={T}", flush=True)
     x = synth.activations(T, synth.GPTOSS_120B.n_embd, seed=95 + T, device=dev)
-    ref = stack(x)
+    stack.decode_chain = False  # the staged modes run add_rms_norm + forward per layer: the folded-norm path's bits
+    try:
+        ref = stack(x)
+    finally:
+        stack.decode_chain = True
     b0 = hs.bytes_from_host
     got = hs(x)
     torch.cuda.synchronize()
