@@ -736,8 +736,10 @@ struct MoeDev {
   int act_kind;
   float alpha, limit;
   // grouped dispatch (pairs sorted by expert)
-  int4* items;           // work items: (expert, first sorted position, tokens, 0)
+  int4* items;           // work items: (expert, first sorted position, tokens, q | pairs of the expert << 16)
   int* n_items;
+  int4* gu_items;        // the MXFP4 gate/up kernel's work items: (expert, first sorted position, tokens, 0)
+  int* gu_bounds;        // [9]: XCD x runs gate/up units [gu_bounds[x], gu_bounds[x + 1])
   int32_t* sorted;       // pair ids, ascending expert, ascending pair id inside
   int32_t* corder;       // per token: its pair ids in ascending expert id
   float* y;              // (pairs, n_embd) expert outputs, bias included
@@ -1308,20 +1310,49 @@ __global__ __launch_bounds__(1024) void moe_gu_chain_kernel(MoeDev a) {
 // ---------------------------------------------------------------------------
 // grouped dispatch (several tokens): the (token, expert) pairs are sorted by
 // expert; a work item is up to GRP_TPI tokens of one expert, and a workgroup
-// is (item, 64-row tile), so an expert's tile is read once per item rather
-// than once per pair. Items of one tile sit on one XCD (consecutive items of
-// an expert share its L2). Each token's columns are computed exactly as the
+// is (item, 64-row tile), so an expert's tile is requested once per item
+// rather than once per pair, and the items of one tile run side by side on
+// one XCD, so HBM serves it once (grp_unit). Each token's columns are computed exactly as the
 // per-pair kernels compute them (same K-chunks, same summation order), and
 // the combine adds the experts in ascending id: the outputs do not depend on
 // the dispatch.
 
 constexpr int GRP_TPI = 16;          // tokens per work item
+constexpr int GRP_GU_T = 64;         // tokens per MXFP4 gate/up work item (GRP_TPI at a time)
 constexpr int GRP_MAX_PAIRS = 4096;  // pairs per sort (nsx_moe_forward splits larger T)
 constexpr int GRP_CHUNKS = GRP_MAX_PAIRS / 64;
 
-__host__ __device__ __forceinline__ int grp_max_items(int E, int P) {
-  return (E < P ? E : P) + (P + GRP_TPI - 1) / GRP_TPI;
+__host__ __device__ __forceinline__ int grp_max_items(int E, int P, int tpi = GRP_TPI) {
+  return (E < P ? E : P) + (P + tpi - 1) / tpi;
 }
+
+// Item q of expert e, whose cnt pairs start at sorted position bc: (e, first
+// sorted position, tokens, q | cnt << 16). The last word lets a unit index
+// find any item of the expert from the record of one of them (grp_unit).
+__device__ __forceinline__ int4 grp_item(int e, int bc, int cnt, int q) {
+  return make_int4(e, bc + q * GRP_TPI, min(GRP_TPI, cnt - q * GRP_TPI), q | (cnt << 16));
+}
+
+// Unit L of a dispatch whose items have `units` units each, given rec = the
+// record of item s = L / units. An expert of m items owns the units
+// [f * units, (f + m) * units), f its first item; they run tile-major -- unit
+// u of the range is unit u / m of item f + u % m -- so the m items that need
+// one weight tile are adjacent on one XCD and share its fetch in L2 (item-major,
+// the XCD streams the expert's other tiles in between and each item re-reads
+// it from HBM). Returns the item; `unit` gets its unit.
+__device__ __forceinline__ int4 grp_unit(int4 rec, int s, int L, int units, int& unit) {
+  const int q = rec.w & 0xffff, cnt = rec.w >> 16, m = (cnt + GRP_TPI - 1) / GRP_TPI;
+  const int u = L - (s - q) * units;
+  unit = u / m;
+  const int qq = u - unit * m;
+  return make_int4(rec.x, rec.y + (qq - q) * GRP_TPI, min(GRP_TPI, cnt - qq * GRP_TPI), 0);
+}
+
+// Relative time of a gate/up unit of z tokens, m = ceil(z / GRP_TPI) passes,
+// fitted to per-unit timestamps of config 3 (T = 128): about 3.8 + 0.31 z +
+// 2.6 m us. A pass past the first is not hidden under the next unit's weight
+// stream, so a unit of 64 tokens costs about four of one token.
+__host__ __device__ __forceinline__ int grp_gu_cost(int z) { return 12 + z + 8 * ((z + GRP_TPI - 1) / GRP_TPI); }
 
 // lanes of this wave whose (valid) expert equals this lane's
 __device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
@@ -1341,6 +1372,7 @@ __device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
 __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   __shared__ uint16_t s_run[GRP_CHUNKS][MAX_EXPERTS];  // chunk counts, then exclusive prefix over chunks
   __shared__ int s_cnt[MAX_EXPERTS], s_off[MAX_EXPERTS];
+  __shared__ int s_bounds[9];
   __shared__ uint8_t s_exp[GRP_MAX_PAIRS];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = __lane_id();
   const int T = a.T, k = a.top_k, E = a.E, P = T * k;
@@ -1409,38 +1441,88 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     s_cnt[e] = run;
   }
   __syncthreads();
-  if (wave == 0) {  // exclusive scans over experts (4 per lane) of the pair and item counts
-    int cn[MAX_EXPERTS / 64], ni[MAX_EXPERTS / 64];
+  if (wave == 0) {  // exclusive scans over experts (4 per lane) of the pair and item counts, and the gate/up items
+    constexpr int EPL = MAX_EXPERTS / 64;
+    const int tiles = (int)a.ggu.tiles;
+    int cn[EPL], ni[EPL];
     int sc = 0, sn = 0;
+    // gate/up items heavy first, in four buckets by passes (GRP_TPI tokens each): bucket 3 holds the full items
+    // (GRP_GU_T tokens) and the partial ones of more than 3 passes, expert by expert; bucket b < 3 the partial
+    // items of b + 1 passes. Per bucket and lane: (cost << 12) | items.
+    int acc[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
-      const int e = lane * (MAX_EXPERTS / 64) + i;
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane * EPL + i;
       cn[i] = e < E ? s_cnt[e] : 0;
       ni[i] = (cn[i] + GRP_TPI - 1) / GRP_TPI;
       sc += cn[i];
       sn += ni[i];
+      const int nf = cn[i] / GRP_GU_T, zr = cn[i] - nf * GRP_GU_T;
+      acc[3] += nf * ((grp_gu_cost(GRP_GU_T) << 12) | 1);
+      if (zr > 0) acc[(zr - 1) / GRP_TPI] += (grp_gu_cost(zr) << 12) | 1;
     }
-    int isc = sc, isn = sn;
+    int isc = sc, isn = sn, ia[4] = {acc[0], acc[1], acc[2], acc[3]};
     for (int d = 1; d < 64; d <<= 1) {
       const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64);
+      int oa[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) oa[b] = __shfl_up(ia[b], d, 64);
       if (lane >= d) {
         isc += oc;
         isn += on;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) ia[b] += oa[b];
       }
     }
+    // bucket bases (items, cost): bucket 3 first
+    int base_n[4], base_c[4], tn = 0, tc = 0;
+#pragma unroll
+    for (int b = 3; b >= 0; --b) {
+      const int tot = __shfl(ia[b], 63, 64);
+      base_n[b] = tn + ((ia[b] - acc[b]) & 4095);
+      base_c[b] = tc + ((ia[b] - acc[b]) >> 12);
+      tn += tot & 4095;
+      tc += tot >> 12;
+    }
+    // XCD x starts at the first unit whose cost prefix reaches x / 8 of the total: unit t of item k (cost prefix P,
+    // unit cost q) starts at tiles * P + t * q
+    int* s_bnd = s_bounds;
+    if (lane <= 8) s_bnd[lane] = lane == 8 ? tn * tiles : 0;
+    auto place = [&](int k, int P, int q) {
+#pragma unroll
+      for (int x = 1; x < 8; ++x) {
+        const int T = (int)((int64_t)x * tiles * tc / 8);
+        const int lo = tiles * P;
+        if (lo <= T && T < lo + tiles * q) s_bnd[x] = k * tiles + (T - lo + q - 1) / q;
+      }
+    };
     int bc = isc - sc, bn = isn - sn;
 #pragma unroll
-    for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
-      const int e = lane * (MAX_EXPERTS / 64) + i;
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane * EPL + i;
       if (e < E) {
         s_off[e] = bc;
-        for (int q = 0; q < ni[i]; ++q)
-          a.items[bn + q] = make_int4(e, bc + q * GRP_TPI, min(GRP_TPI, cn[i] - q * GRP_TPI), 0);
+        for (int q = 0; q < ni[i]; ++q) a.items[bn + q] = grp_item(e, bc, cn[i], q);
+        const int nf = cn[i] / GRP_GU_T, zr = cn[i] - nf * GRP_GU_T, cf = grp_gu_cost(GRP_GU_T);
+        for (int q = 0; q < nf; ++q) {
+          a.gu_items[base_n[3] + q] = make_int4(e, bc + q * GRP_GU_T, GRP_GU_T, 0);
+          place(base_n[3] + q, base_c[3] + q * cf, cf);
+        }
+        base_n[3] += nf;
+        base_c[3] += nf * cf;
+        if (zr > 0) {
+          const int b = (zr - 1) / GRP_TPI, cr = grp_gu_cost(zr);
+          a.gu_items[base_n[b]] = make_int4(e, bc + nf * GRP_GU_T, zr, 0);
+          place(base_n[b], base_c[b], cr);
+          ++base_n[b];
+          base_c[b] += cr;
+        }
       }
       bc += cn[i];
       bn += ni[i];
     }
     if (lane == 63) *a.n_items = isn;
+    if (lane <= 8) a.gu_bounds[lane] = s_bnd[lane];  // (LDS operations of one wave complete in order)
   }
   __syncthreads();
   for (int c = wave; c < nch; c += 16) {  // stable scatter
@@ -1454,9 +1536,10 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
 // Workgroup index -> (unit, item), where an item has `units` work units
 // (its tiles, or tile x row group). Workgroup b runs on XCD b % 8; the
 // units x n_items live work units are cut into 8 contiguous runs, one per
-// XCD, item-major, so that an XCD's L2 holds the activation terms of the few
-// items it is working on (and an expert's items follow each other) while the
-// grid, sized for the most items a sort can make, idles evenly on every XCD.
+// XCD, expert by expert (tile-major within an expert, grp_unit), so that an
+// XCD's L2 holds the weight tile and activation terms of the few items it is
+// working on while the grid, sized for the most items a sort can make, idles
+// evenly on every XCD.
 __device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, int4& item) {
   const int live = units * *a.n_items, per = (live + 7) / 8;
   const int j = (int)(blockIdx.x >> 3);
@@ -1464,14 +1547,14 @@ __device__ __forceinline__ bool grp_work(const MoeDev& a, int units, int& unit, 
   const int L = (int)(blockIdx.x & 7) * per + j;
   if (L >= live) return false;
   const int it = L / units;
-  unit = L - it * units;
-  item = a.items[it];
+  item = grp_unit(a.items[it], it, L, units, unit);
   return true;
 }
 
 // Pairs up to which the grouped gate/up kernel selects the top-k and sorts
 // the pairs itself (one 64-lane chunk), with no sort launch before it.
 constexpr int GRP_SMALL_P = 64;
+static_assert(GRP_SMALL_P <= GRP_GU_T, "a small sort makes one gate/up item per expert");
 
 // LDS-only workgroup barrier: waits on the wave's LDS operations, not on its
 // loads and stores to memory still in flight
@@ -1485,9 +1568,11 @@ __device__ __forceinline__ void grp_lds_barrier() {
 // the router's logits (a wave per token, as the sort kernel), then wave 0
 // sorts the pairs -- a single chunk, so the chunk prefix of the sort kernel
 // is zero and the items, sorted list and combine order are the same values.
-// Every workgroup computes them; the writer also stores ids, weights, items,
-// n_items, sorted and corder for the down and combine phases and the caller.
-// Every thread of the workgroup calls it.
+// Every workgroup computes them, the gate/up items (s_items, one per expert
+// present: at most GRP_SMALL_P <= GRP_GU_T pairs) for itself; the writer also
+// stores ids, weights, the GRP_TPI-token items, n_items, sorted and corder for
+// the down and combine phases and the caller. Every thread of the workgroup
+// calls it.
 __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, int* s_nitems, uint8_t* s_exp,
                                int* s_cnt, int* s_off, bool writer) {
   const int tid = threadIdx.x, nt = blockDim.x, nw = nt >> 6;
@@ -1530,9 +1615,9 @@ __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, in
   const uint64_t m = grp_match(lane < P, e_l);
   if (wave == 0 && lane < P && (m & below) == 0ull) s_cnt[e_l] = (int)__popcll(m);
   grp_lds_barrier();
-  if (wave == 0) {  // exclusive scans over experts (4 per lane) of the pair and item counts
+  if (wave == 0) {  // exclusive scans over experts (4 per lane) of the pair, item and expert counts
     int cn[MAX_EXPERTS / 64], ni[MAX_EXPERTS / 64];
-    int sc = 0, sn = 0;
+    int sc = 0, sn = 0, sb = 0;
 #pragma unroll
     for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
       const int e = lane * (MAX_EXPERTS / 64) + i;
@@ -1540,32 +1625,33 @@ __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, in
       ni[i] = (cn[i] + GRP_TPI - 1) / GRP_TPI;
       sc += cn[i];
       sn += ni[i];
+      sb += cn[i] > 0;
     }
-    int isc = sc, isn = sn;
+    int isc = sc, isn = sn, isb = sb;
     for (int d = 1; d < 64; d <<= 1) {
-      const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64);
+      const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64), ob = __shfl_up(isb, d, 64);
       if (lane >= d) {
         isc += oc;
         isn += on;
+        isb += ob;
       }
     }
-    int bc = isc - sc, bn = isn - sn;
+    int bc = isc - sc, bn = isn - sn, bb = isb - sb;
 #pragma unroll
     for (int i = 0; i < MAX_EXPERTS / 64; ++i) {
       const int e = lane * (MAX_EXPERTS / 64) + i;
       if (e < E) {
         s_off[e] = bc;
-        for (int q = 0; q < ni[i]; ++q) {
-          const int4 it = make_int4(e, bc + q * GRP_TPI, min(GRP_TPI, cn[i] - q * GRP_TPI), 0);
-          s_items[bn + q] = it;
-          if (writer) a.items[bn + q] = it;
-        }
+        if (cn[i] > 0) s_items[bb] = make_int4(e, bc, cn[i], 0);
+        if (writer)
+          for (int q = 0; q < ni[i]; ++q) a.items[bn + q] = grp_item(e, bc, cn[i], q);
       }
       bc += cn[i];
       bn += ni[i];
+      bb += cn[i] > 0;
     }
     if (lane == 63) {
-      *s_nitems = isn;
+      *s_nitems = isb;
       if (writer) *a.n_items = isn;
     }
   }
@@ -1578,20 +1664,26 @@ __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, in
   grp_lds_barrier();
 }
 
-// gate/up for (item, tile) units: one wave per K-chunk, computing that chunk
-// of both the gate and the up tile, so a token's activation terms are read
-// once per (item, tile, chunk) rather than once per matrix. A wave's gate
-// (up) chunk is the (gate (up), chunk) wave of moe_gu_kernel: same steps,
-// same accumulation order, so the activations are bit-identical to the
-// per-pair path. The item's tokens go four at a time (16 MFMA columns = 4
-// tokens x 4 terms). Persistent: the launch is the resident workgroups, 8
-// groups of nx (group x on XCD x: workgroup b runs on XCD b % 8), and group x
-// works through XCD x's contiguous item-major run of units -- workgroup j of
-// it takes units j, j + nx, ... -- so no workgroup is dispatched per unit;
-// the next unit's weights are requested before this unit's epilogue, into
-// the registers its MFMAs have finished with. SIN: every workgroup first
-// selects the top-k and sorts the pairs itself (grp_small_sort; workgroup 0
-// stores the results), so small batches launch no sort kernel.
+// gate/up for (item, tile) units, an item being up to GRP_GU_T tokens of one
+// expert: one wave per K-chunk, computing that chunk of both the gate and the
+// up tile, so a token's activation terms are read once per (item, tile,
+// chunk) rather than once per matrix. A wave's gate (up) chunk is the (gate
+// (up), chunk) wave of moe_gu_kernel: same steps, same accumulation order, so
+// the activations are bit-identical to the per-pair path. The item's tokens
+// go GRP_TPI at a time (one pass through the LDS reduction and epilogue each),
+// four at a time inside (16 MFMA columns = 4 tokens x 4 terms), with the
+// tile's weights held in registers throughout: HBM serves each tile once per
+// item, and the XCD's workgroups, on the tiles of one item together, share its
+// tokens' activation terms in L2. Persistent: the launch is the resident
+// workgroups, 8 groups of nx (group x on XCD x: workgroup b runs on XCD b %
+// 8), and group x works through XCD x's contiguous item-major run of units in
+// rounds of nx (the sort lists the items heavy first and cuts the runs by
+// grp_gu_cost, so the XCDs finish together), so no workgroup is dispatched per
+// unit; the next unit's weights are requested before this unit's last
+// epilogue, into the registers its MFMAs have finished with. SIN:
+// every workgroup first selects the top-k and sorts the pairs itself
+// (grp_small_sort; workgroup 0 stores the results), so small batches launch
+// no sort kernel.
 template <bool SIN>
 __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev a) {
   __shared__ float red[2][MAX_CHUNKS][GRP_TPI][64];
@@ -1600,14 +1692,27 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   __shared__ int s_nitems;
   __shared__ uint8_t s_exp[SIN ? GRP_SMALL_P : 1];
   if constexpr (SIN) grp_small_sort(a, s_items, s_sorted, &s_nitems, s_exp, s_cnt, s_off, blockIdx.x == 0);
-  auto item_at = [&](int i) { return SIN ? s_items[i] : a.items[i]; };
-  auto item_word = [&](int i, int w) { return SIN ? ((const int*)s_items)[4 * i + w] : ((const int*)a.items)[4 * i + w]; };
+  auto item_at = [&](int i) { return SIN ? s_items[i] : a.gu_items[i]; };
+  auto item_word = [&](int i, int w) {
+    return SIN ? ((const int*)s_items)[4 * i + w] : ((const int*)a.gu_items)[4 * i + w];
+  };
   auto sorted_at = [&](int i) { return SIN ? s_sorted[i] : a.sorted[i]; };
   const int tiles = (int)a.ggu.tiles;
-  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7);
-  const int live = tiles * (SIN ? s_nitems : *a.n_items), per = (live + 7) / 8;
-  const int hi = min(live, (xcd + 1) * per);
-  int L = xcd * per + (int)(blockIdx.x >> 3);
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
+  // XCD xcd's run of units [lo, hi): cost-weighted bounds from the sort (a small sort: equal counts); round r of
+  // the run is units lo + r nx .. + nx - 1, taken in alternating directions, so that a workgroup given a costly
+  // unit in one round is given a cheap one in the next
+  int lo, hi;
+  if constexpr (SIN) {
+    const int live = tiles * s_nitems, per = (live + 7) / 8;
+    lo = min(live, xcd * per);
+    hi = min(live, lo + per);
+  } else {
+    lo = a.gu_bounds[xcd];
+    hi = a.gu_bounds[xcd + 1];
+  }
+  int round = 0;
+  int L = lo + j;
   if (L >= hi) return;
   const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
@@ -1618,92 +1723,112 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   int e = clamp_expert(item.x, a.E);
   // the pair list goes out ahead of the weights: loads return in order, and the first token group's
   // activation loads wait on it (behind the weights, they would wait for every weight byte)
-  int my_pair = sorted_at(item.y + min(lane & 15, item.z - 1));  // lane i < 16: the item's token i
+  int my_pair = sorted_at(item.y + min(lane, item.z - 1));  // lane i: the item's token i
   {  // both tiles' addresses before any load: a pointer-table read between the two load groups would wait on the first
     const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e, tile);
     const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e, tile);
     mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
     mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
   }
+  // LDS-only barriers below: a memory-counter wait would hold the epilogue until the next unit's weights land
+  auto lds_barrier = []() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+  };
   for (;;) {
-    const int n = item.z;
-    const int Ln = L + nx;
+    const int z = item.z;
+    const int Ln = lo + (round + 1) * nx + ((round & 1) ? j : nx - 1 - j);
     // the next unit's item, requested now so that it is at hand when this unit's MFMAs are done (the last unit
     // re-reads its own); lane i holds word i & 3 -- a lane-varying load stays in VGPRs, where nothing waits on
     // it before its fields are read after the token loop
     const int iw_n = item_word(min(Ln, hi - 1) / tiles, lane & 3);
-    for (int tg = 0; tg * 4 < n; ++tg) {
-      const int tok = tg * 4 + ((lane & 15) >> 2);
-      const int pr = __shfl(my_pair, min(tok, n - 1), 64);
-      mx_load_b_at<GU_S, false, 4, true>(Rg, a.xq_h + (int64_t)(pr / a.top_k) * xs, 0, s0, s1);
-      asm volatile("" ::: "memory");  // all steps' loads go out before the first step's MFMAs wait on one
-#pragma unroll
-      for (int u = 0; u < GU_S; ++u) {  // the up tile takes the same activation operands
-        Ru.B0[u] = Rg.B0[u];
-        Ru.B1[u] = Rg.B1[u];
-        Ru.SB[u] = Rg.SB[u];
-      }
-      v4f Dg[4] = {}, Du[4] = {};
-      mx_compute<GU_S>(Rg, a.ggu, s0, s1, Dg);
-      mx_compute<GU_S>(Ru, a.ggu, s0, s1, Du);
-      mx_sum_terms(Dg);
-      mx_sum_terms(Du);
-      if ((lane & 3) == 0 && tok < n) {
-        const int r0 = 4 * (lane >> 4);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          *(v4f*)(&red[0][c][tok][16 * g + r0]) = Dg[g];
-          *(v4f*)(&red[1][c][tok][16 * g + r0]) = Du[g];
-        }
-      }
-    }
-    // LDS-only barriers below: a memory-counter wait would hold the epilogue until the next unit's weights land
-    auto lds_barrier = []() {
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-      asm volatile("s_barrier" ::: "memory");
-    };
-    // the biases are read before any next-unit load: loads complete in order, so one issued behind them waits on them
     const int row = tile * 64 + lane;
     const int rowc = min(row, a.n_ff - 1);
-    const float gb = a.gate_bias && c < n ? a.gate_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
-    const float ub = a.up_bias && c < n ? a.up_bias[(int64_t)e * a.n_ff + rowc] : 0.f;
-    auto epilogue = [&]() {
-      if (c >= n) return;
-      for (int w = c; w < n; w += a.cg) {  // token w of the item
-        float gs = 0.f, us = 0.f;
-        for (int cc = 0; cc < a.cg; ++cc) {
-          gs += red[0][cc][w][lane];
-          us += red[1][cc][w][lane];
+    // the biases go out with the first token group's activation terms, with no branch before any load (a branch
+    // between loads costs a wait on every load before it: here, the unit's weights); a layer without biases
+    // reads a word of xq_h in their place. The token loops run at least once and wait on every load they issue,
+    // so the biases have landed on every path into an epilogue -- the epilogue after the next unit's loads must
+    // not wait on a load (the compiler, unsure of one, would wait on them all)
+    const int64_t bo = (int64_t)e * a.n_ff + rowc;
+    const float gbv = *(a.gate_bias ? a.gate_bias + bo : (const float*)a.xq_h);
+    const float ubv = *(a.up_bias ? a.up_bias + bo : (const float*)a.xq_h);
+    const int my_tok = my_pair / a.top_k;  // (after the loads above: it waits on the pair list)
+    for (int q0 = 0;; q0 += GRP_TPI) {  // the item's tokens q0 .. q0 + n - 1
+      const int n = min(GRP_TPI, z - q0);
+      // token groups of 4; the loop runs at least once and waits on every load it issues
+      int tg = 0;
+      do {
+        const int tok = tg * 4 + ((lane & 15) >> 2);
+        MxB<GU_S> B;
+        mx_load_bb<GU_S>(B, a.xq_h + (int64_t)__shfl(my_tok, q0 + min(tok, n - 1), 64) * xs, 0, s0, s1);
+        asm volatile("" ::: "memory");  // all steps' loads go out before the first step's MFMAs wait on one
+        mx_take_b(Rg, B);  // the gate and the up tile take the same activation operands
+        mx_take_b(Ru, B);
+        v4f Dg[4] = {}, Du[4] = {};
+        mx_compute<GU_S>(Rg, a.ggu, s0, s1, Dg);
+        mx_compute<GU_S>(Ru, a.ggu, s0, s1, Du);
+        mx_sum_terms(Dg);
+        mx_sum_terms(Du);
+        if ((lane & 3) == 0 && tok < n) {
+          const int r0 = 4 * (lane >> 4);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            *(v4f*)(&red[0][c][tok][16 * g + r0]) = Dg[g];
+            *(v4f*)(&red[1][c][tok][16 * g + r0]) = Du[g];
+          }
         }
-        const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
-        const int pr = __builtin_amdgcn_readlane(my_pair, w);
-        xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
-        xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+      } while (++tg * 4 < n);
+      // the biases are first used here, after the token loop's waits: an opaque copy, so that the compiler does not
+      // hoist their use to the unit's start, where a wait on them is a wait on the weights issued before them
+      float gb = gbv, ub = ubv;
+      asm volatile("" : "+v"(gb), "+v"(ub));
+      gb = a.gate_bias ? gb : 0.f;
+      ub = a.up_bias ? ub : 0.f;
+      auto epilogue = [&]() {
+        if (c >= n) return;
+        for (int w = c; w < n; w += a.cg) {  // token q0 + w of the item
+          float gs = 0.f, us = 0.f;
+          for (int cc = 0; cc < a.cg; ++cc) {
+            gs += red[0][cc][w][lane];
+            us += red[1][cc][w][lane];
+          }
+          const float av = row < a.n_ff ? moe_act(a.act_kind, gs + gb, us + ub, a.alpha, a.limit) : 0.f;
+          const int pr = __builtin_amdgcn_readlane(my_pair, q0 + w);
+          xq_block(av, 2 * tile + (lane >> 5), a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+          xq_zero_tail(tile, a.ggu, a.gdn, a.xq_a + (int64_t)pr * a.gdn.ns * XQ_STEP);
+        }
+      };
+      const bool more = q0 + GRP_TPI < z;  // more tokens: the weights stay
+      if (!more && Ln >= hi) {  // (a path of its own: the weight registers are not live into a merge with reloaded ones)
+        lds_barrier();
+        epilogue();
+        return;
       }
-    };
-    if (Ln >= hi) {  // (a path of its own: the weight registers are not live into a merge with reloaded ones)
+      int4 item_n;
+      int tile_n = 0, e_n = 0, pair_n = 0;
+      if (!more) {  // the next unit's weights and pair list go out before this unit's last epilogue
+        item_n = int4{__builtin_amdgcn_readlane(iw_n, 0), __builtin_amdgcn_readlane(iw_n, 1),
+                      __builtin_amdgcn_readlane(iw_n, 2), 0};
+        tile_n = Ln - (Ln / tiles) * tiles;
+        e_n = clamp_expert(item_n.x, a.E);
+        pair_n = sorted_at(item_n.y + min(lane, item_n.z - 1));  // (ahead of the weights, as above)
+        const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e_n, tile_n);
+        const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e_n, tile_n);
+        mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
+        mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
+      }
       lds_barrier();
       epilogue();
+      lds_barrier();  // the epilogue's reads of red come before the next tokens' (unit's) writes
+      if (more) continue;
+      L = Ln;
+      ++round;
+      item = item_n;
+      tile = tile_n;
+      e = e_n;
+      my_pair = pair_n;
       break;
     }
-    // the next unit's weights and pair list go out before this unit's epilogue
-    const int4 item_n = {__builtin_amdgcn_readlane(iw_n, 0), __builtin_amdgcn_readlane(iw_n, 1),
-                         __builtin_amdgcn_readlane(iw_n, 2), 0};
-    const int tile_n = Ln - (Ln / tiles) * tiles;
-    const int e_n = clamp_expert(item_n.x, a.E);
-    const int pair_n = sorted_at(item_n.y + min(lane & 15, item_n.z - 1));  // (ahead of the weights, as above)
-    const uint8_t* gt = tile_base(a.gate_base, a.gate_stride, a.gate_ptrs, a.gate_tiles, a.ggu, e_n, tile_n);
-    const uint8_t* ut = tile_base(a.up_base, a.up_stride, a.up_ptrs, a.up_tiles, a.ggu, e_n, tile_n);
-    mx_load_a_flat<GU_S>(Rg, gt, a.ggu, s0, s1);
-    mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
-    lds_barrier();
-    epilogue();
-    lds_barrier();  // the epilogue's reads of red come before the next unit's writes
-    L = Ln;
-    item = item_n;
-    tile = tile_n;
-    e = e_n;
-    my_pair = pair_n;
   }
 }
 
@@ -2949,11 +3074,11 @@ __global__ __launch_bounds__(256, 3) void moe_q4k_mfma_kernel(MoeDev a) {  // (t
 
 struct MoePlan {
   int64_t off_logits, off_act, off_xqh, off_xqa, total;
-  int64_t off_items, off_nitems, off_sorted, off_corder, off_y, off_rpart;
+  int64_t off_items, off_nitems, off_gu_items, off_gu_bounds, off_sorted, off_corder, off_y, off_rpart;
   MxGeom ggu, gdn;
   int cg, cd, sd;
   bool grouped;
-  int max_items, cdg, sdg;
+  int max_items, max_gu_items, cdg, sdg;
   bool mq;  // grouped Q4_K on the matrix cores: xqh / xqa hold activation terms (mq_row_bytes per row)
 };
 
@@ -3008,6 +3133,7 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.cdg = std::max(1, std::min(p.gdn.ns, 4));  // grouped down: 4 row groups x cdg chunks
   p.sdg = (int)nsx_cdiv(p.gdn.ns, p.cdg);
   p.max_items = p.grouped ? grp_max_items(L->n_expert, (int)P) : 0;
+  p.max_gu_items = p.grouped ? grp_max_items(L->n_expert, (int)P, GRP_GU_T) : 0;  // (moe_sort_kernel writes them)
   auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
   int64_t o = 0;
   p.off_logits = o;
@@ -3025,6 +3151,10 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   o = al(o + (int64_t)p.max_items * 16);
   p.off_nitems = o;
   o = al(o + (p.grouped ? 4 : 0));
+  p.off_gu_items = o;
+  o = al(o + (int64_t)p.max_gu_items * 16);
+  p.off_gu_bounds = o;
+  o = al(o + (p.max_gu_items ? 9 * 4 : 0));
   p.off_sorted = o;
   o = al(o + (p.grouped ? P * 4 : 0));
   p.off_corder = o;
@@ -3202,6 +3332,8 @@ static MoeDev make_dev(const nsx_moe_layer* L, const MoePlan& p, char* ws, const
   d.limit = L->limit;
   d.items = (int4*)(ws + p.off_items);
   d.n_items = (int*)(ws + p.off_nitems);
+  d.gu_items = (int4*)(ws + p.off_gu_items);
+  d.gu_bounds = (int*)(ws + p.off_gu_bounds);
   d.sorted = (int32_t*)(ws + p.off_sorted);
   d.corder = (int32_t*)(ws + p.off_corder);
   d.y = (float*)(ws + p.off_y);
@@ -3266,7 +3398,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         // persistent: the resident workgroups (a multiple of 8), no more than the units can use
         const void* kern = sin ? (const void*)moe_gu_grouped_kernel<true> : (const void*)moe_gu_grouped_kernel<false>;
         const int64_t r = std::max<int64_t>(8, nsx_resident_workgroups(kern, 0, 64 * p.cg) / 8 * 8);
-        const dim3 grid((unsigned)std::min<int64_t>(r, 8 * nsx_cdiv(items * p.ggu.tiles, 8)));
+        const dim3 grid((unsigned)std::min<int64_t>(r, 8 * nsx_cdiv((int64_t)p.max_gu_items * p.ggu.tiles, 8)));
         rc = sin ? nsx_launch(moe_gu_grouped_kernel<true>, grid, dim3(64 * p.cg), 0, st, d)
                  : nsx_launch(moe_gu_grouped_kernel<false>, grid, dim3(64 * p.cg), 0, st, d);
       } else if (p.mq) {

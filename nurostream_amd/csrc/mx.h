@@ -253,6 +253,43 @@ __device__ __forceinline__ void mx_load_b_at(MxRegs<S, G>& R, const uint8_t* __r
   }
 }
 
+// Activation operands of S K-steps held apart from the weights: with two of
+// them a token loop requests the next token group's operands before the MFMAs
+// of this one wait on theirs.
+template <int S>
+struct MxB {
+  v4u B0[S], B1[S];
+  uint32_t SB[S];
+};
+
+// mx_load_b_at<S, false, G, true> into an MxB (global terms, no branch between the steps' loads).
+template <int S>
+__device__ __forceinline__ void mx_load_bb(MxB<S>& B, const uint8_t* __restrict__ xtok, int xs0, int s0, int s1) {
+  typedef const __attribute__((address_space(1))) v4u gv4u;
+  typedef const __attribute__((address_space(1))) uint32_t gu32;
+  const int lane = __lane_id();
+  const int grp = lane >> 4, term = lane & (XQ_NT - 1);
+  const uint8_t* xt = xtok + (grp * XQ_NT + term) * 32;
+  const uint8_t* xst = xtok + XQ_CODES + (grp * XQ_NT + term) * 4;
+#pragma unroll
+  for (int u = 0; u < S; ++u) {
+    const int64_t xo = (int64_t)(min(s0 + u, s1 - 1) - xs0) * XQ_STEP;
+    B.B0[u] = *(gv4u*)(xt + xo);
+    B.B1[u] = *(gv4u*)(xt + xo + 16);
+    B.SB[u] = *(gu32*)(xst + xo);
+  }
+}
+
+template <int S, int G>
+__device__ __forceinline__ void mx_take_b(MxRegs<S, G>& R, const MxB<S>& B) {
+#pragma unroll
+  for (int u = 0; u < S; ++u) {
+    R.B0[u] = B.B0[u];
+    R.B1[u] = B.B1[u];
+    R.SB[u] = B.SB[u];
+  }
+}
+
 // The same for tokens laid out xq_stride bytes apart from xq (token 0):
 // column c = token * XQ_NT + term for tokens < ntok; columns of tokens >=
 // ntok repeat token ntok - 1 and are not read back.
