@@ -740,6 +740,7 @@ struct MoeDev {
   int* n_items;
   int4* gu_items;        // the MXFP4 gate/up kernel's work items: (expert, first sorted position, tokens, 0)
   int* gu_bounds;        // [9]: XCD x runs gate/up units [gu_bounds[x], gu_bounds[x + 1])
+  int* dn_bounds;        // [9]: the same for the down kernel's units (same items, its own tiles)
   int32_t* sorted;       // pair ids, ascending expert, ascending pair id inside
   int32_t* corder;       // per token: its pair ids in ascending expert id
   float* y;              // (pairs, n_embd) expert outputs, bias included
@@ -1319,6 +1320,10 @@ __global__ __launch_bounds__(1024) void moe_gu_chain_kernel(MoeDev a) {
 
 constexpr int GRP_TPI = 16;          // tokens per work item
 constexpr int GRP_GU_T = 64;         // tokens per MXFP4 gate/up work item (GRP_TPI at a time)
+// the grouped MXFP4 down runs persistent (moe_down_persistent_kernel) when its units can number this many times
+// the resident workgroups (the 36-layer GPT-OSS stack at T = 8, at most 1485 units on 512 workgroups: 23.7 us per
+// layer one workgroup per unit, 25.8 persistent; config 3, T = 128: 89.7 -> 84.5 us persistent)
+constexpr int GRP_DN_PERSIST = 8;
 constexpr int GRP_MAX_PAIRS = 4096;  // pairs per sort (nsx_moe_forward splits larger T)
 constexpr int GRP_CHUNKS = GRP_MAX_PAIRS / 64;
 
@@ -1353,6 +1358,8 @@ __device__ __forceinline__ int4 grp_unit(int4 rec, int s, int L, int units, int&
 // 2.6 m us. A pass past the first is not hidden under the next unit's weight
 // stream, so a unit of 64 tokens costs about four of one token.
 __host__ __device__ __forceinline__ int grp_gu_cost(int z) { return 12 + z + 8 * ((z + GRP_TPI - 1) / GRP_TPI); }
+// The same for a down unit (half the weight bytes of a gate/up unit, an epilogue of fp32 stores).
+__host__ __device__ __forceinline__ int grp_dn_cost(int z) { return 10 + z + 3 * ((z + GRP_TPI - 1) / GRP_TPI); }
 
 // lanes of this wave whose (valid) expert equals this lane's
 __device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
@@ -1372,7 +1379,7 @@ __device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
 __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
   __shared__ uint16_t s_run[GRP_CHUNKS][MAX_EXPERTS];  // chunk counts, then exclusive prefix over chunks
   __shared__ int s_cnt[MAX_EXPERTS], s_off[MAX_EXPERTS];
-  __shared__ int s_bounds[9];
+  __shared__ int s_pc[2][MAX_EXPERTS + GRP_MAX_PAIRS / GRP_GU_T + 1];  // cost prefixes of the gate/up items: gate/up, down
   __shared__ uint8_t s_exp[GRP_MAX_PAIRS];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = __lane_id();
   const int T = a.T, k = a.top_k, E = a.E, P = T * k;
@@ -1448,8 +1455,8 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     int sc = 0, sn = 0;
     // gate/up items heavy first, in four buckets by passes (GRP_TPI tokens each): bucket 3 holds the full items
     // (GRP_GU_T tokens) and the partial ones of more than 3 passes, expert by expert; bucket b < 3 the partial
-    // items of b + 1 passes. Per bucket and lane: (cost << 12) | items.
-    int acc[4] = {0, 0, 0, 0};
+    // items of b + 1 passes. Per bucket and lane: (gate/up cost << 12) | items, and the down cost.
+    int acc[4] = {0, 0, 0, 0}, acd[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const int e = lane * EPL + i;
@@ -1459,43 +1466,43 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
       sn += ni[i];
       const int nf = cn[i] / GRP_GU_T, zr = cn[i] - nf * GRP_GU_T;
       acc[3] += nf * ((grp_gu_cost(GRP_GU_T) << 12) | 1);
-      if (zr > 0) acc[(zr - 1) / GRP_TPI] += (grp_gu_cost(zr) << 12) | 1;
+      acd[3] += nf * grp_dn_cost(GRP_GU_T);
+      if (zr > 0) {
+        acc[(zr - 1) / GRP_TPI] += (grp_gu_cost(zr) << 12) | 1;
+        acd[(zr - 1) / GRP_TPI] += grp_dn_cost(zr);
+      }
     }
-    int isc = sc, isn = sn, ia[4] = {acc[0], acc[1], acc[2], acc[3]};
+    int isc = sc, isn = sn, ia[4] = {acc[0], acc[1], acc[2], acc[3]}, id[4] = {acd[0], acd[1], acd[2], acd[3]};
     for (int d = 1; d < 64; d <<= 1) {
       const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64);
-      int oa[4];
+      int oa[4], od[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) oa[b] = __shfl_up(ia[b], d, 64);
+      for (int b = 0; b < 4; ++b) {
+        oa[b] = __shfl_up(ia[b], d, 64);
+        od[b] = __shfl_up(id[b], d, 64);
+      }
       if (lane >= d) {
         isc += oc;
         isn += on;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) ia[b] += oa[b];
+        for (int b = 0; b < 4; ++b) {
+          ia[b] += oa[b];
+          id[b] += od[b];
+        }
       }
     }
-    // bucket bases (items, cost): bucket 3 first
-    int base_n[4], base_c[4], tn = 0, tc = 0;
+    // bucket bases (items, gate/up cost, down cost): bucket 3 first
+    int base_n[4], base_c[4], base_d[4], tn = 0, tc = 0, td = 0;
 #pragma unroll
     for (int b = 3; b >= 0; --b) {
-      const int tot = __shfl(ia[b], 63, 64);
+      const int tot = __shfl(ia[b], 63, 64), totd = __shfl(id[b], 63, 64);
       base_n[b] = tn + ((ia[b] - acc[b]) & 4095);
       base_c[b] = tc + ((ia[b] - acc[b]) >> 12);
+      base_d[b] = td + (id[b] - acd[b]);
       tn += tot & 4095;
       tc += tot >> 12;
+      td += totd;
     }
-    // XCD x starts at the first unit whose cost prefix reaches x / 8 of the total: unit t of item k (cost prefix P,
-    // unit cost q) starts at tiles * P + t * q
-    int* s_bnd = s_bounds;
-    if (lane <= 8) s_bnd[lane] = lane == 8 ? tn * tiles : 0;
-    auto place = [&](int k, int P, int q) {
-#pragma unroll
-      for (int x = 1; x < 8; ++x) {
-        const int T = (int)((int64_t)x * tiles * tc / 8);
-        const int lo = tiles * P;
-        if (lo <= T && T < lo + tiles * q) s_bnd[x] = k * tiles + (T - lo + q - 1) / q;
-      }
-    };
     int bc = isc - sc, bn = isn - sn;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
@@ -1503,26 +1510,56 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
       if (e < E) {
         s_off[e] = bc;
         for (int q = 0; q < ni[i]; ++q) a.items[bn + q] = grp_item(e, bc, cn[i], q);
-        const int nf = cn[i] / GRP_GU_T, zr = cn[i] - nf * GRP_GU_T, cf = grp_gu_cost(GRP_GU_T);
+        const int nf = cn[i] / GRP_GU_T, zr = cn[i] - nf * GRP_GU_T;
+        const int cf = grp_gu_cost(GRP_GU_T), df = grp_dn_cost(GRP_GU_T);
         for (int q = 0; q < nf; ++q) {
           a.gu_items[base_n[3] + q] = make_int4(e, bc + q * GRP_GU_T, GRP_GU_T, 0);
-          place(base_n[3] + q, base_c[3] + q * cf, cf);
+          s_pc[0][base_n[3] + q] = base_c[3] + q * cf;
+          s_pc[1][base_n[3] + q] = base_d[3] + q * df;
         }
         base_n[3] += nf;
         base_c[3] += nf * cf;
+        base_d[3] += nf * df;
         if (zr > 0) {
-          const int b = (zr - 1) / GRP_TPI, cr = grp_gu_cost(zr);
+          const int b = (zr - 1) / GRP_TPI;
           a.gu_items[base_n[b]] = make_int4(e, bc + nf * GRP_GU_T, zr, 0);
-          place(base_n[b], base_c[b], cr);
+          s_pc[0][base_n[b]] = base_c[b];
+          s_pc[1][base_n[b]] = base_d[b];
           ++base_n[b];
-          base_c[b] += cr;
+          base_c[b] += grp_gu_cost(zr);
+          base_d[b] += grp_dn_cost(zr);
         }
       }
       bc += cn[i];
       bn += ni[i];
     }
+    if (lane == 0) {
+      s_pc[0][tn] = tc;
+      s_pc[1][tn] = td;
+    }
     if (lane == 63) *a.n_items = isn;
-    if (lane <= 8) a.gu_bounds[lane] = s_bnd[lane];  // (LDS operations of one wave complete in order)
+    // XCD x of kernel g (0: gate/up, 1: down; lane 8 g + x) starts at the first unit whose cost prefix reaches x / 8
+    // of the total: unit t of item k (cost prefix P_k, unit cost q_k = P_k+1 - P_k) starts at nt P_k + t q_k for
+    // nt units per item. The item is the last one with 8 P_k <= x total, found by bisection over the prefixes
+    // (ascending; LDS operations of one wave complete in order).
+    if (lane < 16) {
+      const int g = lane >> 3, x = lane & 7;
+      const int nt = g ? (int)a.gdn.tiles : tiles, tot = g ? td : tc;
+      int L = x == 0 || tn == 0 ? 0 : tn * nt;  // (x = 0: 0; an empty sort: 0)
+      if (x > 0 && tn > 0) {
+        const int tx = x * tot;  // target, in eighths of a cost unit
+        int k0 = 0, k1 = tn - 1;  // 8 P_k0 <= tx (P_0 = 0); find the largest such k
+        while (k0 < k1) {
+          const int m = (k0 + k1 + 1) >> 1;
+          if (8 * s_pc[g][m] <= tx) k0 = m; else k1 = m - 1;
+        }
+        const int P = s_pc[g][k0], q = s_pc[g][k0 + 1] - P;
+        const int t = (nt * (tx - 8 * P) + 8 * q - 1) / (8 * q);  // ceil: the first unit of item k0 at or past tx
+        L = k0 * nt + min(t, nt);
+      }
+      (g ? a.dn_bounds : a.gu_bounds)[x] = L;
+      if (x == 7) (g ? a.dn_bounds : a.gu_bounds)[8] = tn * nt;
+    }
   }
   __syncthreads();
   for (int c = wave; c < nch; c += 16) {  // stable scatter
@@ -1570,9 +1607,9 @@ __device__ __forceinline__ void grp_lds_barrier() {
 // is zero and the items, sorted list and combine order are the same values.
 // Every workgroup computes them, the gate/up items (s_items, one per expert
 // present: at most GRP_SMALL_P <= GRP_GU_T pairs) for itself; the writer also
-// stores ids, weights, the GRP_TPI-token items, n_items, sorted and corder for
-// the down and combine phases and the caller. Every thread of the workgroup
-// calls it.
+// stores ids, weights, the gate/up items and the down kernel's XCD runs, the
+// GRP_TPI-token items, n_items, sorted and corder for the down and combine
+// phases and the caller. Every thread of the workgroup calls it.
 __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, int* s_nitems, uint8_t* s_exp,
                                int* s_cnt, int* s_off, bool writer) {
   const int tid = threadIdx.x, nt = blockDim.x, nw = nt >> 6;
@@ -1642,7 +1679,10 @@ __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, in
       const int e = lane * (MAX_EXPERTS / 64) + i;
       if (e < E) {
         s_off[e] = bc;
-        if (cn[i] > 0) s_items[bb] = make_int4(e, bc, cn[i], 0);
+        if (cn[i] > 0) {
+          s_items[bb] = make_int4(e, bc, cn[i], 0);
+          if (writer) a.gu_items[bb] = s_items[bb];
+        }
         if (writer)
           for (int q = 0; q < ni[i]; ++q) a.items[bn + q] = grp_item(e, bc, cn[i], q);
       }
@@ -1654,6 +1694,8 @@ __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, in
       *s_nitems = isb;
       if (writer) *a.n_items = isn;
     }
+    const int live_d = __shfl(isb, 63, 64) * (int)a.gdn.tiles, per_d = (live_d + 7) / 8;
+    if (writer && lane <= 8) a.dn_bounds[lane] = min(live_d, lane * per_d);  // the down kernel's runs: equal counts
   }
   grp_lds_barrier();
   if (wave == 0 && lane < P) {  // stable scatter
@@ -1832,7 +1874,9 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   }
 }
 
-// down for one (item, tile): one wave per K-chunk over all four 16-row
+// down for one (item, tile), an item being up to GRP_TPI tokens of one expert
+// (the sort's GRP_TPI-token items, tile-major within an expert): one wave per
+// K-chunk over all four 16-row
 // groups, so each token's activation terms are read once per (item, tile)
 // rather than once per row group (they are 4.5 bytes per element and token,
 // more than the weights' 0.53 per element and row). A wave's chunk, row group
@@ -1882,6 +1926,116 @@ __global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(MoeDev a) {
     for (int cc = 0; cc < a.cdg; ++cc) y += red[cc][w][lane];
     const int pr = __builtin_amdgcn_readlane(my_pair, w);
     if (row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y;
+  }
+}
+
+// down for (item, tile) units, an item being up to GRP_GU_T tokens of one
+// expert (the gate/up kernel's items): one wave per K-chunk over all four
+// 16-row groups, so each token's activation terms are read once per (item,
+// tile) rather than once per row group (they are 4.5 bytes per element and
+// token, more than the weights' 0.53 per element and row). A wave's chunk, row
+// group by row group, is the (chunk, row group) wave of moe_down_kernel: same
+// steps, same accumulation order, and the bias joins chunk 0's partial first,
+// so y is bit-identical to the per-pair path. The tile's weights stay in
+// registers over the item's tokens, GRP_TPI at a time. Persistent as the
+// gate/up kernel: 8 groups of nx workgroups, group x on XCD x taking rounds of
+// nx units of its run (cost-weighted by the sort), in alternating directions;
+// the next unit's weights are requested before this unit's last epilogue.
+// y[pair, rows] = the expert's down product plus its bias.
+__global__ __launch_bounds__(256, 2) void moe_down_persistent_kernel(MoeDev a) {
+  __shared__ float red[4][GRP_TPI][64];  // [wave = chunk][token][row of the tile]
+  const int tiles = (int)a.gdn.tiles;
+  const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
+  const int lo = a.dn_bounds[xcd], hi = a.dn_bounds[xcd + 1];
+  int L = lo + j;
+  if (L >= hi) return;
+  int round = 0;
+  const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  const int s0 = c * a.sdg, s1 = min(a.gdn.ns, s0 + a.sdg);
+  const int64_t xs = (int64_t)a.gdn.ns * XQ_STEP;
+  MxRegs<DC_S> R;
+  int4 item = a.gu_items[L / tiles];
+  int tile = L - (L / tiles) * tiles;
+  int e = clamp_expert(item.x, a.E);
+  // the pair list goes out ahead of the weights: loads return in order, and the first token group's
+  // activation loads wait on it (behind the weights, they would wait for every weight byte)
+  int my_pair = a.sorted[item.y + min(lane, item.z - 1)];  // lane i: the item's token i
+  mx_load_a_flat<DC_S>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, tile), a.gdn, s0,
+                       s1);
+  // LDS-only barriers below: a memory-counter wait would hold the epilogue until the next unit's weights land
+  auto lds_barrier = []() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+  };
+  for (;;) {
+    const int z = item.z;
+    const int Ln = lo + (round + 1) * nx + ((round & 1) ? j : nx - 1 - j);
+    // the next unit's item (lane i: word i & 3), requested now so that it is at hand after the token loop
+    const int iw_n = ((const int*)a.gu_items)[4 * (min(Ln, hi - 1) / tiles) + (lane & 3)];
+    const int row = tile * 64 + lane;
+    // this lane's bias, with no branch before any load (a layer without biases reads a word of xq_a instead);
+    // the token loops run at least once and wait on every load before their last, so it has landed before the
+    // epilogue on every path
+    const float bv = *(a.down_bias ? a.down_bias + (int64_t)e * a.n_embd + min(row, a.n_embd - 1)
+                                   : (const float*)a.xq_a);
+    for (int q0 = 0;; q0 += GRP_TPI) {  // the item's tokens q0 .. q0 + n - 1
+      const int n = min(GRP_TPI, z - q0);
+      int tg = 0;
+      do {
+        const int tok = tg * 4 + ((lane & 15) >> 2);
+        const int pr = __shfl(my_pair, q0 + min(tok, n - 1), 64);
+        mx_load_b_at<DC_S, false, 4, true>(R, a.xq_a + (int64_t)pr * xs, 0, s0, s1);
+        asm volatile("" ::: "memory");  // all steps' loads go out before the first step's MFMAs wait on one
+        v4f D[4] = {};
+        mx_compute<DC_S>(R, a.gdn, s0, s1, D);
+        mx_sum_terms<4>(D);
+        if ((lane & 3) == 0 && tok < n) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) *(v4f*)(&red[c][tok][16 * g + 4 * (lane >> 4)]) = D[g];
+        }
+      } while (++tg * 4 < n);
+      // an opaque copy: the compiler does not hoist the bias's first use to the unit's start, where a wait on it
+      // is a wait on the weights issued before it
+      float b = bv;
+      asm volatile("" : "+v"(b));
+      b = a.down_bias ? b : 0.f;
+      auto epilogue = [&]() {
+        for (int w = c; w < n; w += a.cdg) {  // token q0 + w of the item: chunk 0 with the bias, then the others
+          float y = red[0][w][lane] + b;
+          for (int cc = 1; cc < a.cdg; ++cc) y += red[cc][w][lane];
+          const int pr = __builtin_amdgcn_readlane(my_pair, q0 + w);
+          if (row < a.n_embd) a.y[(int64_t)pr * a.n_embd + row] = y;
+        }
+      };
+      const bool more = q0 + GRP_TPI < z;  // more tokens: the weights stay
+      if (!more && Ln >= hi) {  // (a path of its own: the weight registers are not live into a merge with reloaded ones)
+        lds_barrier();
+        epilogue();
+        return;
+      }
+      int4 item_n;
+      int tile_n = 0, e_n = 0, pair_n = 0;
+      if (!more) {  // the next unit's weights and pair list go out before this unit's last epilogue
+        item_n = int4{__builtin_amdgcn_readlane(iw_n, 0), __builtin_amdgcn_readlane(iw_n, 1),
+                      __builtin_amdgcn_readlane(iw_n, 2), 0};
+        tile_n = Ln - (Ln / tiles) * tiles;
+        e_n = clamp_expert(item_n.x, a.E);
+        pair_n = a.sorted[item_n.y + min(lane, item_n.z - 1)];  // (ahead of the weights, as above)
+        mx_load_a_flat<DC_S>(R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e_n, tile_n),
+                             a.gdn, s0, s1);
+      }
+      lds_barrier();
+      epilogue();
+      lds_barrier();  // the epilogue's reads of red come before the next tokens' (unit's) writes
+      if (more) continue;
+      L = Ln;
+      ++round;
+      item = item_n;
+      tile = tile_n;
+      e = e_n;
+      my_pair = pair_n;
+      break;
+    }
   }
 }
 
@@ -3154,7 +3308,7 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.off_gu_items = o;
   o = al(o + (int64_t)p.max_gu_items * 16);
   p.off_gu_bounds = o;
-  o = al(o + (p.max_gu_items ? 9 * 4 : 0));
+  o = al(o + (p.max_gu_items ? 18 * 4 : 0));  // gate/up, then down
   p.off_sorted = o;
   o = al(o + (p.grouped ? P * 4 : 0));
   p.off_corder = o;
@@ -3334,6 +3488,7 @@ static MoeDev make_dev(const nsx_moe_layer* L, const MoePlan& p, char* ws, const
   d.n_items = (int*)(ws + p.off_nitems);
   d.gu_items = (int4*)(ws + p.off_gu_items);
   d.gu_bounds = (int*)(ws + p.off_gu_bounds);
+  d.dn_bounds = d.gu_bounds + 9;
   d.sorted = (int32_t*)(ws + p.off_sorted);
   d.corder = (int32_t*)(ws + p.off_corder);
   d.y = (float*)(ws + p.off_y);
@@ -3421,7 +3576,13 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     }
     if (on(NSX_PHASE_DOWN)) {
       if (t64) {
-        rc = nsx_launch(moe_down_grouped_kernel, grid8(p.gdn.tiles), dim3(64 * p.cdg), 0, st, d);
+        // persistent (the resident workgroups, a multiple of 8) when its units can number GRP_DN_PERSIST times
+        // the resident workgroups, else one workgroup per (GRP_TPI-token item, tile)
+        const int64_t r = std::max<int64_t>(
+            8, nsx_resident_workgroups((const void*)moe_down_persistent_kernel, 0, 64 * p.cdg) / 8 * 8);
+        rc = (int64_t)p.max_gu_items * p.gdn.tiles >= GRP_DN_PERSIST * r
+                 ? nsx_launch(moe_down_persistent_kernel, dim3((unsigned)r), dim3(64 * p.cdg), 0, st, d)
+                 : nsx_launch(moe_down_grouped_kernel, grid8(p.gdn.tiles), dim3(64 * p.cdg), 0, st, d);
       } else if (p.mq) {
         if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
                              (int)L->n_ff, d.xq_a)))
