@@ -2854,6 +2854,26 @@ typedef float mq_f4 __attribute__((ext_vector_type(4)));
 // hi[K], lo[K] (f16), sub-block sums hi[K/32], lo[K/32] (f16), 2^e (f32),
 // padding to 16 bytes.
 __host__ __device__ constexpr int64_t mq_row_bytes(int64_t K) { return 4 * K + K / 8 + 16; }
+// LDS bytes per staged row: whole 1 KB pieces (a direct load's 64 lanes x 16 bytes) and 16 bytes of padding, so
+// that consecutive rows do not start in the same bank
+__host__ __device__ constexpr int64_t mq_lds_row(int64_t K) { return (mq_row_bytes(K) + 1023) / 1024 * 1024 + 16; }
+
+// The term rows of n tokens (n <= MQ_LDS_NT; row w at src(w), tb bytes, a multiple of 16) into LDS at xs + w * tsb
+// by direct loads, each wave instruction one 1 KB piece (lane i: bytes 16 i of it); lanes past the row's end re-read
+// its last 16 bytes into the row's padding. The loads write LDS without registers and are counted by vmcnt: a wave
+// waits on its own, then the workgroup meets at a barrier.
+template <class Src>
+__device__ __forceinline__ void mq_stage_lds(uint8_t* xs, int tsb, int n, int tb, Src src) {
+  typedef const void __attribute__((address_space(1)))* gptr;
+  typedef void __attribute__((address_space(3)))* lptr;
+  const int wave = (int)(threadIdx.x >> 6), lane = __lane_id(), nw = (int)(blockDim.x >> 6);
+  const int nc = (tb + 1023) >> 10;
+  for (int c = wave; c < n * nc; c += nw) {
+    const int w = c / nc, k = c - w * nc;
+    const int off = min(k * 1024 + lane * 16, tb - 16);
+    __builtin_amdgcn_global_load_lds((gptr)(src(w) + off), (lptr)(xs + w * tsb + k * 1024), 16, 0, 0);
+  }
+}
 
 // One workgroup per row of x (K columns): x' = x * 2^-e with max |x'| < 512,
 // hi = f16(x'), lo = f16(x' - hi); the 32-element sums of x' likewise (< 2^14,
@@ -3041,8 +3061,10 @@ __device__ __forceinline__ void mq_superblock2_lds(const v4u& H0, const v4u& QA0
 // into y (moe_combine_kernel adds a token's pairs in ascending expert id).
 // Workgroup = (item, 64 rows), wave = 16 rows over all of K.
 template <bool GU>
-__global__ __launch_bounds__(256, 3) void moe_q4k_mfma_kernel(MoeDev a) {  // (three waves per SIMD)
-  extern __shared__ __align__(16) uint8_t mq_xs[];  // MQ_LDS_NT * (mq_row_bytes(K) + 16): sized at launch
+__global__ __launch_bounds__(256, GU ? 2 : 3) void moe_q4k_mfma_kernel(MoeDev a) {
+  // (waves per SIMD: gate/up's staged rows allow two workgroups per CU, so it takes the registers of two waves per
+  // SIMD; down three)
+  extern __shared__ __align__(16) uint8_t mq_xs[];  // MQ_LDS_NT * mq_lds_row(K): sized at launch
   const int NR = GU ? a.n_ff : a.n_embd, K = GU ? a.n_embd : a.n_ff;
   int tile;
   int4 item;
@@ -3127,7 +3149,7 @@ __global__ __launch_bounds__(256, 3) void moe_q4k_mfma_kernel(MoeDev a) {  // (t
   // tracked apart from the weight loads, so nothing waits on a prefetch.
   // Larger items read each super-block's terms from L2 (through the buffer
   // loads above).
-  const int tsb = (int)tb + 16;  // LDS bytes per token row (16 bytes of padding: rows start 8 banks apart)
+  const int tsb = (int)mq_lds_row(K);  // LDS bytes per token row
   const uint8_t* xrow = mq_xs + min(lr, n - 1) * tsb;
   const int lane_off = 2 * (64 * (g >> 1) + 16 * (g & 1));
   auto run = [&](auto blds) {
@@ -3173,14 +3195,22 @@ __global__ __launch_bounds__(256, 3) void moe_q4k_mfma_kernel(MoeDev a) {  // (t
       }
     };
     W w[AHEAD + 1];
+    // the staged rows go out first (in flight together, no registers), then the weight prefetch; a wave waits on
+    // its staging loads alone -- every load after them is a weight load of known count
+    if constexpr (BLDS)
+      mq_stage_lds(mq_xs, tsb, n, (int)tb, [&](int w) { return tbase + (int64_t)__shfl(brow, w, 64) * tb; });
     if (r0 < NR) {
 #pragma unroll
       for (int j = 0; j < AHEAD; ++j) load_w(j, w[j]);
     }
     if constexpr (BLDS) {
-      q4k_stage_terms(mq_xs, 0, n, (int)(tb / 16), [&](int w) { return tbase + (int64_t)__shfl(brow, w, 64) * tb; },
-                      tsb / 16);
-      __syncthreads();
+      constexpr int NW = AHEAD * 6;  // buffer loads per load_w
+      static_assert(NW < 16, "the wait below encodes vmcnt in its low four bits");
+      if (r0 < NR)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | NW);  // vmcnt(NW), expcnt and lgkmcnt not waited on
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      grp_lds_barrier();  // (a workgroup fence would wait on the weight loads too)
     }
     if (r0 >= NR) return;
     // step sb computes super-block sb and requests sb + AHEAD into the buffer sb - 1 used; one exit, and
@@ -3561,7 +3591,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
                              (uint8_t*)(ws + p.off_xqh))))
           return rc;
         rc = nsx_launch(moe_q4k_mfma_kernel<true>, grid8(nsx_cdiv(L->n_ff, MQ_WG_ROWS)), dim3(256),
-                        (size_t)(MQ_LDS_NT * (mq_row_bytes(L->n_embd) + 16)), st, d);
+                        (size_t)(MQ_LDS_NT * mq_lds_row(L->n_embd)), st, d);
       } else {  // Q4_K on the int8 dot: the tokens' activation terms, then the rows
         if ((rc = nsx_launch(a8_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))
@@ -3588,7 +3618,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
                              (int)L->n_ff, d.xq_a)))
           return rc;
         rc = nsx_launch(moe_q4k_mfma_kernel<false>, grid8(nsx_cdiv(L->n_embd, 2 * MQ_WG_ROWS)), dim3(256),
-                        (size_t)(MQ_LDS_NT * (mq_row_bytes(L->n_ff) + 16)), st, d);
+                        (size_t)(MQ_LDS_NT * mq_lds_row(L->n_ff)), st, d);
       } else {
         if ((rc = nsx_launch(a8_terms_kernel, dim3((unsigned)P), dim3(256), 0, st, (const float*)d.act,
                              (int)L->n_ff, d.xq_a)))
