@@ -1475,19 +1475,26 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     int isc = sc, isn = sn, ia[4] = {acc[0], acc[1], acc[2], acc[3]}, id[4] = {acd[0], acd[1], acd[2], acd[3]};
     for (int d = 1; d < 64; d <<= 1) {
       const int oc = __shfl_up(isc, d, 64), on = __shfl_up(isn, d, 64);
-      int oa[4], od[4];
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        oa[b] = __shfl_up(ia[b], d, 64);
-        od[b] = __shfl_up(id[b], d, 64);
-      }
       if (lane >= d) {
         isc += oc;
         isn += on;
+      }
+    }
+    const bool gi = a.gu_items != nullptr;  // (t64 layers only: the MXFP4 grouped kernels' items and XCD runs)
+    if (gi) {
+      for (int d = 1; d < 64; d <<= 1) {
+        int oa[4], od[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          ia[b] += oa[b];
-          id[b] += od[b];
+          oa[b] = __shfl_up(ia[b], d, 64);
+          od[b] = __shfl_up(id[b], d, 64);
+        }
+        if (lane >= d) {
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            ia[b] += oa[b];
+            id[b] += od[b];
+          }
         }
       }
     }
@@ -1510,7 +1517,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
       if (e < E) {
         s_off[e] = bc;
         for (int q = 0; q < ni[i]; ++q) a.items[bn + q] = grp_item(e, bc, cn[i], q);
-        const int nf = cn[i] / GRP_GU_T, zr = cn[i] - nf * GRP_GU_T;
+        const int nf = gi ? cn[i] / GRP_GU_T : 0, zr = gi ? cn[i] - nf * GRP_GU_T : 0;
         const int cf = grp_gu_cost(GRP_GU_T), df = grp_dn_cost(GRP_GU_T);
         for (int q = 0; q < nf; ++q) {
           a.gu_items[base_n[3] + q] = make_int4(e, bc + q * GRP_GU_T, GRP_GU_T, 0);
@@ -1533,7 +1540,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
       bc += cn[i];
       bn += ni[i];
     }
-    if (lane == 0) {
+    if (gi && lane == 0) {
       s_pc[0][tn] = tc;
       s_pc[1][tn] = td;
     }
@@ -1542,7 +1549,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     // of the total: unit t of item k (cost prefix P_k, unit cost q_k = P_k+1 - P_k) starts at nt P_k + t q_k for
     // nt units per item. The item is the last one with 8 P_k <= x total, found by bisection over the prefixes
     // (ascending; LDS operations of one wave complete in order).
-    if (lane < 16) {
+    if (gi && lane < 16) {
       const int g = lane >> 3, x = lane & 7;
       const int nt = g ? (int)a.gdn.tiles : tiles, tot = g ? td : tc;
       int L = x == 0 || tn == 0 ? 0 : tn * nt;  // (x = 0: 0; an empty sort: 0)
@@ -3317,7 +3324,7 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.cdg = std::max(1, std::min(p.gdn.ns, 4));  // grouped down: 4 row groups x cdg chunks
   p.sdg = (int)nsx_cdiv(p.gdn.ns, p.cdg);
   p.max_items = p.grouped ? grp_max_items(L->n_expert, (int)P) : 0;
-  p.max_gu_items = p.grouped ? grp_max_items(L->n_expert, (int)P, GRP_GU_T) : 0;  // (moe_sort_kernel writes them)
+  p.max_gu_items = p.grouped && t64 ? grp_max_items(L->n_expert, (int)P, GRP_GU_T) : 0;
   auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
   int64_t o = 0;
   p.off_logits = o;
@@ -3516,9 +3523,9 @@ static MoeDev make_dev(const nsx_moe_layer* L, const MoePlan& p, char* ws, const
   d.limit = L->limit;
   d.items = (int4*)(ws + p.off_items);
   d.n_items = (int*)(ws + p.off_nitems);
-  d.gu_items = (int4*)(ws + p.off_gu_items);
-  d.gu_bounds = (int*)(ws + p.off_gu_bounds);
-  d.dn_bounds = d.gu_bounds + 9;
+  d.gu_items = p.max_gu_items ? (int4*)(ws + p.off_gu_items) : nullptr;  // (null: the sort makes no such items)
+  d.gu_bounds = p.max_gu_items ? (int*)(ws + p.off_gu_bounds) : nullptr;
+  d.dn_bounds = p.max_gu_items ? d.gu_bounds + 9 : nullptr;
   d.sorted = (int32_t*)(ws + p.off_sorted);
   d.corder = (int32_t*)(ws + p.off_corder);
   d.y = (float*)(ws + p.off_y);
