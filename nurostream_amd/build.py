@@ -31,6 +31,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
     # kernel arguments preloaded into SGPRs at wave launch (gfx950), not fetched by the first instructions
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
+    # one-lane atomics stay one atomic: the optimizer's wave-wide rewrite reads the result at once, a wait on
+    # every load issued before it (the grouped gate/up kernel takes its next unit while its weights load)
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -741,6 +741,7 @@ struct MoeDev {
   int4* gu_items;        // the MXFP4 gate/up kernel's work items: (expert, first sorted position, tokens, 0)
   int* gu_bounds;        // [9]: XCD x runs gate/up units [gu_bounds[x], gu_bounds[x + 1])
   int* dn_bounds;        // [9]: the same for the down kernel's units (same items, its own tiles)
+  int* gu_ctr;           // [8]: XCD x's gate/up units taken past its first two rounds (the sort zeroes them)
   int32_t* sorted;       // pair ids, ascending expert, ascending pair id inside
   int32_t* corder;       // per token: its pair ids in ascending expert id
   float* y;              // (pairs, n_embd) expert outputs, bias included
@@ -1566,6 +1567,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
       }
       (g ? a.dn_bounds : a.gu_bounds)[x] = L;
       if (x == 7) (g ? a.dn_bounds : a.gu_bounds)[8] = tn * nt;
+      if (g == 0) a.gu_ctr[x] = 0;
     }
   }
   __syncthreads();
@@ -1738,7 +1740,7 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   __shared__ float red[2][MAX_CHUNKS][GRP_TPI][64];
   __shared__ int4 s_items[SIN ? GRP_SMALL_P : 1];
   __shared__ int s_sorted[SIN ? GRP_SMALL_P : 1], s_cnt[SIN ? MAX_EXPERTS : 1], s_off[SIN ? MAX_EXPERTS : 1];
-  __shared__ int s_nitems;
+  __shared__ int s_nitems, s_next;
   __shared__ uint8_t s_exp[SIN ? GRP_SMALL_P : 1];
   if constexpr (SIN) grp_small_sort(a, s_items, s_sorted, &s_nitems, s_exp, s_cnt, s_off, blockIdx.x == 0);
   auto item_at = [&](int i) { return SIN ? s_items[i] : a.gu_items[i]; };
@@ -1750,7 +1752,10 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
   // XCD xcd's run of units [lo, hi): cost-weighted bounds from the sort (a small sort: equal counts); round r of
   // the run is units lo + r nx .. + nx - 1, taken in alternating directions, so that a workgroup given a costly
-  // unit in one round is given a cheap one in the next
+  // unit in one round is given a cheap one in the next. Past round 1 (not for a small sort, which launches no sort
+  // kernel to zero the counters), each workgroup takes units from the XCD's counter, one unit ahead: the run's
+  // heavy-first units go to whichever workgroups are free first. A workgroup's units ascend (a later take returns
+  // more), so it leaves the run at its first unit >= hi with no unit below hi still taken.
   int lo, hi;
   if constexpr (SIN) {
     const int live = tiles * s_nitems, per = (live + 7) / 8;
@@ -1761,7 +1766,7 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
     hi = a.gu_bounds[xcd + 1];
   }
   int round = 0;
-  int L = lo + j;
+  int L = lo + j, Ln = lo + nx + (nx - 1 - j);
   if (L >= hi) return;
   const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int s0 = c * a.sg, s1 = min(a.ggu.ns, s0 + a.sg);
@@ -1786,11 +1791,13 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
   };
   for (;;) {
     const int z = item.z;
-    const int Ln = lo + (round + 1) * nx + ((round & 1) ? j : nx - 1 - j);
+    if (SIN) Ln = lo + (round + 1) * nx + ((round & 1) ? j : nx - 1 - j);
     // the next unit's item, requested now so that it is at hand when this unit's MFMAs are done (the last unit
     // re-reads its own); lane i holds word i & 3 -- a lane-varying load stays in VGPRs, where nothing waits on
     // it before its fields are read after the token loop
     const int iw_n = item_word(min(Ln, hi - 1) / tiles, lane & 3);
+    int take = 0;  // the unit after the next one, from the counter (its answer lands with this unit's loads)
+    if (!SIN && threadIdx.x == 0) take = atomicAdd(a.gu_ctr + xcd, 1);
     const int row = tile * 64 + lane;
     const int rowc = min(row, a.n_ff - 1);
     // the biases go out with the first token group's activation terms, with no branch before any load (a branch
@@ -1853,6 +1860,7 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
         epilogue();
         return;
       }
+      if (!SIN && !more && threadIdx.x == 0) s_next = take;  // read after the barrier below; rewritten after the next
       int4 item_n;
       int tile_n = 0, e_n = 0, pair_n = 0;
       if (!more) {  // the next unit's weights and pair list go out before this unit's last epilogue
@@ -1867,10 +1875,12 @@ __global__ __launch_bounds__(64 * MAX_CHUNKS) void moe_gu_grouped_kernel(MoeDev 
         mx_load_a_flat<GU_S>(Ru, ut, a.ggu, s0, s1);
       }
       lds_barrier();
+      const int Lnn = SIN || more ? 0 : lo + 2 * nx + __builtin_amdgcn_readfirstlane(s_next);
       epilogue();
       lds_barrier();  // the epilogue's reads of red come before the next tokens' (unit's) writes
       if (more) continue;
       L = Ln;
+      if (!SIN) Ln = Lnn;
       ++round;
       item = item_n;
       tile = tile_n;
@@ -3345,7 +3355,7 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.off_gu_items = o;
   o = al(o + (int64_t)p.max_gu_items * 16);
   p.off_gu_bounds = o;
-  o = al(o + (p.max_gu_items ? 18 * 4 : 0));  // gate/up, then down
+  o = al(o + (p.max_gu_items ? 26 * 4 : 0));  // bounds: gate/up, down; then the gate/up counters
   p.off_sorted = o;
   o = al(o + (p.grouped ? P * 4 : 0));
   p.off_corder = o;
@@ -3526,6 +3536,7 @@ static MoeDev make_dev(const nsx_moe_layer* L, const MoePlan& p, char* ws, const
   d.gu_items = p.max_gu_items ? (int4*)(ws + p.off_gu_items) : nullptr;  // (null: the sort makes no such items)
   d.gu_bounds = p.max_gu_items ? (int*)(ws + p.off_gu_bounds) : nullptr;
   d.dn_bounds = p.max_gu_items ? d.gu_bounds + 9 : nullptr;
+  d.gu_ctr = p.max_gu_items ? d.gu_bounds + 18 : nullptr;
   d.sorted = (int32_t*)(ws + p.off_sorted);
   d.corder = (int32_t*)(ws + p.off_corder);
   d.y = (float*)(ws + p.off_y);
