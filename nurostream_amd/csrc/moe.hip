@@ -810,9 +810,11 @@ __device__ __forceinline__ float combine_one(float acc, float w, float y) { retu
 
 // (the table is read as constant memory: for a wave-uniform e that is a scalar
 // load, whose wait does not hold up the wave's vector loads in flight)
+// (the pointer tables are read as constants: scalar loads, whose waits do not
+// wait on the vector loads in flight, such as the pair list read just before)
+typedef const __attribute__((address_space(4))) uint64_t nsx_cu64;
 __device__ __forceinline__ const uint8_t* expert_base(const void* base, int64_t stride, const uint64_t* ptrs, int e) {
-  typedef const __attribute__((address_space(4))) uint64_t cu64;
-  return base ? (const uint8_t*)base + (int64_t)e * stride : (const uint8_t*)*((cu64*)ptrs + e);
+  return base ? (const uint8_t*)base + (int64_t)e * stride : (const uint8_t*)*((nsx_cu64*)ptrs + e);
 }
 
 // tile `tile` of expert e's t64 matrix: from the tile table when there is one
@@ -820,7 +822,7 @@ __device__ __forceinline__ const uint8_t* expert_base(const void* base, int64_t 
 // included), else at its offset in the expert
 __device__ __forceinline__ const uint8_t* tile_base(const void* base, int64_t stride, const uint64_t* ptrs,
                                                     const uint64_t* tiles, const MxGeom& G, int e, int tile) {
-  if (tiles) return (const uint8_t*)tiles[(int64_t)e * G.tiles + tile];
+  if (tiles) return (const uint8_t*)*((nsx_cu64*)tiles + (int64_t)e * G.tiles + tile);
   return expert_base(base, stride, ptrs, e) + (int64_t)tile * G.tile_bytes;
 }
 
