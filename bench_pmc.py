@@ -20,6 +20,13 @@ not split counters over runs):
   util    --pmc MfmaUtil VALUBusy  (rocprofv3's derived metrics:
           100 * sum(SQ_VALU_MFMA_BUSY_CYCLES) / (max(GRBM_GUI_ACTIVE) * SIMDs),
           100 * sum(SQ_ACTIVE_INST_VALU) / CUs / max(GRBM_GUI_ACTIVE))
+  mfma    --pmc SQ_INSTS_VALU_MFMA_F6F4 SQ_INSTS_VALU_MFMA_F8
+          SQ_INSTS_VALU_MFMA_I8 SQ_INSTS_VALU_MFMA_F32
+          SQ_INSTS_VALU_MFMA_MOPS_F8 SQ_INSTS_VALU_MFMA_MOPS_I8
+          SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE
+          (MFMA instructions by operand type -- the block-scaled FP4 x FP8
+          MFMA counts as F6F4 or F8 by its operand formats -- and the
+          matrix cores' busy cycles against the CUs' busy cycles)
 
 Every bench run ends with a plain 256 MiB device copy; its FETCH_SIZE and
 WRITE_SIZE against the 262,144 KiB it moves give the factors that turn the
@@ -52,6 +59,9 @@ PASSES = {
     "sq": ["--pmc", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_F6F4", "SQ_INSTS_VALU_MFMA_MOPS_F16",
            "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_WAVES", "GRBM_GUI_ACTIVE"],
     "util": ["--pmc", "MfmaUtil", "VALUBusy"],
+    "mfma": ["--pmc", "SQ_INSTS_VALU_MFMA_F6F4", "SQ_INSTS_VALU_MFMA_F8", "SQ_INSTS_VALU_MFMA_I8",
+             "SQ_INSTS_VALU_MFMA_F32", "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_I8",
+             "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE"],
 }
 DEFAULT_WORKLOADS = ("gptoss-decode", "gptoss-t128", "qwen3-t1", "qwen3-t32", "q4_0-gemv", "stack-t1", "stack-t8")
 # the stacks launch ~110 kernels a step: fewer steps keep the dispatches under counter collection few
@@ -132,6 +142,9 @@ def main() -> None:
     p.add_argument("--json", default=os.path.join(ROOT, "profiles", "pmc_traffic.json"))
     p.add_argument("--md", default=os.path.join(ROOT, "profiles", "pmc_counters.md"))
     p.add_argument("--timeout", type=int, default=150, help="seconds per pass")
+    p.add_argument("--merge", action="store_true",
+                   help="keep the workloads already in --json when it was made on the same sources (a sweep over "
+                        "several runs)")
     args = p.parse_args()
     sys.path.insert(0, ROOT)
     from bench import csrc_digest
@@ -140,11 +153,18 @@ def main() -> None:
            "--replays 3 (each workload's default steps; " + "; ".join(f"{w}: {' '.join(a)}" for w, a in STEPS.items())
            + ")", "passes": {k: " ".join(v) for k, v in PASSES.items()},
            "workloads": {}}
+    if args.merge and os.path.exists(args.json):
+        with open(args.json) as f:
+            old = json.load(f)
+        if old.get("csrc_digest") == doc["csrc_digest"] and old.get("passes") == doc["passes"]:
+            doc["workloads"] = old.get("workloads", {})
+        else:
+            print(f"[pmc] {args.json} was made on other sources or passes: starting afresh", flush=True)
     for w in args.workloads.split(","):
         got = {pas: run_pass(w, pas, args.raw, args.timeout) for pas in PASSES}
         stats = read_stats(got["trace"])
         cnt, calib = {}, {}
-        for pas in ("fetch", "write", "sq", "util"):
+        for pas in ("fetch", "write", "sq", "util", "mfma"):
             cnt[pas], calib[pas] = read_counters(got[pas])
         if "FETCH_SIZE" not in calib["fetch"] or "WRITE_SIZE" not in calib["write"]:
             raise RuntimeError(f"{w}: no {COPY_KERNEL} dispatch to calibrate the byte counters")
@@ -165,6 +185,8 @@ def main() -> None:
                 rec[c] = round(v, 1)
             for c, (v, _) in sorted(cnt["util"].get(k, {}).items()):
                 rec[c] = round(v, 3)
+            for c, (v, _) in sorted(cnt["mfma"].get(k, {}).items()):
+                rec["mfma_pass." + c if c in rec else c] = round(v, 1)
             kernels[k] = rec
         doc["workloads"][w] = {"fetch_factor": round(ff, 5), "write_factor": round(wf, 5), "kernels": kernels}
         with open(args.json, "w") as f:  # after every workload, so a later failure keeps what was measured
@@ -176,7 +198,7 @@ def main() -> None:
 def write_md(doc: dict, path: str) -> None:
     lines = ["# rocprofv3 counters per kernel and workload",
              "",
-             f"Made by `python bench_pmc.py` (sources digest {doc['csrc_digest']}): for each workload, five rocprofv3 "
+             f"Made by `python bench_pmc.py` (sources digest {doc['csrc_digest']}): for each workload, six rocprofv3 "
              f"runs of `bench.py --workload W {doc['bench_args']}`, one per pass:",
              ""]
     lines += [f"- {k}: `rocprofv3 {v} --output-format csv -- python3 bench.py ...`" for k, v in doc["passes"].items()]
@@ -188,13 +210,17 @@ def write_md(doc: dict, path: str) -> None:
               ""]
     for w, rec in doc["workloads"].items():
         lines += [f"## {w}", "", f"fetch factor {rec['fetch_factor']}, write factor {rec['write_factor']}", "",
-                  "| kernel | calls | avg us | traffic MB | VALU instr | MFMA instr | F6F4 MOPS | MfmaUtil % | VALUBusy % |",
-                  "|---|---|---|---|---|---|---|---|---|"]
+                  "| kernel | calls | avg us | traffic MB | VALU instr | MFMA instr | F6F4 / F8 / I8 / F32 MFMA instr "
+                  "| MFMA busy / CU busy cycles | MfmaUtil % | VALUBusy % |",
+                  "|---|---|---|---|---|---|---|---|---|---|"]
         for k, r in sorted(rec["kernels"].items(), key=lambda kv: -kv[1].get("avg_us", 0) * kv[1].get("calls", 0)):
             tb = r.get("traffic_bytes")
+            mix = " / ".join(str(r.get(f"SQ_INSTS_VALU_MFMA_{t}", "")) for t in ("F6F4", "F8", "I8", "F32"))
+            mb, cb = r.get("SQ_VALU_MFMA_BUSY_CYCLES"), r.get("SQ_BUSY_CU_CYCLES")
+            busy = f"{mb:.0f} / {cb:.0f}" if mb is not None and cb else ""
             lines.append(f"| `{k}` | {r.get('calls', '')} | {r.get('avg_us', '')} | "
                          f"{'' if tb is None else round(tb / 1e6, 2)} | {r.get('SQ_INSTS_VALU', '')} | "
-                         f"{r.get('SQ_INSTS_MFMA', '')} | {r.get('SQ_INSTS_VALU_MFMA_MOPS_F6F4', '')} | "
+                         f"{r.get('SQ_INSTS_MFMA', '')} | {mix} | {busy} | "
                          f"{r.get('MfmaUtil', '')} | {r.get('VALUBusy', '')} |")
         lines.append("")
     with open(path, "w") as f:

@@ -460,6 +460,46 @@ static int launch_topk(const float* logits, int64_t T, int64_t E, int k, int mod
 }
 
 
+// Bytes of one row of the Q4_K matrix-core kernels' activation terms for K
+// columns (K a multiple of 256): hi[K], lo[K] (f16), sub-block sums hi[K/32],
+// lo[K/32] (f16), 2^e (f32), padding to 16 bytes.
+__host__ __device__ constexpr int64_t mq_row_bytes(int64_t K) { return 4 * K + K / 8 + 16; }
+
+// One row x of K columns as those terms, by a workgroup of 256 threads (red:
+// 4 floats of LDS): x' = x * 2^-e with max |x'| < 512, hi = f16(x'), lo =
+// f16(x' - hi); the 32-element sums of x' likewise (< 2^14, inside f16's
+// range); then 2^e.
+__device__ __forceinline__ void mq_terms_row(const float* __restrict__ xr, int K, uint8_t* __restrict__ row,
+                                             float* red) {
+  _Float16* hi = (_Float16*)row;
+  _Float16* lo = hi + K;
+  _Float16* shi = lo + K;
+  _Float16* slo = shi + K / 32;
+  float mx = 0.f;
+  for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  if (mx > 0.f && mx <= 3.4e38f) (void)frexpf(mx, &ex);  // mx < 2^ex
+  const int e = ex - 9;
+  for (int k = threadIdx.x; k < K; k += 256) {
+    const float v = ldexpf(xr[k], -e);
+    const _Float16 h = (_Float16)v;
+    hi[k] = h;
+    lo[k] = (_Float16)(v - (float)h);
+  }
+  for (int sidx = threadIdx.x; sidx < K / 32; sidx += 256) {
+    float acc = 0.f;
+    for (int i = 0; i < 32; ++i) acc += ldexpf(xr[32 * sidx + i], -e);
+    const _Float16 h = (_Float16)acc;
+    shi[sidx] = h;
+    slo[sidx] = (_Float16)(acc - (float)h);
+  }
+  if (threadIdx.x == 0) *(float*)(slo + K / 32) = ldexpf(1.f, e);
+}
+
 // ---------------------------------------------------------------------------
 // Router logits for several tokens (T >= RM_MIN_T) as fp32 MFMA tiles.
 //
@@ -471,7 +511,8 @@ static int launch_topk(const float* logits, int64_t T, int64_t E, int k, int mod
 // a fixed order, adds the bias, writes the logits and selects the top-k. A
 // workgroup is 4 waves: one token tile, 4 adjacent expert tiles (their h
 // loads hit the same lines). Extra workgroups past the tiles build h's
-// activation terms (t64 layers), as in router_logits_kernel.
+// activation terms: the t64 layers' blocks, as in router_logits_kernel, or
+// (xq_mq) the Q4_K matrix-core kernels' term rows, a workgroup per token.
 //
 // Operand layout of v_mfma_f32_16x16x4f32: A[i][k] in lane i + 16 k, B[k][j]
 // in lane j + 16 k, D[i][j] in lane j + 16 (i / 4), register i % 4. Lane
@@ -503,9 +544,15 @@ __device__ __forceinline__ void load4_w(const void* W, int wdt, int64_t off, flo
 __global__ __launch_bounds__(64 * RM_EW) void router_mfma_kernel(const float* __restrict__ h, int T, int K,
                                                                  const void* __restrict__ W, int wdt, int E,
                                                                  float* __restrict__ part, int ntile,
-                                                                 uint8_t* __restrict__ xq) {
+                                                                 uint8_t* __restrict__ xq, int xq_mq) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
+  if (xq_mq && (int)blockIdx.x >= ntile) {  // token blockIdx.x - ntile's term row
+    __shared__ float red[4];
+    const int t = (int)blockIdx.x - ntile;
+    mq_terms_row(h + (int64_t)t * K, K, xq + (int64_t)t * mq_row_bytes(K), red);
+    return;
+  }
   if ((int)blockIdx.x >= ntile) {  // activation terms of h: RM_XQ tasks (two blocks each) per wave
     const int nb = K / 32, ns = (nb + 3) / 4, pairs = 2 * ns;
     const int64_t tasks = (int64_t)T * pairs;
@@ -617,12 +664,12 @@ static int rm_chunks(int64_t K) { return (int)nsx_cdiv(K, RM_KC); }
 
 static int launch_router_mfma(const float* h, int64_t T, int64_t K, const void* w, int wdt, const float* bias,
                               int64_t E, int k, int mode, float* part, float* logits, int32_t* ids, float* wts,
-                              uint8_t* xq, hipStream_t st) {
+                              uint8_t* xq, bool xq_mq, hipStream_t st) {
   const int64_t ntile = nsx_cdiv(E, 16 * RM_EW) * nsx_cdiv(T, 16) * rm_chunks(K);
   const int64_t xq_tasks = T * 2 * nsx_cdiv(K / 32, 4);
-  const int64_t grid = ntile + (xq ? nsx_cdiv(xq_tasks, (int64_t)RM_EW * RM_XQ) : 0);
+  const int64_t grid = ntile + (xq ? (xq_mq ? T : nsx_cdiv(xq_tasks, (int64_t)RM_EW * RM_XQ)) : 0);
   int rc = nsx_launch(router_mfma_kernel, dim3((unsigned)grid), dim3(64 * RM_EW), 0, st, h, (int)T, (int)K, w, wdt,
-                      (int)E, part, (int)ntile, xq);
+                      (int)E, part, (int)ntile, xq, (int)xq_mq);
   if (rc) return rc;
   return nsx_launch(router_reduce_kernel, dim3((unsigned)nsx_cdiv(T, 4)), dim3(256), 0, st, (const float*)part,
                     rm_chunks(K), (int)T, (int)E, bias, k, mode, logits, ids, wts);
@@ -2869,10 +2916,6 @@ typedef _Float16 mq_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mq_h2 __attribute__((ext_vector_type(2)));
 typedef float mq_f4 __attribute__((ext_vector_type(4)));
 
-// Bytes of one row of activation terms for K columns (K a multiple of 256):
-// hi[K], lo[K] (f16), sub-block sums hi[K/32], lo[K/32] (f16), 2^e (f32),
-// padding to 16 bytes.
-__host__ __device__ constexpr int64_t mq_row_bytes(int64_t K) { return 4 * K + K / 8 + 16; }
 // LDS bytes per staged row: whole 1 KB pieces (a direct load's 64 lanes x 16 bytes) and 16 bytes of padding, so
 // that consecutive rows do not start in the same bank
 __host__ __device__ constexpr int64_t mq_lds_row(int64_t K) { return (mq_row_bytes(K) + 1023) / 1024 * 1024 + 16; }
@@ -2894,41 +2937,11 @@ __device__ __forceinline__ void mq_stage_lds(uint8_t* xs, int tsb, int n, int tb
   }
 }
 
-// One workgroup per row of x (K columns): x' = x * 2^-e with max |x'| < 512,
-// hi = f16(x'), lo = f16(x' - hi); the 32-element sums of x' likewise (< 2^14,
-// inside f16's range); then 2^e.
+// One workgroup per row of x (K columns): the row's activation terms (mq_terms_row)
 __global__ __launch_bounds__(256) void mq_terms_kernel(const float* __restrict__ x, int K,
                                                        uint8_t* __restrict__ terms) {
   __shared__ float red[4];
-  const int64_t r = blockIdx.x;
-  const float* xr = x + r * K;
-  _Float16* hi = (_Float16*)(terms + r * mq_row_bytes(K));
-  _Float16* lo = hi + K;
-  _Float16* shi = lo + K;
-  _Float16* slo = shi + K / 32;
-  float mx = 0.f;
-  for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int ex = 0;
-  if (mx > 0.f && mx <= 3.4e38f) (void)frexpf(mx, &ex);  // mx < 2^ex
-  const int e = ex - 9;
-  for (int k = threadIdx.x; k < K; k += 256) {
-    const float v = ldexpf(xr[k], -e);
-    const _Float16 h = (_Float16)v;
-    hi[k] = h;
-    lo[k] = (_Float16)(v - (float)h);
-  }
-  for (int sidx = threadIdx.x; sidx < K / 32; sidx += 256) {
-    float acc = 0.f;
-    for (int i = 0; i < 32; ++i) acc += ldexpf(xr[32 * sidx + i], -e);
-    const _Float16 h = (_Float16)acc;
-    shi[sidx] = h;
-    slo[sidx] = (_Float16)(acc - (float)h);
-  }
-  if (threadIdx.x == 0) *(float*)(slo + K / 32) = ldexpf(1.f, e);
+  mq_terms_row(x + (int64_t)blockIdx.x * K, K, terms + (int64_t)blockIdx.x * mq_row_bytes(K), red);
 }
 
 // A operands of one sub-block pair from its 8 code bytes (elements
@@ -3579,7 +3592,7 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
     if (T >= RM_MIN_T) {  // logits as MFMA tiles, then chunk sums + top-k
       rc = launch_router_mfma(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert, L->top_k,
                               L->router_mode, (float*)(ws + p.off_rpart), (float*)(ws + p.off_logits), ids, weights,
-                              t64 ? (uint8_t*)(ws + p.off_xqh) : nullptr, st);
+                              t64 || p.mq ? (uint8_t*)(ws + p.off_xqh) : nullptr, !t64 && p.mq, st);
       if (rc) return rc;
     } else {
       rc = launch_logits(h, T, L->n_embd, L->router_w, L->router_dtype, L->router_bias, L->n_expert,
@@ -3607,7 +3620,9 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         rc = sin ? nsx_launch(moe_gu_grouped_kernel<true>, grid, dim3(64 * p.cg), 0, st, d)
                  : nsx_launch(moe_gu_grouped_kernel<false>, grid, dim3(64 * p.cg), 0, st, d);
       } else if (p.mq) {
-        if ((rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
+        // h's term rows: from the matrix-core router's extra workgroups when it ran in this call
+        if (!(on(NSX_PHASE_ROUTER) && T >= RM_MIN_T) &&
+            (rc = nsx_launch(mq_terms_kernel, dim3((unsigned)T), dim3(256), 0, st, h, (int)L->n_embd,
                              (uint8_t*)(ws + p.off_xqh))))
           return rc;
         rc = nsx_launch(moe_q4k_mfma_kernel<true>, grid8(nsx_cdiv(L->n_ff, MQ_WG_ROWS)), dim3(256),

@@ -165,12 +165,15 @@ def test_qwen3_layer_decode(dev):
                                                     ("qwen3-small", "gguf", 2, "auto"),
                                                     ("qwen3-small", "gguf", 17, "auto"),
                                                     ("qwen3-small", "gguf", 3, "mfma"),
+                                                    ("qwen3-small", "gguf", 20, "mfma"),
                                                     ("q4_0-small", "gguf", 3, "auto")])
 def test_router_phase_alone_writes_ids(dev, name, layout, T, dispatch):
     """NSX_PHASE_ROUTER run on its own leaves the ids and weights written for
     every layout and dispatch (a caller reads them to queue expert block reads
     before the gate/up phase), equal to what the whole forward writes; the
-    later phases then give the forward's output."""
+    later phases then give the forward's output. (Matrix-core Q4_K at T=20:
+    the forward's router builds h's term rows, the gate/up phase called alone
+    builds them itself -- the same bits.)"""
     from nurostream_amd import _native as N
     from nurostream_amd import synth
     cfg = _small(name)
