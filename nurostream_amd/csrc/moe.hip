@@ -524,7 +524,7 @@ constexpr int RM_MIN_T = 16;  // tokens from which the MFMA router runs
 constexpr int RM_KC = 128;    // K per chunk (8 steps of 16)
 constexpr int RM_EW = 4;      // expert tiles (waves) per workgroup
 constexpr int RM_XQ = 2;      // h block pairs quantized per wave
-constexpr int RM_RB = 16;     // partials per expert slot loaded at once in router_reduce_kernel
+constexpr int RM_RB = 32;     // partials per expert slot loaded at once in router_reduce_kernel (K <= 4096: one round)
 
 __device__ __forceinline__ void load4_w(const void* W, int wdt, int64_t off, float (&w)[4]) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
