@@ -677,7 +677,9 @@ def stack_workload(args, torch, N, synth, dev, stack=None, cpu_cache=None):
         per_layer = [len(torch.unique(ids_cpu[li])) for li in range(n_layers)]
         gu_bytes = sum(_expert_bytes(cfg, d)[0] for d in per_layer) / n_layers
         grouped = args.dispatch == "grouped" or (args.dispatch == "auto" and T >= 3)
-        kname = "moe_gu_chain_kernel" if chain else "moe_gu_grouped_kernel" if grouped else "moe_gu_kernel"
+        # (a gate/up phase launched on its own sorts in moe_sort_kernel, so the grouped phase runs the <false> kernel;
+        # the stack's forward, which also runs the router, takes <true>)
+        kname = ("moe_gu_chain_kernel" if chain else "moe_gu_grouped_kernel<false>" if grouped else "moe_gu_kernel")
         achieved = gu_bytes / (gu_us * 1e-6) / 1e9
         step_alg = sum(sum(_expert_bytes(cfg, d)) for d in per_layer)
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
