@@ -138,6 +138,38 @@ def test_config3_gptoss_t128_zipf(dev):
     print(f"config 3: {distinct} distinct experts, max rel err {err:.2e} over 128 tokens", flush=True)
 
 
+def test_config3_graph_replays_bit_stable(dev):
+    """The config 3 layer captured as a graph: the gate/up workgroups past the
+    first two rounds take units from per-XCD counters that the sort kernel zeroes
+    on every launch, so each replay -- back to back, and after eager forwards of
+    other tokens on the same workspace -- gives the eager output bit for bit."""
+    from nurostream_amd import synth
+    cfg = synth.GPTOSS_120B
+    t, _ = synth.make_zipf_layer(cfg, seed=0, device=dev)
+    lg = _layer(cfg, t, "t64", dispatch="grouped")
+    h = synth.activations(128, cfg.n_embd, seed=5, device=dev)
+    h2 = synth.activations(128, cfg.n_embd, seed=6, device=dev)
+    ref = [x.clone() for x in lg(h)]
+    out, ids, wts = torch.empty_like(ref[0]), torch.empty_like(ref[1]), torch.empty_like(ref[2])
+    lg(h, out=out, ids=ids, weights=wts)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        lg(h, out=out, ids=ids, weights=wts)
+    for i in range(4):
+        out.zero_()
+        ids.fill_(-1)
+        if i % 2:
+            lg(h2)  # eager work on the same workspace between replays
+        torch.cuda.synchronize()
+        g.replay()
+        if i == 3:
+            g.replay()  # and two replays back to back
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref[0]) and torch.equal(ids, ref[1]) and torch.equal(wts, ref[2]), i
+
+
 def _q4k_pair_and_grouped(cfg, t):
     return _layer(cfg, t, "gguf", dispatch="pairs"), _layer(cfg, t, "gguf", dispatch="grouped")
 
