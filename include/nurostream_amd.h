@@ -312,7 +312,7 @@ int nsx_add_rmsnorm(const float *x, const float *r, int64_t T, int64_t n,
  * DMA copy on `stream` (host-to-device from pinned memory, or any direct
  * copy), then `event` (a hipEvent_t, may be NULL) is recorded on the stream.
  * The block prefetcher's host-to-device step: io/stream.py:200-216
- * submit_rows and compute/blockffn.py:341-378 (SURVEY's copy_block_async).
+ * submit_rows and the block copy of compute/blockffn.py:341-378.
  * nsx_gather_copy: the same for device-to-device segments (16-byte aligned
  * addresses and sizes), as one kernel per 128 segments. Every destination
  * (and gather source) range is checked to lie inside one device allocation
