@@ -2106,15 +2106,23 @@ __global__ __launch_bounds__(256, 2) void moe_down_persistent_kernel(MoeDev a) {
 }
 
 // out[t, row] = sum over t's pairs in ascending expert id of w * y (grid: rows/256 x T)
+template <int KMAX>  // top_k <= KMAX: the token's pair indices in one round of loads, then their weights and rows
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev a) {
-  const int t = blockIdx.y, row = blockIdx.x * 256 + threadIdx.x;
-  if (row >= a.n_embd) return;
-  float o = 0.f;
-  for (int jj = 0; jj < a.top_k; ++jj) {
-    const int p = a.corder[t * a.top_k + jj];
-    o = combine_one(o, a.wts[p], a.y[(int64_t)p * a.n_embd + row]);
+  const int t = blockIdx.y, row = min((int)(blockIdx.x * 256 + threadIdx.x), a.n_embd - 1), k = a.top_k;
+  int pj[KMAX];
+  float wj[KMAX], yj[KMAX];
+#pragma unroll
+  for (int jj = 0; jj < KMAX; ++jj) pj[jj] = a.corder[t * k + min(jj, k - 1)];
+#pragma unroll
+  for (int jj = 0; jj < KMAX; ++jj) {
+    wj[jj] = a.wts[pj[jj]];
+    yj[jj] = a.y[(int64_t)pj[jj] * a.n_embd + row];
   }
-  a.out[(int64_t)t * a.n_embd + row] = o;
+  float o = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < KMAX; ++jj)
+    if (jj < k) o = combine_one(o, wj[jj], yj[jj]);
+  if ((int)(blockIdx.x * 256 + threadIdx.x) < a.n_embd) a.out[(int64_t)t * a.n_embd + row] = o;
 }
 
 // The combine fused with the next block's residual add and norm (a stacked
@@ -3672,8 +3680,10 @@ static int moe_run(const nsx_moe_layer* L, const float* h, int64_t T, float* out
         rc = L->top_k <= 4 ? nsx_launch(moe_combine_norm_kernel<4>, dim3((unsigned)T), dim3(1024), 0, st, d, *an)
                            : nsx_launch(moe_combine_norm_kernel<MAX_TOPK>, dim3((unsigned)T), dim3(1024), 0, st, d, *an);
       else
-        rc = nsx_launch(moe_combine_kernel, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T), dim3(256), 0, st,
-                        d);
+        rc = L->top_k <= 4 ? nsx_launch(moe_combine_kernel<4>, dim3((unsigned)nsx_cdiv(L->n_embd, 256), (unsigned)T),
+                                        dim3(256), 0, st, d)
+                           : nsx_launch(moe_combine_kernel<MAX_TOPK>, dim3((unsigned)nsx_cdiv(L->n_embd, 256),
+                                        (unsigned)T), dim3(256), 0, st, d);
       if (rc) return rc;
     }
     return NSX_OK;
