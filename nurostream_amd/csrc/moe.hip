@@ -1455,14 +1455,18 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     }
     __syncthreads();
   }
-  // each pair's expert and its token's combine slot
-  auto expert_of = [&](int p) { return a.topk_in_sort ? (int)s_exp[p] : clamp_expert(a.ids[p], E); };
+  // each pair's expert (one round of loads) into LDS, then its token's combine slot from there
   int pe[(GRP_MAX_PAIRS + 1023) / 1024];
 #pragma unroll
   for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i) {
     const int p = tid + 1024 * i;
-    pe[i] = p < P ? expert_of(p) : 0;
+    pe[i] = p < P ? (a.topk_in_sort ? (int)s_exp[p] : clamp_expert(a.ids[p], E)) : 0;
   }
+  __syncthreads();  // (every read of s_exp above is done before it is written)
+#pragma unroll
+  for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i)
+    if (tid + 1024 * i < P) s_exp[tid + 1024 * i] = (uint8_t)pe[i];
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i) {
     const int p = tid + 1024 * i;
@@ -1471,16 +1475,11 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     const int e = pe[i];
     int rank = 0;
     for (int jj = 0; jj < k; ++jj) {
-      const int ej = expert_of(t * k + jj);
+      const int ej = s_exp[t * k + jj];
       rank += (ej < e || (ej == e && jj < j)) ? 1 : 0;
     }
     a.corder[t * k + rank] = p;
   }
-  __syncthreads();  // (every expert_of read of s_exp is done before it is written)
-#pragma unroll
-  for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i)
-    if (tid + 1024 * i < P) s_exp[tid + 1024 * i] = (uint8_t)pe[i];
-  __syncthreads();
   for (int c = wave; c < nch; c += 16) {  // per-chunk counts (one lane per expert present writes)
     const int p = c * 64 + lane;
     const int e = p < P ? s_exp[p] : 0;
