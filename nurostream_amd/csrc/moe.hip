@@ -789,6 +789,7 @@ struct MoeDev {
   int* gu_bounds;        // [9]: XCD x runs gate/up units [gu_bounds[x], gu_bounds[x + 1])
   int* dn_bounds;        // [9]: the same for the down kernel's units (same items, its own tiles)
   int* gu_ctr;           // [8]: XCD x's gate/up units taken past its first two rounds (the sort zeroes them)
+  int* dn_ctr;           // [9]: the same for the persistent down kernel, then its workgroups done (the last resets all)
   int32_t* sorted;       // pair ids, ascending expert, ascending pair id inside
   int32_t* corder;       // per token: its pair ids in ascending expert id
   float* y;              // (pairs, n_embd) expert outputs, bias included
@@ -1408,8 +1409,13 @@ __device__ __forceinline__ int4 grp_unit(int4 rec, int s, int L, int units, int&
 // 2.6 m us. A pass past the first is not hidden under the next unit's weight
 // stream, so a unit of 64 tokens costs about four of one token.
 __host__ __device__ __forceinline__ int grp_gu_cost(int z) { return 12 + z + 8 * ((z + GRP_TPI - 1) / GRP_TPI); }
-// The same for a down unit (half the weight bytes of a gate/up unit, an epilogue of fp32 stores).
-__host__ __device__ __forceinline__ int grp_dn_cost(int z) { return 10 + z + 3 * ((z + GRP_TPI - 1) / GRP_TPI); }
+// The same for a down unit (half the weight bytes of a gate/up unit; a token's
+// activation terms, 4.5 bytes per element, outweigh them): per-unit stamps of
+// config 3 fit about 7.3 + 0.51 z - 2.3 m us (a pass past the first costs less
+// per token), and of the forms 10 + z + 3m, 12 + z, 14 + z - 4m, 18 + z - 6m and
+// 22 + z - 9m the third gave the shortest step (0.5 us below the first; the last
+// two put too much on the XCD of the heavy items)
+__host__ __device__ __forceinline__ int grp_dn_cost(int z) { return 14 + z - 4 * ((z + GRP_TPI - 1) / GRP_TPI); }
 
 // lanes of this wave whose (valid) expert equals this lane's
 __device__ __forceinline__ uint64_t grp_match(bool valid, int e) {
@@ -1615,7 +1621,8 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
       }
       (g ? a.dn_bounds : a.gu_bounds)[x] = L;
       if (x == 7) (g ? a.dn_bounds : a.gu_bounds)[8] = tn * nt;
-      if (g == 0) a.gu_ctr[x] = 0;
+      (g ? a.dn_ctr : a.gu_ctr)[x] = 0;
+      if (lane == 15) a.dn_ctr[8] = 0;
     }
   }
   __syncthreads();
@@ -1752,7 +1759,10 @@ __device__ void grp_small_sort(const MoeDev& a, int4* s_items, int* s_sorted, in
       if (writer) *a.n_items = isn;
     }
     const int live_d = __shfl(isb, 63, 64) * (int)a.gdn.tiles, per_d = (live_d + 7) / 8;
-    if (writer && lane <= 8) a.dn_bounds[lane] = min(live_d, lane * per_d);  // the down kernel's runs: equal counts
+    if (writer && lane <= 8) {  // the down kernel's runs (equal counts) and its counters
+      a.dn_bounds[lane] = min(live_d, lane * per_d);
+      a.dn_ctr[lane] = 0;
+    }
   }
   grp_lds_barrier();
   if (wave == 0 && lane < P) {  // stable scatter
@@ -2009,12 +2019,23 @@ __global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(MoeDev a) {
 // y[pair, rows] = the expert's down product plus its bias.
 __global__ __launch_bounds__(256, 2) void moe_down_persistent_kernel(MoeDev a) {
   __shared__ float red[4][GRP_TPI][64];  // [wave = chunk][token][row of the tile]
+  __shared__ int s_next;
   const int tiles = (int)a.gdn.tiles;
   const int nx = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
   const int lo = a.dn_bounds[xcd], hi = a.dn_bounds[xcd + 1];
-  int L = lo + j;
-  if (L >= hi) return;
-  int round = 0;
+  // a workgroup leaving counts itself out; the last one to leave zeroes the counters for the next launch (no
+  // workgroup takes a unit after it has counted itself out, so none is in use then). A down phase may run again
+  // without a sort, so the kernel leaves its counters as it found them.
+  auto leave = [&]() {
+    if (threadIdx.x == 0 && atomicAdd(a.dn_ctr + 8, 1) == (int)gridDim.x - 1) {
+      for (int i = 0; i < 9; ++i) atomicExch(a.dn_ctr + i, 0);
+    }
+  };
+  int L = lo + j, Ln = lo + nx + (nx - 1 - j);
+  if (L >= hi) {
+    leave();
+    return;
+  }
   const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   const int s0 = c * a.sdg, s1 = min(a.gdn.ns, s0 + a.sdg);
   const int64_t xs = (int64_t)a.gdn.ns * XQ_STEP;
@@ -2034,9 +2055,10 @@ __global__ __launch_bounds__(256, 2) void moe_down_persistent_kernel(MoeDev a) {
   };
   for (;;) {
     const int z = item.z;
-    const int Ln = lo + (round + 1) * nx + ((round & 1) ? j : nx - 1 - j);
     // the next unit's item (lane i: word i & 3), requested now so that it is at hand after the token loop
     const int iw_n = ((const int*)a.gu_items)[4 * (min(Ln, hi - 1) / tiles) + (lane & 3)];
+    int take = 0;  // the unit after the next one, from the XCD's counter (its answer lands with this unit's loads)
+    if (threadIdx.x == 0) take = atomicAdd(a.dn_ctr + xcd, 1);
     const int row = tile * 64 + lane;
     // this lane's bias, with no branch before any load (a layer without biases reads a word of xq_a instead);
     // the token loops run at least once and wait on every load before their last, so it has landed before the
@@ -2076,8 +2098,10 @@ __global__ __launch_bounds__(256, 2) void moe_down_persistent_kernel(MoeDev a) {
       if (!more && Ln >= hi) {  // (a path of its own: the weight registers are not live into a merge with reloaded ones)
         lds_barrier();
         epilogue();
+        leave();
         return;
       }
+      if (!more && threadIdx.x == 0) s_next = take;  // read after the barrier below; rewritten after the next
       int4 item_n;
       int tile_n = 0, e_n = 0, pair_n = 0;
       if (!more) {  // the next unit's weights and pair list go out before this unit's last epilogue
@@ -2090,11 +2114,12 @@ __global__ __launch_bounds__(256, 2) void moe_down_persistent_kernel(MoeDev a) {
                              a.gdn, s0, s1);
       }
       lds_barrier();
+      const int Lnn = more ? 0 : lo + 2 * nx + __builtin_amdgcn_readfirstlane(s_next);
       epilogue();
       lds_barrier();  // the epilogue's reads of red come before the next tokens' (unit's) writes
       if (more) continue;
       L = Ln;
-      ++round;
+      Ln = Lnn;
       item = item_n;
       tile = tile_n;
       e = e_n;
@@ -3377,7 +3402,7 @@ static MoePlan moe_plan(const nsx_moe_layer* L, int64_t T) {
   p.off_gu_items = o;
   o = al(o + (int64_t)p.max_gu_items * 16);
   p.off_gu_bounds = o;
-  o = al(o + (p.max_gu_items ? 26 * 4 : 0));  // bounds: gate/up, down; then the gate/up counters
+  o = al(o + (p.max_gu_items ? 35 * 4 : 0));  // bounds: gate/up, down; then the gate/up and down counters
   p.off_sorted = o;
   o = al(o + (p.grouped ? P * 4 : 0));
   p.off_corder = o;
@@ -3559,6 +3584,7 @@ static MoeDev make_dev(const nsx_moe_layer* L, const MoePlan& p, char* ws, const
   d.gu_bounds = p.max_gu_items ? (int*)(ws + p.off_gu_bounds) : nullptr;
   d.dn_bounds = p.max_gu_items ? d.gu_bounds + 9 : nullptr;
   d.gu_ctr = p.max_gu_items ? d.gu_bounds + 18 : nullptr;
+  d.dn_ctr = p.max_gu_items ? d.gu_bounds + 26 : nullptr;
   d.sorted = (int32_t*)(ws + p.off_sorted);
   d.corder = (int32_t*)(ws + p.off_corder);
   d.y = (float*)(ws + p.off_y);

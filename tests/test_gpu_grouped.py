@@ -168,6 +168,17 @@ def test_config3_graph_replays_bit_stable(dev):
             g.replay()  # and two replays back to back
         torch.cuda.synchronize()
         assert torch.equal(out, ref[0]) and torch.equal(ids, ref[1]) and torch.equal(wts, ref[2]), i
+    # phase by phase on one workspace, the down phase three times over: its persistent kernel takes units from
+    # counters that no sort zeroes in between, so each launch must leave them as it found them
+    from nurostream_amd import _native as N
+    ws = lg.new_workspace(128)
+    out2, ids2, wts2 = torch.full_like(out, float("nan")), torch.full_like(ids, -1), torch.empty_like(wts)
+    for ph in (N.PHASE_ROUTER, N.PHASE_GATE_UP, N.PHASE_DOWN, N.PHASE_DOWN, N.PHASE_DOWN, N.PHASE_COMBINE):
+        lg.phase(ph, h, out2, ids2, wts2, ws)
+        if ph == N.PHASE_DOWN:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref[0]) and torch.equal(ids2, ref[1])
 
 
 def _q4k_pair_and_grouped(cfg, t):
