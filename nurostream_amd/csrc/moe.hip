@@ -3259,8 +3259,11 @@ __global__ __launch_bounds__(256, GU ? 2 : 3) void moe_q4k_mfma_kernel(MoeDev a)
       }
     };
     W w[AHEAD + 1];
-    // the staged rows go out first (in flight together, no registers), then the weight prefetch; a wave waits on
-    // its staging loads alone -- every load after them is a weight load of known count
+    // the staged rows go out first (in flight together, no registers), then the weight prefetch. A wave then
+    // waits on all of them, the first weights included: until a vmcnt(0) retires the direct-to-LDS loads, the
+    // compiler counts them as loads of another kind whose order against the weight loads it does not know, and
+    // waits vmcnt(0) at each use of a weight register in the loop below -- one drain of the prefetch per round
+    // of steps instead of one per workgroup (config 4 T=32: 0.346 -> 0.337 ms per step)
     if constexpr (BLDS)
       mq_stage_lds(mq_xs, tsb, n, (int)tb, [&](int w) { return tbase + (int64_t)__shfl(brow, w, 64) * tb; });
     if (r0 < NR) {
@@ -3268,13 +3271,8 @@ __global__ __launch_bounds__(256, GU ? 2 : 3) void moe_q4k_mfma_kernel(MoeDev a)
       for (int j = 0; j < AHEAD; ++j) load_w(j, w[j]);
     }
     if constexpr (BLDS) {
-      constexpr int NW = AHEAD * 6;  // buffer loads per load_w
-      static_assert(NW < 16, "the wait below encodes vmcnt in its low four bits");
-      if (r0 < NR)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | NW);  // vmcnt(NW), expcnt and lgkmcnt not waited on
-      else
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      grp_lds_barrier();  // (a workgroup fence would wait on the weight loads too)
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt not waited on
+      grp_lds_barrier();
     }
     if (r0 >= NR) return;
     // step sb computes super-block sb and requests sb + AHEAD into the buffer sb - 1 used; one exit, and
