@@ -548,10 +548,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
       for (int g = 0; g < XQ; ++g) xv[g] = ((const v4f*)x)[min((int)threadIdx.x + g * THREADS, nq - 1)];
       issue(0, S0);
       if constexpr (GV_DEPTH > 1) issue(nitems > 1 ? 1 : 0, S1);
+      // the write is unpredicated (a thread past the end rewrites the last float4 with its own value): under
+      // a branch, x's load sinks into the branch, behind the rows' loads, and its wait then waits on every
+      // row byte
 #pragma unroll
       for (int g = 0; g < XQ; ++g) {
-        const int q = (int)threadIdx.x + g * THREADS;
-        if (q < nq) *(v4f*)(xs + GV_XPAD * (q >> 3) + 4 * (q & 7)) = xv[g];
+        const int q = min((int)threadIdx.x + g * THREADS, nq - 1);
+        *(v4f*)(xs + GV_XPAD * (q >> 3) + 4 * (q & 7)) = xv[g];
       }
     }
     lds_barrier();
@@ -589,7 +592,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
     // every wave has its x in registers before any wave overwrites the area with row bytes
     __builtin_amdgcn_s_waitcnt(0xc07f);
     asm volatile("s_barrier" ::: "memory");
-    if (r0 >= n_rows) return;
   }
   float acc[NT];
 #pragma unroll
@@ -624,7 +626,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         float v = nsx_wave_sum(acc[t]);
-        if (lane == 0 && t < T) {
+        if (lane == 0 && t < T && r < n_rows) {  // (r >= n_rows: a wave past the last row, below)
           // epilogue in the reference's order: resid + (x @ W.T + bias)
           if (bias) v += bias[r];
           if (resid) v = resid[(int64_t)t * ystride + r] + v;
@@ -636,6 +638,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_raw_kernel(
   };
   if constexpr (GV_DEPTH == 1) {
     for (int k = 0; k < nitems; ++k) step(k, S0);
+  } else if constexpr (XREG) {
+    // the first item outside any branch, so its loads (issued before x's staging) are used on every path:
+    // under a branch, the compiler sinks them past the LDS barriers into it, behind x's round trip. A wave
+    // past the last row runs it on the clamped in-range bytes it loaded and stores nothing.
+    step(0, S0);
+    for (int k = 1; k < nitems; k += 2) {
+      step(k, S1);
+      if (k + 1 < nitems) step(k + 1, S0);
+    }
   } else {
     for (int k = 0; k < nitems; k += 2) {
       step(k, S0);
