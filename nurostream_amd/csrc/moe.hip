@@ -995,9 +995,10 @@ constexpr int DC_STAGE = (DC_PIECES + 63) / 64;  // of them per lane
 
 struct DownItem {
   MxRegs<DC_S, 1> R;
-  v4f bias;
+  v4f bias;  // as loaded; used where bias_on
   int item, t, hh, tile, rg, p, s0, s1, id_l;
   float my_w;
+  bool bias_on;
 };
 
 // Decode chain (T = 1): what the down kernel's lanes need past the combine --
@@ -1034,12 +1035,14 @@ __device__ __forceinline__ void down_begin(const MoeDev& a, int item, DownItem& 
   for (int i = 0; i < DC_STAGE; ++i) stage[i] = *(gv4u*)(xsrc + (int64_t)min(lane + 64 * i, npc - 1) * 16);
   d.id_l = clamp_expert(id_raw, a.E);
   const int e = __builtin_amdgcn_readlane(d.id_l, j);
-  mx_load_a<DC_S, 1>(d.R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, d.tile), a.gdn,
-                     d.s0, d.s1, d.rg);
+  mx_load_a_flat<DC_S, 1>(d.R, tile_base(a.down_base, a.down_stride, a.down_ptrs, a.down_tiles, a.gdn, e, d.tile),
+                          a.gdn, d.s0, d.s1, d.rg);
   const int r0 = d.tile * 64 + 16 * d.rg + 4 * (lane >> 4);
-  d.bias = v4f{0.f, 0.f, 0.f, 0.f};  // chunk 0's bias rows, requested while the weights stream
-  if (c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd)
-    d.bias = *(const v4f*)(a.down_bias + (int64_t)e * a.n_embd + r0);
+  // chunk 0's bias rows, requested while the weights stream: loaded on every lane (a lane without a bias row
+  // reads the activation terms' first bytes) and selected where used -- a load under a branch merges into
+  // a copy that waits for it, and for every weight load before it
+  d.bias_on = c == 0 && a.down_bias && (lane & 15) == 0 && r0 < a.n_embd;
+  d.bias = *(const v4f*)(d.bias_on ? a.down_bias + (int64_t)e * a.n_embd + r0 : (const float*)a.xq_a);
 #pragma unroll
   for (int i = 0; i < DC_STAGE; ++i) {  // (clamped duplicates rewrite the same bytes)
     const int pc = min(lane + 64 * i, npc - 1);
@@ -1058,7 +1061,7 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
   v4f D[1] = {};
   mx_compute<DC_S, 1>(d.R, a.gdn, d.s0, d.s1, D, d.rg);
   mx_sum_terms<1>(D);
-  if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = D[0] + d.bias;
+  if ((lane & 15) == 0) *(v4f*)(&red[wave][4 * (lane >> 4)]) = d.bias_on ? D[0] + d.bias : D[0];
   // chain: waves 1 .. nlg compute the next layer's router shares from this item's rows (each combines them too)
   const int nlg = CHAIN && a.cn_w ? (a.cn_E + 63) >> 6 : 0;
   // wave 0 (and the share waves), while the others finish: the slots in ascending expert id
@@ -1119,7 +1122,7 @@ __device__ __forceinline__ void down_end(const MoeDev& a, DownItem& d, float (&r
         if (lane == 0) a.cp_out[(int64_t)a.cp_groups * a.cn_E + d.item] = q;
       }
     } else {
-      const float xw = live ? xn * ch->w : 0.f;
+      const float xw = live ? (a.cn_norm_w ? xn * ch->w : xn) : 0.f;
       float acc = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -1205,7 +1208,7 @@ __global__ __launch_bounds__(1024) void moe_down_chain_kernel(MoeDev a) {
   const int r0 = d.tile * 64 + 16 * d.rg;
   const int row = min(r0 + (lane & 15), a.n_embd - 1);
   ch.x = a.cx[(int64_t)d.t * a.n_embd + row];
-  ch.w = a.cn_norm_w ? a.cn_norm_w[row] : 1.f;
+  ch.w = (a.cn_norm_w ? a.cn_norm_w : a.cx)[row];  // (no norm weight: unused, read from x)
   const int nlg = a.cn_w ? (a.cn_E + 63) >> 6 : 0;
   if (wave >= 1 && wave <= nlg) {  // router row e over the item's rows (n_embd % 16 == 0: all 16 inside the row,
                                     // or none: a group of the last tile past n_embd)

@@ -303,7 +303,10 @@ __device__ __forceinline__ void mx_load_b(MxRegs<S, G>& R, const uint8_t* __rest
 
 // mx_load_a and mx_load_b (global activation terms) of the same steps,
 // interleaved step by step: the loads retire in issue order, so step u's
-// MFMAs wait only for steps 0..u, weights and activations alike.
+// MFMAs wait only for steps 0..u, weights and activations alike. No branch
+// between the steps' loads (s1 > s0): steps past s1 reload step s1 - 1, which
+// mx_compute skips -- with a branch per step the compiler waits at each merge
+// for the loads before it, and the steps' loads go out one round trip apart.
 template <int S, int G = 4>
 __device__ __forceinline__ void mx_load_ab(MxRegs<S, G>& R, const uint8_t* __restrict__ tile, const MxGeom& G_,
                                            int s0, int s1, const uint8_t* __restrict__ xq, int xs0,
@@ -319,19 +322,17 @@ __device__ __forceinline__ void mx_load_ab(MxRegs<S, G>& R, const uint8_t* __res
   const uint8_t* xst = xtok + XQ_CODES + (grp * XQ_NT + term) * 4;
 #pragma unroll
   for (int u = 0; u < S; ++u) {
-    const int s = s0 + u;
-    if (s < s1) {
-      const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
-      const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
-      const int la = grp < rs ? lane : 16 * rs - 1;
+    const int s = min(s0 + u, s1 - 1);
+    const int rs = s < G_.ns - 1 ? 4 : G_.rlast;
+    const uint8_t* ch = tile + (int64_t)s * MX_STEP_BYTES;
+    const int la = grp < rs ? lane : 16 * rs - 1;
 #pragma unroll
-      for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
-      R.SA[u] = mx_load_sa<G>(ch, rs, lane, g0);
-      const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
-      R.B0[u] = *(gv4u*)(xt + xo);
-      R.B1[u] = *(gv4u*)(xt + xo + 16);
-      R.SB[u] = *(gu32*)(xst + xo);
-    }
+    for (int g = 0; g < G; ++g) R.A[u][g] = __builtin_nontemporal_load((gv4u*)(ch + (g0 + g) * rs * 256 + la * 16));
+    R.SA[u] = mx_load_sa<G>(ch, rs, lane, g0);
+    const int64_t xo = (int64_t)(s - xs0) * XQ_STEP;
+    R.B0[u] = *(gv4u*)(xt + xo);
+    R.B1[u] = *(gv4u*)(xt + xo + 16);
+    R.SB[u] = *(gu32*)(xst + xo);
   }
 }
 

@@ -121,16 +121,19 @@ def test_forward_addnorm_short_last_pass(dev, name, layout, T):
     assert torch.equal(xo, xr) and torch.equal(ho, hr)
 
 
-def test_decode_chain_matches_separate_norm_and_oracle(dev):
+@pytest.mark.parametrize("router_dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_decode_chain_matches_separate_norm_and_oracle(dev, router_dtype):
     """One token through a stack as a decode chain (nsx_moe_chain_t1: after the
     first layer no router launch; each down kernel leaves the next layer's
     router shares, each gate/up kernel sums them and quantizes h itself):
     the same routing as the separate-norm path and its outputs to rounding
     (non-unit norm weights), the oracle's chain within the MFMA bound (unit
-    weights), and graph replays bit-stable with eager work between them."""
+    weights), and graph replays bit-stable with eager work between them.
+    Each router weight dtype the down kernel converts (f32, bf16, f16)."""
+    import dataclasses
     from nurostream_amd import synth
     from nurostream_amd.model.gpt_oss import GptOssFFNStack
-    cfg = _small("gptoss-small")
+    cfg = dataclasses.replace(_small("gptoss-small"), router_dtype=router_dtype)
     L = 4
     stack = GptOssFFNStack.synthetic(cfg, L, seed=27, device=dev)
     assert all(layer.chain_share_bytes() > 0 for layer in stack.layers)
