@@ -2618,7 +2618,7 @@ __device__ __forceinline__ int q4k_gu_prologue(const MoeDev& a, int p, int r0, u
 // terms in xs. The item's activations (RPG of them, whole 16-element blocks)
 // meet in s_act, and the pair's activation terms for the down phase go out
 // from there.
-template <int LPR>
+template <int LPR, bool BIAS>
 __device__ __forceinline__ void q4k_gu_rows(const MoeDev& a, int p, int r0, int e, const uint8_t* xs,
                                             float* s_act) {
   constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * (64 / LPR);
@@ -2639,6 +2639,18 @@ __device__ __forceinline__ void q4k_gu_rows(const MoeDev& a, int p, int r0, int 
   };
 #pragma unroll
   for (int j = 0; j < Q4K_GU_AHEAD; ++j) load(j);
+  // BIAS (a layer with a gate or up bias): the rows' biases, behind the first rows' loads and unpredicated
+  // (a missing one reads the logits' first float, not used) -- a load under a branch, inside the loop or
+  // merging into it, waits for every row load before it
+  float gbv[Q4K_GU_STEPS], ubv[Q4K_GU_STEPS];
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int j = 0; j < Q4K_GU_STEPS; ++j) {
+      const int64_t o = (int64_t)e * a.n_ff + min(rw + j * RS, a.n_ff - 1);
+      gbv[j] = *(a.gate_bias ? a.gate_bias + o : a.logits);
+      ubv[j] = *(a.up_bias ? a.up_bias + o : a.logits);
+    }
+  }
   A8Pair X;
   a8_load(xs, q, nq, X);
 #pragma unroll
@@ -2655,8 +2667,10 @@ __device__ __forceinline__ void q4k_gu_rows(const MoeDev& a, int p, int r0, int 
     us = a8_group_sum<LPR>(live ? us : 0.f);
     const int row = rw + j * RS;
     if (lane % LPR == 0 && row < a.n_ff) {
-      if (a.gate_bias) gs += a.gate_bias[(int64_t)e * a.n_ff + row];
-      if (a.up_bias) us += a.up_bias[(int64_t)e * a.n_ff + row];
+      if constexpr (BIAS) {
+        if (a.gate_bias) gs += gbv[j];
+        if (a.up_bias) us += ubv[j];
+      }
       s_act[row - r0] = moe_act(a.act_kind, gs, us, a.alpha, a.limit);
     }
   }
@@ -2677,7 +2691,7 @@ __device__ __forceinline__ void q4k_gu_rows(const MoeDev& a, int p, int r0, int 
 
 // gate/up: workgroup = (pair, RPG rows); it writes the pair's activation terms
 // for those rows (the down kernel reads terms, not activations)
-template <int LPR>  // (16 waves: one workgroup per compute unit, VGPRs <= 128)
+template <int LPR, bool BIAS>  // (16 waves: one workgroup per compute unit, VGPRs <= 128)
 __global__ __launch_bounds__(1024) void moe_gu_q4k_kernel(MoeDev a) {
   constexpr int RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * (64 / LPR);
   __shared__ __align__(16) uint8_t xs[a8_bytes(Q4K_KMAX)];
@@ -2687,7 +2701,7 @@ __global__ __launch_bounds__(1024) void moe_gu_q4k_kernel(MoeDev a) {
   const int groups = (a.n_ff + RPG - 1) / RPG;
   const int p = blockIdx.x / groups, r0 = (blockIdx.x - p * groups) * RPG;
   const int e = q4k_gu_prologue(a, p, r0, xs, &s_e);
-  q4k_gu_rows<LPR>(a, p, r0, e, xs, s_act);
+  q4k_gu_rows<LPR, BIAS>(a, p, r0, e, xs, s_act);
 }
 
 // down and combine: workgroup = (token, RPG output rows), two waves per
@@ -2696,7 +2710,7 @@ __global__ __launch_bounds__(1024) void moe_gu_q4k_kernel(MoeDev a) {
 // loads; the slots' outputs are added in ascending expert id.
 constexpr int Q4K_DN_SLICES = (int)((a8_bytes(Q4K_KMAX) / 16 + 127) / 128);  // 16-byte term chunks per thread (k pairs, 128 k threads)
 
-template <int LPR>
+template <int LPR, bool BIAS>
 __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
   constexpr int RS = 64 / LPR, RPW = Q4K_DN_STEPS * RS, RPG = 2 * RPW;
   extern __shared__ __align__(16) uint8_t q4k_xa[];  // k vectors of terms
@@ -2741,6 +2755,11 @@ __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
   Q4kRow R[Q4K_DN_STEPS];
 #pragma unroll
   for (int j = 0; j < Q4K_DN_AHEAD; ++j) q4k_row_load(dm, min(rw + j * RS, a.n_embd - 1), rb, q, R[j]);
+  float bv[Q4K_DN_STEPS];  // BIAS: the rows' biases, as in the gate/up kernel
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int j = 0; j < Q4K_DN_STEPS; ++j) bv[j] = a.down_bias[(int64_t)e * a.n_embd + min(rw + j * RS, a.n_embd - 1)];
+  }
   A8Pair X;
   a8_load(q4k_xa + slot * a8_bytes(K), q, nq, X);
 #pragma unroll
@@ -2754,7 +2773,9 @@ __global__ __launch_bounds__(1024) void moe_down_q4k_kernel(MoeDev a) {
     y = a8_group_sum<LPR>(live ? y : 0.f);
     const int row = rw + j * RS;
     if (lane % LPR == 0) {
-      if (a.down_bias && row < a.n_embd) y += a.down_bias[(int64_t)e * a.n_embd + row];
+      if constexpr (BIAS) {
+        if (row < a.n_embd) y += bv[j];
+      }
       red[slot][row - r0] = y;
     }
   }
@@ -3484,10 +3505,12 @@ static int with_q4k_lpr(int K, F&& f) {
 static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, bool down) {
   const int64_t P = T * d.top_k;
   if (gate_up) {
+    const bool bias = d.gate_bias || d.up_bias;
     const int rc = with_q4k_lpr(d.n_embd, [&](auto lpr) {
       constexpr int LPR = decltype(lpr)::value, RPG = Q4K_GU_WAVES * Q4K_GU_STEPS * (64 / LPR);
-      return nsx_launch(moe_gu_q4k_kernel<LPR>, dim3((unsigned)(P * nsx_cdiv(d.n_ff, RPG))),
-                        dim3(64 * Q4K_GU_WAVES), 0, st, d);
+      const dim3 g((unsigned)(P * nsx_cdiv(d.n_ff, RPG))), b(64 * Q4K_GU_WAVES);
+      return bias ? nsx_launch(moe_gu_q4k_kernel<LPR, true>, g, b, 0, st, d)
+                  : nsx_launch(moe_gu_q4k_kernel<LPR, false>, g, b, 0, st, d);
     });
     if (rc) return rc;
   }
@@ -3495,11 +3518,11 @@ static int launch_q4k(const MoeDev& d, int64_t T, hipStream_t st, bool gate_up, 
   return with_q4k_lpr(d.n_ff, [&](auto lpr) {
     constexpr int LPR = decltype(lpr)::value, RPG = 2 * Q4K_DN_STEPS * (64 / LPR);
     const size_t lds = (size_t)d.top_k * (size_t)a8_bytes(d.n_ff);
-    if (lds > 64 * 1024)
-      NSX_HIP(hipFuncSetAttribute((const void*)moe_down_q4k_kernel<LPR>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds));
-    return nsx_launch(moe_down_q4k_kernel<LPR>, dim3((unsigned)(T * nsx_cdiv(d.n_embd, RPG))),
-                      dim3(128 * d.top_k), lds, st, d);
+    const void* k = d.down_bias ? (const void*)moe_down_q4k_kernel<LPR, true> : (const void*)moe_down_q4k_kernel<LPR, false>;
+    if (lds > 64 * 1024) NSX_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const dim3 g((unsigned)(T * nsx_cdiv(d.n_embd, RPG))), b(128 * d.top_k);
+    return d.down_bias ? nsx_launch(moe_down_q4k_kernel<LPR, true>, g, b, lds, st, d)
+                       : nsx_launch(moe_down_q4k_kernel<LPR, false>, g, b, lds, st, d);
   });
 }
 

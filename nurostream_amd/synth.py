@@ -109,7 +109,9 @@ def make_layer(cfg: MoEConfig, seed: int, device, layer: int = 0):
     g = generator(layer_seed(seed, layer), device)
     out = {}
     out["router_w"] = (torch.randn(cfg.n_expert, cfg.n_embd, generator=g, device=device) * 0.02).to(cfg.router_dtype)
-    out["router_b"] = (torch.randn(cfg.n_expert, generator=g, device=device) * 0.02) if cfg.bias else None
+    # a router bias where the router uses one (GPT-OSS's; Qwen3's router has none, moe/router.py:59-69)
+    rb = cfg.bias and cfg.router_mode == "gptoss"
+    out["router_b"] = (torch.randn(cfg.n_expert, generator=g, device=device) * 0.02) if rb else None
     for kind in ("gate", "up", "down"):
         rows, K = cfg.rows_K(kind)
         out[kind] = matrix_bytes(cfg.ggml_type, cfg.n_expert * rows, K, g, device)

@@ -57,6 +57,9 @@ def _small(name):
     if name == "qwen3-small":
         return synth.MoEConfig("qwen3-small", synth.GGMLType.Q4_K, 12, 8, 512, 256, "qwen3", "silu_mul", False,
                                torch.float32)
+    if name == "qwen3b-small":  # Q4_K with expert biases (a GGUF of a biased model, as GPT-OSS in Q4_K)
+        return synth.MoEConfig("qwen3b-small", synth.GGMLType.Q4_K, 12, 8, 512, 256, "qwen3", "silu_mul", True,
+                               torch.float32)
     if name == "q4_0-small":
         return synth.MoEConfig("q40-small", synth.GGMLType.Q4_0, 8, 2, 128, 96, "gptoss", "silu_mul", True,
                                torch.float32)

@@ -92,6 +92,7 @@ def test_router_mfma_tiles(dev, name, layout, T):
 @pytest.mark.parametrize("name,layout,slabs", [("gptoss-small", "t64", False), ("gptoss-small", "t64", True),
                                                ("gptoss-small", "gguf", False), ("gptoss-small", "gguf", True),
                                                ("qwen3-small", "gguf", False), ("qwen3-small", "gguf", True),
+                                               ("qwen3b-small", "gguf", False),
                                                ("q4_0-small", "gguf", False), ("q8_0-small", "gguf", False),
                                                ("q8_0-small", "gguf", True)])
 @pytest.mark.parametrize("T", [1, 2, 9])
@@ -108,6 +109,23 @@ def test_moe_small_layers(dev, name, layout, slabs, T):
     # a second call reuses the workspace
     out2, _, _ = layer(h.to(dev))
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dispatch,T", [("pairs", 1), ("pairs", 20), ("grouped", 20), ("mfma", 20)])
+def test_q4k_biases_every_dispatch(dev, dispatch, T):
+    """Q4_K experts with gate, up and down biases through each Q4_K path (the
+    per-pair int8-dot kernels, their grouped form, the matrix-core kernels)
+    against the oracle."""
+    from nurostream_amd import synth
+    cfg = _small("qwen3b-small")
+    t = synth.make_layer(cfg, seed=8, device=dev)
+    assert t["down_b"] is not None
+    layer = _layer(cfg, t, "gguf", dispatch=dispatch)
+    h = synth.activations(T, cfg.n_embd, seed=80 + T, device="cpu")
+    out, ids, w = layer(h.to(dev))
+    ref, rid, rw, rlog = _oracle_layer(cfg, t, h.numpy())
+    np.testing.assert_array_equal(np.sort(to_np(ids), 1), np.sort(rid, 1))
+    assert rel_max(to_np(out), ref) < _tol("gguf", cfg)
 
 
 N_DECODE = 8  # single-token calls per full-shape decode test
