@@ -469,35 +469,52 @@ __host__ __device__ constexpr int64_t mq_row_bytes(int64_t K) { return 4 * K + K
 // 4 floats of LDS): x' = x * 2^-e with max |x'| < 512, hi = f16(x'), lo =
 // f16(x' - hi); the 32-element sums of x' likewise (< 2^14, inside f16's
 // range); then 2^e.
+// K <= MQ_TR_MAXK; 256 threads; sx: K floats of LDS. Each thread's elements (k = thread + 256 i) are loaded
+// once, all in flight together (a loop with one load per pass waits a round trip per pass), then the max,
+// the terms and, from the scaled values staged in sx, the sub-block sums in element order.
+constexpr int MQ_TR_MAXK = 4096;
 __device__ __forceinline__ void mq_terms_row(const float* __restrict__ xr, int K, uint8_t* __restrict__ row,
-                                             float* red) {
+                                             float* red, float* sx) {
+  constexpr int NV = MQ_TR_MAXK / 256;
   _Float16* hi = (_Float16*)row;
   _Float16* lo = hi + K;
   _Float16* shi = lo + K;
   _Float16* slo = shi + K / 32;
+  const int tid = (int)threadIdx.x;
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = xr[min(tid + 256 * i, K - 1)];
   float mx = 0.f;
-  for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (tid + 256 * i < K) mx = fmaxf(mx, fabsf(v[i]));
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   int ex = 0;
   if (mx > 0.f && mx <= 3.4e38f) (void)frexpf(mx, &ex);  // mx < 2^ex
   const int e = ex - 9;
-  for (int k = threadIdx.x; k < K; k += 256) {
-    const float v = ldexpf(xr[k], -e);
-    const _Float16 h = (_Float16)v;
-    hi[k] = h;
-    lo[k] = (_Float16)(v - (float)h);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = tid + 256 * i;
+    if (k < K) {
+      const float vs = ldexpf(v[i], -e);
+      const _Float16 h = (_Float16)vs;
+      hi[k] = h;
+      lo[k] = (_Float16)(vs - (float)h);
+      sx[k] = vs;
+    }
   }
-  for (int sidx = threadIdx.x; sidx < K / 32; sidx += 256) {
+  __syncthreads();
+  for (int sidx = tid; sidx < K / 32; sidx += 256) {
     float acc = 0.f;
-    for (int i = 0; i < 32; ++i) acc += ldexpf(xr[32 * sidx + i], -e);
+    for (int i = 0; i < 32; ++i) acc += sx[32 * sidx + i];
     const _Float16 h = (_Float16)acc;
     shi[sidx] = h;
     slo[sidx] = (_Float16)(acc - (float)h);
   }
-  if (threadIdx.x == 0) *(float*)(slo + K / 32) = ldexpf(1.f, e);
+  if (tid == 0) *(float*)(slo + K / 32) = ldexpf(1.f, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -526,31 +543,36 @@ constexpr int RM_EW = 4;      // expert tiles (waves) per workgroup
 constexpr int RM_XQ = 2;      // h block pairs quantized per wave
 constexpr int RM_RB = 32;     // partials per expert slot loaded at once in router_reduce_kernel (K <= 4096: one round)
 
-__device__ __forceinline__ void load4_w(const void* W, int wdt, int64_t off, float (&w)[4]) {
+// (the dtype known at compile time: a run-time branch around the load converts inside the branch, and each
+// such load is waited for before the next one goes out)
+template <int WDT>
+__device__ __forceinline__ void load4_w(const void* W, int64_t off, float (&w)[4]) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
   typedef const __attribute__((address_space(1))) u32x2 gu2;
-  if (wdt == NSX_F32) {
+  if constexpr (WDT == NSX_F32) {
     const v4f a = *(gv4f*)((const float*)W + off);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   } else {
     const u32x2 q = *(gu2*)((const uint16_t*)W + off);
     const uint32_t v[4] = {q.x & 0xffffu, q.x >> 16, q.y & 0xffffu, q.y >> 16};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = wdt == NSX_BF16 ? nsx_bf2f(v[i]) : nsx_h2f(v[i]);
+    for (int i = 0; i < 4; ++i) w[i] = WDT == NSX_BF16 ? nsx_bf2f(v[i]) : nsx_h2f(v[i]);
   }
 }
 
+template <int WDT>
 __global__ __launch_bounds__(64 * RM_EW) void router_mfma_kernel(const float* __restrict__ h, int T, int K,
-                                                                 const void* __restrict__ W, int wdt, int E,
+                                                                 const void* __restrict__ W, int E,
                                                                  float* __restrict__ part, int ntile,
                                                                  uint8_t* __restrict__ xq, int xq_mq) {
   typedef const __attribute__((address_space(1))) v4f gv4f;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = __lane_id();
   if (xq_mq && (int)blockIdx.x >= ntile) {  // token blockIdx.x - ntile's term row
     __shared__ float red[4];
+    __shared__ float sx[MQ_TR_MAXK];
     const int t = (int)blockIdx.x - ntile;
-    mq_terms_row(h + (int64_t)t * K, K, xq + (int64_t)t * mq_row_bytes(K), red);
+    mq_terms_row(h + (int64_t)t * K, K, xq + (int64_t)t * mq_row_bytes(K), red, sx);
     return;
   }
   if ((int)blockIdx.x >= ntile) {  // activation terms of h: RM_XQ tasks (two blocks each) per wave
@@ -589,16 +611,22 @@ __global__ __launch_bounds__(64 * RM_EW) void router_mfma_kernel(const float* __
     const int k = k_lo + 16 * s + 4 * q;
     const int kk = k < k_hi ? k : k_hi - 4;  // (K is a multiple of 16: a chunk ends on a whole step)
     a[s] = *(gv4f*)(h + (int64_t)ti * K + kk);
-    load4_w(W, wdt, (int64_t)ei * K + kk, w[s]);
+    load4_w<WDT>(W, (int64_t)ei * K + kk, w[s]);
   }
+  // every step computed, those past the chunk's end on zeros (both operands: a weight may be infinite): a
+  // loop exit at the end would sink each step's loads into its own block, a round trip per step
   v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < RM_KC / 16; ++s) {
-    if (k_lo + 16 * s >= k_hi) break;
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].x, w[s][0], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].y, w[s][1], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].z, w[s][2], acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s].w, w[s][3], acc, 0, 0, 0);
+    const bool on = k_lo + 16 * s < k_hi;
+    const v4f as = on ? a[s] : v4f{0.f, 0.f, 0.f, 0.f};
+    float ws[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ws[i] = on ? w[s][i] : 0.f;
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(as.x, ws[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(as.y, ws[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(as.z, ws[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(as.w, ws[3], acc, 0, 0, 0);
   }
   const int e = e0 + (lane & 15);
 #pragma unroll
@@ -616,9 +644,14 @@ __device__ __forceinline__ void router_reduce_token(const float* __restrict__ pa
                                                     float* __restrict__ logits, int32_t* __restrict__ ids,
                                                     float* __restrict__ wts) {
   const int lane = __lane_id();
-  float acc[NV];
+  float acc[NV], bv[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+  for (int i = 0; i < NV; ++i) {
+    acc[i] = 0.f;
+    // the bias first, unpredicated (no bias: a partial, not used): behind a branch after the partials it
+    // would be one more round trip
+    bv[i] = *(bias ? bias + min(lane + 64 * i, E - 1) : part);
+  }
   for (int c0 = 0; c0 < nkc; c0 += RM_RB) {  // NV x RM_RB loads in flight, then the adds in chunk order
     float pv[NV][RM_RB];
 #pragma unroll
@@ -634,8 +667,7 @@ __device__ __forceinline__ void router_reduce_token(const float* __restrict__ pa
   float v[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int e = min(lane + 64 * i, E - 1);
-    v[i] = bias ? acc[i] + bias[e] : acc[i];
+    v[i] = bias ? acc[i] + bv[i] : acc[i];
     if (lane + 64 * i < E) logits[(int64_t)t * E + lane + 64 * i] = v[i];
   }
   int si[MAX_TOPK];
@@ -668,8 +700,13 @@ static int launch_router_mfma(const float* h, int64_t T, int64_t K, const void* 
   const int64_t ntile = nsx_cdiv(E, 16 * RM_EW) * nsx_cdiv(T, 16) * rm_chunks(K);
   const int64_t xq_tasks = T * 2 * nsx_cdiv(K / 32, 4);
   const int64_t grid = ntile + (xq ? (xq_mq ? T : nsx_cdiv(xq_tasks, (int64_t)RM_EW * RM_XQ)) : 0);
-  int rc = nsx_launch(router_mfma_kernel, dim3((unsigned)grid), dim3(64 * RM_EW), 0, st, h, (int)T, (int)K, w, wdt,
-                      (int)E, part, (int)ntile, xq, (int)xq_mq);
+  const dim3 g((unsigned)grid), b(64 * RM_EW);
+  int rc = wdt == NSX_F32    ? nsx_launch(router_mfma_kernel<NSX_F32>, g, b, 0, st, h, (int)T, (int)K, w, (int)E, part,
+                                          (int)ntile, xq, (int)xq_mq)
+           : wdt == NSX_BF16 ? nsx_launch(router_mfma_kernel<NSX_BF16>, g, b, 0, st, h, (int)T, (int)K, w, (int)E, part,
+                                          (int)ntile, xq, (int)xq_mq)
+                             : nsx_launch(router_mfma_kernel<NSX_F16>, g, b, 0, st, h, (int)T, (int)K, w, (int)E, part,
+                                          (int)ntile, xq, (int)xq_mq);
   if (rc) return rc;
   return nsx_launch(router_reduce_kernel, dim3((unsigned)nsx_cdiv(T, 4)), dim3(256), 0, st, (const float*)part,
                     rm_chunks(K), (int)T, (int)E, bias, k, mode, logits, ids, wts);
@@ -2534,6 +2571,7 @@ __global__ __launch_bounds__(64 * RAW_WAVES) void moe_down_raw_kernel(MoeDev a) 
 // kernels give identical bits.
 
 constexpr int Q4K_KMAX = 4096;   // K of the Q4_K kernels (nq <= 64)
+static_assert(Q4K_KMAX <= MQ_TR_MAXK, "mq_terms_row holds a row of K <= MQ_TR_MAXK");
 constexpr int Q4K_GU_WAVES = 16;
 constexpr int Q4K_GU_STEPS = 3;  // row steps of gate and of up per wave (per-pair kernel)
 constexpr int Q4K_GU_AHEAD = 2;  // steps whose loads are in flight before the first compute
@@ -2997,7 +3035,8 @@ __device__ __forceinline__ void mq_stage_lds(uint8_t* xs, int tsb, int n, int tb
 __global__ __launch_bounds__(256) void mq_terms_kernel(const float* __restrict__ x, int K,
                                                        uint8_t* __restrict__ terms) {
   __shared__ float red[4];
-  mq_terms_row(x + (int64_t)blockIdx.x * K, K, terms + (int64_t)blockIdx.x * mq_row_bytes(K), red);
+  __shared__ float sx[MQ_TR_MAXK];
+  mq_terms_row(x + (int64_t)blockIdx.x * K, K, terms + (int64_t)blockIdx.x * mq_row_bytes(K), red, sx);
 }
 
 // A operands of one sub-block pair from its 8 code bytes (elements
