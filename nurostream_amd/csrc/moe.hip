@@ -1502,11 +1502,14 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(MoeDev a) {
     __syncthreads();
   }
   // each pair's expert (one round of loads) into LDS, then its token's combine slot from there
-  int pe[(GRP_MAX_PAIRS + 1023) / 1024];
+  int pe[(GRP_MAX_PAIRS + 1023) / 1024], idv[(GRP_MAX_PAIRS + 1023) / 1024];
+#pragma unroll
+  for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i)  // every id load at once (clamped, unpredicated: under
+    idv[i] = a.ids[min(tid + 1024 * i, P - 1)];             // the branches below each would be a round trip)
 #pragma unroll
   for (int i = 0; i < (GRP_MAX_PAIRS + 1023) / 1024; ++i) {
     const int p = tid + 1024 * i;
-    pe[i] = p < P ? (a.topk_in_sort ? (int)s_exp[p] : clamp_expert(a.ids[p], E)) : 0;
+    pe[i] = p < P ? (a.topk_in_sort ? (int)s_exp[p] : clamp_expert(idv[i], E)) : 0;
   }
   __syncthreads();  // (every read of s_exp above is done before it is written)
 #pragma unroll
